@@ -1,0 +1,285 @@
+#!/usr/bin/env python3
+"""Benchmark of the hot path: FlashAttention fwd and fwd+bwd on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+Workload (BASELINE.json metric): (B, S, H, D) = (1, 4096, 16, 64), causal,
+fp16, synthetic N(0,1)*0.5 inputs already resident in HBM.  A step is one
+``flash_attn`` forward + ``.backward(dO)`` -- the same boundary as the
+reference's bench/backward.py:52-66 (autograd, delta pre-pass and all
+kernels inside the timed region).  FLOPs follow the reference convention,
+dense-counted even when causal: forward 4*B*H*S^2*D (bench/bench.py:69-71),
+fwd+bwd 5x that (bench/backward.py:89-91).
+
+Prints ONE JSON line on stdout.  `value` is the fwd+bwd TFLOP/s; the
+forward-only figure, per-kernel HIP-event timings with their MFMA-roofline
+fractions, and the CPU baseline (the reference's fp32 eager path, restated
+in oracle/, timed on this host's cores) ride along in the same object.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_PARENT = os.path.join(ROOT, "flash-attn-volta_amd")
+for _p in (ROOT, PKG_PARENT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "fwd & fwd+bwd TFLOP/s + % fp16 MFMA peak at (1,4096,16,64) causal fp16"
+PEAK_FP16_TFLOPS = 2516.6        # MI355X dense fp16 MFMA: 256 CU * 2.4 GHz * 4096 FLOP/clk
+PEAK_HBM_GBS = 8000.0
+B, S, H, D, CAUSAL = 1, 4096, 16, 64, True
+# Reference's published fwd+bwd figure for this exact shape and metric
+# (V100-SXM2, results/backward_bench.json:65-70).
+REF_FWD_BWD_TFLOPS = 61.83
+REF_FWD_TFLOPS = 59.68
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def fwd_flops(b, s, h, d):
+    return 4.0 * b * h * s * s * d
+
+
+def causal_useful_fwd_flops(b, s, h, d):
+    return 2.0 * b * h * d * s * (s + 1)
+
+
+def make_inputs(device):
+    import torch
+    g = torch.Generator(device="cpu").manual_seed(0)
+    shape = (B, S, H, D)
+    q, k, v, do = (torch.randn(shape, generator=g).half().mul_(0.5).to(device) for _ in range(4))
+    return q, k, v, do
+
+
+def time_loop(fn, steps, warmup):
+    """Wall-clock and HIP-event time of `steps` calls after `warmup` calls."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return wall / steps, e0.elapsed_time(e1) / 1e3 / steps
+
+
+def kernel_times(q, k, v, do, steps, warmup):
+    """Average duration per launch of each kernel, by HIP events around
+    back-to-back launches through the C ABI on torch's current stream
+    (which is the stream the kernels are launched on)."""
+    import torch
+    from flash_attn_volta import _capi, flash_attn_forward
+    from flash_attn_volta.forward import kernel_strides
+    lib = _capi.load()
+    out, lse = flash_attn_forward(q, k, v, causal=CAUSAL, return_softmax_lse=True)
+    delta = torch.empty((B, H, S), dtype=torch.float32, device=q.device)
+    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+    st = {name: kernel_strides(t) for name, t in
+          (("q", q), ("k", k), ("v", v), ("do", do), ("o", out), ("dq", dq), ("dk", dk), ("dv", dv))}
+    scale = 1.0 / math.sqrt(D)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def fwd():
+        _capi.check(lib.fa_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), None,
+                               B, S, H, D, st["q"], st["k"], st["v"], st["o"], scale, int(CAUSAL),
+                               stream), "fa_fwd")
+
+    def pre():
+        _capi.check(lib.fa_bwd_preprocess(out.data_ptr(), do.data_ptr(), delta.data_ptr(), B, S, H, D,
+                                          st["o"], st["do"], stream), "fa_bwd_preprocess")
+
+    def dkdv():
+        _capi.check(lib.fa_bwd_dkdv(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                    lse.data_ptr(), delta.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                    B, S, H, D, st["do"], st["q"], st["k"], st["v"], st["dk"], st["dv"],
+                                    scale, int(CAUSAL), stream), "fa_bwd_dkdv")
+
+    def dqk():
+        _capi.check(lib.fa_bwd_dq(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                  lse.data_ptr(), delta.data_ptr(), dq.data_ptr(),
+                                  B, S, H, D, st["do"], st["q"], st["k"], st["v"], st["dq"],
+                                  scale, int(CAUSAL), stream), "fa_bwd_dq")
+
+    pre()
+    base = 2.0 * B * H * S * S * D          # one dense S x S x D GEMM
+    io = B * S * H * D * 2                  # bytes of one fp16 (B,S,H,D) tensor
+    rows = B * H * S * 4                    # bytes of one fp32 (B,H,S) vector
+    table = [
+        # name, fn, kernel symbol, algorithmic dense FLOPs per launch, algorithmic HBM bytes
+        ("fwd", fwd, "fa_fwd_kernel<64, true, 4>", 2 * base, 4 * io),
+        ("bwd_preprocess", pre, "fa_bwd_preprocess_kernel<64>", 2.0 * B * H * S * D, 2 * io + rows),
+        ("bwd_dkdv", dkdv, "fa_bwd_dkdv_kernel<64, true, 4>", 4 * base, 6 * io + 2 * rows),
+        ("bwd_dq", dqk, "fa_bwd_dq_kernel<64, true, 4>", 3 * base, 5 * io + 2 * rows),
+    ]
+    res = {}
+    for name, fn, sym, flops, nbytes in table:
+        _, ev = time_loop(fn, steps, warmup)
+        res[name] = {"kernel": sym, "avg_us": ev * 1e6, "flops": flops, "bytes": nbytes,
+                     "tflops": flops / ev / 1e12, "gbs": nbytes / ev / 1e9}
+    return res
+
+
+def cpu_baseline(max_seconds=30.0):
+    """The reference's CPU path (ref.py eager fp32 attention, restated in
+    oracle/attention.py) timed on this host: fwd+bwd through autograd on the
+    full benchmark workload, 1 warmup + up to 3 timed iterations (median)."""
+    import torch
+    from oracle.attention import attention_ref_fp32
+    threads = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
+    torch.set_num_threads(threads)
+    g = torch.Generator(device="cpu").manual_seed(0)
+    q, k, v, do = (torch.randn((B, S, H, D), generator=g).half().mul_(0.5) for _ in range(4))
+    qs, ks, vs = (t.clone().requires_grad_() for t in (q, k, v))
+
+    def step():
+        qs.grad = ks.grad = vs.grad = None
+        out = attention_ref_fp32(qs, ks, vs, causal=CAUSAL)
+        out.backward(do)
+
+    t0 = time.perf_counter()
+    step()
+    first = time.perf_counter() - t0
+    n = max(1, min(3, int(max_seconds // max(first, 1e-3))))
+    ts = []
+    for _ in range(n):
+        t0 = time.perf_counter()
+        step()
+        ts.append(time.perf_counter() - t0)
+    t = statistics.median(ts)
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": 5.0 * fwd_flops(B, S, H, D) / t / 1e12,
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"full workload (1,4096,16,64) causal fwd+bwd through autograd of the fp32 "
+                   f"eager path; 1 warmup + {n} timed iteration(s), median {t:.2f} s"),
+        "seconds_per_step": t,
+        "host": {"cpu_model": model, "os_cpu_count": os.cpu_count(),
+                 "affinity": len(os.sched_getaffinity(0)), "platform": platform.platform()},
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}); "
+              "this build has no multi-GPU path, see DESIGN.md for how it would shard.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from flash_attn_volta import flash_attn, flash_attn_forward
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    q, k, v, do = make_inputs(dev)
+    qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
+
+    def fwd_bwd():
+        qg.grad = kg.grad = vg.grad = None
+        out = flash_attn(qg, kg, vg, causal=CAUSAL)
+        out.backward(do)
+
+    def fwd():
+        flash_attn_forward(q, k, v, causal=CAUSAL)
+
+    log(f"[bench] device={torch.cuda.get_device_name(0)} workload=(1,4096,16,64) causal fp16")
+    wall_fb, ev_fb = time_loop(fwd_bwd, args.steps, args.warmup)
+    log(f"[bench] fwd+bwd {ev_fb * 1e3:.3f} ms/step (events), {wall_fb * 1e3:.3f} ms (wall)")
+    wall_f, ev_f = time_loop(fwd, args.steps, args.warmup)
+    log(f"[bench] fwd {ev_f * 1e3:.3f} ms/step (events), {wall_f * 1e3:.3f} ms (wall)")
+    kt = kernel_times(q, k, v, do, args.steps, args.warmup)
+    for name, r in kt.items():
+        log(f"[bench] kernel {name:15s} {r['avg_us']:9.2f} us  {r['tflops']:8.1f} TFLOP/s  {r['gbs']:8.1f} GB/s")
+
+    flops_f = fwd_flops(B, S, H, D)
+    t_step = max(wall_fb, ev_fb)
+    t_fwd = max(wall_f, ev_f)
+    value = 5.0 * flops_f / t_step / 1e12
+    fwd_tf = flops_f / t_fwd / 1e12
+
+    step_kernels = ("bwd_preprocess", "bwd_dkdv", "bwd_dq", "fwd")
+    dom = max(step_kernels, key=lambda n: kt[n]["avg_us"])
+    d = kt[dom]
+    roofline = {"bound": "mfma", "achieved": d["tflops"], "peak": PEAK_FP16_TFLOPS,
+                "unit": "TFLOP/s", "frac": d["tflops"] / PEAK_FP16_TFLOPS, "traffic": None,
+                "kernel": d["kernel"], "avg_us": d["avg_us"],
+                "flops_per_launch": d["flops"]}
+    all_kernels = {n: {"kernel": r["kernel"], "avg_us": round(r["avg_us"], 3),
+                       "tflops": round(r["tflops"], 2), "frac_mfma": round(r["tflops"] / PEAK_FP16_TFLOPS, 4),
+                       "gbs": round(r["gbs"], 1), "frac_hbm": round(r["gbs"] / PEAK_HBM_GBS, 4)}
+                   for n, r in kt.items()}
+
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] timing the CPU baseline (fp32 eager attention, fwd+bwd) ...")
+        cpu = cpu_baseline()
+        log(f"[bench] cpu baseline {cpu['value']:.4f} TFLOP/s on {cpu['cores']} threads")
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(t_step * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(value / REF_FWD_BWD_TFLOPS, 3),
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {"workload": "flash_attn fwd+bwd step (autograd), (B,S,H,D)=(1,4096,16,64) causal",
+                   "B": B, "S": S, "H": H, "D": D, "causal": CAUSAL, "sm_scale": 1.0 / math.sqrt(D),
+                   "flops_convention": "fwd 4*B*H*S^2*D dense-counted, fwd+bwd 5x"},
+        "pct_peak": round(100.0 * value / PEAK_FP16_TFLOPS, 2),
+        "fwd": {"value": round(fwd_tf, 3), "unit": "TFLOP/s", "ms": round(t_fwd * 1e3, 4),
+                "pct_peak": round(100.0 * fwd_tf / PEAK_FP16_TFLOPS, 2),
+                "vs_baseline": round(fwd_tf / REF_FWD_TFLOPS, 3),
+                "causal_useful_tflops": round(causal_useful_fwd_flops(B, S, H, D) / t_fwd / 1e12, 3)},
+        "baseline": {"fwd_bwd": REF_FWD_BWD_TFLOPS, "fwd": REF_FWD_TFLOPS,
+                     "hardware": "V100-SXM2-32GB (reference's published numbers)"},
+        "roofline": roofline,
+        "kernels": all_kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

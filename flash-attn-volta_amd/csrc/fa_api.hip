@@ -1,0 +1,348 @@
+// fa_api.hip -- the extern "C" entry points declared in include/fa_mi355x.h.
+//
+// Each entry point validates its arguments on the host (before any HIP call,
+// so the checks behave the same without a GPU), picks the kernel
+// instantiation for (D, causal) and launches it asynchronously on the
+// caller's stream.  Nothing here allocates device memory.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+
+#include "../../include/fa_mi355x.h"
+#include "fa_bwd.hpp"
+#include "fa_fwd.hpp"
+
+namespace {
+
+using fa::f16;
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_sizes(int B, int S, int H, int D) {
+  if (B <= 0 || S <= 0 || H <= 0) return FA_ERR_SHAPE;
+  if (D != 32 && D != 64 && D != 128) return FA_ERR_HEAD_DIM;
+  // Per-(b,h) row offsets use 32-bit query/key indices and the grid is 1-D.
+  if (S > (1 << 30)) return FA_ERR_TOO_LARGE;
+  const int64_t bh = (int64_t)B * H;
+  if (bh > (int64_t)1 << 30) return FA_ERR_TOO_LARGE;
+  if (bh * (int64_t)S > ((int64_t)1 << 40)) return FA_ERR_TOO_LARGE;
+  return FA_OK;
+}
+
+// A (B, S, H, D) tensor with the given element strides.
+int check_tensor(const void *p, const int64_t *st, int B, int S, int H, int D) {
+  if (p == nullptr || st == nullptr) return FA_ERR_NULL_POINTER;
+  if (!aligned16(p)) return FA_ERR_ALIGNMENT;
+  if (st[3] != 1) return FA_ERR_STRIDE;
+  for (int i = 0; i < 3; ++i) {
+    if (st[i] < 0 || (st[i] & 7) != 0) return FA_ERR_STRIDE;
+  }
+  // Largest element offset must fit comfortably in int64.
+  const double span = (double)(B - 1) * st[0] + (double)(S - 1) * st[1] +
+                      (double)(H - 1) * st[2] + D;
+  if (span > 4.0e18) return FA_ERR_TOO_LARGE;
+  return FA_OK;
+}
+
+fa::TensorDesc desc(const void *p, const int64_t *st) {
+  return fa::TensorDesc{static_cast<const f16 *>(p), st[0], st[1], st[2]};
+}
+
+// Kernel-side score scale: |sm_scale| * log2(e), never exactly zero so that
+// masked (-inf) scores stay -inf; a zero scale then gives scores of ~1e-30,
+// whose exp2 is 1 to fp32 precision, i.e. uniform attention as intended.
+float kernel_scale(float sm_scale) {
+  float c = fabsf(sm_scale) * fa::kLog2e;
+  return c < 1e-30f ? 1e-30f : c;
+}
+
+int launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
+}
+
+constexpr int kFwdWaves = 4;
+
+template <int D, bool CAUSAL>
+int launch_fwd(const fa::FwdArgs &args, hipStream_t stream) {
+  constexpr int BM = fa::FwdTile<D, kFwdWaves>::BM;
+  fa::FwdArgs a = args;
+  a.n_qtiles = (a.S + BM - 1) / BM;
+  const int64_t grid = (int64_t)a.n_qtiles * a.B * a.H;
+  if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
+  hipLaunchKernelGGL((fa::fa_fwd_kernel<D, CAUSAL, kFwdWaves>), dim3((unsigned)grid),
+                     dim3(64 * kFwdWaves), 0, stream, a);
+  return launch_status();
+}
+
+constexpr int kBwdWaves = 4;
+
+template <int D>
+int launch_pre(const fa::PreArgs &a, hipStream_t stream) {
+  constexpr int RPB = 256 / (D / 8);
+  const int64_t rows = (int64_t)a.B * a.H * a.S;
+  const int64_t grid = (rows + RPB - 1) / RPB;
+  if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
+  hipLaunchKernelGGL((fa::fa_bwd_preprocess_kernel<D>), dim3((unsigned)grid), dim3(256), 0,
+                     stream, a);
+  return launch_status();
+}
+
+template <int D, bool CAUSAL>
+int launch_dkdv(const fa::BwdArgs &args, hipStream_t stream) {
+  fa::BwdArgs a = args;
+  constexpr int BK = fa::DkdvTile<D, kBwdWaves>::BK;
+  a.n_blocks = (a.S + BK - 1) / BK;
+  const int64_t grid = (int64_t)a.n_blocks * a.B * a.H;
+  if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
+  hipLaunchKernelGGL((fa::fa_bwd_dkdv_kernel<D, CAUSAL, kBwdWaves>), dim3((unsigned)grid),
+                     dim3(64 * kBwdWaves), 0, stream, a);
+  return launch_status();
+}
+
+template <int D, bool CAUSAL>
+int launch_dq(const fa::BwdArgs &args, hipStream_t stream) {
+  fa::BwdArgs a = args;
+  constexpr int BM = fa::DqTile<D, kBwdWaves>::BM;
+  a.n_blocks = (a.S + BM - 1) / BM;
+  const int64_t grid = (int64_t)a.n_blocks * a.B * a.H;
+  if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
+  hipLaunchKernelGGL((fa::fa_bwd_dq_kernel<D, CAUSAL, kBwdWaves>), dim3((unsigned)grid),
+                     dim3(64 * kBwdWaves), 0, stream, a);
+  return launch_status();
+}
+
+template <bool CAUSAL>
+int dispatch_dkdv(int D, const fa::BwdArgs &a, hipStream_t st) {
+  switch (D) {
+    case 32: return launch_dkdv<32, CAUSAL>(a, st);
+    case 64: return launch_dkdv<64, CAUSAL>(a, st);
+    default: return launch_dkdv<128, CAUSAL>(a, st);
+  }
+}
+
+template <bool CAUSAL>
+int dispatch_dq(int D, const fa::BwdArgs &a, hipStream_t st) {
+  switch (D) {
+    case 32: return launch_dq<32, CAUSAL>(a, st);
+    case 64: return launch_dq<64, CAUSAL>(a, st);
+    default: return launch_dq<128, CAUSAL>(a, st);
+  }
+}
+
+// Backward arguments common to fa_bwd, fa_bwd_dkdv and fa_bwd_dq; the
+// output pointers that a step does not write stay NULL.
+fa::BwdArgs bwd_args(const void *dout, const void *q, const void *k, const void *v,
+                     const float *lse, const float *delta, int B, int S, int H,
+                     const int64_t *do_st, const int64_t *q_st, const int64_t *k_st,
+                     const int64_t *v_st, float sm_scale) {
+  fa::BwdArgs a{};
+  a.q = desc(q, q_st);
+  a.k = desc(k, k_st);
+  a.v = desc(v, v_st);
+  a.dout = desc(dout, do_st);
+  a.lse = lse;
+  a.delta = delta;
+  a.B = B;
+  a.S = S;
+  a.H = H;
+  a.c = kernel_scale(sm_scale);
+  a.sm_scale = sm_scale;
+  a.neg = sm_scale < 0.0f;
+  return a;
+}
+
+int check_bwd_inputs(const void *dout, const void *q, const void *k, const void *v,
+                     const float *lse, int B, int S, int H, int D,
+                     const int64_t *do_st, const int64_t *q_st, const int64_t *k_st,
+                     const int64_t *v_st, float sm_scale) {
+  int rc = check_sizes(B, S, H, D);
+  if (rc) return rc;
+  if ((rc = check_tensor(dout, do_st, B, S, H, D))) return rc;
+  if ((rc = check_tensor(q, q_st, B, S, H, D))) return rc;
+  if ((rc = check_tensor(k, k_st, B, S, H, D))) return rc;
+  if ((rc = check_tensor(v, v_st, B, S, H, D))) return rc;
+  if (lse == nullptr) return FA_ERR_NULL_POINTER;
+  if (!aligned16(lse)) return FA_ERR_ALIGNMENT;
+  if (!isfinite(sm_scale)) return FA_ERR_SCALE;
+  return FA_OK;
+}
+
+size_t delta_bytes(int B, int S, int H) {
+  const size_t n = (size_t)B * (size_t)H * (size_t)S * sizeof(float);
+  return (n + 255) & ~(size_t)255;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fa_abi_version(void) { return FA_ABI_VERSION; }
+
+const char *fa_strerror(int status) {
+  switch (status) {
+    case FA_OK: return "success";
+    case FA_ERR_NULL_POINTER: return "a required pointer is NULL";
+    case FA_ERR_HEAD_DIM: return "unsupported head_dim (supported: 32, 64, 128)";
+    case FA_ERR_SHAPE: return "B, S and H must be positive";
+    case FA_ERR_STRIDE:
+      return "bad stride: the head_dim stride must be 1 and the other strides "
+             "non-negative multiples of 8 elements";
+    case FA_ERR_ALIGNMENT: return "tensor data pointer is not 16-byte aligned";
+    case FA_ERR_SCALE: return "sm_scale is not finite";
+    case FA_ERR_WORKSPACE: return "workspace is NULL or smaller than fa_bwd_workspace_bytes()";
+    case FA_ERR_TOO_LARGE: return "sizes exceed the kernel's index or grid limits";
+    case FA_ERR_LAUNCH: return "the HIP runtime rejected a kernel launch";
+    default: return "unknown status code";
+  }
+}
+
+int fa_fwd(const void *q, const void *k, const void *v, void *o, float *lse,
+           int B, int S, int H, int D,
+           const int64_t q_strides[4], const int64_t k_strides[4],
+           const int64_t v_strides[4], const int64_t o_strides[4],
+           float sm_scale, int causal, void *stream) {
+  int rc = check_sizes(B, S, H, D);
+  if (rc) return rc;
+  if ((rc = check_tensor(q, q_strides, B, S, H, D))) return rc;
+  if ((rc = check_tensor(k, k_strides, B, S, H, D))) return rc;
+  if ((rc = check_tensor(v, v_strides, B, S, H, D))) return rc;
+  if ((rc = check_tensor(o, o_strides, B, S, H, D))) return rc;
+  if (lse != nullptr && !aligned16(lse)) return FA_ERR_ALIGNMENT;
+  if (!isfinite(sm_scale)) return FA_ERR_SCALE;
+
+  fa::FwdArgs a{};
+  a.q = desc(q, q_strides);
+  a.k = desc(k, k_strides);
+  a.v = desc(v, v_strides);
+  a.o = static_cast<f16 *>(o);
+  a.o_sb = o_strides[0];
+  a.o_ss = o_strides[1];
+  a.o_sh = o_strides[2];
+  a.lse = lse;
+  a.B = B;
+  a.S = S;
+  a.H = H;
+  a.c = kernel_scale(sm_scale);
+  a.neg = sm_scale < 0.0f;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (D) {
+    case 32: return causal ? launch_fwd<32, true>(a, st) : launch_fwd<32, false>(a, st);
+    case 64: return causal ? launch_fwd<64, true>(a, st) : launch_fwd<64, false>(a, st);
+    default: return causal ? launch_fwd<128, true>(a, st) : launch_fwd<128, false>(a, st);
+  }
+}
+
+int fa_bwd_preprocess(const void *o, const void *dout, float *delta,
+                      int B, int S, int H, int D,
+                      const int64_t o_strides[4], const int64_t do_strides[4],
+                      void *stream) {
+  int rc = check_sizes(B, S, H, D);
+  if (rc) return rc;
+  if ((rc = check_tensor(o, o_strides, B, S, H, D))) return rc;
+  if ((rc = check_tensor(dout, do_strides, B, S, H, D))) return rc;
+  if (delta == nullptr) return FA_ERR_NULL_POINTER;
+  if (!aligned16(delta)) return FA_ERR_ALIGNMENT;
+  fa::PreArgs a{};
+  a.o = desc(o, o_strides);
+  a.dout = desc(dout, do_strides);
+  a.delta = delta;
+  a.B = B;
+  a.S = S;
+  a.H = H;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (D) {
+    case 32: return launch_pre<32>(a, st);
+    case 64: return launch_pre<64>(a, st);
+    default: return launch_pre<128>(a, st);
+  }
+}
+
+size_t fa_bwd_workspace_bytes(int B, int S, int H, int D) {
+  if (check_sizes(B, S, H, D) != FA_OK) return 0;
+  return delta_bytes(B, S, H);
+}
+
+int fa_bwd(const void *dout, const void *q, const void *k, const void *v,
+           const void *o, const float *lse,
+           void *dq, void *dk, void *dv,
+           void *workspace, size_t workspace_bytes,
+           int B, int S, int H, int D,
+           const int64_t do_strides[4], const int64_t q_strides[4],
+           const int64_t k_strides[4], const int64_t v_strides[4],
+           const int64_t o_strides[4], const int64_t dq_strides[4],
+           const int64_t dk_strides[4], const int64_t dv_strides[4],
+           float sm_scale, int causal, void *stream) {
+  int rc = check_bwd_inputs(dout, q, k, v, lse, B, S, H, D, do_strides, q_strides, k_strides,
+                            v_strides, sm_scale);
+  if (rc) return rc;
+  if ((rc = check_tensor(o, o_strides, B, S, H, D))) return rc;
+  if ((rc = check_tensor(dq, dq_strides, B, S, H, D))) return rc;
+  if ((rc = check_tensor(dk, dk_strides, B, S, H, D))) return rc;
+  if ((rc = check_tensor(dv, dv_strides, B, S, H, D))) return rc;
+  if (workspace == nullptr || workspace_bytes < delta_bytes(B, S, H)) return FA_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return FA_ERR_ALIGNMENT;
+
+  float *delta = static_cast<float *>(workspace);
+  rc = fa_bwd_preprocess(o, dout, delta, B, S, H, D, o_strides, do_strides, stream);
+  if (rc) return rc;
+  rc = fa_bwd_dkdv(dout, q, k, v, lse, delta, dk, dv, B, S, H, D, do_strides, q_strides,
+                   k_strides, v_strides, dk_strides, dv_strides, sm_scale, causal, stream);
+  if (rc) return rc;
+  return fa_bwd_dq(dout, q, k, v, lse, delta, dq, B, S, H, D, do_strides, q_strides, k_strides,
+                   v_strides, dq_strides, sm_scale, causal, stream);
+}
+
+int fa_bwd_dkdv(const void *dout, const void *q, const void *k, const void *v,
+                const float *lse, const float *delta, void *dk, void *dv,
+                int B, int S, int H, int D,
+                const int64_t do_strides[4], const int64_t q_strides[4],
+                const int64_t k_strides[4], const int64_t v_strides[4],
+                const int64_t dk_strides[4], const int64_t dv_strides[4],
+                float sm_scale, int causal, void *stream) {
+  int rc = check_bwd_inputs(dout, q, k, v, lse, B, S, H, D, do_strides, q_strides, k_strides,
+                            v_strides, sm_scale);
+  if (rc) return rc;
+  if ((rc = check_tensor(dk, dk_strides, B, S, H, D))) return rc;
+  if ((rc = check_tensor(dv, dv_strides, B, S, H, D))) return rc;
+  if (delta == nullptr) return FA_ERR_NULL_POINTER;
+  if (!aligned16(delta)) return FA_ERR_ALIGNMENT;
+  fa::BwdArgs a = bwd_args(dout, q, k, v, lse, delta, B, S, H, do_strides, q_strides, k_strides,
+                           v_strides, sm_scale);
+  a.dk = static_cast<f16 *>(dk);
+  a.dv = static_cast<f16 *>(dv);
+  a.dk_sb = dk_strides[0];
+  a.dk_ss = dk_strides[1];
+  a.dk_sh = dk_strides[2];
+  a.dv_sb = dv_strides[0];
+  a.dv_ss = dv_strides[1];
+  a.dv_sh = dv_strides[2];
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return causal ? dispatch_dkdv<true>(D, a, st) : dispatch_dkdv<false>(D, a, st);
+}
+
+int fa_bwd_dq(const void *dout, const void *q, const void *k, const void *v,
+              const float *lse, const float *delta, void *dq,
+              int B, int S, int H, int D,
+              const int64_t do_strides[4], const int64_t q_strides[4],
+              const int64_t k_strides[4], const int64_t v_strides[4],
+              const int64_t dq_strides[4],
+              float sm_scale, int causal, void *stream) {
+  int rc = check_bwd_inputs(dout, q, k, v, lse, B, S, H, D, do_strides, q_strides, k_strides,
+                            v_strides, sm_scale);
+  if (rc) return rc;
+  if ((rc = check_tensor(dq, dq_strides, B, S, H, D))) return rc;
+  if (delta == nullptr) return FA_ERR_NULL_POINTER;
+  if (!aligned16(delta)) return FA_ERR_ALIGNMENT;
+  fa::BwdArgs a = bwd_args(dout, q, k, v, lse, delta, B, S, H, do_strides, q_strides, k_strides,
+                           v_strides, sm_scale);
+  a.dq = static_cast<f16 *>(dq);
+  a.dq_sb = dq_strides[0];
+  a.dq_ss = dq_strides[1];
+  a.dq_sh = dq_strides[2];
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return causal ? dispatch_dq<true>(D, a, st) : dispatch_dq<false>(D, a, st);
+}
+
+}  // extern "C"

@@ -1,0 +1,108 @@
+// fa_common.hpp -- shared device helpers for the gfx950 FlashAttention kernels.
+//
+// Everything here is written for CDNA4 wave64 and the 32x32x16 fp16 MFMA
+// (v_mfma_f32_32x32x16_f16, 8 passes, 32768 FLOP per wave instruction).
+//
+// MFMA fragment conventions used by every kernel (lane = 0..63,
+// l32 = lane % 32, g = lane / 32):
+//   A operand  (32 x 16): lane holds A[row = l32][k = 8g .. 8g+7]
+//   B operand  (16 x 32): lane holds B[k = 8g .. 8g+7][col = l32]
+//   C/D result (32 x 32): lane holds C[row = 8*(i/4) + 4g + i%4][col = l32],
+//                         i = 0..15
+// The hardware's k order inside an operand is irrelevant as long as A and B
+// agree, which they do because both are indexed by the same (lane, slot).
+//
+// The kernels compute transposed score tiles S^T = K Q^T, so a lane owns one
+// query (the result column) and a per-lane subset of 16 keys (result rows).
+// The A-operand rows of K are permuted with kperm() so that result slot i of
+// lane group g is key 16*(i/8) + 8g + i%8: each 8-slot half of a lane's
+// results is then 8 consecutive keys, exactly the k-slice the lane supplies
+// when those probabilities are re-used as the B operand of the next MFMA.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fa {
+
+typedef _Float16 f16;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2 __attribute__((ext_vector_type(2)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_inff();
+constexpr float kPosInf = __builtin_inff();
+
+__device__ __forceinline__ floatx16 mfma32(half8 a, half8 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Key (or query) index, inside a 32-block, of result slot i for lane group g.
+__device__ __forceinline__ constexpr int slot_row(int i, int g) {
+  return 16 * (i >> 3) + 8 * g + (i & 7);
+}
+
+// A-operand row permutation: the key that A-row r must hold so that the
+// result row 8*(i/4) + 4g + i%4 (= r) carries key slot_row(i, g).
+__device__ __forceinline__ int kperm(int r) {
+  return 16 * (r >> 4) + 8 * ((r >> 2) & 1) + 4 * ((r >> 3) & 1) + (r & 3);
+}
+
+// Result-row index (inside a 32x32 C tile) of slot i for lane group g.
+__device__ __forceinline__ constexpr int c_row(int i, int g) {
+  return 8 * (i >> 2) + 4 * g + (i & 3);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) {
+  return __builtin_amdgcn_exp2f(x);
+}
+
+__device__ __forceinline__ float fast_log2(float x) {
+  return __builtin_amdgcn_logf(x);
+}
+
+// Value held by lane (lane ^ 32): the other half-wave owns the same query.
+__device__ __forceinline__ float xor32(float x) {
+  return __shfl_xor(x, 32, 64);
+}
+
+// Sum of the two fp16 values of `p` accumulated into fp32 `acc`
+// (v_dot2_f32_f16 against (1, 1)).
+__device__ __forceinline__ float dot2_acc(half2 p, float acc) {
+  const half2 ones = {(f16)1.0f, (f16)1.0f};
+  return __builtin_amdgcn_fdot2(p, ones, acc, false);
+}
+
+// Pack the low (or high) halves of two dwords into one dword.
+__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
+  return (a & 0xffffu) | (b << 16);
+}
+__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
+  return (a >> 16) | (b & 0xffff0000u);
+}
+
+// Flip the sign of 8 packed fp16 values (exact).
+__device__ __forceinline__ half8 neg8(half8 x) {
+  u32x4 u = __builtin_bit_cast(u32x4, x);
+  u ^= 0x80008000u;
+  return __builtin_bit_cast(half8, u);
+}
+
+// Kernel arguments shared by the forward and backward launches. Strides are
+// in elements of a (B, S, H, D) tensor whose D stride is 1.
+struct TensorDesc {
+  const f16 *ptr;
+  int64_t sb, ss, sh;
+  __device__ __forceinline__ const f16 *head(int b, int h) const {
+    return ptr + b * sb + h * sh;
+  }
+};
+
+}  // namespace fa

@@ -1,0 +1,29 @@
+"""flash_attn_volta -- FlashAttention forward + backward for AMD Instinct MI355X (gfx950).
+
+Drop-in replacement for the reference package of the same name
+(flash_attn_volta/__init__.py:1-24): the same public functions, signatures
+and (B, N, H, D) fp16 layout, backed by hand-written HIP kernels in the
+C-ABI library libfa_mi355x.so instead of Triton.
+
+Public API:
+    flash_attn_forward(q, k, v, causal=False, sm_scale=None,
+                       return_softmax_lse=False)         -> out [, lse]
+    flash_attn_volta  (alias of flash_attn_forward)
+    flash_attn(q, k, v, causal=False, sm_scale=None)     -> out  (autograd-aware)
+    flash_attn_backward(do, q, k, v, o, lse,
+                        causal=False, sm_scale=None)     -> (dq, dk, dv)
+
+q, k, v, out: (batch, seq, n_heads, head_dim) fp16; lse: (B, H, N) fp32.
+"""
+
+from .forward import flash_attn_forward, flash_attn_volta
+from .backward import flash_attn_backward
+from .autograd import flash_attn
+
+__all__ = [
+    "flash_attn_forward",
+    "flash_attn_volta",
+    "flash_attn_backward",
+    "flash_attn",
+]
+__version__ = "0.2.0"

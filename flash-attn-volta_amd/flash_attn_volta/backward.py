@@ -1,0 +1,100 @@
+"""Backward attention over (B, S, H, D) fp16 tensors on an MI355X.
+
+Drop-in for the reference's ``flash_attn_backward``
+(flash_attn_volta/triton_fa_bwd.py:587-700): same signature and return
+value.  One ``fa_bwd`` call (include/fa_mi355x.h) runs three gfx950 kernels
+on the current stream: the delta = rowsum(dO * O) pre-pass into a
+caller-owned workspace, the dK/dV kernel and the dQ kernel.  No permute
+copies; D = 16 is zero-padded to 32 like the forward.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _capi
+from .forward import (NATIVE_HEAD_DIMS, SUPPORTED_HEAD_DIMS, _kernel_ready, _pad_d, _require,
+                      _stream_ptr, kernel_strides)
+
+
+def flash_attn_backward(
+    do: torch.Tensor,
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    o: torch.Tensor,
+    lse: torch.Tensor,
+    causal: bool = False,
+    sm_scale: float | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """FlashAttention backward: fp16 in/out, fp32 accumulation.
+
+    Args:
+        do: (B, N, H, D) fp16, gradient of the loss w.r.t. the output.
+        q, k, v, o: (B, N, H, D) fp16 forward inputs and output.
+        lse: (B, H, N) fp32 from ``flash_attn_forward(..., return_softmax_lse=True)``.
+        causal, sm_scale: must match the forward call.
+
+    Returns:
+        (dq, dk, dv), each (B, N, H, D) fp16 contiguous.
+    """
+    _require(q.is_cuda and k.is_cuda and v.is_cuda and o.is_cuda and do.is_cuda,
+             "tensors must be on CUDA")
+    _require(q.dtype == torch.float16 == k.dtype == v.dtype == o.dtype == do.dtype, "fp16 only")
+    _require(lse.dtype == torch.float32, "lse must be fp32")
+    _require(q.shape == k.shape == v.shape == o.shape == do.shape, "shape mismatch")
+    _require(q.dim() == 4, f"expected (B, N, H, D) tensors, got {tuple(q.shape)}")
+    B, N, H, D = q.shape
+    _require(D in SUPPORTED_HEAD_DIMS, f"unsupported head_dim {D}")
+    _require(tuple(lse.shape) == (B, H, N), f"lse shape {tuple(lse.shape)} expected ({B},{H},{N})")
+    _require(lse.is_cuda and lse.device == q.device, "lse must be on the same device")
+
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+
+    if D not in NATIVE_HEAD_DIMS:
+        dq, dk, dv = _run_bwd(_pad_d(do, 32), _pad_d(q, 32), _pad_d(k, 32), _pad_d(v, 32),
+                              _pad_d(o, 32), lse, causal, sm_scale)
+        return dq[..., :D].contiguous(), dk[..., :D].contiguous(), dv[..., :D].contiguous()
+    return _run_bwd(do, q, k, v, o, lse, causal, sm_scale)
+
+
+def _run_bwd(do, q, k, v, o, lse, causal, sm_scale):
+    lib = _capi.load()
+    B, N, H, D = q.shape
+    do, q, k, v, o = (_kernel_ready(t) for t in (do, q, k, v, o))
+    lse = lse.contiguous()
+    dq = torch.empty((B, N, H, D), dtype=torch.float16, device=q.device)
+    dk = torch.empty_like(dq)
+    dv = torch.empty_like(dq)
+    if dq.numel() == 0:
+        return dq, dk, dv
+    ws_bytes = lib.fa_bwd_workspace_bytes(B, N, H, D)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    with torch.cuda.device(q.device):
+        rc = lib.fa_bwd(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                        lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                        ws.data_ptr(), ws_bytes, B, N, H, D,
+                        kernel_strides(do), kernel_strides(q), kernel_strides(k), kernel_strides(v),
+                        kernel_strides(o), kernel_strides(dq), kernel_strides(dk), kernel_strides(dv),
+                        float(sm_scale), int(bool(causal)), _stream_ptr(q.device))
+    _capi.check(rc, "fa_bwd")
+    return dq, dk, dv
+
+
+def bwd_preprocess(o: torch.Tensor, do: torch.Tensor) -> torch.Tensor:
+    """delta[b, h, s] = sum_d o * do in fp32, (B, H, S) -- the pre-pass of the
+    backward (reference: triton_fa_bwd.py:649-650), exposed for testing."""
+    lib = _capi.load()
+    _require(o.shape == do.shape and o.dim() == 4, "shape mismatch")
+    _require(o.dtype == torch.float16 == do.dtype, "fp16 only")
+    B, N, H, D = o.shape
+    _require(D in NATIVE_HEAD_DIMS, f"unsupported head_dim {D}")
+    o, do = _kernel_ready(o), _kernel_ready(do)
+    delta = torch.empty((B, H, N), dtype=torch.float32, device=o.device)
+    with torch.cuda.device(o.device):
+        rc = lib.fa_bwd_preprocess(o.data_ptr(), do.data_ptr(), delta.data_ptr(), B, N, H, D,
+                                   kernel_strides(o), kernel_strides(do), _stream_ptr(o.device))
+    _capi.check(rc, "fa_bwd_preprocess")
+    return delta

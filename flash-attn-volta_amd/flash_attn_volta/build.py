@@ -1,0 +1,58 @@
+"""In-tree build of the gfx950 C-ABI library ``libfa_mi355x.so``.
+
+    python -m flash_attn_volta.build         (from flash-attn-volta_amd/)
+
+hipcc cross-compiles for gfx950 on a machine without a GPU.  Every HIP
+source is compiled with packed-fp32 instructions disabled
+(-Xclang -target-feature -Xclang -packed-fp32-ops).
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG_DIR)                  # flash-attn-volta_amd/
+CSRC = os.path.join(ROOT, "csrc")
+SOURCES = [os.path.join(CSRC, "fa_api.hip")]
+HEADERS = [os.path.join(CSRC, f) for f in ("fa_common.hpp", "fa_fwd.hpp", "fa_bwd.hpp")]
+OUT = os.path.join(PKG_DIR, "libfa_mi355x.so")
+
+HIPCC_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-shared",
+    "-fPIC",
+    "-Wall",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def hipcc() -> str:
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    p = os.path.join(rocm, "bin", "hipcc")
+    return p if os.path.exists(p) else "hipcc"
+
+
+def build_library(verbose: bool = True) -> str:
+    """Compile libfa_mi355x.so in place (always recompiles) and return its path."""
+    tmp = OUT + ".tmp"
+    cmd = [hipcc()] + HIPCC_FLAGS + SOURCES + ["-o", tmp]
+    if verbose:
+        print("[build]", " ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass warns that it does not know the packed-fp32 feature.
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
+    if err.strip() and verbose:
+        print(err, file=sys.stderr)
+    os.replace(tmp, OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    print(build_library())

@@ -1,0 +1,133 @@
+/*
+ * fa_mi355x.h -- C ABI of the MI355X (gfx950) FlashAttention library.
+ *
+ * Plain C: raw device pointers, element strides, sizes, an opaque stream
+ * handle (a hipStream_t passed as void*; NULL means the default stream).
+ * No torch, HIP or C++ types cross this boundary, nothing throws, and the
+ * library never allocates or frees device memory: the caller passes every
+ * output and the backward workspace.
+ *
+ * Tensor convention (same as the Python API this library backs):
+ *   q, k, v, o, do, dq, dk, dv : (B, S, H, D) fp16 (IEEE binary16), any
+ *                                 strides with the D stride equal to 1;
+ *   lse, delta                 : (B, H, S) fp32, contiguous.
+ * Strides are in elements and given per tensor as {b, s, h, d}.
+ * All launches are asynchronous on `stream`; no call synchronises the host.
+ *
+ * Status codes: 0 on success, a negative FA_ERR_* otherwise. Argument
+ * validation runs before any HIP call, so it behaves the same on a machine
+ * without a GPU.
+ */
+#ifndef FA_MI355X_H
+#define FA_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FA_ABI_VERSION 1
+
+enum fa_status {
+  FA_OK = 0,
+  FA_ERR_NULL_POINTER = -1,   /* a required pointer is NULL                 */
+  FA_ERR_HEAD_DIM = -2,       /* D not in {32, 64, 128}                     */
+  FA_ERR_SHAPE = -3,          /* B, S or H <= 0                             */
+  FA_ERR_STRIDE = -4,         /* D stride != 1, or a stride not a multiple
+                                 of 8 elements (16-byte vector access)      */
+  FA_ERR_ALIGNMENT = -5,      /* a base pointer not 16-byte aligned         */
+  FA_ERR_SCALE = -6,          /* sm_scale not finite                        */
+  FA_ERR_WORKSPACE = -7,      /* workspace NULL or smaller than required    */
+  FA_ERR_TOO_LARGE = -8,      /* sizes whose element offsets overflow int64
+                                 or whose grid exceeds the launch limits    */
+  FA_ERR_LAUNCH = -9          /* the HIP runtime rejected a kernel launch   */
+};
+
+/* Version of this ABI (FA_ABI_VERSION of the build). */
+int fa_abi_version(void);
+
+/* Static, NUL-terminated description of a status code. Never NULL. */
+const char *fa_strerror(int status);
+
+/*
+ * Forward attention: o = softmax(sm_scale * q k^T [+ causal mask]) v.
+ * When `lse` is non-NULL it receives the natural-log log-sum-exp of each
+ * score row, (B, H, S) fp32 contiguous; +inf marks a row with no visible key.
+ *
+ * Replaces flash_attn_volta/triton_fa.py:291-397 (flash_attn_forward and
+ * _run_kernel, launching _fa_fwd_kernel_d64 / _fa_fwd_kernel_d128 at
+ * triton_fa.py:381-392). Unlike that wrapper it reads the (B,S,H,D)
+ * strides directly, so no permute copies and no zero padding of D=32.
+ */
+int fa_fwd(const void *q, const void *k, const void *v, void *o, float *lse,
+           int B, int S, int H, int D,
+           const int64_t q_strides[4], const int64_t k_strides[4],
+           const int64_t v_strides[4], const int64_t o_strides[4],
+           float sm_scale, int causal, void *stream);
+
+/*
+ * Backward pre-pass: delta[b,h,s] = sum_d o[b,s,h,d] * do[b,s,h,d] in fp32.
+ * Replaces the torch expression at flash_attn_volta/triton_fa_bwd.py:649-650.
+ */
+int fa_bwd_preprocess(const void *o, const void *dout, float *delta,
+                      int B, int S, int H, int D,
+                      const int64_t o_strides[4], const int64_t do_strides[4],
+                      void *stream);
+
+/* Bytes of device workspace fa_bwd needs for these sizes (0 on bad sizes). */
+size_t fa_bwd_workspace_bytes(int B, int S, int H, int D);
+
+/*
+ * Backward attention: (dq, dk, dv) of L = <o, dout> with o = fa_fwd(q,k,v),
+ * given the forward's `lse`. Runs fa_bwd_preprocess into the workspace,
+ * then fa_bwd_dkdv (one workgroup per key block) and fa_bwd_dq (one
+ * workgroup per query block). No atomics: results are bit-reproducible.
+ *
+ * Replaces flash_attn_volta/triton_fa_bwd.py:587-700 (flash_attn_backward
+ * and _run_bwd_kernels, launching _fa_bwd_dq_kernel_* and
+ * _fa_bwd_dkdv_kernel_* at triton_fa_bwd.py:667-695).
+ */
+int fa_bwd(const void *dout, const void *q, const void *k, const void *v,
+           const void *o, const float *lse,
+           void *dq, void *dk, void *dv,
+           void *workspace, size_t workspace_bytes,
+           int B, int S, int H, int D,
+           const int64_t do_strides[4], const int64_t q_strides[4],
+           const int64_t k_strides[4], const int64_t v_strides[4],
+           const int64_t o_strides[4], const int64_t dq_strides[4],
+           const int64_t dk_strides[4], const int64_t dv_strides[4],
+           float sm_scale, int causal, void *stream);
+
+/*
+ * The two main backward kernels as separate steps (fa_bwd runs
+ * fa_bwd_preprocess, then fa_bwd_dkdv, then fa_bwd_dq).  `delta` is the
+ * fa_bwd_preprocess output, (B, H, S) fp32 contiguous.
+ *
+ * fa_bwd_dkdv replaces the launch of _fa_bwd_dkdv_kernel_{d64,d128}
+ * (flash_attn_volta/triton_fa_bwd.py:682-695): dK, dV per key block.
+ * fa_bwd_dq replaces the launch of _fa_bwd_dq_kernel_{d64,d128}
+ * (triton_fa_bwd.py:667-679): dQ per query block.
+ */
+int fa_bwd_dkdv(const void *dout, const void *q, const void *k, const void *v,
+                const float *lse, const float *delta, void *dk, void *dv,
+                int B, int S, int H, int D,
+                const int64_t do_strides[4], const int64_t q_strides[4],
+                const int64_t k_strides[4], const int64_t v_strides[4],
+                const int64_t dk_strides[4], const int64_t dv_strides[4],
+                float sm_scale, int causal, void *stream);
+
+int fa_bwd_dq(const void *dout, const void *q, const void *k, const void *v,
+              const float *lse, const float *delta, void *dq,
+              int B, int S, int H, int D,
+              const int64_t do_strides[4], const int64_t q_strides[4],
+              const int64_t k_strides[4], const int64_t v_strides[4],
+              const int64_t dq_strides[4],
+              float sm_scale, int causal, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA_MI355X_H */

@@ -1,0 +1,209 @@
+"""CPU oracle for the FlashAttention hot path -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import this module, and only as the checker (or, for
+``attention_ref_fp32``, as the timed CPU baseline).  The product path in
+``flash_attn_volta`` never touches it.
+
+It restates, from the mathematics, what the reference computes:
+
+* ``attention_fwd``  -- O = softmax(sm_scale * Q K^T [+ causal -inf]) V and
+  the natural-log row LSE in float64.  Follows the reference eager path
+  flash_attn_volta/ref.py:9-36 (layout (B,N,H,D), causal mask = strict upper
+  triangle -inf, ref.py:26-31) and the forward kernel's output contract
+  triton_fa.py:146-159 (O = acc / l, LSE = m + ln l, +inf when a row sees no
+  key).
+* ``attention_bwd``  -- dQ, dK, dV (and delta) in float64 by the closed-form
+  softmax backward the reference kernels implement: delta = rowsum(dO * O)
+  from the *stored* fp16 O (triton_fa_bwd.py:649-650), P = exp(S - LSE)
+  (:165), dP = dO V^T (:168-169), dS = P (dP - delta) (:172),
+  dQ = sm_scale dS K (:175-178), dV = P^T dO (:415),
+  dK = sm_scale dS^T Q (:426-429).
+* ``attention_ref_fp32`` -- the reference's float32 eager CPU path
+  (ref.py:9-36) restated in torch; this is the CPU baseline bench.py times.
+* ``make_inputs`` -- the seeded fp16 inputs every test and bench uses.
+
+How each function is pinned (tests/test_oracle.py):
+  attention_fwd : golden vectors written by torch's float64
+                  scaled_dot_product_attention (tests/golden/), the plain-C
+                  brute force oracle/attention_ref.c, closed forms (S = 1,
+                  causal row 0, identical keys, convex hull of V, LSE bounds,
+                  LSE = logsumexp by definition).
+  attention_bwd : golden vectors from torch float64 autograd, the C brute
+                  force, and central finite differences of attention_fwd.
+  attention_ref_fp32 : agreement with attention_fwd to fp32 rounding.
+"""
+from __future__ import annotations
+
+import math
+import os
+from concurrent.futures import ThreadPoolExecutor
+
+import numpy as np
+
+__all__ = ["make_inputs", "attention_fwd", "attention_bwd", "attention_ref_fp32"]
+
+
+def make_inputs(B: int, S: int, H: int, D: int, seed: int = 0, scale: float = 1.0,
+                with_grad: bool = True):
+    """Seeded (B, S, H, D) fp16 inputs as torch CPU tensors.
+
+    q, k, v come from ``torch.Generator('cpu').manual_seed(seed)`` (randn in
+    fp32, cast to fp16, then multiplied by ``scale`` in fp16); dO comes from
+    seed + 1.  Identical bits on every machine, so the GPU and the oracle see
+    the same inputs (the reference tests seed q,k,v with 0 and the upstream
+    gradient with 1: tests/test_backward.py:193-204).
+    """
+    import torch
+    gen = torch.Generator("cpu").manual_seed(seed)
+    shape = (B, S, H, D)
+    q = torch.randn(shape, generator=gen, dtype=torch.float32).half()
+    k = torch.randn(shape, generator=gen, dtype=torch.float32).half()
+    v = torch.randn(shape, generator=gen, dtype=torch.float32).half()
+    if scale != 1.0:
+        q, k, v = q * scale, k * scale, v * scale
+    if not with_grad:
+        return q, k, v
+    gen2 = torch.Generator("cpu").manual_seed(seed + 1)
+    do = torch.randn(shape, generator=gen2, dtype=torch.float32).half()
+    if scale != 1.0:
+        do = do * scale
+    return q, k, v, do
+
+
+def _np64(x) -> np.ndarray:
+    if hasattr(x, "detach"):
+        x = x.detach().cpu().double().numpy()
+    return np.asarray(x, dtype=np.float64)
+
+
+_UPPER = {}
+
+
+def _upper(n: int) -> np.ndarray:
+    """Boolean strict upper triangle (j > i) of an n x n score matrix."""
+    m = _UPPER.get(n)
+    if m is None:
+        m = np.triu(np.ones((n, n), dtype=bool), k=1)
+        _UPPER.clear()
+        _UPPER[n] = m
+    return m
+
+
+def _scores(qh, kh, sm_scale, causal):
+    """sm_scale * q k^T for one (b, h), with the causal strict upper
+    triangle set to -inf (ref.py:25-31)."""
+    s = qh @ kh.T
+    s *= sm_scale
+    if causal:
+        np.putmask(s, _upper(s.shape[0]), -np.inf)
+    return s
+
+
+def _fwd_head(qh, kh, vh, sm_scale, causal):
+    s = _scores(qh, kh, sm_scale, causal)
+    m = s.max(axis=1, keepdims=True)
+    empty = ~np.isfinite(m[:, 0])
+    m_safe = np.where(np.isfinite(m), m, 0.0)
+    s -= m_safe
+    e = np.exp(s, out=s)
+    l = e.sum(axis=1, keepdims=True)
+    e /= np.where(l > 0, l, 1.0)
+    o = e @ vh
+    lse = np.where(empty, np.inf, m_safe[:, 0] + np.log(np.where(l[:, 0] > 0, l[:, 0], 1.0)))
+    return o, lse
+
+
+def _workers() -> int:
+    return max(1, min(8, os.cpu_count() or 1))
+
+
+def _map_heads(fn, B, H):
+    """Run fn(b, h) for every (b, h); heads are independent, so a thread pool
+    (numpy releases the GIL inside BLAS and ufuncs) only changes speed."""
+    pairs = [(b, h) for b in range(B) for h in range(H)]
+    if len(pairs) == 1:
+        return [fn(*pairs[0])]
+    with ThreadPoolExecutor(_workers()) as ex:
+        return list(ex.map(lambda bh: fn(*bh), pairs))
+
+
+def attention_fwd(q, k, v, causal: bool = False, sm_scale: float | None = None):
+    """float64 attention. Returns (o (B,S,H,D), lse (B,H,S)), natural log."""
+    q, k, v = _np64(q), _np64(k), _np64(v)
+    B, S, H, D = q.shape
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    o = np.zeros((B, S, H, D))
+    lse = np.zeros((B, H, S))
+    res = _map_heads(lambda b, h: _fwd_head(q[b, :, h], k[b, :, h], v[b, :, h], sm_scale, causal),
+                     B, H)
+    for (b, h), (oh, lh) in zip([(b, h) for b in range(B) for h in range(H)], res):
+        o[b, :, h] = oh
+        lse[b, h] = lh
+    return o, lse
+
+
+def _bwd_head(qh, kh, vh, doh, oh, sm_scale, causal):
+    s = _scores(qh, kh, sm_scale, causal)
+    m = s.max(axis=1, keepdims=True)
+    m = np.where(np.isfinite(m), m, 0.0)
+    s -= m
+    p = np.exp(s, out=s)
+    l = p.sum(axis=1, keepdims=True)
+    p /= np.where(l > 0, l, 1.0)
+    dl = (oh * doh).sum(axis=1)
+    dv = p.T @ doh
+    ds = doh @ vh.T
+    ds -= dl[:, None]
+    ds *= p
+    dq = sm_scale * (ds @ kh)
+    dk = sm_scale * (ds.T @ qh)
+    return dq, dk, dv, dl
+
+
+def attention_bwd(do, q, k, v, causal: bool = False, sm_scale: float | None = None, o=None):
+    """float64 gradients of L = <O, dO>. Returns (dq, dk, dv, delta).
+
+    ``o`` is the forward output the backward is given (the fp16-stored O in
+    the reference, triton_fa_bwd.py:649-650); if None the exact float64 O is
+    used, which makes delta exactly rowsum(dO * O).
+    """
+    do, q, k, v = _np64(do), _np64(q), _np64(k), _np64(v)
+    B, S, H, D = q.shape
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    if o is None:
+        o, _ = attention_fwd(q, k, v, causal, sm_scale)
+    o = _np64(o)
+    dq = np.zeros_like(q)
+    dk = np.zeros_like(k)
+    dv = np.zeros_like(v)
+    delta = np.zeros((B, H, S))
+    res = _map_heads(lambda b, h: _bwd_head(q[b, :, h], k[b, :, h], v[b, :, h], do[b, :, h],
+                                            o[b, :, h], sm_scale, causal), B, H)
+    for (b, h), (gq, gk, gv, dl) in zip([(b, h) for b in range(B) for h in range(H)], res):
+        dq[b, :, h], dk[b, :, h], dv[b, :, h], delta[b, h] = gq, gk, gv, dl
+    return dq, dk, dv, delta
+
+
+def attention_ref_fp32(q, k, v, causal: bool = False, sm_scale: float | None = None):
+    """The reference's float32 eager CPU path (ref.py:9-36), restated in torch:
+    permute to (B,H,N,D), fp32 scores, -inf strict upper triangle when causal,
+    softmax, PV, permute back, cast to fp16.  Differentiable (autograd runs
+    through it for the fwd+bwd CPU baseline)."""
+    import torch
+    B, N, H, D = q.shape
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    q_ = q.permute(0, 2, 1, 3).float()
+    k_ = k.permute(0, 2, 1, 3).float()
+    v_ = v.permute(0, 2, 1, 3).float()
+    scores = torch.matmul(q_, k_.transpose(-2, -1)) * sm_scale
+    if causal:
+        mask = torch.triu(torch.full((N, N), float("-inf"), dtype=torch.float32), diagonal=1)
+        scores = scores + mask
+    probs = torch.softmax(scores, dim=-1)
+    out = torch.matmul(probs, v_)
+    return out.permute(0, 2, 1, 3).contiguous().to(torch.float16)
+

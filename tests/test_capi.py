@@ -1,0 +1,120 @@
+"""The C-ABI library: loads, exports every declared symbol, and rejects bad
+arguments with the documented status codes before touching the GPU.
+
+These run without a GPU: validation happens on the host before any HIP call,
+so the pointers below are fake (aligned or deliberately misaligned) integers
+that are never dereferenced.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from flash_attn_volta import _capi
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                      "include", "fa_mi355x.h")
+
+P = 0x10000          # fake 16-byte aligned device pointer
+BAD = 0x10002        # fake misaligned pointer
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fa_[a-z0-9_]+)\s*\(", text)))
+
+
+def _st(B, S, H, D):
+    """contiguous (B,S,H,D) strides"""
+    return (ctypes.c_int64 * 4)(S * H * D, H * D, D, 1)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _capi.load()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    declared = _declared_functions()
+    assert set(declared) == set(_capi.EXPORTED_SYMBOLS)
+    for name in declared:
+        assert hasattr(lib, name), f"{name} missing from {_capi.LIB_PATH}"
+
+
+def test_abi_version(lib):
+    assert lib.fa_abi_version() == _capi.ABI_VERSION == 1
+
+
+def test_strerror_covers_every_code(lib):
+    codes = [0, -1, -2, -3, -4, -5, -6, -7, -8, -9]
+    msgs = [lib.fa_strerror(c).decode() for c in codes]
+    assert len(set(msgs)) == len(codes)
+    assert "unknown" in lib.fa_strerror(-1234).decode()
+
+
+def _fwd(lib, B=1, S=128, H=2, D=64, q=P, k=P, v=P, o=P, lse=None, st=None, scale=0.125,
+         causal=0):
+    s = st or _st(B, S, H, D)
+    return lib.fa_fwd(q, k, v, o, lse, B, S, H, D, s, s, s, s, scale, causal, None)
+
+
+def test_fwd_validation(lib):
+    assert _fwd(lib, D=48) == _capi.FA_ERR_HEAD_DIM
+    assert _fwd(lib, D=16) == _capi.FA_ERR_HEAD_DIM
+    assert _fwd(lib, D=256) == _capi.FA_ERR_HEAD_DIM
+    assert _fwd(lib, B=0) == _capi.FA_ERR_SHAPE
+    assert _fwd(lib, S=-1) == _capi.FA_ERR_SHAPE
+    assert _fwd(lib, H=0) == _capi.FA_ERR_SHAPE
+    assert _fwd(lib, q=None) == _capi.FA_ERR_NULL_POINTER
+    assert _fwd(lib, o=None) == _capi.FA_ERR_NULL_POINTER
+    assert _fwd(lib, k=BAD) == _capi.FA_ERR_ALIGNMENT
+    assert _fwd(lib, lse=BAD) == _capi.FA_ERR_ALIGNMENT
+    assert _fwd(lib, st=(ctypes.c_int64 * 4)(128 * 128, 128, 64, 2)) == _capi.FA_ERR_STRIDE
+    assert _fwd(lib, st=(ctypes.c_int64 * 4)(128 * 128, 124, 64, 1)) == _capi.FA_ERR_STRIDE
+    assert _fwd(lib, st=(ctypes.c_int64 * 4)(-8, 128, 64, 1)) == _capi.FA_ERR_STRIDE
+    assert _fwd(lib, scale=float("nan")) == _capi.FA_ERR_SCALE
+    assert _fwd(lib, scale=float("inf")) == _capi.FA_ERR_SCALE
+    assert _fwd(lib, S=(1 << 30) + 1) == _capi.FA_ERR_TOO_LARGE
+
+
+def _bwd(lib, ws=P, ws_bytes=None, lse=P, B=1, S=128, H=2, D=64, scale=0.125, dq=P):
+    s = _st(B, S, H, D)
+    if ws_bytes is None:
+        ws_bytes = lib.fa_bwd_workspace_bytes(B, S, H, D)
+    return lib.fa_bwd(P, P, P, P, P, lse, dq, P, P, ws, ws_bytes, B, S, H, D,
+                      s, s, s, s, s, s, s, s, scale, 1, None)
+
+
+def test_workspace_bytes(lib):
+    assert lib.fa_bwd_workspace_bytes(1, 4096, 16, 64) == 4 * 4096 * 16
+    assert lib.fa_bwd_workspace_bytes(1, 3, 1, 64) == 256          # rounded to 256 B
+    assert lib.fa_bwd_workspace_bytes(1, 3, 1, 48) == 0            # bad D
+    assert lib.fa_bwd_workspace_bytes(0, 3, 1, 64) == 0            # bad B
+
+
+def test_bwd_validation(lib):
+    assert _bwd(lib, ws=None) == _capi.FA_ERR_WORKSPACE
+    assert _bwd(lib, ws_bytes=16) == _capi.FA_ERR_WORKSPACE
+    assert _bwd(lib, ws=BAD) == _capi.FA_ERR_ALIGNMENT
+    assert _bwd(lib, lse=None) == _capi.FA_ERR_NULL_POINTER
+    assert _bwd(lib, lse=BAD) == _capi.FA_ERR_ALIGNMENT
+    assert _bwd(lib, dq=None) == _capi.FA_ERR_NULL_POINTER
+    assert _bwd(lib, D=96) == _capi.FA_ERR_HEAD_DIM
+    assert _bwd(lib, scale=float("nan")) == _capi.FA_ERR_SCALE
+
+
+def test_preprocess_validation(lib):
+    s = _st(1, 64, 1, 64)
+    assert lib.fa_bwd_preprocess(P, P, None, 1, 64, 1, 64, s, s, None) == _capi.FA_ERR_NULL_POINTER
+    assert lib.fa_bwd_preprocess(P, P, BAD, 1, 64, 1, 64, s, s, None) == _capi.FA_ERR_ALIGNMENT
+    assert lib.fa_bwd_preprocess(P, None, P, 1, 64, 1, 64, s, s, None) == _capi.FA_ERR_NULL_POINTER
+    assert lib.fa_bwd_preprocess(P, P, P, 1, 64, 1, 40, s, s, None) == _capi.FA_ERR_HEAD_DIM
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(_capi.LibraryNotBuilt):
+        _capi.load(str(tmp_path / "nope.so"))
