@@ -137,6 +137,24 @@ def kernel_times(q, k, v, do, steps, warmup):
     return res
 
 
+def profiled_traffic(kernel_sym):
+    """HBM bytes per launch of `kernel_sym` from the committed rocprofv3 PMC
+    summary (profiles/*_hbm_traffic.md: FETCH_SIZE and WRITE_SIZE runs,
+    each scaled by the same counter's reading for a copy of known size).
+    Returns (bytes, source) or (None, None) when no summary covers it."""
+    import glob
+    import re
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*_hbm_traffic.md"))):
+        text = open(path).read()
+        m = re.search(r"```json\s*(\{.*?\})\s*```", text, re.S)
+        if not m:
+            continue
+        table = json.loads(m.group(1)).get("traffic_bytes_per_launch", {})
+        if kernel_sym in table:
+            return float(table[kernel_sym]), os.path.relpath(path, ROOT)
+    return None, None
+
+
 def cpu_baseline(max_seconds=30.0):
     """The reference's CPU path (ref.py eager fp32 attention, restated in
     oracle/attention.py) timed on this host: fwd+bwd through autograd on the
@@ -194,6 +212,10 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="instead of the benchmark, run 10 plain device copies of MIB MiB "
+                         "(a kernel of known HBM traffic, to scale rocprofv3 FETCH_SIZE / "
+                         "WRITE_SIZE readings) and exit")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -204,6 +226,15 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.copy_calibration:
+        n = args.copy_calibration * (1 << 20)
+        src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] copy calibration: 10 x {n} bytes read + {n} bytes written")
+        return
     from flash_attn_volta import flash_attn, flash_attn_forward
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -236,9 +267,12 @@ def main():
     step_kernels = ("bwd_preprocess", "bwd_dkdv", "bwd_dq", "fwd")
     dom = max(step_kernels, key=lambda n: kt[n]["avg_us"])
     d = kt[dom]
-    roofline = {"bound": "mfma", "achieved": d["tflops"], "peak": PEAK_FP16_TFLOPS,
-                "unit": "TFLOP/s", "frac": d["tflops"] / PEAK_FP16_TFLOPS, "traffic": None,
-                "kernel": d["kernel"], "avg_us": d["avg_us"],
+    traffic, traffic_src = profiled_traffic(d["kernel"])
+    roofline = {"bound": "mfma", "achieved": round(d["tflops"], 2), "peak": PEAK_FP16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(d["tflops"] / PEAK_FP16_TFLOPS, 4),
+                "traffic": traffic, "traffic_source": traffic_src,
+                "algorithmic_bytes": d["bytes"],
+                "kernel": d["kernel"], "avg_us": round(d["avg_us"], 3),
                 "flops_per_launch": d["flops"]}
     all_kernels = {n: {"kernel": r["kernel"], "avg_us": round(r["avg_us"], 3),
                        "tflops": round(r["tflops"], 2), "frac_mfma": round(r["tflops"] / PEAK_FP16_TFLOPS, 4),
