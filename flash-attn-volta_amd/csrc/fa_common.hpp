@@ -95,6 +95,29 @@ __device__ __forceinline__ half8 neg8(half8 x) {
   return __builtin_bit_cast(half8, u);
 }
 
+// Buffer resource over rows [n0, S) of one (b, h) of a (B, S, H, D) tensor
+// with row stride `ss` elements: raw (stride-0) buffer whose extent ends at
+// the last element of row S-1, so a 16-byte load at byte offset
+// r*ss*2 + 16*c (c < D/8) returns zeros for rows n0 + r >= S when ss >= D
+// (and stays inside the tensor otherwise).  gfx9-family descriptor word 3.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const f16 *head, int64_t ss, int n0,
+                                                            int S, int D) {
+  const f16 *base = head + (int64_t)n0 * ss;
+  int64_t extent = (int64_t)(S - 1 - n0) * ss * 2 + 2 * D;
+  extent = extent < 0 ? 0 : (extent > 0xffffffffll ? 0xffffffffll : extent);
+  return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)(uint32_t)extent,
+                                           0x00020000);
+}
+
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+
+// Index of this thread's wave, as a wave-uniform (scalar) value.
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+}
+
 // Kernel arguments shared by the forward and backward launches. Strides are
 // in elements of a (B, S, H, D) tensor whose D stride is 1.
 struct TensorDesc {

@@ -10,20 +10,26 @@
 // MI355X layout of the work:
 //   * workgroup = NW waves; each wave owns 32 consecutive queries, so a
 //     workgroup covers BM = 32*NW queries of one (b, h);
-//   * key/value tiles of BN = 64 rows stream through LDS, double-buffered:
-//     K row-major [key][d] (A operand of S^T = K Q^T), V transposed [d][key]
-//     (A operand of O^T = V^T P^T), each row padded by 8 halves;
+//   * key/value tiles of BN = 64 rows stream through LDS.  K lives in a
+//     3-slot ring, one tile ahead of V (2-slot ring), so the S^T MFMAs of
+//     tile t+1 are issued before the softmax of tile t and run under it;
+//   * K rows are stored in kperm order so every lane's A-operand read is a
+//     plain 16-byte ds_read of LDS row (lane % 32); V stays row-major and the
+//     V^T operand of O^T = V^T P^T is read with ds_read_b64_tr_b16;
 //   * the wave's Q fragment stays in registers for the whole sweep;
 //   * a lane owns one query row: the running max / sum and the O^T
 //     accumulator column live in that lane, the only cross-lane step is one
-//     exchange with lane ^ 32 per key tile for the row max;
+//     v_permlane32_swap per key tile for the row max;
 //   * probabilities are rounded to fp16 once and the row sum accumulates
 //     those rounded values (v_dot2_f32_f16), so numerator and denominator
 //     see the same weights;
 //   * the accumulator is rescaled only when a row max grows by more than
 //     kRescaleLog2 (in log2 units): the stale max keeps p <= 2^kRescaleLog2,
 //     well inside fp16, and the final O and LSE use the same max, so the
-//     result is exact either way.
+//     result is exact either way;
+//   * K/V tiles are fetched with raw buffer loads whose extent ends at row
+//     S-1, so rows past the end read as zeros without any branch (they only
+//     ever meet -inf scores); the Q row index is clamped (never stored).
 #pragma once
 
 #include "fa_common.hpp"
@@ -48,21 +54,43 @@ struct FwdTile {
   static constexpr int BM = 32 * NW;
   static constexpr int BN = 64;
   static constexpr int NT = 64 * NW;
-  static constexpr int KS = D + 8;   // K tile row stride (halves)
-  static constexpr int VS = BN + 8;  // V^T tile row stride (halves)
-  static constexpr int K_CHUNKS = BN * D / 8;               // 16-byte chunks
-  static constexpr int K_PER_T = (K_CHUNKS + NT - 1) / NT;
-  static constexpr int V_UNITS = (BN / 8) * (D / 2);        // 8 keys x 2 d
-  static constexpr int V_PER_T = (V_UNITS + NT - 1) / NT;
+  static constexpr int KS = D + 8;    // K slot row stride (halves)
+  static constexpr int VS = D + 16;   // V slot row stride (halves)
+  static constexpr int CHUNKS = BN * D / 8;                // 16-byte chunks per tile
+  static constexpr int PER_T = (CHUNKS + NT - 1) / NT;
   static constexpr int LDS_K = BN * KS;
-  static constexpr int LDS_V = D * VS;
+  static constexpr int LDS_V = BN * VS;
 };
+
+// max(x, value of lane ^ 32).  v_permlane32_swap exchanges the upper half of
+// its first operand with the lower half of its second; with both operands x,
+// each lane ends up holding {own, partner} in some order.
+__device__ __forceinline__ float max_xor32(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(x, fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])));
+}
+
+// A-operand (32 x 16) fragment of V^T read from a row-major V tile with two
+// transpose loads: lane gets V[kb + j][d0 + lane % 32] for j = 0..7, where
+// kb = key base of this lane group's 8-key slice.
+template <int VS>
+__device__ __forceinline__ half8 load_vt(const f16 *tile, int kb, int d0, int lane) {
+  const int l16 = lane & 15;
+  const f16 *p = tile + (kb + (l16 >> 2)) * VS + d0 + 16 * ((lane >> 4) & 1) + 4 * (l16 & 3);
+  typedef __fp16 h4 __attribute__((vector_size(8)));
+  h4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) h4 *)p);
+  h4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) h4 *)(p + 4 * VS));
+  half8 r;
+  r[0] = (f16)lo[0]; r[1] = (f16)lo[1]; r[2] = (f16)lo[2]; r[3] = (f16)lo[3];
+  r[4] = (f16)hi[0]; r[5] = (f16)hi[1]; r[6] = (f16)hi[2]; r[7] = (f16)hi[3];
+  return r;
+}
 
 template <int D, bool CAUSAL, int NW>
 __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
   using T = FwdTile<D, NW>;
   constexpr int BM = T::BM, BN = T::BN, NT = T::NT, KS = T::KS, VS = T::VS;
-  __shared__ __attribute__((aligned(16))) f16 sk[2][T::LDS_K];
+  __shared__ __attribute__((aligned(16))) f16 sk[3][T::LDS_K];
   __shared__ __attribute__((aligned(16))) f16 sv[2][T::LDS_V];
 
   const int S = a.S;
@@ -74,7 +102,7 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
   const int qt = a.n_qtiles - 1 - bid / BH;
   const int b = bh / a.H, h = bh % a.H;
   const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
+  const int lane = tid & 63, w = wave_id();
   const int g = lane >> 5, l32 = lane & 31;
   const int q0 = qt * BM;
   const int wq0 = q0 + 32 * w;   // first query of this wave
@@ -84,144 +112,131 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
   const f16 *kb = a.k.head(b, h);
   const f16 *vb = a.v.head(b, h);
 
-  // ---- Q fragment (B operand of S^T = K Q^T): Q[qrow][16c + 8g .. +7]
-  half8 qf[D / 16];
-  if (qrow < S) {
-    const f16 *qr = qb + (int64_t)qrow * a.q.ss + 8 * g;
+  int kv_end = S;
+  if (CAUSAL) kv_end = min(S, q0 + BM);
+  const int n_tiles = (kv_end + BN - 1) / BN;   // >= 1
+
+  // ---- global -> register -> LDS staging of K (kperm row order) and V.
+  // Thread-constant chunk coordinates; per tile only the scalar buffer base
+  // moves, and rows past S come back as zeros from the buffer range check.
+  int ch_off[T::PER_T], ch_row[T::PER_T], ch_col[T::PER_T];
 #pragma unroll
-    for (int c = 0; c < D / 16; ++c) qf[c] = *(const half8 *)(qr + 16 * c);
+  for (int i = 0; i < T::PER_T; ++i) {
+    const int idx = tid + i * NT;
+    ch_row[i] = idx / (D / 8);
+    ch_col[i] = 8 * (idx % (D / 8));
+    ch_off[i] = ch_row[i] * (int)a.k.ss * 2 + 2 * ch_col[i];
+  }
+  const int v_off_delta = (int)(a.v.ss - a.k.ss) * 2;   // V rows use the V stride
+  u32x4 kreg[T::PER_T], vreg[T::PER_T];
+  auto load_k = [&](int n0) {
+    const __amdgpu_buffer_rsrc_t r = rows_rsrc(kb, a.k.ss, n0, S, D);
+#pragma unroll
+    for (int i = 0; i < T::PER_T; ++i)
+      if (T::CHUNKS % NT == 0 || tid + i * NT < T::CHUNKS) kreg[i] = buf_load16(r, ch_off[i]);
+  };
+  auto load_v = [&](int n0) {
+    const __amdgpu_buffer_rsrc_t r = rows_rsrc(vb, a.v.ss, n0, S, D);
+#pragma unroll
+    for (int i = 0; i < T::PER_T; ++i)
+      if (T::CHUNKS % NT == 0 || tid + i * NT < T::CHUNKS)
+        vreg[i] = buf_load16(r, ch_off[i] + ch_row[i] * v_off_delta);
+  };
+  auto store_k = [&](int slot) {
+#pragma unroll
+    for (int i = 0; i < T::PER_T; ++i) {
+      if (T::CHUNKS % NT == 0 || tid + i * NT < T::CHUNKS) {
+        const int r = ch_row[i];
+        const int row = (r & 32) + kperm(r & 31);
+        *(u32x4 *)(&sk[slot][row * KS + ch_col[i]]) = kreg[i];
+      }
+    }
+  };
+  auto store_v = [&](int slot) {
+#pragma unroll
+    for (int i = 0; i < T::PER_T; ++i)
+      if (T::CHUNKS % NT == 0 || tid + i * NT < T::CHUNKS)
+        *(u32x4 *)(&sv[slot][ch_row[i] * VS + ch_col[i]]) = vreg[i];
+  };
+
+  // ---- S^T = K Q^T for one 64-key tile (two 32-key sub-blocks)
+  half8 qf[D / 16];
+  auto qk = [&](int slot, int n0, floatx16 (&s)[2]) {
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      // A sub-block entirely above this wave's diagonal is skipped; its
+      // scores are then overwritten with -inf by the diagonal-tile mask.
+      if (CAUSAL && n0 + 32 * sb > wq0 + 31) continue;
+      const f16 *kr = &sk[slot][(32 * sb + l32) * KS + 8 * g];
+      floatx16 acc = mfma32(*(const half8 *)kr, qf[0], floatx16{});
+#pragma unroll
+      for (int cc = 1; cc < D / 16; ++cc) acc = mfma32(*(const half8 *)(kr + 16 * cc), qf[cc], acc);
+      s[sb] = acc;
+    }
+  };
+
+  // ---- prologue: K(0), V(0) -> slot 0, K(1) -> K slot 1
+  load_k(0);
+  load_v(0);
+  {
+    const int qr = min(qrow, S - 1);
+    const f16 *qp = qb + (int64_t)qr * a.q.ss + 8 * g;
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) qf[c] = *(const half8 *)(qp + 16 * c);
     if (a.neg) {
 #pragma unroll
       for (int c = 0; c < D / 16; ++c) qf[c] = neg8(qf[c]);
     }
-  } else {
-#pragma unroll
-    for (int c = 0; c < D / 16; ++c) qf[c] = half8{};
   }
-
-  int kv_end = S;
-  if (CAUSAL) kv_end = min(S, q0 + BM);
-  const int n_tiles = (kv_end + BN - 1) / BN;
-
-  // ---- global -> register staging of one K/V tile
-  u32x4 kreg[T::K_PER_T];
-  uint32_t vreg[T::V_PER_T][8];
-
-  auto load_tile = [&](int n0) {
-#pragma unroll
-    for (int i = 0; i < T::K_PER_T; ++i) {
-      const int idx = tid + i * NT;
-      if (idx < T::K_CHUNKS) {
-        const int r = idx / (D / 8), c8 = idx % (D / 8);
-        const int n = n0 + r;
-        kreg[i] = (n < S) ? *(const u32x4 *)(kb + (int64_t)n * a.k.ss + 8 * c8)
-                          : u32x4{0u, 0u, 0u, 0u};
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < T::V_PER_T; ++i) {
-      const int u = tid + i * NT;
-      if (u < T::V_UNITS) {
-        const int kg = u / (D / 2), dp = u % (D / 2);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int n = n0 + 8 * kg + j;
-          vreg[i][j] = (n < S) ? *(const uint32_t *)(vb + (int64_t)n * a.v.ss + 2 * dp) : 0u;
-        }
-      }
-    }
-  };
-
-  auto store_tile = [&](int st) {
-#pragma unroll
-    for (int i = 0; i < T::K_PER_T; ++i) {
-      const int idx = tid + i * NT;
-      if (idx < T::K_CHUNKS) {
-        const int r = idx / (D / 8), c8 = idx % (D / 8);
-        *(u32x4 *)(&sk[st][r * KS + 8 * c8]) = kreg[i];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < T::V_PER_T; ++i) {
-      const int u = tid + i * NT;
-      if (u < T::V_UNITS) {
-        const int kg = u / (D / 2), dp = u % (D / 2);
-        u32x4 lo, hi;
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          lo[jj] = pack_lo(vreg[i][2 * jj], vreg[i][2 * jj + 1]);
-          hi[jj] = pack_hi(vreg[i][2 * jj], vreg[i][2 * jj + 1]);
-        }
-        *(u32x4 *)(&sv[st][(2 * dp) * VS + 8 * kg]) = lo;
-        *(u32x4 *)(&sv[st][(2 * dp + 1) * VS + 8 * kg]) = hi;
-      }
-    }
-  };
-
-  // ---- per-lane running state
-  floatx16 oacc[D / 32];
-#pragma unroll
-  for (int d = 0; d < D / 32; ++d) oacc[d] = floatx16{};
-  float m_run = kNegInf;   // running max of c*s (log2 units)
-  float l_run = 0.0f;      // this lane's share of the running sum
-
-  const int krow = kperm(l32);
-  const float c = a.c;
-
-  if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
+  // Q must be resident before the loop: otherwise the waitcnt pass cannot
+  // prove it and stalls every iteration's MFMAs on the prefetch loads.
+  __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
+  store_k(0);
+  store_v(0);
+  if (n_tiles > 1) {
+    load_k(BN);
+    store_k(1);
   }
   __syncthreads();
 
+  floatx16 s_cur[2], s_nxt[2];
+  qk(0, 0, s_cur);
+
+  floatx16 oacc[D / 32];
+#pragma unroll
+  for (int d = 0; d < D / 32; ++d) oacc[d] = floatx16{};
+  float m_run = kNegInf;   // running max of c*s (log2 units), stale by <= kRescaleLog2
+  float l_run = 0.0f;      // this lane's share of the running sum
+  const float c = a.c;
+
   for (int t = 0; t < n_tiles; ++t) {
-    const int st = t & 1;
     const int n0 = t * BN;
-    if (t + 1 < n_tiles) load_tile(n0 + BN);
+    const bool more1 = t + 1 < n_tiles, more2 = t + 2 < n_tiles;
+    if (more2) load_k(n0 + 2 * BN);
+    if (more1) load_v(n0 + BN);
+    if (more1) qk((t + 1) % 3, n0 + BN, s_nxt);
 
-    // ---- S^T = K Q^T for the two 32-key sub-blocks
-    floatx16 s[2];
-    bool live[2];
+    // ---- masking (diagonal / ragged tiles only)
+    const bool need_mask = (CAUSAL && n0 + BN - 1 > wq0) || (n0 + BN > S);
+    if (need_mask) {
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-      const int ns = n0 + 32 * sb;
-      live[sb] = !CAUSAL || ns <= wq0 + 31;
-      s[sb] = floatx16{};
-      if (live[sb]) {
-        const f16 *kr = &sk[st][(32 * sb + krow) * KS + 8 * g];
-#pragma unroll
-        for (int cc = 0; cc < D / 16; ++cc)
-          s[sb] = mfma32(*(const half8 *)(kr + 16 * cc), qf[cc], s[sb]);
-      }
-    }
-
-    // ---- masking (diagonal / ragged tiles only) and the tile row max
-    float mx = kNegInf;
-#pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-      const int ns = n0 + 32 * sb;
-      if (!live[sb]) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) s[sb][i] = kNegInf;
-        continue;
-      }
-      const bool need_mask = (CAUSAL && ns + 31 > wq0) || (ns + 31 >= S);
-      if (need_mask) {
+      for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int key = ns + slot_row(i, g);
+          const int key = n0 + 32 * sb + slot_row(i, g);
           const bool vis = key < S && (!CAUSAL || key <= qrow);
-          s[sb][i] = vis ? s[sb][i] : kNegInf;
+          s_cur[sb][i] = vis ? s_cur[sb][i] : kNegInf;
         }
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[sb][i]);
     }
-    mx = fmaxf(mx, xor32(mx));
-    const float m_tile = mx * c;
 
-    // ---- lazy rescale of the running state
-    const float m_new = fmaxf(m_run, m_tile);
+    // ---- tile row max and lazy rescale
+    float mx = s_cur[0][0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s_cur[0][i]);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s_cur[1][i]);
+    mx = max_xor32(mx);
+    const float m_new = fmaxf(m_run, mx * c);
     const bool grow = m_new > m_run + kRescaleLog2;
     if (__any(grow)) {
       const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f;
@@ -234,32 +249,36 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
     }
     const float neg_m = (m_run == kNegInf) ? 0.0f : -m_run;
 
-    // ---- P = exp2(c*s - m), rounded to fp16; O^T += V^T P^T
+    // ---- P = exp2(c*s - m) rounded to fp16; O^T += V^T P^T
+    const int vslot = t & 1;
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
-      if (!live[sb]) continue;
+      if (CAUSAL && n0 + 32 * sb > wq0 + 31) continue;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         half8 pf;
 #pragma unroll
         for (int j = 0; j < 8; j += 2) {
           half2 pr = __builtin_convertvector(
-              (floatx2){fast_exp2(__builtin_fmaf(s[sb][8 * hh + j], c, neg_m)),
-                        fast_exp2(__builtin_fmaf(s[sb][8 * hh + j + 1], c, neg_m))},
+              (floatx2){fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + j], c, neg_m)),
+                        fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + j + 1], c, neg_m))},
               half2);
           l_run = dot2_acc(pr, l_run);
           pf[j] = pr[0];
           pf[j + 1] = pr[1];
         }
-        const f16 *vr = &sv[st][l32 * VS + 32 * sb + 16 * hh + 8 * g];
+        const int kbase = 32 * sb + 16 * hh + 8 * g;
 #pragma unroll
         for (int d = 0; d < D / 32; ++d)
-          oacc[d] = mfma32(*(const half8 *)(vr + 32 * d * VS), pf, oacc[d]);
+          oacc[d] = mfma32(load_vt<VS>(sv[vslot], kbase, 32 * d, lane), pf, oacc[d]);
       }
     }
 
-    if (t + 1 < n_tiles) store_tile(st ^ 1);
+    if (more2) store_k((t + 2) % 3);
+    if (more1) store_v((t + 1) & 1);
     __syncthreads();
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) s_cur[sb] = s_nxt[sb];
   }
 
   // ---- epilogue: O = acc / l, LSE = (m + log2 l) * ln2

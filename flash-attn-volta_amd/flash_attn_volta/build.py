@@ -27,6 +27,8 @@ HIPCC_FLAGS = [
     "-fPIC",
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # keep MFMA accumulators in VGPRs (no AGPR<->VGPR copies around softmax)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 
