@@ -16,12 +16,24 @@
 // causal query row's dQ never reads a key block it cannot see.
 //
 // Fragment layouts follow fa_common.hpp.  The dK/dV kernel computes S = Q K^T
-// with queries as the (permuted) A rows, so a lane owns one key and its
+// with queries as the (kperm-ordered) A rows, so a lane owns one key and its
 // P / dS values are directly the B operand of dV^T = dO^T P and
 // dK^T = Q^T dS.  The dQ kernel computes S^T = K Q^T like the forward, so a
-// lane owns one query and its dS^T values feed dQ^T = K^T dS^T.  The
-// transposed tiles (Q^T, dO^T, K^T) are built in LDS from register
-// transposes while staging.
+// lane owns one query and its dS^T values feed dQ^T = K^T dS^T.  Every tile
+// is staged row-major (kperm row order) with 16-byte buffer loads; the
+// transposed operands (Q^T, dO^T, K^T) come from ds_read_b64_tr_b16.
+//
+// dS scaling.  dS is rounded to fp16 for the MFMAs.  Its magnitude follows
+// the upstream gradient and can sit far below the fp16 normal range (a
+// loss averaged over thousands of tokens gives |dS| ~ 1e-9 deep in a
+// network), where fp16 would flush it to zero.  Each lane therefore keeps
+// a running power-of-two scale 2^e for its output row (a key in dK, a query
+// in dQ), chosen from the largest |dS| it has produced so that scaled values
+// stay in [2^10, 2^15]: dS * 2^e is rounded to fp16, the fp32 accumulator is
+// rescaled exactly (by a power of two) whenever e changes, and the result is
+// divided by 2^e at the end.  Scaling by powers of two changes no rounding
+// in the normal range, never overflows fp16, and depends only on the lane's
+// own data, so results stay deterministic.
 #pragma once
 
 #include "fa_common.hpp"
@@ -77,89 +89,65 @@ __global__ __launch_bounds__(256) void fa_bwd_preprocess_kernel(PreArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Staging of a ROWS x D fp16 tile (rows r0 .. r0+ROWS-1 of one (b,h), rows
-// >= S read as zero) into LDS, optionally both row-major [row][d] (stride
-// RS halves) and transposed [d][row] (stride TS halves).  A unit is 8 rows x
-// 2 columns: eight dword loads, then the row-major copy is eight dword
-// stores and the transposed copy two 16-byte stores after a register
-// transpose.
-template <int ROWS, int D, int NT>
-struct TileStager {
-  static constexpr int UNITS = (ROWS / 8) * (D / 2);
-  static constexpr int PER_T = (UNITS + NT - 1) / NT;
-  uint32_t r[PER_T][8];
+// Running power-of-two scale of one lane's dS column (see the header).
+struct DsScale {
+  int e = 0;
+  float mul = 1.0f;   // 2^e
 
-  __device__ __forceinline__ void load(const f16 *base, int64_t ss, int r0, int S, int tid) {
-#pragma unroll
-    for (int i = 0; i < PER_T; ++i) {
-      const int u = tid + i * NT;
-      if (u < UNITS) {
-        const int rg = u / (D / 2), dp = u % (D / 2);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int n = r0 + 8 * rg + j;
-          r[i][j] = (n < S) ? *(const uint32_t *)(base + (int64_t)n * ss + 2 * dp) : 0u;
-        }
-      }
+  // `m` = largest unscaled |dS| of the current block over this lane and its
+  // lane^32 partner (same output row).  Returns the factor by which the
+  // lane's accumulator must be multiplied (1 when e is unchanged).
+  __device__ __forceinline__ float update(float m) {
+    const float sm = m * mul;
+    if (m > 0.0f && (sm > 32768.0f || sm < 1024.0f)) {
+      // m = f * 2^x, f in [0.5, 1): new e puts m * 2^e in [2^13, 2^14)
+      int en = 14 - __builtin_amdgcn_frexp_expf(m);
+      en = en > 100 ? 100 : (en < -100 ? -100 : en);
+      const float f = __builtin_amdgcn_ldexpf(1.0f, en - e);
+      e = en;
+      mul = __builtin_amdgcn_ldexpf(1.0f, en);
+      return f;
     }
-  }
-
-  template <int RS, int TS>
-  __device__ __forceinline__ void store(f16 *rowm, f16 *trans, int tid) const {
-#pragma unroll
-    for (int i = 0; i < PER_T; ++i) {
-      const int u = tid + i * NT;
-      if (u < UNITS) {
-        const int rg = u / (D / 2), dp = u % (D / 2);
-        if (rowm != nullptr) {
-#pragma unroll
-          for (int j = 0; j < 8; ++j)
-            *(uint32_t *)(rowm + (8 * rg + j) * RS + 2 * dp) = r[i][j];
-        }
-        if (trans != nullptr) {
-          u32x4 lo, hi;
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
-            lo[jj] = pack_lo(r[i][2 * jj], r[i][2 * jj + 1]);
-            hi[jj] = pack_hi(r[i][2 * jj], r[i][2 * jj + 1]);
-          }
-          *(u32x4 *)(trans + (2 * dp) * TS + 8 * rg) = lo;
-          *(u32x4 *)(trans + (2 * dp + 1) * TS + 8 * rg) = hi;
-        }
-      }
-    }
+    return 1.0f;
   }
 };
 
-// Row-major staging of a ROWS x D tile with 16-byte loads and stores.
-template <int ROWS, int D, int NT>
-struct RowStager {
-  static constexpr int CHUNKS = ROWS * D / 8;
+__device__ __forceinline__ float absmax16(const floatx16 &x) {
+  float m = fabsf(x[0]);
+#pragma unroll
+  for (int i = 1; i < 16; ++i) m = fmaxf(m, fabsf(x[i]));
+  return m;
+}
+
+// Row-major staging of a 64-row x D tile (rows r0.. of one (b,h)) into an LDS
+// slot with 32-row blocks in kperm order.  16-byte buffer loads; rows past S
+// read as zeros.
+template <int D, int NT, int RS>
+struct KpermStager {
+  static constexpr int CHUNKS = 64 * D / 8;
   static constexpr int PER_T = (CHUNKS + NT - 1) / NT;
   u32x4 r[PER_T];
+  int off[PER_T], lds[PER_T];
 
-  __device__ __forceinline__ void load(const f16 *base, int64_t ss, int r0, int S, int tid) {
+  __device__ __forceinline__ void init(int tid, int64_t ss) {
 #pragma unroll
     for (int i = 0; i < PER_T; ++i) {
       const int idx = tid + i * NT;
-      if (idx < CHUNKS) {
-        const int rr = idx / (D / 8), c8 = idx % (D / 8);
-        const int n = r0 + rr;
-        r[i] = (n < S) ? *(const u32x4 *)(base + (int64_t)n * ss + 8 * c8) : u32x4{0u, 0u, 0u, 0u};
-      }
+      const int row = idx / (D / 8), c8 = idx % (D / 8);
+      off[i] = row * (int)ss * 2 + 16 * c8;
+      lds[i] = kperm_row(row) * RS + 8 * c8;
     }
   }
-
-  template <int RS>
-  __device__ __forceinline__ void store(f16 *rowm, int tid) const {
+  __device__ __forceinline__ void load(const f16 *head, int64_t ss, int r0, int S, int tid) {
+    const __amdgpu_buffer_rsrc_t rs = rows_rsrc(head, ss, r0, S, D);
 #pragma unroll
-    for (int i = 0; i < PER_T; ++i) {
-      const int idx = tid + i * NT;
-      if (idx < CHUNKS) {
-        const int rr = idx / (D / 8), c8 = idx % (D / 8);
-        *(u32x4 *)(rowm + rr * RS + 8 * c8) = r[i];
-      }
-    }
+    for (int i = 0; i < PER_T; ++i)
+      if (CHUNKS % NT == 0 || tid + i * NT < CHUNKS) r[i] = buf_load16(rs, off[i]);
+  }
+  __device__ __forceinline__ void store(f16 *slot, int tid) const {
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i)
+      if (CHUNKS % NT == 0 || tid + i * NT < CHUNKS) *(u32x4 *)(slot + lds[i]) = r[i];
   }
 };
 
@@ -179,29 +167,34 @@ __device__ __forceinline__ void store_row_fp16(f16 *dst, const floatx16 (&acc)[D
   }
 }
 
+// Load a lane's D/16 B-operand fragments of row `row` (clamped to S-1).
+template <int D>
+__device__ __forceinline__ void load_row_frags(half8 (&f)[D / 16], const f16 *head, int64_t ss,
+                                               int row, int S, int g) {
+  const f16 *p = head + (int64_t)min(row, S - 1) * ss + 8 * g;
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) f[c] = *(const half8 *)(p + 16 * c);
+}
+
 // ---------------------------------------------------------------------------
 // dK / dV: workgroup = NW waves, wave w owns keys k0 + 32w .. +31 (lane l32
-// owns key k0 + 32w + l32).  Query tiles of BQ = 64 rows stream through LDS
-// as Q, Q^T, dO, dO^T plus their LSE and delta.
+// owns key k0 + 32w + l32).  Query tiles of BQ = 64 rows stream through
+// double-buffered LDS as Q and dO (kperm row order) plus LSE and delta.
 template <int D, int NW>
 struct DkdvTile {
   static constexpr int BK = 32 * NW;
   static constexpr int BQ = 64;
   static constexpr int NT = 64 * NW;
   static constexpr int RS = D + 8;
-  static constexpr int TS = BQ + 8;
   static constexpr int LDS_ROW = BQ * RS;
-  static constexpr int LDS_T = D * TS;
 };
 
 template <int D, bool CAUSAL, int NW>
 __global__ __launch_bounds__(64 * NW) void fa_bwd_dkdv_kernel(BwdArgs a) {
   using T = DkdvTile<D, NW>;
-  constexpr int BK = T::BK, BQ = T::BQ, NT = T::NT, RS = T::RS, TS = T::TS;
+  constexpr int BK = T::BK, BQ = T::BQ, NT = T::NT, RS = T::RS;
   __shared__ __attribute__((aligned(16))) f16 s_q[2][T::LDS_ROW];
-  __shared__ __attribute__((aligned(16))) f16 s_qt[2][T::LDS_T];
   __shared__ __attribute__((aligned(16))) f16 s_do[2][T::LDS_ROW];
-  __shared__ __attribute__((aligned(16))) f16 s_dot[2][T::LDS_T];
   __shared__ __attribute__((aligned(16))) float s_lse[2][BQ];
   __shared__ __attribute__((aligned(16))) float s_dl[2][BQ];
 
@@ -212,39 +205,24 @@ __global__ __launch_bounds__(64 * NW) void fa_bwd_dkdv_kernel(BwdArgs a) {
   // Causal: low key blocks see the most queries, so run them first.
   const int kt = CAUSAL ? bid / BH : a.n_blocks - 1 - bid / BH;
   const int b = bh / a.H, h = bh % a.H;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int g = lane >> 5, l32 = lane & 31;
   const int k0 = kt * BK;
   const int wk0 = k0 + 32 * w;
   const int key = wk0 + l32;
 
   const f16 *qb = a.q.head(b, h);
-  const f16 *kb = a.k.head(b, h);
-  const f16 *vb = a.v.head(b, h);
   const f16 *gb = a.dout.head(b, h);
   const float *lse_b = a.lse + (int64_t)bh * S;
   const float *dl_b = a.delta + (int64_t)bh * S;
 
   // K^T and V^T fragments (B operands): K[key][16c + 8g .. +7]
   half8 kf[D / 16], vf[D / 16];
-  if (key < S) {
-    const f16 *kr = kb + (int64_t)key * a.k.ss + 8 * g;
-    const f16 *vr = vb + (int64_t)key * a.v.ss + 8 * g;
+  load_row_frags<D>(kf, a.k.head(b, h), a.k.ss, key, S, g);
+  load_row_frags<D>(vf, a.v.head(b, h), a.v.ss, key, S, g);
+  if (a.neg) {
 #pragma unroll
-    for (int c = 0; c < D / 16; ++c) {
-      kf[c] = *(const half8 *)(kr + 16 * c);
-      vf[c] = *(const half8 *)(vr + 16 * c);
-    }
-    if (a.neg) {
-#pragma unroll
-      for (int c = 0; c < D / 16; ++c) kf[c] = neg8(kf[c]);
-    }
-  } else {
-#pragma unroll
-    for (int c = 0; c < D / 16; ++c) {
-      kf[c] = half8{};
-      vf[c] = half8{};
-    }
+    for (int c = 0; c < D / 16; ++c) kf[c] = neg8(kf[c]);
   }
 
   floatx16 dk[D / 32], dv[D / 32];
@@ -253,13 +231,15 @@ __global__ __launch_bounds__(64 * NW) void fa_bwd_dkdv_kernel(BwdArgs a) {
     dk[d] = floatx16{};
     dv[d] = floatx16{};
   }
+  DsScale sc;
 
   const int m_begin = CAUSAL ? (k0 / BQ) * BQ : 0;
   const int n_tiles = (S > m_begin) ? (S - m_begin + BQ - 1) / BQ : 0;
-  const int qperm = kperm(l32);
   const float c = a.c;
 
-  TileStager<BQ, D, NT> stq, stg;
+  KpermStager<D, NT, RS> stq, stg;
+  stq.init(tid, a.q.ss);
+  stg.init(tid, a.dout.ss);
   float lse_r = 0.0f, dl_r = 0.0f;
   auto load_tile = [&](int m0) {
     stq.load(qb, a.q.ss, m0, S, tid);
@@ -272,14 +252,15 @@ __global__ __launch_bounds__(64 * NW) void fa_bwd_dkdv_kernel(BwdArgs a) {
     }
   };
   auto store_tile = [&](int st) {
-    stq.template store<RS, TS>(s_q[st], s_qt[st], tid);
-    stg.template store<RS, TS>(s_do[st], s_dot[st], tid);
+    stq.store(s_q[st], tid);
+    stg.store(s_do[st], tid);
     if (tid < BQ) {
       s_lse[st][tid] = lse_r;
       s_dl[st][tid] = dl_r;
     }
   };
 
+  __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): K/V fragments resident
   if (n_tiles > 0) {
     load_tile(m_begin);
     store_tile(0);
@@ -298,17 +279,21 @@ __global__ __launch_bounds__(64 * NW) void fa_bwd_dkdv_kernel(BwdArgs a) {
       if (CAUSAL && ms + 31 < wk0) continue;
       if (ms >= S) continue;
 
-      floatx16 sacc = floatx16{}, dpacc = floatx16{};
-      const f16 *qr = &s_q[st][(32 * qs + qperm) * RS + 8 * g];
-      const f16 *gr = &s_do[st][(32 * qs + qperm) * RS + 8 * g];
+      floatx16 sacc, dpacc;
+      {
+        const f16 *qr = &s_q[st][(32 * qs + l32) * RS + 8 * g];
+        const f16 *gr = &s_do[st][(32 * qs + l32) * RS + 8 * g];
+        sacc = mfma32(*(const half8 *)qr, kf[0], floatx16{});
+        dpacc = mfma32(*(const half8 *)gr, vf[0], floatx16{});
 #pragma unroll
-      for (int cc = 0; cc < D / 16; ++cc) {
-        sacc = mfma32(*(const half8 *)(qr + 16 * cc), kf[cc], sacc);
-        dpacc = mfma32(*(const half8 *)(gr + 16 * cc), vf[cc], dpacc);
+        for (int cc = 1; cc < D / 16; ++cc) {
+          sacc = mfma32(*(const half8 *)(qr + 16 * cc), kf[cc], sacc);
+          dpacc = mfma32(*(const half8 *)(gr + 16 * cc), vf[cc], dpacc);
+        }
       }
       // slot i <-> query ms + slot_row(i, g); lane <-> key
       const bool need_mask = (CAUSAL && ms < wk0 + 31) || (ms + 31 >= S) || (wk0 + 31 >= S);
-      half8 pf[2], dsf[2];
+      floatx16 p, ds;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const floatx4 lse_lo = *(const floatx4 *)&s_lse[st][32 * qs + 16 * hh + 8 * g];
@@ -320,26 +305,42 @@ __global__ __launch_bounds__(64 * NW) void fa_bwd_dkdv_kernel(BwdArgs a) {
           const int i = 8 * hh + j;
           const float l2 = j < 4 ? lse_lo[j] : lse_hi[j - 4];
           const float dl = j < 4 ? dl_lo[j] : dl_hi[j - 4];
-          float p = fast_exp2(__builtin_fmaf(sacc[i], c, -l2));
+          float pv = fast_exp2(__builtin_fmaf(sacc[i], c, -l2));
           if (need_mask) {
             const int m = ms + slot_row(i, g);
             const bool vis = m < S && key < S && (!CAUSAL || key <= m);
-            p = vis ? p : 0.0f;
+            pv = vis ? pv : 0.0f;
           }
-          const float ds = p * (dpacc[i] - dl);
-          pf[hh][j] = (f16)p;
-          dsf[hh][j] = (f16)ds;
+          p[i] = pv;
+          ds[i] = pv * (dpacc[i] - dl);
         }
+      }
+      // adaptive power-of-two scale of this key's dS column
+      const float m = fmaxf(absmax16(ds), 0.0f);
+      const float mk = fmaxf(m, __shfl_xor(m, 32, 64));
+      {
+        const float f = sc.update(mk);
+        if (__any(f != 1.0f)) {
+#pragma unroll
+          for (int d = 0; d < D / 32; ++d)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) dk[d][i] *= f;
+        }
+      }
+      half8 pf[2], dsf[2];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        pf[i >> 3][i & 7] = (f16)p[i];
+        dsf[i >> 3][i & 7] = (f16)(ds[i] * sc.mul);
       }
       // dV^T += dO^T P ; dK^T += Q^T dS   (k = queries ms + 16hh + 8g ..)
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        const f16 *gt = &s_dot[st][l32 * TS + 32 * qs + 16 * hh + 8 * g];
-        const f16 *qt = &s_qt[st][l32 * TS + 32 * qs + 16 * hh + 8 * g];
+        const int rlo = 32 * qs + 16 * hh + 4 * g;   // kperm rows of this 8-query slice
 #pragma unroll
         for (int d = 0; d < D / 32; ++d) {
-          dv[d] = mfma32(*(const half8 *)(gt + 32 * d * TS), pf[hh], dv[d]);
-          dk[d] = mfma32(*(const half8 *)(qt + 32 * d * TS), dsf[hh], dk[d]);
+          dv[d] = mfma32(load_tr8<RS>(s_do[st], rlo, rlo + 8, 32 * d, lane), pf[hh], dv[d]);
+          dk[d] = mfma32(load_tr8<RS>(s_q[st], rlo, rlo + 8, 32 * d, lane), dsf[hh], dk[d]);
         }
       }
     }
@@ -349,32 +350,30 @@ __global__ __launch_bounds__(64 * NW) void fa_bwd_dkdv_kernel(BwdArgs a) {
   }
 
   if (key < S) {
-    store_row_fp16<D>(a.dk + b * a.dk_sb + h * a.dk_sh + (int64_t)key * a.dk_ss, dk, a.sm_scale, g);
+    store_row_fp16<D>(a.dk + b * a.dk_sb + h * a.dk_sh + (int64_t)key * a.dk_ss, dk,
+                      a.sm_scale / sc.mul, g);
     store_row_fp16<D>(a.dv + b * a.dv_sb + h * a.dv_sh + (int64_t)key * a.dv_ss, dv, 1.0f, g);
   }
 }
 
 // ---------------------------------------------------------------------------
 // dQ: workgroup = NW waves, wave w owns queries q0 + 32w .. +31 (lane l32
-// owns one query).  Key tiles of BN = 64 rows stream through LDS as K, K^T
-// and V.
+// owns one query).  Key tiles of BN = 64 rows stream through double-buffered
+// LDS as K and V (kperm row order).
 template <int D, int NW>
 struct DqTile {
   static constexpr int BM = 32 * NW;
   static constexpr int BN = 64;
   static constexpr int NT = 64 * NW;
   static constexpr int RS = D + 8;
-  static constexpr int TS = BN + 8;
   static constexpr int LDS_ROW = BN * RS;
-  static constexpr int LDS_T = D * TS;
 };
 
 template <int D, bool CAUSAL, int NW>
 __global__ __launch_bounds__(64 * NW) void fa_bwd_dq_kernel(BwdArgs a) {
   using T = DqTile<D, NW>;
-  constexpr int BM = T::BM, BN = T::BN, NT = T::NT, RS = T::RS, TS = T::TS;
+  constexpr int BM = T::BM, BN = T::BN, NT = T::NT, RS = T::RS;
   __shared__ __attribute__((aligned(16))) f16 s_k[2][T::LDS_ROW];
-  __shared__ __attribute__((aligned(16))) f16 s_kt[2][T::LDS_T];
   __shared__ __attribute__((aligned(16))) f16 s_v[2][T::LDS_ROW];
 
   const int S = a.S;
@@ -383,66 +382,51 @@ __global__ __launch_bounds__(64 * NW) void fa_bwd_dq_kernel(BwdArgs a) {
   const int bh = bid % BH;
   const int qt = a.n_blocks - 1 - bid / BH;   // heaviest causal blocks first
   const int b = bh / a.H, h = bh % a.H;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int g = lane >> 5, l32 = lane & 31;
   const int q0 = qt * BM;
   const int wq0 = q0 + 32 * w;
   const int qrow = wq0 + l32;
 
-  const f16 *qb = a.q.head(b, h);
   const f16 *kb = a.k.head(b, h);
   const f16 *vb = a.v.head(b, h);
-  const f16 *gb = a.dout.head(b, h);
 
   half8 qf[D / 16], gf[D / 16];
-  float l2 = kPosInf, dl = 0.0f;
-  if (qrow < S) {
-    const f16 *qr = qb + (int64_t)qrow * a.q.ss + 8 * g;
-    const f16 *gr = gb + (int64_t)qrow * a.dout.ss + 8 * g;
+  load_row_frags<D>(qf, a.q.head(b, h), a.q.ss, qrow, S, g);
+  load_row_frags<D>(gf, a.dout.head(b, h), a.dout.ss, qrow, S, g);
+  if (a.neg) {
 #pragma unroll
-    for (int c = 0; c < D / 16; ++c) {
-      qf[c] = *(const half8 *)(qr + 16 * c);
-      gf[c] = *(const half8 *)(gr + 16 * c);
-    }
-    if (a.neg) {
-#pragma unroll
-      for (int c = 0; c < D / 16; ++c) qf[c] = neg8(qf[c]);
-    }
-    l2 = a.lse[(int64_t)bh * S + qrow] * kLog2e;
-    dl = a.delta[(int64_t)bh * S + qrow];
-  } else {
-#pragma unroll
-    for (int c = 0; c < D / 16; ++c) {
-      qf[c] = half8{};
-      gf[c] = half8{};
-    }
+    for (int c = 0; c < D / 16; ++c) qf[c] = neg8(qf[c]);
   }
+  const int qc = min(qrow, S - 1);
+  const float l2 = qrow < S ? a.lse[(int64_t)bh * S + qc] * kLog2e : kPosInf;
+  const float dl = qrow < S ? a.delta[(int64_t)bh * S + qc] : 0.0f;
 
   floatx16 dq[D / 32];
 #pragma unroll
   for (int d = 0; d < D / 32; ++d) dq[d] = floatx16{};
+  DsScale sc;
 
   int kv_end = S;
   if (CAUSAL) kv_end = min(S, q0 + BM);
   const int n_tiles = (kv_end + BN - 1) / BN;
-  const int krow = kperm(l32);
   const float c = a.c;
 
-  TileStager<BN, D, NT> stk;
-  RowStager<BN, D, NT> stv;
+  KpermStager<D, NT, RS> stk, stv;
+  stk.init(tid, a.k.ss);
+  stv.init(tid, a.v.ss);
   auto load_tile = [&](int n0) {
     stk.load(kb, a.k.ss, n0, S, tid);
     stv.load(vb, a.v.ss, n0, S, tid);
   };
   auto store_tile = [&](int st) {
-    stk.template store<RS, TS>(s_k[st], s_kt[st], tid);
-    stv.template store<RS>(s_v[st], tid);
+    stk.store(s_k[st], tid);
+    stv.store(s_v[st], tid);
   };
 
-  if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
+  __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): Q/dO fragments resident
+  load_tile(0);
+  store_tile(0);
   __syncthreads();
 
   for (int t = 0; t < n_tiles; ++t) {
@@ -455,16 +439,20 @@ __global__ __launch_bounds__(64 * NW) void fa_bwd_dq_kernel(BwdArgs a) {
       const int ns = n0 + 32 * sb;
       if (CAUSAL && ns > wq0 + 31) continue;
       if (ns >= S) continue;
-      floatx16 sacc = floatx16{}, dpacc = floatx16{};
-      const f16 *kr = &s_k[st][(32 * sb + krow) * RS + 8 * g];
-      const f16 *vr = &s_v[st][(32 * sb + krow) * RS + 8 * g];
+      floatx16 sacc, dpacc;
+      {
+        const f16 *kr = &s_k[st][(32 * sb + l32) * RS + 8 * g];
+        const f16 *vr = &s_v[st][(32 * sb + l32) * RS + 8 * g];
+        sacc = mfma32(*(const half8 *)kr, qf[0], floatx16{});
+        dpacc = mfma32(*(const half8 *)vr, gf[0], floatx16{});
 #pragma unroll
-      for (int cc = 0; cc < D / 16; ++cc) {
-        sacc = mfma32(*(const half8 *)(kr + 16 * cc), qf[cc], sacc);
-        dpacc = mfma32(*(const half8 *)(vr + 16 * cc), gf[cc], dpacc);
+        for (int cc = 1; cc < D / 16; ++cc) {
+          sacc = mfma32(*(const half8 *)(kr + 16 * cc), qf[cc], sacc);
+          dpacc = mfma32(*(const half8 *)(vr + 16 * cc), gf[cc], dpacc);
+        }
       }
       const bool need_mask = (CAUSAL && ns + 31 > wq0) || (ns + 31 >= S);
-      half8 dsf[2];
+      floatx16 ds;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         float p = fast_exp2(__builtin_fmaf(sacc[i], c, -l2));
@@ -473,14 +461,28 @@ __global__ __launch_bounds__(64 * NW) void fa_bwd_dq_kernel(BwdArgs a) {
           const bool vis = n < S && (!CAUSAL || n <= qrow);
           p = vis ? p : 0.0f;
         }
-        dsf[i >> 3][i & 7] = (f16)(p * (dpacc[i] - dl));
+        ds[i] = p * (dpacc[i] - dl);
       }
+      const float m = absmax16(ds);
+      const float mq = fmaxf(m, __shfl_xor(m, 32, 64));
+      {
+        const float f = sc.update(mq);
+        if (__any(f != 1.0f)) {
+#pragma unroll
+          for (int d = 0; d < D / 32; ++d)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) dq[d][i] *= f;
+        }
+      }
+      half8 dsf[2];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) dsf[i >> 3][i & 7] = (f16)(ds[i] * sc.mul);
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        const f16 *ktr = &s_kt[st][l32 * TS + 32 * sb + 16 * hh + 8 * g];
+        const int rlo = 32 * sb + 16 * hh + 4 * g;   // kperm rows of this 8-key slice
 #pragma unroll
         for (int d = 0; d < D / 32; ++d)
-          dq[d] = mfma32(*(const half8 *)(ktr + 32 * d * TS), dsf[hh], dq[d]);
+          dq[d] = mfma32(load_tr8<RS>(s_k[st], rlo, rlo + 8, 32 * d, lane), dsf[hh], dq[d]);
       }
     }
 
@@ -489,7 +491,8 @@ __global__ __launch_bounds__(64 * NW) void fa_bwd_dq_kernel(BwdArgs a) {
   }
 
   if (qrow < S)
-    store_row_fp16<D>(a.dq + b * a.dq_sb + h * a.dq_sh + (int64_t)qrow * a.dq_ss, dq, a.sm_scale, g);
+    store_row_fp16<D>(a.dq + b * a.dq_sb + h * a.dq_sh + (int64_t)qrow * a.dq_ss, dq,
+                      a.sm_scale / sc.mul, g);
 }
 
 }  // namespace fa

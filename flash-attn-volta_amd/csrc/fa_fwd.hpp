@@ -70,22 +70,6 @@ __device__ __forceinline__ float max_xor32(float x) {
   return fmaxf(x, fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])));
 }
 
-// A-operand (32 x 16) fragment of V^T read from a row-major V tile with two
-// transpose loads: lane gets V[kb + j][d0 + lane % 32] for j = 0..7, where
-// kb = key base of this lane group's 8-key slice.
-template <int VS>
-__device__ __forceinline__ half8 load_vt(const f16 *tile, int kb, int d0, int lane) {
-  const int l16 = lane & 15;
-  const f16 *p = tile + (kb + (l16 >> 2)) * VS + d0 + 16 * ((lane >> 4) & 1) + 4 * (l16 & 3);
-  typedef __fp16 h4 __attribute__((vector_size(8)));
-  h4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) h4 *)p);
-  h4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) h4 *)(p + 4 * VS));
-  half8 r;
-  r[0] = (f16)lo[0]; r[1] = (f16)lo[1]; r[2] = (f16)lo[2]; r[3] = (f16)lo[3];
-  r[4] = (f16)hi[0]; r[5] = (f16)hi[1]; r[6] = (f16)hi[2]; r[7] = (f16)hi[3];
-  return r;
-}
-
 template <int D, bool CAUSAL, int NW>
 __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
   using T = FwdTile<D, NW>;
@@ -270,7 +254,7 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
         const int kbase = 32 * sb + 16 * hh + 8 * g;
 #pragma unroll
         for (int d = 0; d < D / 32; ++d)
-          oacc[d] = mfma32(load_vt<VS>(sv[vslot], kbase, 32 * d, lane), pf, oacc[d]);
+          oacc[d] = mfma32(load_tr8<VS>(sv[vslot], kbase, kbase + 4, 32 * d, lane), pf, oacc[d]);
       }
     }
 

@@ -1,0 +1,309 @@
+"""Route HuggingFace transformers attention through ``flash_attn_volta``.
+
+Same public surface as the reference's patch module
+(flash_attn_volta/patch_hf.py): ``patch_{gpt2,qwen2,qwen3,llama}(model) ->
+int``, the matching ``unpatch_*``, ``patch_model(model) -> (family, n)``
+with the same dispatch order (GPT-2, Qwen3, Qwen2, Llama; :409-417) and the
+same loud refusal of linear-attention / state-space models (:358-407), and
+``_is_causal_only_mask`` (:29-48).
+
+The reference replaces whole attention ``forward`` methods written against
+transformers 4.44.  transformers 5.x changed those signatures; every
+decoder attention module now computes post-RoPE, post-cache (B, H, S, D)
+query/key/value and hands them to
+``ALL_ATTENTION_FUNCTIONS.get_interface(self.config._attn_implementation,
+eager_attention_forward)``.  This module therefore registers one attention
+function, ``"flash_attn_volta"``, in transformers' ``AttentionInterface``
+and routes each patched module to it by giving that module a shallow copy
+of its config whose ``_attn_implementation`` names it.  Unpatching restores
+the module's own config object.  Projections, QK-norm, RoPE, caches and the
+output projection stay HuggingFace's own code for every family.
+
+The fast path is taken under the reference's conditions (:68-75, :145-162,
+:443-452): self-attention with q_len == kv_len (prefill, or training; a KV
+cache with content gives kv_len > q_len), no ``output_attentions``, no
+attention dropout, no sliding window narrower than the sequence, and an
+attention mask that is absent (the module is causal) or causal-only.
+Otherwise the module's original attention implementation runs unchanged.
+GQA/MQA key/value heads are expanded to the query heads, as the
+reference's ``repeat_kv`` calls do (:186-188, :470-471).
+"""
+from __future__ import annotations
+
+import copy
+import sys
+from typing import Optional, Tuple
+
+import torch
+
+from .autograd import flash_attn
+
+ATTN_IMPLEMENTATION = "flash_attn_volta"
+
+_GPT2_NAMES = {"GPT2Attention"}
+_QWEN2_NAMES = {"Qwen2Attention", "Qwen2SdpaAttention", "Qwen2FlashAttention2"}
+_QWEN3_NAMES = {"Qwen3Attention", "Qwen3SdpaAttention", "Qwen3FlashAttention2"}
+_LLAMA_NAMES = {"LlamaAttention", "LlamaSdpaAttention", "LlamaFlashAttention2"}
+
+
+def _is_causal_only_mask(mask: torch.Tensor, q_len: int) -> bool:
+    """True if ``mask`` (4-D, (.., q_len, kv_len >= q_len)) is the plain causal
+    mask on its top-left q_len x q_len block.
+
+    Float masks (added to scores): lower triangle incl. diagonal |m| <= 1e-3,
+    strict upper triangle <= -1 (the reference's rule, patch_hf.py:29-48).
+    Bool masks (transformers 5.x; True = attend): lower triangle incl.
+    diagonal True, strict upper triangle False.
+    """
+    if mask is None or mask.dim() != 4:
+        return False
+    if mask.size(-2) != q_len or mask.size(-1) < q_len:
+        return False
+    m = mask[..., :q_len, :q_len]
+    tri = torch.tril(torch.ones(q_len, q_len, device=mask.device, dtype=torch.bool))
+    if m.dtype == torch.bool:
+        return bool(m[..., tri].all()) and not bool(m[..., ~tri].any())
+    if (m[..., tri].abs() > 1e-3).any():
+        return False
+    if (m[..., ~tri] > -1.0).any():
+        return False
+    return True
+
+
+def _original_interface(module):
+    """The attention function the module would use unpatched."""
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+    impl = getattr(module, "_fav_orig_impl", None)
+    eager = getattr(sys.modules.get(type(module).__module__), "eager_attention_forward", None)
+    if eager is None:
+        from transformers.models.llama.modeling_llama import eager_attention_forward as eager
+    if impl is None or impl == "eager":
+        return eager
+    return ALL_ATTENTION_FUNCTIONS.get_interface(impl, eager)
+
+
+def _expand_kv(x: torch.Tensor, n_rep: int) -> torch.Tensor:
+    """(B, Hkv, S, D) -> (B, Hkv * n_rep, S, D), each kv head repeated n_rep
+    times consecutively (transformers' repeat_kv)."""
+    if n_rep == 1:
+        return x
+    B, Hkv, S, D = x.shape
+    return x[:, :, None].expand(B, Hkv, n_rep, S, D).reshape(B, Hkv * n_rep, S, D)
+
+
+def fast_path_causal(module, q_len: int, kv_len: int, head_dim: int,
+                     attention_mask: Optional[torch.Tensor], dropout: Optional[float],
+                     sliding_window: Optional[int], kwargs: dict) -> Optional[bool]:
+    """Decide whether an attention call may run on the flash kernel.
+
+    Returns None to fall back to the module's original implementation, else
+    the causal flag to run the kernel with.  Fallbacks mirror the reference
+    (patch_hf.py:68-75, :145-162, :443-452): a KV cache with content
+    (kv_len != q_len), output_attentions, cross-attention, a head mask, a
+    mask that is not causal-only; plus what the kernel does not implement
+    here: attention dropout, a sliding window narrower than the sequence,
+    head dims outside {16, 32, 64, 128}.
+    """
+    causal = bool(getattr(module, "is_causal", True))
+    if q_len != kv_len or kwargs.get("output_attentions", False):
+        return None
+    if getattr(module, "is_cross_attention", False) or kwargs.get("head_mask") is not None:
+        return None
+    if dropout not in (None, 0.0):
+        return None
+    if sliding_window is not None and sliding_window < kv_len:
+        return None
+    if head_dim not in (16, 32, 64, 128):
+        return None
+    if attention_mask is not None:
+        if not (causal and _is_causal_only_mask(attention_mask, q_len)):
+            return None
+    return causal
+
+
+def flash_attn_volta_attention(
+    module: torch.nn.Module,
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    attention_mask: Optional[torch.Tensor],
+    dropout: float = 0.0,
+    scaling: Optional[float] = None,
+    sliding_window: Optional[int] = None,
+    **kwargs,
+) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """transformers 5.x attention function: (B, H, S, D) in, (B, S, H, D) out."""
+    causal = None
+    if query.is_cuda:
+        causal = fast_path_causal(module, query.shape[2], key.shape[2], query.shape[-1],
+                                  attention_mask, dropout, sliding_window, kwargs)
+    if causal is None:
+        return _original_interface(module)(module, query, key, value, attention_mask,
+                                           dropout=dropout, scaling=scaling,
+                                           sliding_window=sliding_window, **kwargs)
+
+    n_rep = query.shape[1] // key.shape[1]
+    key = _expand_kv(key, n_rep)
+    value = _expand_kv(value, n_rep)
+    out_dtype = query.dtype
+    q = query.transpose(1, 2).to(torch.float16)
+    k = key.transpose(1, 2).to(torch.float16)
+    v = value.transpose(1, 2).to(torch.float16)
+    if scaling is None:
+        scaling = query.shape[-1] ** -0.5
+    out = flash_attn(q, k, v, causal=causal, sm_scale=float(scaling))
+    return out.to(out_dtype), None
+
+
+_registered = False
+
+
+def _register() -> None:
+    global _registered
+    if _registered:
+        return
+    from transformers.modeling_utils import AttentionInterface
+    AttentionInterface.register(ATTN_IMPLEMENTATION, flash_attn_volta_attention)
+    _registered = True
+
+
+def _patch(model: torch.nn.Module, names) -> int:
+    _register()
+    n = 0
+    for mod in model.modules():
+        if type(mod).__name__ not in names or not hasattr(mod, "config"):
+            continue
+        if not hasattr(mod, "_fav_orig_config"):
+            cfg = mod.config
+            mod._fav_orig_config = cfg
+            mod._fav_orig_impl = getattr(cfg, "_attn_implementation", None)
+            routed = copy.copy(cfg)
+            # set the backing field directly: the property setter would also
+            # rewrite sub-configs, which the shallow copy shares
+            routed._attn_implementation_internal = ATTN_IMPLEMENTATION
+            mod.config = routed
+            mod._orig_forward = mod.forward
+        n += 1
+    return n
+
+
+def _unpatch(model: torch.nn.Module, names) -> int:
+    n = 0
+    for mod in model.modules():
+        if type(mod).__name__ in names and hasattr(mod, "_fav_orig_config"):
+            mod.config = mod._fav_orig_config
+            del mod._fav_orig_config
+            del mod._fav_orig_impl
+            if "_orig_forward" in mod.__dict__:
+                del mod._orig_forward
+            n += 1
+    return n
+
+
+def patch_gpt2(model: torch.nn.Module) -> int:
+    """Patch every GPT2Attention block on ``model``. Returns count patched."""
+    return _patch(model, _GPT2_NAMES)
+
+
+def unpatch_gpt2(model: torch.nn.Module) -> int:
+    return _unpatch(model, _GPT2_NAMES)
+
+
+def patch_qwen2(model: torch.nn.Module) -> int:
+    """Patch every Qwen2 attention block on ``model``. Returns count patched."""
+    return _patch(model, _QWEN2_NAMES)
+
+
+def unpatch_qwen2(model: torch.nn.Module) -> int:
+    return _unpatch(model, _QWEN2_NAMES)
+
+
+def patch_qwen3(model: torch.nn.Module) -> int:
+    """Patch every Qwen3 attention block (QK-norm is HuggingFace's own code,
+    applied before the routed attention call). Returns count patched; 0 when
+    the installed transformers has no Qwen3."""
+    try:
+        from transformers.models.qwen3 import modeling_qwen3  # noqa: F401
+    except ImportError:
+        return 0
+    return _patch(model, _QWEN3_NAMES)
+
+
+def unpatch_qwen3(model: torch.nn.Module) -> int:
+    return _unpatch(model, _QWEN3_NAMES)
+
+
+def patch_llama(model: torch.nn.Module) -> int:
+    """Patch every Llama attention block on ``model``. Returns count patched."""
+    return _patch(model, _LLAMA_NAMES)
+
+
+def unpatch_llama(model: torch.nn.Module) -> int:
+    return _unpatch(model, _LLAMA_NAMES)
+
+
+def _is_qwen2_attention(mod) -> bool:
+    return type(mod).__name__ in _QWEN2_NAMES
+
+
+def _is_qwen3_attention(mod) -> bool:
+    return type(mod).__name__ in _QWEN3_NAMES
+
+
+def _is_llama_attention(mod) -> bool:
+    return type(mod).__name__ in _LLAMA_NAMES
+
+
+# Linear-attention / state-space families the kernel must refuse
+# (reference patch_hf.py:358-387).
+_LINEAR_ATTN_CLASS_NAMES = {
+    "MambaMixer", "MambaModel", "MambaForCausalLM",
+    "Mamba2Mixer", "Mamba2Model", "Mamba2ForCausalLM",
+    "RwkvSelfAttention", "RwkvLinearAttention", "RwkvModel", "RwkvForCausalLM",
+    "RecurrentGemmaRecurrentBlock", "RecurrentGemmaModel", "RecurrentGemmaForCausalLM",
+    "RetNetAttention", "RetNetModel", "RetNetForCausalLM",
+}
+
+
+def _linear_attn_family(model: torch.nn.Module) -> Optional[str]:
+    """Family name (mamba / mamba2 / rwkv / recurrent_gemma / retnet) of a
+    linear-attention or state-space model, else None."""
+    seen = {type(m).__name__ for m in model.modules()}
+    seen.add(type(model).__name__)
+    if "MambaMixer" in seen:
+        return "mamba"
+    if "Mamba2Mixer" in seen:
+        return "mamba2"
+    if "RwkvSelfAttention" in seen or "RwkvLinearAttention" in seen:
+        return "rwkv"
+    if "RecurrentGemmaRecurrentBlock" in seen:
+        return "recurrent_gemma"
+    if "RetNetAttention" in seen:
+        return "retnet"
+    return None
+
+
+def patch_model(model: torch.nn.Module) -> Tuple[str, int]:
+    """Detect the model family and patch it. Returns ``(family, n_patched)``.
+
+    Raises ``RuntimeError`` for linear-attention / state-space models, for
+    which softmax attention would be mathematically wrong, and
+    ``ValueError`` for an unknown family.
+    """
+    fam = _linear_attn_family(model)
+    if fam is not None:
+        raise RuntimeError(
+            f"flash-attn-volta only supports softmax MHA / GQA — model uses {fam}. "
+            "Refusing to patch a linear-attention / state-space architecture."
+        )
+    cls = type(model).__name__
+    mods = list(model.modules())
+    if "GPT2" in cls or any(type(m).__name__ in _GPT2_NAMES for m in mods):
+        return "gpt2", patch_gpt2(model)
+    if "Qwen3" in cls or any(_is_qwen3_attention(m) for m in mods):
+        return "qwen3", patch_qwen3(model)
+    if "Qwen2" in cls or any(_is_qwen2_attention(m) for m in mods):
+        return "qwen2", patch_qwen2(model)
+    if "Llama" in cls or any(_is_llama_attention(m) for m in mods):
+        return "llama", patch_llama(model)
+    raise ValueError(f"no patch known for model class {cls}")

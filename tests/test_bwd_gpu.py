@@ -166,3 +166,29 @@ def test_backward_is_deterministic():
     b = _autograd(q, k, v, do, True, None)
     for x, y in zip(a, b):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_backward_tiny_upstream_gradient(D):
+    """dO ~ 1e-6 (fp16 subnormals, as deep in an fp16 network trained without
+    loss scaling): dS then lies far below the fp16 normal range, and rounding
+    it to fp16 unscaled flushes ~all of it to zero.  The kernels' per-row
+    power-of-two dS scaling must keep the gradients as good as an fp32 eager
+    attention whose gradients are likewise returned in fp16."""
+    B, S, H = 1, 1024, 4
+    q, k, v, do = orc.make_inputs(B, S, H, D, seed=9)
+    do = (do.float() * 2.0 ** -20).half()
+    _, gq, gk, gv = _autograd(q, k, v, do, True, None)
+    qh, kh, vh = (t.cuda().requires_grad_() for t in (q, k, v))
+    q32, k32, v32 = (t.float().permute(0, 2, 1, 3).contiguous() for t in (qh, kh, vh))
+    s = torch.matmul(q32, k32.transpose(-1, -2).contiguous()) / math.sqrt(D)
+    s = s.masked_fill(torch.triu(torch.ones(S, S, dtype=torch.bool, device="cuda"), 1), float("-inf"))
+    o = torch.matmul(torch.softmax(s, -1), v32).permute(0, 2, 1, 3).half()
+    o.backward(do.cuda())
+    for name, ours, ref in (("dq", gq, qh.grad), ("dk", gk, kh.grad), ("dv", gv, vh.grad)):
+        a, b = ours.double().flatten(), ref.double().flatten()
+        cos = float(a @ b / (a.norm() * b.norm()))
+        zeros = (ours == 0).float().mean().item()
+        print(f"[tiny-dO] D={D} {name}: cos vs fp32-eager {cos:.6f}, zero fraction {zeros:.4f}", flush=True)
+        assert cos >= 0.9999, f"{name} cos {cos}"
+        assert zeros <= (ref == 0).float().mean().item() + 1e-3

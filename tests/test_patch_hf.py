@@ -1,0 +1,132 @@
+"""patch_hf on the CPU: patch/unpatch bookkeeping, family dispatch, the
+linear-attention refusal, the causal-only mask rule and every fast-path
+fallback decision, on tiny random-init transformers models (no downloads).
+
+On the CPU the routed attention always falls back (the kernel needs the
+GPU), so a patched model must reproduce the unpatched outputs bit for bit;
+the GPU side (tests/test_patch_hf_gpu.py) checks the fast path numerically.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import hf_models
+from flash_attn_volta import patch_hf
+
+
+def _attn_modules(model, names):
+    return [m for m in model.modules() if type(m).__name__ in names]
+
+
+@pytest.mark.parametrize("family,make,names,patch,unpatch", [
+    ("llama", hf_models.tiny_llama, patch_hf._LLAMA_NAMES, patch_hf.patch_llama, patch_hf.unpatch_llama),
+    ("qwen2", hf_models.tiny_qwen2, patch_hf._QWEN2_NAMES, patch_hf.patch_qwen2, patch_hf.unpatch_qwen2),
+    ("qwen3", hf_models.tiny_qwen3, patch_hf._QWEN3_NAMES, patch_hf.patch_qwen3, patch_hf.unpatch_qwen3),
+    ("gpt2", hf_models.tiny_gpt2, patch_hf._GPT2_NAMES, patch_hf.patch_gpt2, patch_hf.unpatch_gpt2),
+])
+def test_patch_unpatch_and_cpu_fallback_is_exact(family, make, names, patch, unpatch):
+    model = make()
+    ids = hf_models.token_ids(24)
+    with torch.no_grad():
+        ref = model(ids).logits
+    assert patch(model) == 2
+    mods = _attn_modules(model, names)
+    assert all(m.config._attn_implementation == patch_hf.ATTN_IMPLEMENTATION for m in mods)
+    assert all(hasattr(m, "_orig_forward") for m in mods)
+    # the model-level config (used to build masks) is untouched
+    assert model.config._attn_implementation != patch_hf.ATTN_IMPLEMENTATION
+    assert patch(model) == 2            # idempotent
+    with torch.no_grad():
+        out = model(ids).logits
+    assert torch.equal(out, ref)        # CPU tensors -> original implementation
+    assert unpatch(model) == 2
+    assert all(m.config is model.config for m in mods)
+    assert not any(hasattr(m, "_orig_forward") for m in mods)
+    assert unpatch(model) == 0
+
+
+@pytest.mark.parametrize("make,family", [(hf_models.tiny_llama, "llama"), (hf_models.tiny_qwen2, "qwen2"),
+                                         (hf_models.tiny_qwen3, "qwen3"), (hf_models.tiny_gpt2, "gpt2")])
+def test_patch_model_dispatch(make, family):
+    model = make()
+    assert patch_hf.patch_model(model) == (family, 2)
+
+
+def test_patch_model_refuses_linear_attention():
+    model = hf_models.tiny_mamba()
+    with pytest.raises(RuntimeError) as e:
+        patch_hf.patch_model(model)
+    msg = str(e.value)
+    assert "flash-attn-volta" in msg and "mamba" in msg and "softmax" in msg
+
+
+def test_patch_model_unknown_family():
+    with pytest.raises(ValueError):
+        patch_hf.patch_model(torch.nn.Linear(4, 4))
+
+
+def test_family_patchers_ignore_other_families():
+    model = hf_models.tiny_llama()
+    assert patch_hf.patch_qwen2(model) == 0
+    assert patch_hf.patch_gpt2(model) == 0
+
+
+def _float_causal(n, kv=None, neg=-1e4):
+    kv = kv or n
+    m = torch.zeros(1, 1, n, kv)
+    m[..., torch.triu(torch.ones(n, kv, dtype=torch.bool), 1)] = neg
+    return m
+
+
+def test_causal_only_mask_rule():
+    n = 8
+    assert patch_hf._is_causal_only_mask(_float_causal(n), n)
+    assert patch_hf._is_causal_only_mask(_float_causal(n, neg=torch.finfo(torch.float16).min), n)
+    assert patch_hf._is_causal_only_mask(_float_causal(n, kv=12), n)       # top-left block only
+    pad = _float_causal(n)
+    pad[..., 0] = -1e4                                                     # left padding
+    assert not patch_hf._is_causal_only_mask(pad, n)
+    assert not patch_hf._is_causal_only_mask(torch.zeros(1, 1, n, n), n)  # bidirectional
+    assert not patch_hf._is_causal_only_mask(_float_causal(n)[0, 0], n)   # not 4-D
+    assert not patch_hf._is_causal_only_mask(_float_causal(n), n + 1)
+    b = torch.tril(torch.ones(1, 1, n, n, dtype=torch.bool))
+    assert patch_hf._is_causal_only_mask(b, n)
+    b2 = b.clone()
+    b2[..., 3, 1] = False
+    assert not patch_hf._is_causal_only_mask(b2, n)
+    assert not patch_hf._is_causal_only_mask(torch.ones(1, 1, n, n, dtype=torch.bool), n)
+
+
+class _Mod:
+    is_causal = True
+
+
+class _Enc:
+    is_causal = False
+
+
+def test_fast_path_decisions():
+    f = patch_hf.fast_path_causal
+    m, n = _Mod(), 16
+    assert f(m, n, n, 64, None, 0.0, None, {}) is True
+    assert f(m, n, n, 64, _float_causal(n), 0.0, None, {}) is True
+    assert f(_Enc(), n, n, 64, None, 0.0, None, {}) is False       # non-causal module, no mask
+    assert f(m, 1, n, 64, None, 0.0, None, {}) is None             # KV cache with content
+    assert f(m, n, n, 64, None, 0.0, None, {"output_attentions": True}) is None
+    assert f(m, n, n, 64, None, 0.1, None, {}) is None             # attention dropout
+    assert f(m, n, n, 64, None, 0.0, 8, {}) is None                # narrow sliding window
+    assert f(m, n, n, 64, None, 0.0, 4096, {}) is True             # window wider than S
+    assert f(m, n, n, 96, None, 0.0, None, {}) is None             # head dim
+    assert f(m, n, n, 64, torch.zeros(1, 1, n, n), 0.0, None, {}) is None
+    assert f(_Enc(), n, n, 64, _float_causal(n), 0.0, None, {}) is None
+    cross = _Mod()
+    cross.is_cross_attention = True
+    assert f(cross, n, n, 64, None, 0.0, None, {}) is None
+
+
+def test_expand_kv_matches_transformers_repeat_kv():
+    from transformers.models.llama.modeling_llama import repeat_kv
+    x = torch.randn(2, 3, 5, 8)
+    assert torch.equal(patch_hf._expand_kv(x, 4), repeat_kv(x, 4))
+    assert patch_hf._expand_kv(x, 1) is x
