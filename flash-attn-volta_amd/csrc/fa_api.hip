@@ -62,18 +62,45 @@ int launch_status() {
   return e == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
 }
 
-constexpr int kFwdWaves = 4;
+// Compute units of the current device (cached per device; 256 on MI355X).
+int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
 
-template <int D, bool CAUSAL>
-int launch_fwd(const fa::FwdArgs &args, hipStream_t stream) {
-  constexpr int BM = fa::FwdTile<D, kFwdWaves>::BM;
+// Split each tile's keys across two waves when the grid of 128-query
+// workgroups would leave the GPU under-filled (fewer than 2 per CU; 4 for
+// causal, whose light query tiles finish early and leave the last tiles'
+// long key sweeps as the critical path).
+bool fwd_key_split(int S, int BH, bool causal) {
+  const int64_t wgs = (int64_t)((S + 127) / 128) * BH;
+  return wgs < (int64_t)(causal ? 4 : 2) * device_cus();
+}
+
+template <int D, bool CAUSAL, int KSPLIT>
+int launch_fwd_split(const fa::FwdArgs &args, hipStream_t stream) {
+  using T = fa::FwdTile<D, KSPLIT>;
   fa::FwdArgs a = args;
-  a.n_qtiles = (a.S + BM - 1) / BM;
+  a.n_qtiles = (a.S + T::BM - 1) / T::BM;
   const int64_t grid = (int64_t)a.n_qtiles * a.B * a.H;
   if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
-  hipLaunchKernelGGL((fa::fa_fwd_kernel<D, CAUSAL, kFwdWaves>), dim3((unsigned)grid),
-                     dim3(64 * kFwdWaves), 0, stream, a);
+  hipLaunchKernelGGL((fa::fa_fwd_kernel<D, CAUSAL, KSPLIT>), dim3((unsigned)grid), dim3(T::NT), 0,
+                     stream, a);
   return launch_status();
+}
+
+template <int D, bool CAUSAL>
+int launch_fwd(const fa::FwdArgs &a, hipStream_t stream) {
+  return fwd_key_split(a.S, a.B * a.H, CAUSAL) ? launch_fwd_split<D, CAUSAL, 2>(a, stream)
+                                                : launch_fwd_split<D, CAUSAL, 1>(a, stream);
 }
 
 constexpr int kBwdWaves = 4;

@@ -202,8 +202,8 @@ __global__ __launch_bounds__(64 * NW) void fa_bwd_dkdv_kernel(BwdArgs a) {
   const int BH = a.B * a.H;
   const int bid = blockIdx.x;
   const int bh = bid % BH;
-  // Causal: low key blocks see the most queries, so run them first.
-  const int kt = CAUSAL ? bid / BH : a.n_blocks - 1 - bid / BH;
+  // Causal: low key blocks see the most queries; zigzag heavy/light.
+  const int kt = CAUSAL ? zigzag_rank(bid / BH, a.n_blocks) : bid / BH;
   const int b = bh / a.H, h = bh % a.H;
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int g = lane >> 5, l32 = lane & 31;
@@ -380,7 +380,8 @@ __global__ __launch_bounds__(64 * NW) void fa_bwd_dq_kernel(BwdArgs a) {
   const int BH = a.B * a.H;
   const int bid = blockIdx.x;
   const int bh = bid % BH;
-  const int qt = a.n_blocks - 1 - bid / BH;   // heaviest causal blocks first
+  // Causal: late query blocks see the most keys; zigzag heavy/light.
+  const int qt = CAUSAL ? a.n_blocks - 1 - zigzag_rank(bid / BH, a.n_blocks) : bid / BH;
   const int b = bh / a.H, h = bh % a.H;
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int g = lane >> 5, l32 = lane & 31;

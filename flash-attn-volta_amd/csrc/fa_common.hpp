@@ -140,6 +140,18 @@ __device__ __forceinline__ half8 load_tr8(const f16 *tile, int row_lo, int row_h
 // (kperm swaps bits 2 and 3, so it is its own inverse).
 __device__ __forceinline__ int kperm_row(int r) { return (r & ~31) + kperm(r & 31); }
 
+// Causal work balance.  Workgroups are numbered bid = r * BH + bh; blocks
+// with larger `heavy_rank` cost more (causal: more visible tiles).  Ranks are
+// dealt heaviest-first for the first half of the grid and lightest-first for
+// the second half, so the first-round and second-round workgroups that the
+// dispatcher places on one CU (bid and bid + half * BH) carry complementary
+// loads; with more workgroups than slots it degrades to longest-first.
+// Returns the heavy rank (0 = heaviest) of rank r out of n.
+__device__ __forceinline__ int zigzag_rank(int r, int n) {
+  const int half = (n + 1) / 2;
+  return r < half ? r : n - 1 - (r - half);
+}
+
 // Index of this thread's wave, as a wave-uniform (scalar) value.
 __device__ __forceinline__ int wave_id() {
   return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);

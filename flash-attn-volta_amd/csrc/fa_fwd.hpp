@@ -8,10 +8,10 @@
 // (:146-150) and LSE = m + ln(l), +inf when a row saw no key (:152-159).
 //
 // MI355X layout of the work:
-//   * workgroup = NW waves; each wave owns 32 consecutive queries, so a
-//     workgroup covers BM = 32*NW queries of one (b, h);
+//   * workgroup = 4 waves over 64 queries of one (b, h): 2 query groups of
+//     32 x 2 key halves of every tile, merged at the end (see the kernel);
 //   * key/value tiles of BN = 64 rows stream through LDS.  K lives in a
-//     3-slot ring, one tile ahead of V (2-slot ring), so the S^T MFMAs of
+//     2-slot ring one tile ahead of V (2-slot ring), so the S^T MFMAs of
 //     tile t+1 are issued before the softmax of tile t and run under it;
 //   * K rows are stored in kperm order so every lane's A-operand read is a
 //     plain 16-byte ds_read of LDS row (lane % 32); V stays row-major and the
@@ -19,7 +19,7 @@
 //   * the wave's Q fragment stays in registers for the whole sweep;
 //   * a lane owns one query row: the running max / sum and the O^T
 //     accumulator column live in that lane, the only cross-lane step is one
-//     v_permlane32_swap per key tile for the row max;
+//     v_permlane32_swap per key half for the row max;
 //   * probabilities are rounded to fp16 once and the row sum accumulates
 //     those rounded values (v_dot2_f32_f16), so numerator and denominator
 //     see the same weights;
@@ -49,17 +49,23 @@ struct FwdArgs {
   int neg;             // 1 when sm_scale < 0: Q is negated on load
 };
 
-template <int D, int NW>
+template <int D, int KSPLIT>
 struct FwdTile {
-  static constexpr int BM = 32 * NW;
-  static constexpr int BN = 64;
-  static constexpr int NT = 64 * NW;
+  static_assert(KSPLIT == 1 || KSPLIT == 2, "key split is 1 or 2");
+  static constexpr int NQG = 4 / KSPLIT;   // query groups of 32 per workgroup
+  static constexpr int NSUB = 2 / KSPLIT;  // 32-key sub-blocks per wave per tile
+  static constexpr int BM = 32 * NQG;      // queries per workgroup
+  static constexpr int BN = 64;            // keys per tile
+  static constexpr int NT = 256;           // 4 waves
   static constexpr int KS = D + 8;    // K slot row stride (halves)
   static constexpr int VS = D + 16;   // V slot row stride (halves)
   static constexpr int CHUNKS = BN * D / 8;                // 16-byte chunks per tile
   static constexpr int PER_T = (CHUNKS + NT - 1) / NT;
   static constexpr int LDS_K = BN * KS;
   static constexpr int LDS_V = BN * VS;
+  // per-lane softmax state of a key-half wave handed over for the final merge
+  static constexpr int MERGE_FLOATS = 2 * 64 * (D / 2 + 2);
+  static_assert(MERGE_FLOATS * 4 <= 2 * LDS_K * 2, "merge buffer must fit in the K slots");
 };
 
 // max(x, value of lane ^ 32).  v_permlane32_swap exchanges the upper half of
@@ -70,27 +76,41 @@ __device__ __forceinline__ float max_xor32(float x) {
   return fmaxf(x, fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])));
 }
 
-template <int D, bool CAUSAL, int NW>
-__global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
-  using T = FwdTile<D, NW>;
+// Workgroup = 4 waves.  KSPLIT = 1: each wave owns 32 queries (BM = 128)
+// and both 32-key halves of every 64-key tile.  KSPLIT = 2: wave w owns
+// query group qg = w / 2 (BM = 64) and key half kh = w % 2 of every tile;
+// each wave runs its own online softmax over its key half and the two halves
+// of a query group merge through LDS at the end (lane l of both waves holds
+// the same query and the same O^T rows, so the merge is element-wise).
+// Splitting keys halves each wave's work per tile and doubles the waves in
+// flight: it pays when the grid is too small to fill the GPU, and for
+// causal attention, whose last query tile walks every key tile.  The
+// launcher picks KSPLIT from the grid size.
+template <int D, bool CAUSAL, int KSPLIT>
+__global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
+  using T = FwdTile<D, KSPLIT>;
+  constexpr int NSUB = T::NSUB;
   constexpr int BM = T::BM, BN = T::BN, NT = T::NT, KS = T::KS, VS = T::VS;
-  __shared__ __attribute__((aligned(16))) f16 sk[3][T::LDS_K];
+  __shared__ __attribute__((aligned(16))) f16 sk[2][T::LDS_K];
   __shared__ __attribute__((aligned(16))) f16 sv[2][T::LDS_V];
 
   const int S = a.S;
   const int BH = a.B * a.H;
   const int bid = blockIdx.x;
   const int bh = bid % BH;
-  // Heaviest causal tiles first; consecutive workgroups of one (b, h) are BH
-  // apart, so with BH % 8 == 0 they land on one XCD and share its L2.
-  const int qt = a.n_qtiles - 1 - bid / BH;
+  // Causal: zigzag heavy/light query tiles (heavy = late tiles); workgroups
+  // of one (b, h) are BH apart, so with BH % 8 == 0 they land on one XCD and
+  // share its L2.
+  const int qt = CAUSAL ? a.n_qtiles - 1 - zigzag_rank(bid / BH, a.n_qtiles) : bid / BH;
   const int b = bh / a.H, h = bh % a.H;
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = wave_id();
+  const int qg = KSPLIT == 2 ? (w >> 1) : w;
+  const int kh = KSPLIT == 2 ? (w & 1) : 0;
   const int g = lane >> 5, l32 = lane & 31;
   const int q0 = qt * BM;
-  const int wq0 = q0 + 32 * w;   // first query of this wave
-  const int qrow = wq0 + l32;    // query owned by this lane
+  const int wq0 = q0 + 32 * qg;   // first query of this wave
+  const int qrow = wq0 + l32;     // query owned by this lane
 
   const f16 *qb = a.q.head(b, h);
   const f16 *kb = a.k.head(b, h);
@@ -131,8 +151,7 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
     for (int i = 0; i < T::PER_T; ++i) {
       if (T::CHUNKS % NT == 0 || tid + i * NT < T::CHUNKS) {
         const int r = ch_row[i];
-        const int row = (r & 32) + kperm(r & 31);
-        *(u32x4 *)(&sk[slot][row * KS + ch_col[i]]) = kreg[i];
+        *(u32x4 *)(&sk[slot][kperm_row(r) * KS + ch_col[i]]) = kreg[i];
       }
     }
   };
@@ -143,15 +162,20 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
         *(u32x4 *)(&sv[slot][ch_row[i] * VS + ch_col[i]]) = vreg[i];
   };
 
-  // ---- S^T = K Q^T for one 64-key tile (two 32-key sub-blocks)
+  // Sub-block sb (32 keys) of this wave in the tile at n0 starts at key
+  // n0 + 32 * (NSUB * kh + sb); it is dead when it lies entirely above the
+  // wave's causal diagonal.
+  auto sub_key = [&](int n0, int sb) { return n0 + 32 * (NSUB * kh + sb); };
+  auto dead = [&](int n0, int sb) { return CAUSAL && sub_key(n0, sb) > wq0 + 31; };
+
+  // ---- S^T = K Q^T for this wave's sub-blocks of a tile
   half8 qf[D / 16];
-  auto qk = [&](int slot, int n0, floatx16 (&s)[2]) {
+  auto qk = [&](int slot, int n0, floatx16 (&s)[NSUB]) {
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-      // A sub-block entirely above this wave's diagonal is skipped; its
-      // scores are then overwritten with -inf by the diagonal-tile mask.
-      if (CAUSAL && n0 + 32 * sb > wq0 + 31) continue;
-      const f16 *kr = &sk[slot][(32 * sb + l32) * KS + 8 * g];
+    for (int sb = 0; sb < NSUB; ++sb) {
+      // dead sub-blocks are skipped; the diagonal mask overwrites them
+      if (dead(n0, sb)) continue;
+      const f16 *kr = &sk[slot][(32 * (NSUB * kh + sb) + l32) * KS + 8 * g];
       floatx16 acc = mfma32(*(const half8 *)kr, qf[0], floatx16{});
 #pragma unroll
       for (int cc = 1; cc < D / 16; ++cc) acc = mfma32(*(const half8 *)(kr + 16 * cc), qf[cc], acc);
@@ -183,8 +207,10 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
   }
   __syncthreads();
 
-  floatx16 s_cur[2], s_nxt[2];
+  floatx16 s_cur[NSUB], s_nxt[NSUB];
   qk(0, 0, s_cur);
+  // K slot 0 is refilled with K(2) at the end of the first iteration
+  __syncthreads();
 
   floatx16 oacc[D / 32];
 #pragma unroll
@@ -198,71 +224,104 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
     const bool more1 = t + 1 < n_tiles, more2 = t + 2 < n_tiles;
     if (more2) load_k(n0 + 2 * BN);
     if (more1) load_v(n0 + BN);
-    if (more1) qk((t + 1) % 3, n0 + BN, s_nxt);
+    if (more1) qk((t + 1) & 1, n0 + BN, s_nxt);
 
-    // ---- masking (diagonal / ragged tiles only)
-    const bool need_mask = (CAUSAL && n0 + BN - 1 > wq0) || (n0 + BN > S);
-    if (need_mask) {
+    if (!dead(n0, 0)) {
+      // ---- masking (diagonal / ragged sub-blocks only)
 #pragma unroll
-      for (int sb = 0; sb < 2; ++sb)
+      for (int sb = 0; sb < NSUB; ++sb) {
+        const int ns = sub_key(n0, sb);
+        if ((CAUSAL && ns + 31 > wq0) || (ns + 31 >= S)) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = n0 + 32 * sb + slot_row(i, g);
-          const bool vis = key < S && (!CAUSAL || key <= qrow);
-          s_cur[sb][i] = vis ? s_cur[sb][i] : kNegInf;
+          for (int i = 0; i < 16; ++i) {
+            const int key = ns + slot_row(i, g);
+            const bool vis = key < S && (!CAUSAL || key <= qrow);
+            s_cur[sb][i] = vis ? s_cur[sb][i] : kNegInf;
+          }
         }
-    }
+      }
 
-    // ---- tile row max and lazy rescale
-    float mx = s_cur[0][0];
+      // ---- row max over this wave's keys of the tile and lazy rescale
+      float mx = s_cur[0][0];
 #pragma unroll
-    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s_cur[0][i]);
+      for (int sb = 0; sb < NSUB; ++sb)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s_cur[1][i]);
-    mx = max_xor32(mx);
-    const float m_new = fmaxf(m_run, mx * c);
-    const bool grow = m_new > m_run + kRescaleLog2;
-    if (__any(grow)) {
-      const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f;
-      m_run = grow ? m_new : m_run;
-      l_run *= alpha;
-#pragma unroll
-      for (int d = 0; d < D / 32; ++d)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) oacc[d][i] *= alpha;
-    }
-    const float neg_m = (m_run == kNegInf) ? 0.0f : -m_run;
-
-    // ---- P = exp2(c*s - m) rounded to fp16; O^T += V^T P^T
-    const int vslot = t & 1;
-#pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-      if (CAUSAL && n0 + 32 * sb > wq0 + 31) continue;
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        half8 pf;
-#pragma unroll
-        for (int j = 0; j < 8; j += 2) {
-          half2 pr = __builtin_convertvector(
-              (floatx2){fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + j], c, neg_m)),
-                        fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + j + 1], c, neg_m))},
-              half2);
-          l_run = dot2_acc(pr, l_run);
-          pf[j] = pr[0];
-          pf[j + 1] = pr[1];
-        }
-        const int kbase = 32 * sb + 16 * hh + 8 * g;
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s_cur[sb][i]);
+      mx = max_xor32(mx);
+      const float m_new = fmaxf(m_run, mx * c);
+      const bool grow = m_new > m_run + kRescaleLog2;
+      if (__any(grow)) {
+        const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f;
+        m_run = grow ? m_new : m_run;
+        l_run *= alpha;
 #pragma unroll
         for (int d = 0; d < D / 32; ++d)
-          oacc[d] = mfma32(load_tr8<VS>(sv[vslot], kbase, kbase + 4, 32 * d, lane), pf, oacc[d]);
+#pragma unroll
+          for (int i = 0; i < 16; ++i) oacc[d][i] *= alpha;
+      }
+      const float neg_m = (m_run == kNegInf) ? 0.0f : -m_run;
+
+      // ---- P = exp2(c*s - m) rounded to fp16; O^T += V^T P^T
+      const int vslot = t & 1;
+#pragma unroll
+      for (int sb = 0; sb < NSUB; ++sb) {
+        if (dead(n0, sb)) continue;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          half8 pf;
+#pragma unroll
+          for (int j = 0; j < 8; j += 2) {
+            half2 pr = __builtin_convertvector(
+                (floatx2){fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + j], c, neg_m)),
+                          fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + j + 1], c, neg_m))},
+                half2);
+            l_run = dot2_acc(pr, l_run);
+            pf[j] = pr[0];
+            pf[j + 1] = pr[1];
+          }
+          const int kbase = 32 * (NSUB * kh + sb) + 16 * hh + 8 * g;
+#pragma unroll
+          for (int d = 0; d < D / 32; ++d)
+            oacc[d] = mfma32(load_tr8<VS>(sv[vslot], kbase, kbase + 4, 32 * d, lane), pf, oacc[d]);
+        }
       }
     }
 
-    if (more2) store_k((t + 2) % 3);
+    if (more2) store_k(t & 1);
     if (more1) store_v((t + 1) & 1);
     __syncthreads();
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb) s_cur[sb] = s_nxt[sb];
+    for (int sb = 0; sb < NSUB; ++sb) s_cur[sb] = s_nxt[sb];
+  }
+
+  // ---- merge the two key halves of each query group (K slots reused; the
+  // loop's last barrier ordered every read of them before these writes)
+  if (KSPLIT == 2) {
+  float *mbuf = reinterpret_cast<float *>(&sk[0][0]) + qg * 64 * (D / 2 + 2);
+  if (kh == 1) {
+    mbuf[lane] = m_run;
+    mbuf[64 + lane] = l_run;
+#pragma unroll
+    for (int d = 0; d < D / 32; ++d)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mbuf[(2 + 16 * d + i) * 64 + lane] = oacc[d][i];
+  }
+  __syncthreads();
+  if (kh == 1) return;
+  {
+    const float m_b = mbuf[lane];
+    const float l_b = mbuf[64 + lane];
+    const float m = fmaxf(m_run, m_b);
+    const float fa = (m == kNegInf) ? 0.0f : fast_exp2(m_run - m);
+    const float fb = (m == kNegInf) ? 0.0f : fast_exp2(m_b - m);
+    l_run = l_run * fa + l_b * fb;
+#pragma unroll
+    for (int d = 0; d < D / 32; ++d)
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        oacc[d][i] = oacc[d][i] * fa + mbuf[(2 + 16 * d + i) * 64 + lane] * fb;
+    m_run = m;
+  }
   }
 
   // ---- epilogue: O = acc / l, LSE = (m + log2 l) * ln2

@@ -139,3 +139,18 @@ def test_forward_argument_errors():
     with pytest.raises(ValueError):
         z = torch.zeros(1, 8, 1, 48, dtype=torch.float16, device="cuda")
         flash_attn_forward(z, z, z)
+
+
+# The launcher splits each tile's keys across two waves only when the grid of
+# 128-query workgroups is small (< 2 per CU, < 4 causal; 256 CUs on MI355X).
+# These ragged shapes are large enough to run the unsplit variant; the shapes
+# above run the split one.
+@pytest.mark.parametrize("shape,causal", [((4, 1000, 32, 64), False), ((8, 1000, 32, 64), True),
+                                          ((4, 777, 32, 128), False), ((8, 520, 32, 32), True)])
+def test_forward_large_grid_variant(shape, causal):
+    B, S, H, D = shape
+    print(f"[case] fwd large-grid {shape} causal={causal}", flush=True)
+    (q, k, v, _), o_ref, lse_ref = _oracle_fwd(B, S, H, D, causal, None, 1.0, 10)
+    out, lse = _run(q, k, v, causal, None)
+    assert max_abs(out, o_ref) < TOL
+    assert max_abs(lse, lse_ref) < TOL
