@@ -76,10 +76,12 @@ int device_cus() {
   return cache[dev];
 }
 
-// Split each tile's keys across two waves when the grid of 128-query
+// Split each tile's rows across two waves when the grid of 128-row
 // workgroups would leave the GPU under-filled (fewer than 2 per CU; 4 for
-// causal, whose light query tiles finish early and leave the last tiles'
-// long key sweeps as the critical path).
+// causal, whose light blocks finish early and leave the heavy blocks' long
+// sweeps as the critical path).  Used by the forward and both backward
+// kernels (the split is over keys in the forward and dQ, over queries in
+// dK/dV).
 bool fwd_key_split(int S, int BH, bool causal) {
   const int64_t wgs = (int64_t)((S + 127) / 128) * BH;
   return wgs < (int64_t)(causal ? 4 : 2) * device_cus();
@@ -103,8 +105,6 @@ int launch_fwd(const fa::FwdArgs &a, hipStream_t stream) {
                                                 : launch_fwd_split<D, CAUSAL, 1>(a, stream);
 }
 
-constexpr int kBwdWaves = 4;
-
 template <int D>
 int launch_pre(const fa::PreArgs &a, hipStream_t stream) {
   constexpr int RPB = 256 / (D / 8);
@@ -116,28 +116,40 @@ int launch_pre(const fa::PreArgs &a, hipStream_t stream) {
   return launch_status();
 }
 
-template <int D, bool CAUSAL>
-int launch_dkdv(const fa::BwdArgs &args, hipStream_t stream) {
+template <int D, bool CAUSAL, int SPLIT>
+int launch_dkdv_split(const fa::BwdArgs &args, hipStream_t stream) {
+  using T = fa::DkdvTile<D, SPLIT>;
   fa::BwdArgs a = args;
-  constexpr int BK = fa::DkdvTile<D, kBwdWaves>::BK;
-  a.n_blocks = (a.S + BK - 1) / BK;
+  a.n_blocks = (a.S + T::BK - 1) / T::BK;
   const int64_t grid = (int64_t)a.n_blocks * a.B * a.H;
   if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
-  hipLaunchKernelGGL((fa::fa_bwd_dkdv_kernel<D, CAUSAL, kBwdWaves>), dim3((unsigned)grid),
-                     dim3(64 * kBwdWaves), 0, stream, a);
+  hipLaunchKernelGGL((fa::fa_bwd_dkdv_kernel<D, CAUSAL, SPLIT>), dim3((unsigned)grid), dim3(T::NT),
+                     0, stream, a);
+  return launch_status();
+}
+
+template <int D, bool CAUSAL, int SPLIT>
+int launch_dq_split(const fa::BwdArgs &args, hipStream_t stream) {
+  using T = fa::DqTile<D, SPLIT>;
+  fa::BwdArgs a = args;
+  a.n_blocks = (a.S + T::BM - 1) / T::BM;
+  const int64_t grid = (int64_t)a.n_blocks * a.B * a.H;
+  if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
+  hipLaunchKernelGGL((fa::fa_bwd_dq_kernel<D, CAUSAL, SPLIT>), dim3((unsigned)grid), dim3(T::NT), 0,
+                     stream, a);
   return launch_status();
 }
 
 template <int D, bool CAUSAL>
-int launch_dq(const fa::BwdArgs &args, hipStream_t stream) {
-  fa::BwdArgs a = args;
-  constexpr int BM = fa::DqTile<D, kBwdWaves>::BM;
-  a.n_blocks = (a.S + BM - 1) / BM;
-  const int64_t grid = (int64_t)a.n_blocks * a.B * a.H;
-  if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
-  hipLaunchKernelGGL((fa::fa_bwd_dq_kernel<D, CAUSAL, kBwdWaves>), dim3((unsigned)grid),
-                     dim3(64 * kBwdWaves), 0, stream, a);
-  return launch_status();
+int launch_dkdv(const fa::BwdArgs &a, hipStream_t stream) {
+  return fwd_key_split(a.S, a.B * a.H, CAUSAL) ? launch_dkdv_split<D, CAUSAL, 2>(a, stream)
+                                                : launch_dkdv_split<D, CAUSAL, 1>(a, stream);
+}
+
+template <int D, bool CAUSAL>
+int launch_dq(const fa::BwdArgs &a, hipStream_t stream) {
+  return fwd_key_split(a.S, a.B * a.H, CAUSAL) ? launch_dq_split<D, CAUSAL, 2>(a, stream)
+                                                : launch_dq_split<D, CAUSAL, 1>(a, stream);
 }
 
 template <bool CAUSAL>

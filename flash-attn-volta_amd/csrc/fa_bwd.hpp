@@ -177,22 +177,56 @@ __device__ __forceinline__ void load_row_frags(half8 (&f)[D / 16], const f16 *he
 }
 
 // ---------------------------------------------------------------------------
-// dK / dV: workgroup = NW waves, wave w owns keys k0 + 32w .. +31 (lane l32
-// owns key k0 + 32w + l32).  Query tiles of BQ = 64 rows stream through
-// double-buffered LDS as Q and dO (kperm row order) plus LSE and delta.
-template <int D, int NW>
+// Partial-sum merge of two waves that own the same output rows (lane l of
+// both waves holds the same row and the same D^T slots).  `buf` is LDS with
+// room for 64 * (D/2 + 1) floats; every thread calls it (it has a barrier).
+// The writer hands over acc * 2^-e (its power-of-two dS scale undone), the
+// reader adds it to its own acc * 2^-e and returns the unscaled sum in acc.
+template <int D>
+__device__ __forceinline__ void merge_pair(float *buf, bool writer, floatx16 (&acc)[D / 32],
+                                           const DsScale &sc, int lane) {
+  const float inv = __builtin_amdgcn_ldexpf(1.0f, -sc.e);
+  if (writer) {
+#pragma unroll
+    for (int d = 0; d < D / 32; ++d)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) buf[(16 * d + i) * 64 + lane] = acc[d][i] * inv;
+  }
+  __syncthreads();
+  if (!writer) {
+#pragma unroll
+    for (int d = 0; d < D / 32; ++d)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[d][i] = acc[d][i] * inv + buf[(16 * d + i) * 64 + lane];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dK / dV: workgroup = 4 waves.  SPLIT = 1: wave w owns 32 keys (BK = 128)
+// and both 32-query halves of every 64-query tile.  SPLIT = 2: wave w owns
+// key group kg = w / 2 (BK = 64) and query half qh = w % 2 of every tile;
+// the two query halves of a key group merge their dK / dV partial sums
+// through LDS at the end.  The split doubles the waves in flight for grids
+// too small to fill the GPU (the launcher decides).  Query tiles of
+// BQ = 64 rows stream through double-buffered LDS as Q and dO (kperm row
+// order) plus LSE and delta.
+template <int D, int SPLIT>
 struct DkdvTile {
-  static constexpr int BK = 32 * NW;
+  static_assert(SPLIT == 1 || SPLIT == 2, "split is 1 or 2");
+  static constexpr int NKG = 4 / SPLIT;    // key groups of 32 per workgroup
+  static constexpr int NSUB = 2 / SPLIT;   // 32-query sub-blocks per wave per tile
+  static constexpr int BK = 32 * NKG;
   static constexpr int BQ = 64;
-  static constexpr int NT = 64 * NW;
+  static constexpr int NT = 256;
   static constexpr int RS = D + 8;
   static constexpr int LDS_ROW = BQ * RS;
+  static_assert(2 * 64 * (D / 2 + 1) * 4 <= 2 * LDS_ROW * 2, "merge buffer must fit in a tile ring");
 };
 
-template <int D, bool CAUSAL, int NW>
-__global__ __launch_bounds__(64 * NW) void fa_bwd_dkdv_kernel(BwdArgs a) {
-  using T = DkdvTile<D, NW>;
-  constexpr int BK = T::BK, BQ = T::BQ, NT = T::NT, RS = T::RS;
+template <int D, bool CAUSAL, int SPLIT>
+__global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
+  using T = DkdvTile<D, SPLIT>;
+  constexpr int BK = T::BK, BQ = T::BQ, NT = T::NT, RS = T::RS, NSUB = T::NSUB;
   __shared__ __attribute__((aligned(16))) f16 s_q[2][T::LDS_ROW];
   __shared__ __attribute__((aligned(16))) f16 s_do[2][T::LDS_ROW];
   __shared__ __attribute__((aligned(16))) float s_lse[2][BQ];
@@ -206,9 +240,11 @@ __global__ __launch_bounds__(64 * NW) void fa_bwd_dkdv_kernel(BwdArgs a) {
   const int kt = CAUSAL ? zigzag_rank(bid / BH, a.n_blocks) : bid / BH;
   const int b = bh / a.H, h = bh % a.H;
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+  const int kg = SPLIT == 2 ? (w >> 1) : w;
+  const int qh = SPLIT == 2 ? (w & 1) : 0;
   const int g = lane >> 5, l32 = lane & 31;
   const int k0 = kt * BK;
-  const int wk0 = k0 + 32 * w;
+  const int wk0 = k0 + 32 * kg;
   const int key = wk0 + l32;
 
   const f16 *qb = a.q.head(b, h);
@@ -273,7 +309,8 @@ __global__ __launch_bounds__(64 * NW) void fa_bwd_dkdv_kernel(BwdArgs a) {
     if (t + 1 < n_tiles) load_tile(m0 + BQ);
 
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
+    for (int sb = 0; sb < NSUB; ++sb) {
+      const int qs = NSUB * qh + sb;   // 32-query sub-block of the tile
       const int ms = m0 + 32 * qs;
       // whole sub-block above this wave's keys' diagonal: nothing visible
       if (CAUSAL && ms + 31 < wk0) continue;
@@ -316,10 +353,9 @@ __global__ __launch_bounds__(64 * NW) void fa_bwd_dkdv_kernel(BwdArgs a) {
         }
       }
       // adaptive power-of-two scale of this key's dS column
-      const float m = fmaxf(absmax16(ds), 0.0f);
-      const float mk = fmaxf(m, __shfl_xor(m, 32, 64));
+      const float mk = absmax16(ds);
       {
-        const float f = sc.update(mk);
+        const float f = sc.update(fmaxf(mk, __shfl_xor(mk, 32, 64)));
         if (__any(f != 1.0f)) {
 #pragma unroll
           for (int d = 0; d < D / 32; ++d)
@@ -349,30 +385,47 @@ __global__ __launch_bounds__(64 * NW) void fa_bwd_dkdv_kernel(BwdArgs a) {
     __syncthreads();
   }
 
+  float dk_mul = a.sm_scale / sc.mul;
+  if (SPLIT == 2) {
+    // the loop's last barrier ordered every tile read before these writes
+    const DsScale unit;
+    merge_pair<D>(reinterpret_cast<float *>(&s_q[0][0]) + kg * 64 * (D / 2 + 1), qh == 1, dk, sc,
+                  lane);
+    merge_pair<D>(reinterpret_cast<float *>(&s_do[0][0]) + kg * 64 * (D / 2 + 1), qh == 1, dv,
+                  unit, lane);
+    if (qh == 1) return;
+    dk_mul = a.sm_scale;
+  }
   if (key < S) {
-    store_row_fp16<D>(a.dk + b * a.dk_sb + h * a.dk_sh + (int64_t)key * a.dk_ss, dk,
-                      a.sm_scale / sc.mul, g);
+    store_row_fp16<D>(a.dk + b * a.dk_sb + h * a.dk_sh + (int64_t)key * a.dk_ss, dk, dk_mul, g);
     store_row_fp16<D>(a.dv + b * a.dv_sb + h * a.dv_sh + (int64_t)key * a.dv_ss, dv, 1.0f, g);
   }
 }
 
 // ---------------------------------------------------------------------------
-// dQ: workgroup = NW waves, wave w owns queries q0 + 32w .. +31 (lane l32
-// owns one query).  Key tiles of BN = 64 rows stream through double-buffered
-// LDS as K and V (kperm row order).
-template <int D, int NW>
+// dQ: workgroup = 4 waves.  SPLIT = 1: wave w owns 32 queries (BM = 128)
+// and both 32-key halves of every 64-key tile.  SPLIT = 2: wave w owns query
+// group qg = w / 2 (BM = 64) and key half kh = w % 2 of every tile; the two
+// key halves of a query group merge their dQ partial sums through LDS at
+// the end.  Key tiles of BN = 64 rows stream through double-buffered LDS as
+// K and V (kperm row order).
+template <int D, int SPLIT>
 struct DqTile {
-  static constexpr int BM = 32 * NW;
+  static_assert(SPLIT == 1 || SPLIT == 2, "split is 1 or 2");
+  static constexpr int NQG = 4 / SPLIT;
+  static constexpr int NSUB = 2 / SPLIT;
+  static constexpr int BM = 32 * NQG;
   static constexpr int BN = 64;
-  static constexpr int NT = 64 * NW;
+  static constexpr int NT = 256;
   static constexpr int RS = D + 8;
   static constexpr int LDS_ROW = BN * RS;
+  static_assert(2 * 64 * (D / 2 + 1) * 4 <= 2 * LDS_ROW * 2, "merge buffer must fit in a tile ring");
 };
 
-template <int D, bool CAUSAL, int NW>
-__global__ __launch_bounds__(64 * NW) void fa_bwd_dq_kernel(BwdArgs a) {
-  using T = DqTile<D, NW>;
-  constexpr int BM = T::BM, BN = T::BN, NT = T::NT, RS = T::RS;
+template <int D, bool CAUSAL, int SPLIT>
+__global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
+  using T = DqTile<D, SPLIT>;
+  constexpr int BM = T::BM, BN = T::BN, NT = T::NT, RS = T::RS, NSUB = T::NSUB;
   __shared__ __attribute__((aligned(16))) f16 s_k[2][T::LDS_ROW];
   __shared__ __attribute__((aligned(16))) f16 s_v[2][T::LDS_ROW];
 
@@ -384,9 +437,11 @@ __global__ __launch_bounds__(64 * NW) void fa_bwd_dq_kernel(BwdArgs a) {
   const int qt = CAUSAL ? a.n_blocks - 1 - zigzag_rank(bid / BH, a.n_blocks) : bid / BH;
   const int b = bh / a.H, h = bh % a.H;
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
+  const int qg = SPLIT == 2 ? (w >> 1) : w;
+  const int kh = SPLIT == 2 ? (w & 1) : 0;
   const int g = lane >> 5, l32 = lane & 31;
   const int q0 = qt * BM;
-  const int wq0 = q0 + 32 * w;
+  const int wq0 = q0 + 32 * qg;
   const int qrow = wq0 + l32;
 
   const f16 *kb = a.k.head(b, h);
@@ -436,14 +491,15 @@ __global__ __launch_bounds__(64 * NW) void fa_bwd_dq_kernel(BwdArgs a) {
     if (t + 1 < n_tiles) load_tile(n0 + BN);
 
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-      const int ns = n0 + 32 * sb;
+    for (int sb = 0; sb < NSUB; ++sb) {
+      const int ks = NSUB * kh + sb;   // 32-key sub-block of the tile
+      const int ns = n0 + 32 * ks;
       if (CAUSAL && ns > wq0 + 31) continue;
       if (ns >= S) continue;
       floatx16 sacc, dpacc;
       {
-        const f16 *kr = &s_k[st][(32 * sb + l32) * RS + 8 * g];
-        const f16 *vr = &s_v[st][(32 * sb + l32) * RS + 8 * g];
+        const f16 *kr = &s_k[st][(32 * ks + l32) * RS + 8 * g];
+        const f16 *vr = &s_v[st][(32 * ks + l32) * RS + 8 * g];
         sacc = mfma32(*(const half8 *)kr, qf[0], floatx16{});
         dpacc = mfma32(*(const half8 *)vr, gf[0], floatx16{});
 #pragma unroll
@@ -465,9 +521,8 @@ __global__ __launch_bounds__(64 * NW) void fa_bwd_dq_kernel(BwdArgs a) {
         ds[i] = p * (dpacc[i] - dl);
       }
       const float m = absmax16(ds);
-      const float mq = fmaxf(m, __shfl_xor(m, 32, 64));
       {
-        const float f = sc.update(mq);
+        const float f = sc.update(fmaxf(m, __shfl_xor(m, 32, 64)));
         if (__any(f != 1.0f)) {
 #pragma unroll
           for (int d = 0; d < D / 32; ++d)
@@ -480,7 +535,7 @@ __global__ __launch_bounds__(64 * NW) void fa_bwd_dq_kernel(BwdArgs a) {
       for (int i = 0; i < 16; ++i) dsf[i >> 3][i & 7] = (f16)(ds[i] * sc.mul);
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        const int rlo = 32 * sb + 16 * hh + 4 * g;   // kperm rows of this 8-key slice
+        const int rlo = 32 * ks + 16 * hh + 4 * g;   // kperm rows of this 8-key slice
 #pragma unroll
         for (int d = 0; d < D / 32; ++d)
           dq[d] = mfma32(load_tr8<RS>(s_k[st], rlo, rlo + 8, 32 * d, lane), dsf[hh], dq[d]);
@@ -491,9 +546,16 @@ __global__ __launch_bounds__(64 * NW) void fa_bwd_dq_kernel(BwdArgs a) {
     __syncthreads();
   }
 
+  float dq_mul = a.sm_scale / sc.mul;
+  if (SPLIT == 2) {
+    // the loop's last barrier ordered every tile read before these writes
+    merge_pair<D>(reinterpret_cast<float *>(&s_k[0][0]) + qg * 64 * (D / 2 + 1), kh == 1, dq, sc,
+                  lane);
+    if (kh == 1) return;
+    dq_mul = a.sm_scale;
+  }
   if (qrow < S)
-    store_row_fp16<D>(a.dq + b * a.dq_sb + h * a.dq_sh + (int64_t)qrow * a.dq_ss, dq,
-                      a.sm_scale / sc.mul, g);
+    store_row_fp16<D>(a.dq + b * a.dq_sb + h * a.dq_sh + (int64_t)qrow * a.dq_ss, dq, dq_mul, g);
 }
 
 }  // namespace fa

@@ -192,3 +192,15 @@ def test_backward_tiny_upstream_gradient(D):
         print(f"[tiny-dO] D={D} {name}: cos vs fp32-eager {cos:.6f}, zero fraction {zeros:.4f}", flush=True)
         assert cos >= 0.9999, f"{name} cos {cos}"
         assert zeros <= (ref == 0).float().mean().item() + 1e-3
+
+
+# Large enough grids to run the unsplit backward kernels (the launcher splits
+# rows across waves only for grids under 2 / 4 (causal) workgroups per CU).
+@pytest.mark.parametrize("shape,causal", [((4, 1000, 32, 64), False), ((8, 600, 32, 32), True),
+                                          ((2, 1100, 64, 128), False)])
+def test_backward_large_grid_variant(shape, causal):
+    B, S, H, D = shape
+    print(f"[case] bwd large-grid {shape} causal={causal}", flush=True)
+    (q, k, v, do), (o, lse, dq, dk, dv, _) = _oracle(B, S, H, D, causal, None, 1.0, 11)
+    out, gq, gk, gv = _autograd(q, k, v, do, causal, None)
+    assert max(max_abs(gq, dq), max_abs(gk, dk), max_abs(gv, dv), max_abs(out, o)) < TOL
