@@ -14,8 +14,8 @@ import math
 import torch
 
 from . import _capi
-from .forward import (NATIVE_HEAD_DIMS, SUPPORTED_HEAD_DIMS, _kernel_ready, _pad_d, _require,
-                      _stream_ptr, kernel_strides)
+from .forward import (NATIVE_HEAD_DIMS, SUPPORTED_HEAD_DIMS, _kernel_ready, _on_device, _pad_d,
+                      _require, _stream_ptr, kernel_strides)
 
 
 def flash_attn_backward(
@@ -72,12 +72,13 @@ def _run_bwd(do, q, k, v, o, lse, causal, sm_scale):
         return dq, dk, dv
     ws_bytes = lib.fa_bwd_workspace_bytes(B, N, H, D)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
-    with torch.cuda.device(q.device):
+    sg = kernel_strides(dq)
+    with _on_device(q.device):
         rc = lib.fa_bwd(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                         lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                         ws.data_ptr(), ws_bytes, B, N, H, D,
                         kernel_strides(do), kernel_strides(q), kernel_strides(k), kernel_strides(v),
-                        kernel_strides(o), kernel_strides(dq), kernel_strides(dk), kernel_strides(dv),
+                        kernel_strides(o), sg, sg, sg,
                         float(sm_scale), int(bool(causal)), _stream_ptr(q.device))
     _capi.check(rc, "fa_bwd")
     return dq, dk, dv
@@ -93,7 +94,7 @@ def bwd_preprocess(o: torch.Tensor, do: torch.Tensor) -> torch.Tensor:
     _require(D in NATIVE_HEAD_DIMS, f"unsupported head_dim {D}")
     o, do = _kernel_ready(o), _kernel_ready(do)
     delta = torch.empty((B, H, N), dtype=torch.float32, device=o.device)
-    with torch.cuda.device(o.device):
+    with _on_device(o.device):
         rc = lib.fa_bwd_preprocess(o.data_ptr(), do.data_ptr(), delta.data_ptr(), B, N, H, D,
                                    kernel_strides(o), kernel_strides(do), _stream_ptr(o.device))
     _capi.check(rc, "fa_bwd_preprocess")

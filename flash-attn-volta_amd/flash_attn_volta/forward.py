@@ -12,6 +12,7 @@ columns contribute exactly zero to every dot product).
 """
 from __future__ import annotations
 
+import ctypes
 import math
 
 import torch
@@ -46,15 +47,45 @@ def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
     return t if ok else t.contiguous()
 
 
+_STRIDES = {}
+
+
 def kernel_strides(t: torch.Tensor):
-    """C int64[4] strides, with 0 for size-1 dims (their stride is never used)."""
-    import ctypes
-    st = [0 if t.size(i) == 1 and i < 3 else int(t.stride(i)) for i in range(4)]
-    return (ctypes.c_int64 * 4)(*st)
+    """C int64[4] strides, with 0 for size-1 dims (their stride is never
+    used).  The ctypes arrays are cached per layout: they are read-only."""
+    key = (t.shape, t.stride())
+    arr = _STRIDES.get(key)
+    if arr is None:
+        st = [0 if t.size(i) == 1 and i < 3 else int(t.stride(i)) for i in range(4)]
+        arr = (ctypes.c_int64 * 4)(*st)
+        if len(_STRIDES) > 4096:
+            _STRIDES.clear()
+        _STRIDES[key] = arr
+    return arr
 
 
 def _stream_ptr(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+class _on_device:
+    """Make `device` current for the duration of a launch, skipping the
+    context switch in the common case where it already is."""
+    __slots__ = ("idx", "prev")
+
+    def __init__(self, device: torch.device):
+        self.idx = device.index
+
+    def __enter__(self):
+        self.prev = torch.cuda.current_device()
+        if self.prev != self.idx:
+            torch.cuda.set_device(self.idx)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev != self.idx:
+            torch.cuda.set_device(self.prev)
+        return False
 
 
 def _pad_d(t: torch.Tensor, d_to: int) -> torch.Tensor:
@@ -113,7 +144,7 @@ def _run_fwd(q, k, v, causal, sm_scale, write_lse):
         if lse is not None:
             lse.fill_(float("inf"))
         return out, lse
-    with torch.cuda.device(q.device):
+    with _on_device(q.device):
         rc = lib.fa_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                         lse.data_ptr() if lse is not None else None,
                         B, N, H, D,
