@@ -122,12 +122,15 @@ def kernel_times(q, k, v, do, steps, warmup):
     base = 2.0 * B * H * S * S * D          # one dense S x S x D GEMM
     io = B * S * H * D * 2                  # bytes of one fp16 (B,S,H,D) tensor
     rows = B * H * S * 4                    # bytes of one fp32 (B,H,S) vector
+    cb = "true" if CAUSAL else "false"
     table = [
-        # name, fn, kernel symbol, algorithmic dense FLOPs per launch, algorithmic HBM bytes
-        ("fwd", fwd, "fa_fwd_kernel<64, true, 4>", 2 * base, 4 * io),
-        ("bwd_preprocess", pre, "fa_bwd_preprocess_kernel<64>", 2.0 * B * H * S * D, 2 * io + rows),
-        ("bwd_dkdv", dkdv, "fa_bwd_dkdv_kernel<64, true, 4>", 4 * base, 6 * io + 2 * rows),
-        ("bwd_dq", dqk, "fa_bwd_dq_kernel<64, true, 4>", 3 * base, 5 * io + 2 * rows),
+        # name, fn, kernel symbol prefix (the last template argument, the
+        # in-workgroup split, is chosen by the launcher from the grid size),
+        # algorithmic dense FLOPs per launch, algorithmic HBM bytes
+        ("fwd", fwd, f"fa_fwd_kernel<{D}, {cb}, ", 2 * base, 4 * io),
+        ("bwd_preprocess", pre, f"fa_bwd_preprocess_kernel<{D}>", 2.0 * B * H * S * D, 2 * io + rows),
+        ("bwd_dkdv", dkdv, f"fa_bwd_dkdv_kernel<{D}, {cb}, ", 4 * base, 6 * io + 2 * rows),
+        ("bwd_dq", dqk, f"fa_bwd_dq_kernel<{D}, {cb}, ", 3 * base, 5 * io + 2 * rows),
     ]
     res = {}
     for name, fn, sym, flops, nbytes in table:
@@ -138,10 +141,12 @@ def kernel_times(q, k, v, do, steps, warmup):
 
 
 def profiled_traffic(kernel_sym):
-    """HBM bytes per launch of `kernel_sym` from the committed rocprofv3 PMC
-    summary (profiles/*_hbm_traffic.md: FETCH_SIZE and WRITE_SIZE runs,
-    each scaled by the same counter's reading for a copy of known size).
-    Returns (bytes, source) or (None, None) when no summary covers it."""
+    """HBM bytes per launch of the kernel whose symbol starts with
+    `kernel_sym`, from the committed rocprofv3 PMC summary
+    (profiles/*_hbm_traffic.md: FETCH_SIZE and WRITE_SIZE runs, each scaled
+    by the same counter's reading for a copy of known size).
+    Returns (bytes, source, full symbol) or (None, None, kernel_sym) when no
+    summary covers it."""
     import glob
     import re
     for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*_hbm_traffic.md"))):
@@ -150,9 +155,10 @@ def profiled_traffic(kernel_sym):
         if not m:
             continue
         table = json.loads(m.group(1)).get("traffic_bytes_per_launch", {})
-        if kernel_sym in table:
-            return float(table[kernel_sym]), os.path.relpath(path, ROOT)
-    return None, None
+        for sym, nbytes in table.items():
+            if sym == kernel_sym or (kernel_sym.endswith(" ") and sym.startswith(kernel_sym)):
+                return float(nbytes), os.path.relpath(path, ROOT), sym
+    return None, None, kernel_sym
 
 
 def cpu_baseline(max_seconds=30.0):
@@ -267,14 +273,14 @@ def main():
     step_kernels = ("bwd_preprocess", "bwd_dkdv", "bwd_dq", "fwd")
     dom = max(step_kernels, key=lambda n: kt[n]["avg_us"])
     d = kt[dom]
-    traffic, traffic_src = profiled_traffic(d["kernel"])
+    traffic, traffic_src, sym = profiled_traffic(d["kernel"])
     roofline = {"bound": "mfma", "achieved": round(d["tflops"], 2), "peak": PEAK_FP16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(d["tflops"] / PEAK_FP16_TFLOPS, 4),
                 "traffic": traffic, "traffic_source": traffic_src,
                 "algorithmic_bytes": d["bytes"],
-                "kernel": d["kernel"], "avg_us": round(d["avg_us"], 3),
+                "kernel": sym, "avg_us": round(d["avg_us"], 3),
                 "flops_per_launch": d["flops"]}
-    all_kernels = {n: {"kernel": r["kernel"], "avg_us": round(r["avg_us"], 3),
+    all_kernels = {n: {"kernel": profiled_traffic(r["kernel"])[2], "avg_us": round(r["avg_us"], 3),
                        "tflops": round(r["tflops"], 2), "frac_mfma": round(r["tflops"] / PEAK_FP16_TFLOPS, 4),
                        "gbs": round(r["gbs"], 1), "frac_hbm": round(r["gbs"] / PEAK_HBM_GBS, 4)}
                    for n, r in kt.items()}
