@@ -252,13 +252,22 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
   const float *lse_b = a.lse + (int64_t)bh * S;
   const float *dl_b = a.delta + (int64_t)bh * S;
 
-  // K^T and V^T fragments (B operands): K[key][16c + 8g .. +7]
+  // K^T and V^T fragments (B operands): K[key][16c + 8g .. +7].  K is
+  // pre-multiplied by +-ck = +-min(c, 1) and rounded to fp16 (as the
+  // reference pre-scales K^T, triton_fa_bwd.py:355), so the S MFMAs produce
+  // ck * s directly; ck <= 1 keeps the product inside the fp16 range.  The
+  // rest of c, cr = c / ck, is 1 unless |sm_scale| > ln 2.
   half8 kf[D / 16], vf[D / 16];
   load_row_frags<D>(kf, a.k.head(b, h), a.k.ss, key, S, g);
   load_row_frags<D>(vf, a.v.head(b, h), a.v.ss, key, S, g);
-  if (a.neg) {
+  const float ck = fminf(a.c, 1.0f);
+  const float cr = a.c / ck;
+  {
+    const float kmul = a.neg ? -ck : ck;
 #pragma unroll
-    for (int c = 0; c < D / 16; ++c) kf[c] = neg8(kf[c]);
+    for (int c = 0; c < D / 16; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) kf[c][j] = (f16)((float)kf[c][j] * kmul);
   }
 
   floatx16 dk[D / 32], dv[D / 32];
@@ -271,23 +280,27 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
 
   const int m_begin = CAUSAL ? (k0 / BQ) * BQ : 0;
   const int n_tiles = (S > m_begin) ? (S - m_begin + BQ - 1) / BQ : 0;
-  const float c = a.c;
 
+  // Per-query rows staged beside each tile, laid out as MFMA accumulator
+  // seeds: s_lse = -LSE * log2(e) / cr (-inf past S, so P = 0 there) and
+  // s_dl = -delta.  Seeding the S and dP MFMAs with them yields
+  // ck * s - LSE' and dP - delta with no per-score VALU work.
   KpermStager<D, NT, RS> stq, stg;
   stq.init(tid, a.q.ss);
   stg.init(tid, a.dout.ss);
+  const float lse_mul = -kLog2e / cr;
   float lse_r = 0.0f, dl_r = 0.0f;
   auto load_tile = [&](int m0) {
     stq.load(qb, a.q.ss, m0, S, tid);
     stg.load(gb, a.dout.ss, m0, S, tid);
     if (tid < BQ) {
       const int m = m0 + tid;
-      // rows past S: +inf LSE makes P exactly 0 there
-      lse_r = (m < S) ? lse_b[m] * kLog2e : kPosInf;
-      dl_r = (m < S) ? dl_b[m] : 0.0f;
+      lse_r = (m < S) ? lse_b[m] * lse_mul : kNegInf;
+      dl_r = (m < S) ? -dl_b[m] : 0.0f;
     }
   };
-  auto store_tile = [&](int st) {
+  auto store_tile = [&](auto stc) {
+    constexpr int st = decltype(stc)::value;
     stq.store(s_q[st], tid);
     stg.store(s_do[st], tid);
     if (tid < BQ) {
@@ -299,14 +312,17 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
   __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): K/V fragments resident
   if (n_tiles > 0) {
     load_tile(m_begin);
-    store_tile(0);
+    store_tile(std::integral_constant<int, 0>{});
   }
   __syncthreads();
 
-  for (int t = 0; t < n_tiles; ++t) {
-    const int st = t & 1;
+  // One query tile; the LDS stage is a compile-time constant (the loop below
+  // is unrolled by two) so every LDS address is a base plus an immediate.
+  auto tile_step = [&](auto stc, int t) {
+    constexpr int st = decltype(stc)::value;
     const int m0 = m_begin + t * BQ;
-    if (t + 1 < n_tiles) load_tile(m0 + BQ);
+    const bool more = t + 1 < n_tiles;
+    if (more) load_tile(m0 + BQ);
 
 #pragma unroll
     for (int sb = 0; sb < NSUB; ++sb) {
@@ -316,41 +332,52 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
       if (CAUSAL && ms + 31 < wk0) continue;
       if (ms >= S) continue;
 
+      // slot i <-> query ms + slot_row(i, g); lane <-> key.  Accumulator
+      // seeds: slots 8hh + j hold rows 32qs + 16hh + 8g + j.
       floatx16 sacc, dpacc;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int r = 32 * qs + 16 * hh + 8 * g;
+        const floatx4 l_lo = *(const floatx4 *)&s_lse[st][r];
+        const floatx4 l_hi = *(const floatx4 *)&s_lse[st][r + 4];
+        const floatx4 d_lo = *(const floatx4 *)&s_dl[st][r];
+        const floatx4 d_hi = *(const floatx4 *)&s_dl[st][r + 4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          sacc[8 * hh + j] = l_lo[j];
+          sacc[8 * hh + 4 + j] = l_hi[j];
+          dpacc[8 * hh + j] = d_lo[j];
+          dpacc[8 * hh + 4 + j] = d_hi[j];
+        }
+      }
       {
         const f16 *qr = &s_q[st][(32 * qs + l32) * RS + 8 * g];
         const f16 *gr = &s_do[st][(32 * qs + l32) * RS + 8 * g];
-        sacc = mfma32(*(const half8 *)qr, kf[0], floatx16{});
-        dpacc = mfma32(*(const half8 *)gr, vf[0], floatx16{});
 #pragma unroll
-        for (int cc = 1; cc < D / 16; ++cc) {
+        for (int cc = 0; cc < D / 16; ++cc) {
           sacc = mfma32(*(const half8 *)(qr + 16 * cc), kf[cc], sacc);
           dpacc = mfma32(*(const half8 *)(gr + 16 * cc), vf[cc], dpacc);
         }
       }
-      // slot i <-> query ms + slot_row(i, g); lane <-> key
-      const bool need_mask = (CAUSAL && ms < wk0 + 31) || (ms + 31 >= S) || (wk0 + 31 >= S);
+      // Invisible scores become -inf (P = 0) in one pass, taken only by
+      // diagonal and ragged sub-blocks, so the softmax below is branch-free.
+      if ((CAUSAL && ms < wk0 + 31) || (ms + 31 >= S) || (wk0 + 31 >= S)) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int m = ms + slot_row(i, g);
+          const bool vis = m < S && key < S && (!CAUSAL || key <= m);
+          sacc[i] = vis ? sacc[i] : kNegInf;
+        }
+      }
+      if (cr != 1.0f) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sacc[i] *= cr;
+      }
       floatx16 p, ds;
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const floatx4 lse_lo = *(const floatx4 *)&s_lse[st][32 * qs + 16 * hh + 8 * g];
-        const floatx4 lse_hi = *(const floatx4 *)&s_lse[st][32 * qs + 16 * hh + 8 * g + 4];
-        const floatx4 dl_lo = *(const floatx4 *)&s_dl[st][32 * qs + 16 * hh + 8 * g];
-        const floatx4 dl_hi = *(const floatx4 *)&s_dl[st][32 * qs + 16 * hh + 8 * g + 4];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int i = 8 * hh + j;
-          const float l2 = j < 4 ? lse_lo[j] : lse_hi[j - 4];
-          const float dl = j < 4 ? dl_lo[j] : dl_hi[j - 4];
-          float pv = fast_exp2(__builtin_fmaf(sacc[i], c, -l2));
-          if (need_mask) {
-            const int m = ms + slot_row(i, g);
-            const bool vis = m < S && key < S && (!CAUSAL || key <= m);
-            pv = vis ? pv : 0.0f;
-          }
-          p[i] = pv;
-          ds[i] = pv * (dpacc[i] - dl);
-        }
+      for (int i = 0; i < 16; ++i) {
+        p[i] = fast_exp2(sacc[i]);
+        ds[i] = p[i] * dpacc[i];
       }
       // adaptive power-of-two scale of this key's dS column
       const float mk = absmax16(ds);
@@ -381,8 +408,13 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
       }
     }
 
-    if (t + 1 < n_tiles) store_tile(st ^ 1);
+    if (more) store_tile(std::integral_constant<int, st ^ 1>{});
     __syncthreads();
+  };
+
+  for (int t = 0; t < n_tiles; t += 2) {
+    tile_step(std::integral_constant<int, 0>{}, t);
+    if (t + 1 < n_tiles) tile_step(std::integral_constant<int, 1>{}, t + 1);
   }
 
   float dk_mul = a.sm_scale / sc.mul;
@@ -508,16 +540,19 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
           dpacc = mfma32(*(const half8 *)(vr + 16 * cc), gf[cc], dpacc);
         }
       }
-      const bool need_mask = (CAUSAL && ns + 31 > wq0) || (ns + 31 >= S);
+      // invisible scores -> -inf (P = 0), diagonal / ragged sub-blocks only
+      if ((CAUSAL && ns + 31 > wq0) || (ns + 31 >= S)) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int n = ns + slot_row(i, g);
+          const bool vis = n < S && (!CAUSAL || n <= qrow);
+          sacc[i] = vis ? sacc[i] : kNegInf;
+        }
+      }
       floatx16 ds;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        float p = fast_exp2(__builtin_fmaf(sacc[i], c, -l2));
-        if (need_mask) {
-          const int n = ns + slot_row(i, g);
-          const bool vis = n < S && (!CAUSAL || n <= qrow);
-          p = vis ? p : 0.0f;
-        }
+        const float p = fast_exp2(__builtin_fmaf(sacc[i], c, -l2));
         ds[i] = p * (dpacc[i] - dl);
       }
       const float m = absmax16(ds);
