@@ -218,19 +218,22 @@ struct DkdvTile {
   static constexpr int BK = 32 * NKG;
   static constexpr int BQ = 64;
   static constexpr int NT = 256;
-  static constexpr int RS = D + 8;
-  static constexpr int LDS_ROW = BQ * RS;
-  static_assert(2 * 64 * (D / 2 + 1) * 4 <= 2 * LDS_ROW * 2, "merge buffer must fit in a tile ring");
+  static constexpr int LDS_TILE = BQ * D;   // swizzled, unpadded (fa_common.hpp)
+  static_assert(64 * (D / 2) * 4 * 2 <= 2 * LDS_TILE * 2, "merge buffers must fit in a tile ring");
 };
 
 template <int D, bool CAUSAL, int SPLIT>
 __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
   using T = DkdvTile<D, SPLIT>;
-  constexpr int BK = T::BK, BQ = T::BQ, NT = T::NT, RS = T::RS, NSUB = T::NSUB;
-  __shared__ __attribute__((aligned(16))) f16 s_q[2][T::LDS_ROW];
-  __shared__ __attribute__((aligned(16))) f16 s_do[2][T::LDS_ROW];
+  constexpr int BK = T::BK, BQ = T::BQ, NSUB = T::NSUB;
+  // One LDS object per stage: the compiler then sees that the DMA into one
+  // stage cannot alias reads of the other and does not wait for it early.
+  __shared__ __attribute__((aligned(16))) f16 s_q0[T::LDS_TILE], s_q1[T::LDS_TILE];
+  __shared__ __attribute__((aligned(16))) f16 s_do0[T::LDS_TILE], s_do1[T::LDS_TILE];
   __shared__ __attribute__((aligned(16))) float s_lse[2][BQ];
   __shared__ __attribute__((aligned(16))) float s_dl[2][BQ];
+  auto q_st = [&](auto stc) -> f16 * { return decltype(stc)::value ? s_q1 : s_q0; };
+  auto do_st = [&](auto stc) -> f16 * { return decltype(stc)::value ? s_do1 : s_do0; };
 
   const int S = a.S;
   const int BH = a.B * a.H;
@@ -285,33 +288,55 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
   // seeds: s_lse = -LSE * log2(e) / cr (-inf past S, so P = 0 there) and
   // s_dl = -delta.  Seeding the S and dP MFMAs with them yields
   // ck * s - LSE' and dP - delta with no per-score VALU work.
-  KpermStager<D, NT, RS> stq, stg;
-  stq.init(tid, a.q.ss);
-  stg.init(tid, a.dout.ss);
+  DmaStager<D> stq, stg;
+  stq.init(w, lane, a.q.ss);
+  stg.init(w, lane, a.dout.ss);
   const float lse_mul = -kLog2e / cr;
-  float lse_r = 0.0f, dl_r = 0.0f;
-  auto load_tile = [&](int m0) {
-    stq.load(qb, a.q.ss, m0, S, tid);
-    stg.load(gb, a.dout.ss, m0, S, tid);
+  float lse_r = 0.0f, dl_r = 0.0f;   // raw LSE / delta of row m0 + tid
+  // Q and dO go straight to LDS stage `st`; LSE / delta through VGPRs.
+  auto load_tile = [&](int m0, auto stc) {
+    constexpr int st = decltype(stc)::value;
+    stq.load(q_st(stc), qb, a.q.ss, m0, S, w);
+    stg.load(do_st(stc), gb, a.dout.ss, m0, S, w);
     if (tid < BQ) {
       const int m = m0 + tid;
-      lse_r = (m < S) ? lse_b[m] * lse_mul : kNegInf;
-      dl_r = (m < S) ? -dl_b[m] : 0.0f;
+      // rows past S: +inf LSE, so the seed below is -inf and P = 0
+      lse_r = (m < S) ? lse_b[m] : kPosInf;
+      dl_r = (m < S) ? dl_b[m] : 0.0f;
     }
   };
+  // Publishing a stage: its LSE / delta rows go to LDS, then every DMA of
+  // this wave is waited for (vmcnt(0)); the barrier after it makes the
+  // whole tile visible.
   auto store_tile = [&](auto stc) {
     constexpr int st = decltype(stc)::value;
-    stq.store(s_q[st], tid);
-    stg.store(s_do[st], tid);
     if (tid < BQ) {
-      s_lse[st][tid] = lse_r;
-      s_dl[st][tid] = dl_r;
+      s_lse[st][tid] = lse_r * lse_mul;
+      s_dl[st][tid] = -dl_r;
     }
+    __builtin_amdgcn_s_waitcnt(0x0f70);
   };
+
+  // Per-lane LDS element offsets inside a stage (fa_common.hpp swizzle).
+  // A-operand rows (Q, dO of this wave's 32-query sub-block): row l32, chunk
+  // 2cc + g; transposed reads: rows 4g + (l16 >> 2), column chunk
+  // 4d + 2((lane >> 4) & 1) + ((l16 >> 1) & 1), half 4 * (l16 & 1).
+  int a_off[D / 16], t_off[D / 32];
+  {
+    const int sa = swz<D>(l32);
+#pragma unroll
+    for (int cc = 0; cc < D / 16; ++cc) a_off[cc] = l32 * D + (((2 * cc + g) ^ sa) << 3);
+    const int l16 = lane & 15, tr = 4 * g + (l16 >> 2);
+    const int st_ = swz<D>(tr);
+#pragma unroll
+    for (int d = 0; d < D / 32; ++d)
+      t_off[d] = tr * D + (((4 * d + 2 * ((lane >> 4) & 1) + ((l16 >> 1) & 1)) ^ st_) << 3) +
+                 4 * (l16 & 1);
+  }
 
   __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): K/V fragments resident
   if (n_tiles > 0) {
-    load_tile(m_begin);
+    load_tile(m_begin, std::integral_constant<int, 0>{});
     store_tile(std::integral_constant<int, 0>{});
   }
   __syncthreads();
@@ -322,7 +347,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
     constexpr int st = decltype(stc)::value;
     const int m0 = m_begin + t * BQ;
     const bool more = t + 1 < n_tiles;
-    if (more) load_tile(m0 + BQ);
+    if (more) load_tile(m0 + BQ, std::integral_constant<int, st ^ 1>{});
 
 #pragma unroll
     for (int sb = 0; sb < NSUB; ++sb) {
@@ -351,12 +376,12 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
         }
       }
       {
-        const f16 *qr = &s_q[st][(32 * qs + l32) * RS + 8 * g];
-        const f16 *gr = &s_do[st][(32 * qs + l32) * RS + 8 * g];
+        const f16 *qr = q_st(stc) + 32 * qs * D;
+        const f16 *gr = do_st(stc) + 32 * qs * D;
 #pragma unroll
         for (int cc = 0; cc < D / 16; ++cc) {
-          sacc = mfma32(*(const half8 *)(qr + 16 * cc), kf[cc], sacc);
-          dpacc = mfma32(*(const half8 *)(gr + 16 * cc), vf[cc], dpacc);
+          sacc = mfma32(*(const half8 *)(qr + a_off[cc]), kf[cc], sacc);
+          dpacc = mfma32(*(const half8 *)(gr + a_off[cc]), vf[cc], dpacc);
         }
       }
       // Invisible scores become -inf (P = 0) in one pass, taken only by
@@ -399,11 +424,12 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
       // dV^T += dO^T P ; dK^T += Q^T dS   (k = queries ms + 16hh + 8g ..)
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        const int rlo = 32 * qs + 16 * hh + 4 * g;   // kperm rows of this 8-query slice
+        // kperm rows 32qs + 16hh + 4g + (0..3) and +8: this 8-query slice
+        const int rb = (32 * qs + 16 * hh) * D;
 #pragma unroll
         for (int d = 0; d < D / 32; ++d) {
-          dv[d] = mfma32(load_tr8<RS>(s_do[st], rlo, rlo + 8, 32 * d, lane), pf[hh], dv[d]);
-          dk[d] = mfma32(load_tr8<RS>(s_q[st], rlo, rlo + 8, 32 * d, lane), dsf[hh], dk[d]);
+          dv[d] = mfma32(load_tr_pair(do_st(stc) + rb + t_off[d], 8 * D), pf[hh], dv[d]);
+          dk[d] = mfma32(load_tr_pair(q_st(stc) + rb + t_off[d], 8 * D), dsf[hh], dk[d]);
         }
       }
     }
@@ -421,9 +447,9 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
   if (SPLIT == 2) {
     // the loop's last barrier ordered every tile read before these writes
     const DsScale unit;
-    merge_pair<D>(reinterpret_cast<float *>(&s_q[0][0]) + kg * 64 * (D / 2 + 1), qh == 1, dk, sc,
+    merge_pair<D>(reinterpret_cast<float *>(kg ? s_q1 : s_q0), qh == 1, dk, sc,
                   lane);
-    merge_pair<D>(reinterpret_cast<float *>(&s_do[0][0]) + kg * 64 * (D / 2 + 1), qh == 1, dv,
+    merge_pair<D>(reinterpret_cast<float *>(kg ? s_do1 : s_do0), qh == 1, dv,
                   unit, lane);
     if (qh == 1) return;
     dk_mul = a.sm_scale;

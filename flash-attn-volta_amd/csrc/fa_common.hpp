@@ -159,6 +159,75 @@ __device__ __forceinline__ int wave_id() {
   return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 }
 
+// ---------------------------------------------------------------------------
+// Swizzled 64-row tiles staged straight from global memory into LDS.
+//
+// A tile is 64 rows x D fp16, unpadded (row stride 2*D bytes), with 32-row
+// blocks in kperm row order.  Each row's 16-byte chunks are XOR-permuted by
+// swz<D>(row): physical chunk = logical chunk ^ swz(row).  swz takes 8
+// distinct values over any 8 consecutive rows (so eight lanes reading the
+// same logical chunk of consecutive rows with ds_read_b128 hit eight
+// different 16-byte bank groups), and over any aligned group of 4 rows it
+// maps the chunk pair {2j, 2j+1} to 4 disjoint pairs (the 4-row x 32-byte
+// footprint of ds_read_b64_tr_b16).  For D = 32 (4 chunks per row, two rows
+// per 128 bytes) the same holds for rows of equal parity.
+template <int D>
+__device__ __forceinline__ constexpr int swz(int r) {
+  return D >= 64 ? (((r & 3) << 1) | ((r >> 2) & 1)) : ((((r >> 1) & 1) << 1) | ((r >> 2) & 1));
+}
+
+// Element offset of (row, col) in a swizzled tile.
+template <int D>
+__device__ __forceinline__ constexpr int sw_off(int row, int col) {
+  return row * D + ((((col >> 3) ^ swz<D>(row))) << 3) + (col & 7);
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// One buffer_load_dwordx4 ... lds: lane i's 16 bytes at byte offset `voff`
+// of `rs` land at LDS byte (lds + 16 * i) (layout measured on gfx950); M0
+// holds `lds`, which must be wave-uniform.  Tracked by vmcnt.
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, const void *lds, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)lds, 16, voff, 0, 0, 0);
+}
+
+// Loads one 64-row tile (rows r0 .. r0+63 of a (b, h) head, zeros past S)
+// into a swizzled LDS slot: 64*D*2 bytes = D/8 wave instructions of 1 KiB,
+// D/32 per wave of a 4-wave workgroup.  No VGPRs hold tile data.
+template <int D>
+struct DmaStager {
+  static constexpr int PER_WAVE = D / 32;
+  int off[PER_WAVE];   // global byte offset of this lane's chunk, relative to row r0
+
+  __device__ __forceinline__ void init(int w, int lane, int64_t ss) {
+#pragma unroll
+    for (int j = 0; j < PER_WAVE; ++j) {
+      const int byte = (w * PER_WAVE + j) * 1024 + 16 * lane;
+      const int p = byte / (2 * D), pc = (byte % (2 * D)) / 16;
+      off[j] = kperm_row(p) * (int)ss * 2 + 16 * (pc ^ swz<D>(p));
+    }
+  }
+  __device__ __forceinline__ void load(f16 *slot, const f16 *head, int64_t ss, int r0, int S,
+                                       int w) const {
+    const __amdgpu_buffer_rsrc_t rs = rows_rsrc(head, ss, r0, S, D);
+#pragma unroll
+    for (int j = 0; j < PER_WAVE; ++j) lds_dma16(rs, slot + (w * PER_WAVE + j) * 512, off[j]);
+  }
+};
+
+// Two ds_read_b64_tr_b16 at `p` and `p + hi` (elements): the A-operand
+// fragment whose slots 0..3 come from the 4-row block at p and 4..7 from the
+// block `hi` elements further (lane addresses precomputed by the caller).
+__device__ __forceinline__ half8 load_tr_pair(const f16 *p, int hi) {
+  typedef __fp16 h4 __attribute__((vector_size(8)));
+  h4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) h4 *)p);
+  h4 up = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) h4 *)(p + hi));
+  half8 r;
+  r[0] = (f16)lo[0]; r[1] = (f16)lo[1]; r[2] = (f16)lo[2]; r[3] = (f16)lo[3];
+  r[4] = (f16)up[0]; r[5] = (f16)up[1]; r[6] = (f16)up[2]; r[7] = (f16)up[3];
+  return r;
+}
+
 // Kernel arguments shared by the forward and backward launches. Strides are
 // in elements of a (B, S, H, D) tensor whose D stride is 1.
 struct TensorDesc {
