@@ -104,11 +104,17 @@ __device__ __forceinline__ half8 neg8(half8 x) {
 // (and stays inside the tensor otherwise).  gfx9-family descriptor word 3.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const f16 *head, int64_t ss, int n0,
                                                             int S, int D) {
+  // Scalar-only arithmetic (32-bit compares), so no VGPR temporaries: a
+  // VALU 64-bit compare here would make the compiler wait for outstanding
+  // tile loads that target the same registers.
   const f16 *base = head + (int64_t)n0 * ss;
-  int64_t extent = (int64_t)(S - 1 - n0) * ss * 2 + 2 * D;
-  extent = extent < 0 ? 0 : (extent > 0xffffffffll ? 0xffffffffll : extent);
-  return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)(uint32_t)extent,
-                                           0x00020000);
+  const int rows = S - n0;
+  uint32_t ext = 0;
+  if (rows > 0) {
+    const uint64_t e = (uint64_t)(uint32_t)(rows - 1) * (uint64_t)(ss * 2) + (uint64_t)(2 * D);
+    ext = (uint32_t)(e >> 32) != 0u ? 0xffffffffu : (uint32_t)e;
+  }
+  return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)ext, 0x00020000);
 }
 
 __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, int byte_off) {
