@@ -475,17 +475,19 @@ struct DqTile {
   static constexpr int BM = 32 * NQG;
   static constexpr int BN = 64;
   static constexpr int NT = 256;
-  static constexpr int RS = D + 8;
-  static constexpr int LDS_ROW = BN * RS;
-  static_assert(2 * 64 * (D / 2 + 1) * 4 <= 2 * LDS_ROW * 2, "merge buffer must fit in a tile ring");
+  static constexpr int LDS_TILE = BN * D;   // swizzled, unpadded (fa_common.hpp)
+  static_assert(64 * (D / 2) * 4 <= LDS_TILE * 2, "a merge buffer must fit in one K stage");
 };
 
 template <int D, bool CAUSAL, int SPLIT>
 __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
   using T = DqTile<D, SPLIT>;
-  constexpr int BM = T::BM, BN = T::BN, NT = T::NT, RS = T::RS, NSUB = T::NSUB;
-  __shared__ __attribute__((aligned(16))) f16 s_k[2][T::LDS_ROW];
-  __shared__ __attribute__((aligned(16))) f16 s_v[2][T::LDS_ROW];
+  constexpr int BM = T::BM, BN = T::BN, NSUB = T::NSUB;
+  // One LDS object per stage (see the dK/dV kernel).
+  __shared__ __attribute__((aligned(16))) f16 s_k0[T::LDS_TILE], s_k1[T::LDS_TILE];
+  __shared__ __attribute__((aligned(16))) f16 s_v0[T::LDS_TILE], s_v1[T::LDS_TILE];
+  auto k_st = [&](auto stc) -> f16 * { return decltype(stc)::value ? s_k1 : s_k0; };
+  auto v_st = [&](auto stc) -> f16 * { return decltype(stc)::value ? s_v1 : s_v0; };
 
   const int S = a.S;
   const int BH = a.B * a.H;
@@ -526,27 +528,41 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
   const int n_tiles = (kv_end + BN - 1) / BN;
   const float c = a.c;
 
-  KpermStager<D, NT, RS> stk, stv;
-  stk.init(tid, a.k.ss);
-  stv.init(tid, a.v.ss);
-  auto load_tile = [&](int n0) {
-    stk.load(kb, a.k.ss, n0, S, tid);
-    stv.load(vb, a.v.ss, n0, S, tid);
-  };
-  auto store_tile = [&](int st) {
-    stk.store(s_k[st], tid);
-    stv.store(s_v[st], tid);
+  // K and V tiles go straight to LDS (fa_common.hpp DmaStager).
+  DmaStager<D> stk, stv;
+  stk.init(w, lane, a.k.ss);
+  stv.init(w, lane, a.v.ss);
+  auto load_tile = [&](int n0, auto stc) {
+    stk.load(k_st(stc), kb, a.k.ss, n0, S, w);
+    stv.load(v_st(stc), vb, a.v.ss, n0, S, w);
   };
 
-  __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): Q/dO fragments resident
-  load_tile(0);
-  store_tile(0);
+  // Per-lane LDS element offsets inside a stage (as in the dK/dV kernel):
+  // A-operand rows l32, chunk 2cc + g; transposed reads of K rows
+  // 4g + (l16 >> 2).
+  int a_off[D / 16], t_off[D / 32];
+  {
+    const int sa = swz<D>(l32);
+#pragma unroll
+    for (int cc = 0; cc < D / 16; ++cc) a_off[cc] = l32 * D + (((2 * cc + g) ^ sa) << 3);
+    const int l16 = lane & 15, tr = 4 * g + (l16 >> 2);
+    const int st_ = swz<D>(tr);
+#pragma unroll
+    for (int d = 0; d < D / 32; ++d)
+      t_off[d] = tr * D + (((4 * d + 2 * ((lane >> 4) & 1) + ((l16 >> 1) & 1)) ^ st_) << 3) +
+                 4 * (l16 & 1);
+  }
+
+  __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): Q/dO fragments, LSE, delta resident
+  load_tile(0, std::integral_constant<int, 0>{});
+  __builtin_amdgcn_s_waitcnt(0x0f70);
   __syncthreads();
 
-  for (int t = 0; t < n_tiles; ++t) {
-    const int st = t & 1;
+  auto tile_step = [&](auto stc, int t) {
+    constexpr int st = decltype(stc)::value;
     const int n0 = t * BN;
-    if (t + 1 < n_tiles) load_tile(n0 + BN);
+    const bool more = t + 1 < n_tiles;
+    if (more) load_tile(n0 + BN, std::integral_constant<int, st ^ 1>{});
 
 #pragma unroll
     for (int sb = 0; sb < NSUB; ++sb) {
@@ -556,14 +572,14 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
       if (ns >= S) continue;
       floatx16 sacc, dpacc;
       {
-        const f16 *kr = &s_k[st][(32 * ks + l32) * RS + 8 * g];
-        const f16 *vr = &s_v[st][(32 * ks + l32) * RS + 8 * g];
-        sacc = mfma32(*(const half8 *)kr, qf[0], floatx16{});
-        dpacc = mfma32(*(const half8 *)vr, gf[0], floatx16{});
+        const f16 *kr = k_st(stc) + 32 * ks * D;
+        const f16 *vr = v_st(stc) + 32 * ks * D;
+        sacc = mfma32(*(const half8 *)(kr + a_off[0]), qf[0], floatx16{});
+        dpacc = mfma32(*(const half8 *)(vr + a_off[0]), gf[0], floatx16{});
 #pragma unroll
         for (int cc = 1; cc < D / 16; ++cc) {
-          sacc = mfma32(*(const half8 *)(kr + 16 * cc), qf[cc], sacc);
-          dpacc = mfma32(*(const half8 *)(vr + 16 * cc), gf[cc], dpacc);
+          sacc = mfma32(*(const half8 *)(kr + a_off[cc]), qf[cc], sacc);
+          dpacc = mfma32(*(const half8 *)(vr + a_off[cc]), gf[cc], dpacc);
         }
       }
       // invisible scores -> -inf (P = 0), diagonal / ragged sub-blocks only
@@ -596,22 +612,27 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
       for (int i = 0; i < 16; ++i) dsf[i >> 3][i & 7] = (f16)(ds[i] * sc.mul);
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        const int rlo = 32 * ks + 16 * hh + 4 * g;   // kperm rows of this 8-key slice
+        // kperm rows 32ks + 16hh + 4g + (0..3) and +8: this 8-key slice
+        const int rb = (32 * ks + 16 * hh) * D;
 #pragma unroll
         for (int d = 0; d < D / 32; ++d)
-          dq[d] = mfma32(load_tr8<RS>(s_k[st], rlo, rlo + 8, 32 * d, lane), dsf[hh], dq[d]);
+          dq[d] = mfma32(load_tr_pair(k_st(stc) + rb + t_off[d], 8 * D), dsf[hh], dq[d]);
       }
     }
 
-    if (t + 1 < n_tiles) store_tile(st ^ 1);
+    if (more) __builtin_amdgcn_s_waitcnt(0x0f70);   // this wave's DMAs of the next stage
     __syncthreads();
+  };
+
+  for (int t = 0; t < n_tiles; t += 2) {
+    tile_step(std::integral_constant<int, 0>{}, t);
+    if (t + 1 < n_tiles) tile_step(std::integral_constant<int, 1>{}, t + 1);
   }
 
   float dq_mul = a.sm_scale / sc.mul;
   if (SPLIT == 2) {
     // the loop's last barrier ordered every tile read before these writes
-    merge_pair<D>(reinterpret_cast<float *>(&s_k[0][0]) + qg * 64 * (D / 2 + 1), kh == 1, dq, sc,
-                  lane);
+    merge_pair<D>(reinterpret_cast<float *>(qg ? s_k1 : s_k0), kh == 1, dq, sc, lane);
     if (kh == 1) return;
     dq_mul = a.sm_scale;
   }
