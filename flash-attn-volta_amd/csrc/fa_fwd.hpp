@@ -13,9 +13,12 @@
 //   * key/value tiles of BN = 64 rows stream through LDS.  K lives in a
 //     2-slot ring one tile ahead of V (2-slot ring), so the S^T MFMAs of
 //     tile t+1 are issued before the softmax of tile t and run under it;
-//   * K rows are stored in kperm order so every lane's A-operand read is a
-//     plain 16-byte ds_read of LDS row (lane % 32); V stays row-major and the
-//     V^T operand of O^T = V^T P^T is read with ds_read_b64_tr_b16;
+//   * K and V tiles go from global memory straight into LDS (buffer loads
+//     with the LDS-direct bit: no VGPRs hold tile data), 32-row blocks in
+//     kperm order and 16-byte chunks XOR-swizzled per row, so every lane's
+//     K A-operand read is a conflict-free 16-byte ds_read of LDS row
+//     (lane % 32), and the V^T operand of O^T = V^T P^T is read with
+//     ds_read_b64_tr_b16 (fa_common.hpp);
 //   * the wave's Q fragment stays in registers for the whole sweep;
 //   * a lane owns one query row: the running max / sum and the O^T
 //     accumulator column live in that lane, the only cross-lane step is one
@@ -27,7 +30,7 @@
 //     kRescaleLog2 (in log2 units): the stale max keeps p <= 2^kRescaleLog2,
 //     well inside fp16, and the final O and LSE use the same max, so the
 //     result is exact either way;
-//   * K/V tiles are fetched with raw buffer loads whose extent ends at row
+//   * the tile loads use raw buffer descriptors whose extent ends at row
 //     S-1, so rows past the end read as zeros without any branch (they only
 //     ever meet -inf scores); the Q row index is clamped (never stored).
 #pragma once
@@ -57,15 +60,9 @@ struct FwdTile {
   static constexpr int BM = 32 * NQG;      // queries per workgroup
   static constexpr int BN = 64;            // keys per tile
   static constexpr int NT = 256;           // 4 waves
-  static constexpr int KS = D + 8;    // K slot row stride (halves)
-  static constexpr int VS = D + 16;   // V slot row stride (halves)
-  static constexpr int CHUNKS = BN * D / 8;                // 16-byte chunks per tile
-  static constexpr int PER_T = (CHUNKS + NT - 1) / NT;
-  static constexpr int LDS_K = BN * KS;
-  static constexpr int LDS_V = BN * VS;
-  // per-lane softmax state of a key-half wave handed over for the final merge
-  static constexpr int MERGE_FLOATS = 2 * 64 * (D / 2 + 2);
-  static_assert(MERGE_FLOATS * 4 <= 2 * LDS_K * 2, "merge buffer must fit in the K slots");
+  static constexpr int LDS_TILE = BN * D;  // swizzled, unpadded (fa_common.hpp)
+  // O^T partial sums of a key-half wave handed over for the final merge
+  static_assert(64 * (D / 2) * 4 <= LDS_TILE * 2, "a merge buffer must fit in one K slot");
 };
 
 // max(x, value of lane ^ 32).  v_permlane32_swap exchanges the upper half of
@@ -90,9 +87,14 @@ template <int D, bool CAUSAL, int KSPLIT>
 __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   using T = FwdTile<D, KSPLIT>;
   constexpr int NSUB = T::NSUB;
-  constexpr int BM = T::BM, BN = T::BN, NT = T::NT, KS = T::KS, VS = T::VS;
-  __shared__ __attribute__((aligned(16))) f16 sk[2][T::LDS_K];
-  __shared__ __attribute__((aligned(16))) f16 sv[2][T::LDS_V];
+  constexpr int BM = T::BM, BN = T::BN;
+  // One LDS object per slot, so the compiler sees that a DMA into one slot
+  // cannot alias reads of another and does not wait for it early.
+  __shared__ __attribute__((aligned(16))) f16 sk0[T::LDS_TILE], sk1[T::LDS_TILE];
+  __shared__ __attribute__((aligned(16))) f16 sv0[T::LDS_TILE], sv1[T::LDS_TILE];
+  __shared__ __attribute__((aligned(16))) float s_ml[2][2][64];   // merge: m, l per query group
+  auto k_sl = [&](auto sc) -> f16 * { return decltype(sc)::value ? sk1 : sk0; };
+  auto v_sl = [&](auto sc) -> f16 * { return decltype(sc)::value ? sv1 : sv0; };
 
   const int S = a.S;
   const int BH = a.B * a.H;
@@ -120,47 +122,29 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   if (CAUSAL) kv_end = min(S, q0 + BM);
   const int n_tiles = (kv_end + BN - 1) / BN;   // >= 1
 
-  // ---- global -> register -> LDS staging of K (kperm row order) and V.
-  // Thread-constant chunk coordinates; per tile only the scalar buffer base
-  // moves, and rows past S come back as zeros from the buffer range check.
-  int ch_off[T::PER_T], ch_row[T::PER_T], ch_col[T::PER_T];
+  // ---- K and V tiles go straight to LDS (fa_common.hpp DmaStager): both
+  // in kperm row order, chunks swizzled; rows past S read as zeros.
+  DmaStager<D> stk, stv;
+  stk.init(w, lane, a.k.ss);
+  stv.init(w, lane, a.v.ss);
+  auto load_k = [&](int n0, auto sc) { stk.load(k_sl(sc), kb, a.k.ss, n0, S, w); };
+  auto load_v = [&](int n0, auto sc) { stv.load(v_sl(sc), vb, a.v.ss, n0, S, w); };
+
+  // Per-lane LDS element offsets inside a slot: K rows l32 (A operand of
+  // S^T = K Q^T), chunk 2cc + g; V^T transpose reads of rows 4g + (l16 >> 2)
+  // (and + 8), i.e. natural V rows 8g + (l16 >> 2) (and + 4).
+  int a_off[D / 16], t_off[D / 32];
+  {
+    const int sa = swz<D>(l32);
 #pragma unroll
-  for (int i = 0; i < T::PER_T; ++i) {
-    const int idx = tid + i * NT;
-    ch_row[i] = idx / (D / 8);
-    ch_col[i] = 8 * (idx % (D / 8));
-    ch_off[i] = ch_row[i] * (int)a.k.ss * 2 + 2 * ch_col[i];
+    for (int cc = 0; cc < D / 16; ++cc) a_off[cc] = l32 * D + (((2 * cc + g) ^ sa) << 3);
+    const int l16 = lane & 15, tr = 4 * g + (l16 >> 2);
+    const int st_ = swz<D>(tr);
+#pragma unroll
+    for (int d = 0; d < D / 32; ++d)
+      t_off[d] = tr * D + (((4 * d + 2 * ((lane >> 4) & 1) + ((l16 >> 1) & 1)) ^ st_) << 3) +
+                 4 * (l16 & 1);
   }
-  const int v_off_delta = (int)(a.v.ss - a.k.ss) * 2;   // V rows use the V stride
-  u32x4 kreg[T::PER_T], vreg[T::PER_T];
-  auto load_k = [&](int n0) {
-    const __amdgpu_buffer_rsrc_t r = rows_rsrc(kb, a.k.ss, n0, S, D);
-#pragma unroll
-    for (int i = 0; i < T::PER_T; ++i)
-      if (T::CHUNKS % NT == 0 || tid + i * NT < T::CHUNKS) kreg[i] = buf_load16(r, ch_off[i]);
-  };
-  auto load_v = [&](int n0) {
-    const __amdgpu_buffer_rsrc_t r = rows_rsrc(vb, a.v.ss, n0, S, D);
-#pragma unroll
-    for (int i = 0; i < T::PER_T; ++i)
-      if (T::CHUNKS % NT == 0 || tid + i * NT < T::CHUNKS)
-        vreg[i] = buf_load16(r, ch_off[i] + ch_row[i] * v_off_delta);
-  };
-  auto store_k = [&](int slot) {
-#pragma unroll
-    for (int i = 0; i < T::PER_T; ++i) {
-      if (T::CHUNKS % NT == 0 || tid + i * NT < T::CHUNKS) {
-        const int r = ch_row[i];
-        *(u32x4 *)(&sk[slot][kperm_row(r) * KS + ch_col[i]]) = kreg[i];
-      }
-    }
-  };
-  auto store_v = [&](int slot) {
-#pragma unroll
-    for (int i = 0; i < T::PER_T; ++i)
-      if (T::CHUNKS % NT == 0 || tid + i * NT < T::CHUNKS)
-        *(u32x4 *)(&sv[slot][ch_row[i] * VS + ch_col[i]]) = vreg[i];
-  };
 
   // Sub-block sb (32 keys) of this wave in the tile at n0 starts at key
   // n0 + 32 * (NSUB * kh + sb); it is dead when it lies entirely above the
@@ -170,22 +154,25 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
 
   // ---- S^T = K Q^T for this wave's sub-blocks of a tile
   half8 qf[D / 16];
-  auto qk = [&](int slot, int n0, floatx16 (&s)[NSUB]) {
+  auto qk = [&](auto sc, int n0, floatx16 (&s)[NSUB]) {
 #pragma unroll
     for (int sb = 0; sb < NSUB; ++sb) {
       // dead sub-blocks are skipped; the diagonal mask overwrites them
       if (dead(n0, sb)) continue;
-      const f16 *kr = &sk[slot][(32 * (NSUB * kh + sb) + l32) * KS + 8 * g];
-      floatx16 acc = mfma32(*(const half8 *)kr, qf[0], floatx16{});
+      const f16 *kr = k_sl(sc) + 32 * (NSUB * kh + sb) * D;
+      floatx16 acc = mfma32(*(const half8 *)(kr + a_off[0]), qf[0], floatx16{});
 #pragma unroll
-      for (int cc = 1; cc < D / 16; ++cc) acc = mfma32(*(const half8 *)(kr + 16 * cc), qf[cc], acc);
+      for (int cc = 1; cc < D / 16; ++cc) acc = mfma32(*(const half8 *)(kr + a_off[cc]), qf[cc], acc);
       s[sb] = acc;
     }
   };
 
+  using C0 = std::integral_constant<int, 0>;
+  using C1 = std::integral_constant<int, 1>;
   // ---- prologue: K(0), V(0) -> slot 0, K(1) -> K slot 1
-  load_k(0);
-  load_v(0);
+  load_k(0, C0{});
+  load_v(0, C0{});
+  if (n_tiles > 1) load_k(BN, C1{});
   {
     const int qr = min(qrow, S - 1);
     const f16 *qp = qb + (int64_t)qr * a.q.ss + 8 * g;
@@ -196,20 +183,15 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
       for (int c = 0; c < D / 16; ++c) qf[c] = neg8(qf[c]);
     }
   }
-  // Q must be resident before the loop: otherwise the waitcnt pass cannot
-  // prove it and stalls every iteration's MFMAs on the prefetch loads.
+  // Q (and this wave's tile DMAs) must be complete before the loop:
+  // otherwise the waitcnt pass cannot prove Q resident and stalls every
+  // iteration's MFMAs on the prefetch loads.
   __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
-  store_k(0);
-  store_v(0);
-  if (n_tiles > 1) {
-    load_k(BN);
-    store_k(1);
-  }
   __syncthreads();
 
   floatx16 s_cur[NSUB], s_nxt[NSUB];
-  qk(0, 0, s_cur);
-  // K slot 0 is refilled with K(2) at the end of the first iteration
+  qk(C0{}, 0, s_cur);
+  // K slot 0 is refilled with K(2) at the start of the first iteration
   __syncthreads();
 
   floatx16 oacc[D / 32];
@@ -219,12 +201,19 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   float l_run = 0.0f;      // this lane's share of the running sum
   const float c = a.c;
 
-  for (int t = 0; t < n_tiles; ++t) {
+  // One key tile; `pc` = t & 1 as a compile-time constant (the loop is
+  // unrolled by two): S^T of tile t+1 reads K slot pc^1, P V reads V slot
+  // pc, and the DMAs of K(t+2) / V(t+1) refill K slot pc / V slot pc^1,
+  // whose last readers finished before the previous barrier.
+  auto tile_step = [&](auto pcc, int t) {
+    constexpr int pc = decltype(pcc)::value;
+    using CP = std::integral_constant<int, pc>;
+    using CQ = std::integral_constant<int, pc ^ 1>;
     const int n0 = t * BN;
     const bool more1 = t + 1 < n_tiles, more2 = t + 2 < n_tiles;
-    if (more2) load_k(n0 + 2 * BN);
-    if (more1) load_v(n0 + BN);
-    if (more1) qk((t + 1) & 1, n0 + BN, s_nxt);
+    if (more2) load_k(n0 + 2 * BN, CP{});
+    if (more1) load_v(n0 + BN, CQ{});
+    if (more1) qk(CQ{}, n0 + BN, s_nxt);
 
     if (!dead(n0, 0)) {
       // ---- masking (diagonal / ragged sub-blocks only)
@@ -262,7 +251,6 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
       const float neg_m = (m_run == kNegInf) ? 0.0f : -m_run;
 
       // ---- P = exp2(c*s - m) rounded to fp16; O^T += V^T P^T
-      const int vslot = t & 1;
 #pragma unroll
       for (int sb = 0; sb < NSUB; ++sb) {
         if (dead(n0, sb)) continue;
@@ -279,38 +267,42 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
             pf[j] = pr[0];
             pf[j + 1] = pr[1];
           }
-          const int kbase = 32 * (NSUB * kh + sb) + 16 * hh + 8 * g;
+          // kperm rows 32 * (sub-block) + 16hh + 4g (+8): keys 16hh + 8g + 0..7
+          const int rb = (32 * (NSUB * kh + sb) + 16 * hh) * D;
 #pragma unroll
           for (int d = 0; d < D / 32; ++d)
-            oacc[d] = mfma32(load_tr8<VS>(sv[vslot], kbase, kbase + 4, 32 * d, lane), pf, oacc[d]);
+            oacc[d] = mfma32(load_tr_pair(v_sl(CP{}) + rb + t_off[d], 8 * D), pf, oacc[d]);
         }
       }
     }
 
-    if (more2) store_k(t & 1);
-    if (more1) store_v((t + 1) & 1);
+    if (more1) __builtin_amdgcn_s_waitcnt(0x0f70);   // this wave's DMAs into the next slots
     __syncthreads();
 #pragma unroll
     for (int sb = 0; sb < NSUB; ++sb) s_cur[sb] = s_nxt[sb];
+  };
+
+  for (int t = 0; t < n_tiles; t += 2) {
+    tile_step(C0{}, t);
+    if (t + 1 < n_tiles) tile_step(C1{}, t + 1);
   }
 
   // ---- merge the two key halves of each query group (K slots reused; the
   // loop's last barrier ordered every read of them before these writes)
   if (KSPLIT == 2) {
-  float *mbuf = reinterpret_cast<float *>(&sk[0][0]) + qg * 64 * (D / 2 + 2);
-  if (kh == 1) {
-    mbuf[lane] = m_run;
-    mbuf[64 + lane] = l_run;
+    float *mbuf = reinterpret_cast<float *>(qg ? sk1 : sk0);
+    if (kh == 1) {
+      s_ml[qg][0][lane] = m_run;
+      s_ml[qg][1][lane] = l_run;
 #pragma unroll
-    for (int d = 0; d < D / 32; ++d)
+      for (int d = 0; d < D / 32; ++d)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) mbuf[(2 + 16 * d + i) * 64 + lane] = oacc[d][i];
-  }
-  __syncthreads();
-  if (kh == 1) return;
-  {
-    const float m_b = mbuf[lane];
-    const float l_b = mbuf[64 + lane];
+        for (int i = 0; i < 16; ++i) mbuf[(16 * d + i) * 64 + lane] = oacc[d][i];
+    }
+    __syncthreads();
+    if (kh == 1) return;
+    const float m_b = s_ml[qg][0][lane];
+    const float l_b = s_ml[qg][1][lane];
     const float m = fmaxf(m_run, m_b);
     const float fa = (m == kNegInf) ? 0.0f : fast_exp2(m_run - m);
     const float fb = (m == kNegInf) ? 0.0f : fast_exp2(m_b - m);
@@ -319,9 +311,8 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
     for (int d = 0; d < D / 32; ++d)
 #pragma unroll
       for (int i = 0; i < 16; ++i)
-        oacc[d][i] = oacc[d][i] * fa + mbuf[(2 + 16 * d + i) * 64 + lane] * fb;
+        oacc[d][i] = oacc[d][i] * fa + mbuf[(16 * d + i) * 64 + lane] * fb;
     m_run = m;
-  }
   }
 
   // ---- epilogue: O = acc / l, LSE = (m + log2 l) * ln2
