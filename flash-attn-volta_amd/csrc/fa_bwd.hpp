@@ -110,6 +110,21 @@ struct DsScale {
     }
     return 1.0f;
   }
+
+  // Same update when `m` is the largest |dS * 2^e| (values already scaled
+  // by the current mul): rescales to keep them in [2^10, 2^15].
+  __device__ __forceinline__ float update_scaled(float m) {
+    if (m > 0.0f && (m > 32768.0f || m < 1024.0f)) {
+      // m = f * 2^x, f in [0.5, 1): the unscaled max is m * 2^-e
+      int en = 14 - (__builtin_amdgcn_frexp_expf(m) - e);
+      en = en > 100 ? 100 : (en < -100 ? -100 : en);
+      const float f = __builtin_amdgcn_ldexpf(1.0f, en - e);
+      e = en;
+      mul = __builtin_amdgcn_ldexpf(1.0f, en);
+      return f;
+    }
+    return 1.0f;
+  }
 };
 
 __device__ __forceinline__ float absmax16(const floatx16 &x) {
@@ -522,6 +537,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
 #pragma unroll
   for (int d = 0; d < D / 32; ++d) dq[d] = floatx16{};
   DsScale sc;
+  float shift = -l2;   // exponent offset: e - LSE * log2(e)
 
   int kv_end = S;
   if (CAUSAL) kv_end = min(S, q0 + BM);
@@ -591,25 +607,30 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
           sacc[i] = vis ? sacc[i] : kNegInf;
         }
       }
+      // The lane's dS scale 2^e rides in the exponent: P * 2^e =
+      // exp2(c s - LSE' + e), so ds below is already dS * 2^e.
       floatx16 ds;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float p = fast_exp2(__builtin_fmaf(sacc[i], c, -l2));
+        const float p = fast_exp2(__builtin_fmaf(sacc[i], c, shift));
         ds[i] = p * (dpacc[i] - dl);
       }
       const float m = absmax16(ds);
       {
-        const float f = sc.update(fmaxf(m, __shfl_xor(m, 32, 64)));
+        const float f = sc.update_scaled(fmaxf(m, __shfl_xor(m, 32, 64)));
         if (__any(f != 1.0f)) {
+          shift = (float)sc.e - l2;
 #pragma unroll
           for (int d = 0; d < D / 32; ++d)
 #pragma unroll
             for (int i = 0; i < 16; ++i) dq[d][i] *= f;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) ds[i] *= f;
         }
       }
       half8 dsf[2];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) dsf[i >> 3][i & 7] = (f16)(ds[i] * sc.mul);
+      for (int i = 0; i < 16; ++i) dsf[i >> 3][i & 7] = (f16)ds[i];
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         // kperm rows 32ks + 16hh + 4g + (0..3) and +8: this 8-key slice
