@@ -189,8 +189,11 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
   __syncthreads();
 
-  floatx16 s_cur[NSUB], s_nxt[NSUB];
-  qk(C0{}, 0, s_cur);
+  // Scores ping-pong between two register sets (no copy at the end of a
+  // tile, which would wait for the next tile's S MFMAs right after issuing
+  // them): tile t's scores live in s_a when t is even, s_b when odd.
+  floatx16 s_a[NSUB], s_b[NSUB];
+  qk(C0{}, 0, s_a);
   // K slot 0 is refilled with K(2) at the start of the first iteration
   __syncthreads();
 
@@ -205,7 +208,7 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   // unrolled by two): S^T of tile t+1 reads K slot pc^1, P V reads V slot
   // pc, and the DMAs of K(t+2) / V(t+1) refill K slot pc / V slot pc^1,
   // whose last readers finished before the previous barrier.
-  auto tile_step = [&](auto pcc, int t) {
+  auto tile_step = [&](auto pcc, int t, floatx16 (&s_cur)[NSUB], floatx16 (&s_nxt)[NSUB]) {
     constexpr int pc = decltype(pcc)::value;
     using CP = std::integral_constant<int, pc>;
     using CQ = std::integral_constant<int, pc ^ 1>;
@@ -278,13 +281,11 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
 
     if (more1) __builtin_amdgcn_s_waitcnt(0x0f70);   // this wave's DMAs into the next slots
     __syncthreads();
-#pragma unroll
-    for (int sb = 0; sb < NSUB; ++sb) s_cur[sb] = s_nxt[sb];
   };
 
   for (int t = 0; t < n_tiles; t += 2) {
-    tile_step(C0{}, t);
-    if (t + 1 < n_tiles) tile_step(C1{}, t + 1);
+    tile_step(C0{}, t, s_a, s_b);
+    if (t + 1 < n_tiles) tile_step(C1{}, t + 1, s_b, s_a);
   }
 
   // ---- merge the two key halves of each query group (K slots reused; the
