@@ -19,14 +19,21 @@ using fa::f16;
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-int check_sizes(int B, int S, int H, int D) {
-  if (B <= 0 || S <= 0 || H <= 0) return FA_ERR_SHAPE;
-  if (D != 32 && D != 64 && D != 128) return FA_ERR_HEAD_DIM;
+// Problem sizes: q, o, dout, dq are (B, Sq, H, D); k, v, dk, dv are
+// (B, Sk, Hk, D); query head h uses key/value head h / (H / Hk).
+struct Shape {
+  int B, Sq, Sk, H, Hk, D;
+};
+
+int check_shape(const Shape &s) {
+  if (s.B <= 0 || s.Sq <= 0 || s.Sk <= 0 || s.H <= 0 || s.Hk <= 0) return FA_ERR_SHAPE;
+  if (s.H % s.Hk != 0) return FA_ERR_SHAPE;
+  if (s.D != 32 && s.D != 64 && s.D != 128) return FA_ERR_HEAD_DIM;
   // Per-(b,h) row offsets use 32-bit query/key indices and the grid is 1-D.
-  if (S > (1 << 30)) return FA_ERR_TOO_LARGE;
-  const int64_t bh = (int64_t)B * H;
+  if (s.Sq > (1 << 30) || s.Sk > (1 << 30)) return FA_ERR_TOO_LARGE;
+  const int64_t bh = (int64_t)s.B * s.H;
   if (bh > (int64_t)1 << 30) return FA_ERR_TOO_LARGE;
-  if (bh * (int64_t)S > ((int64_t)1 << 40)) return FA_ERR_TOO_LARGE;
+  if (bh * (int64_t)s.Sq > ((int64_t)1 << 40)) return FA_ERR_TOO_LARGE;
   return FA_OK;
 }
 
@@ -43,6 +50,14 @@ int check_tensor(const void *p, const int64_t *st, int B, int S, int H, int D) {
                       (double)(H - 1) * st[2] + D;
   if (span > 4.0e18) return FA_ERR_TOO_LARGE;
   return FA_OK;
+}
+
+int check_q_like(const void *p, const int64_t *st, const Shape &s) {
+  return check_tensor(p, st, s.B, s.Sq, s.H, s.D);
+}
+
+int check_kv_like(const void *p, const int64_t *st, const Shape &s) {
+  return check_tensor(p, st, s.B, s.Sk, s.Hk, s.D);
 }
 
 fa::TensorDesc desc(const void *p, const int64_t *st) {
@@ -81,9 +96,10 @@ int device_cus() {
 // causal, whose light blocks finish early and leave the heavy blocks' long
 // sweeps as the critical path).  Used by the forward and both backward
 // kernels (the split is over keys in the forward and dQ, over queries in
-// dK/dV).
-bool fwd_key_split(int S, int BH, bool causal) {
-  const int64_t wgs = (int64_t)((S + 127) / 128) * BH;
+// dK/dV); `rows` is the length of the blocked dimension, `heads` the
+// number of (b, head) pairs the grid covers.
+bool row_split(int rows, int64_t heads, bool causal) {
+  const int64_t wgs = (int64_t)((rows + 127) / 128) * heads;
   return wgs < (int64_t)(causal ? 4 : 2) * device_cus();
 }
 
@@ -91,7 +107,7 @@ template <int D, bool CAUSAL, int KSPLIT>
 int launch_fwd_split(const fa::FwdArgs &args, hipStream_t stream) {
   using T = fa::FwdTile<D, KSPLIT>;
   fa::FwdArgs a = args;
-  a.n_qtiles = (a.S + T::BM - 1) / T::BM;
+  a.n_qtiles = (a.Sq + T::BM - 1) / T::BM;
   const int64_t grid = (int64_t)a.n_qtiles * a.B * a.H;
   if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
   hipLaunchKernelGGL((fa::fa_fwd_kernel<D, CAUSAL, KSPLIT>), dim3((unsigned)grid), dim3(T::NT), 0,
@@ -101,8 +117,8 @@ int launch_fwd_split(const fa::FwdArgs &args, hipStream_t stream) {
 
 template <int D, bool CAUSAL>
 int launch_fwd(const fa::FwdArgs &a, hipStream_t stream) {
-  return fwd_key_split(a.S, a.B * a.H, CAUSAL) ? launch_fwd_split<D, CAUSAL, 2>(a, stream)
-                                                : launch_fwd_split<D, CAUSAL, 1>(a, stream);
+  return row_split(a.Sq, (int64_t)a.B * a.H, CAUSAL) ? launch_fwd_split<D, CAUSAL, 2>(a, stream)
+                                                     : launch_fwd_split<D, CAUSAL, 1>(a, stream);
 }
 
 template <int D>
@@ -120,8 +136,8 @@ template <int D, bool CAUSAL, int SPLIT>
 int launch_dkdv_split(const fa::BwdArgs &args, hipStream_t stream) {
   using T = fa::DkdvTile<D, SPLIT>;
   fa::BwdArgs a = args;
-  a.n_blocks = (a.S + T::BK - 1) / T::BK;
-  const int64_t grid = (int64_t)a.n_blocks * a.B * a.H;
+  a.n_blocks = (a.Sk + T::BK - 1) / T::BK;
+  const int64_t grid = (int64_t)a.n_blocks * a.B * a.Hk;
   if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
   hipLaunchKernelGGL((fa::fa_bwd_dkdv_kernel<D, CAUSAL, SPLIT>), dim3((unsigned)grid), dim3(T::NT),
                      0, stream, a);
@@ -132,7 +148,7 @@ template <int D, bool CAUSAL, int SPLIT>
 int launch_dq_split(const fa::BwdArgs &args, hipStream_t stream) {
   using T = fa::DqTile<D, SPLIT>;
   fa::BwdArgs a = args;
-  a.n_blocks = (a.S + T::BM - 1) / T::BM;
+  a.n_blocks = (a.Sq + T::BM - 1) / T::BM;
   const int64_t grid = (int64_t)a.n_blocks * a.B * a.H;
   if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
   hipLaunchKernelGGL((fa::fa_bwd_dq_kernel<D, CAUSAL, SPLIT>), dim3((unsigned)grid), dim3(T::NT), 0,
@@ -142,14 +158,14 @@ int launch_dq_split(const fa::BwdArgs &args, hipStream_t stream) {
 
 template <int D, bool CAUSAL>
 int launch_dkdv(const fa::BwdArgs &a, hipStream_t stream) {
-  return fwd_key_split(a.S, a.B * a.H, CAUSAL) ? launch_dkdv_split<D, CAUSAL, 2>(a, stream)
-                                                : launch_dkdv_split<D, CAUSAL, 1>(a, stream);
+  return row_split(a.Sk, (int64_t)a.B * a.Hk, CAUSAL) ? launch_dkdv_split<D, CAUSAL, 2>(a, stream)
+                                                      : launch_dkdv_split<D, CAUSAL, 1>(a, stream);
 }
 
 template <int D, bool CAUSAL>
 int launch_dq(const fa::BwdArgs &a, hipStream_t stream) {
-  return fwd_key_split(a.S, a.B * a.H, CAUSAL) ? launch_dq_split<D, CAUSAL, 2>(a, stream)
-                                                : launch_dq_split<D, CAUSAL, 1>(a, stream);
+  return row_split(a.Sq, (int64_t)a.B * a.H, CAUSAL) ? launch_dq_split<D, CAUSAL, 2>(a, stream)
+                                                     : launch_dq_split<D, CAUSAL, 1>(a, stream);
 }
 
 template <bool CAUSAL>
@@ -170,12 +186,80 @@ int dispatch_dq(int D, const fa::BwdArgs &a, hipStream_t st) {
   }
 }
 
-// Backward arguments common to fa_bwd, fa_bwd_dkdv and fa_bwd_dq; the
+int run_fwd(const void *q, const void *k, const void *v, void *o, float *lse, const Shape &s,
+            const int64_t *q_st, const int64_t *k_st, const int64_t *v_st, const int64_t *o_st,
+            float sm_scale, int causal, void *stream) {
+  int rc = check_shape(s);
+  if (rc) return rc;
+  if ((rc = check_q_like(q, q_st, s))) return rc;
+  if ((rc = check_kv_like(k, k_st, s))) return rc;
+  if ((rc = check_kv_like(v, v_st, s))) return rc;
+  if ((rc = check_q_like(o, o_st, s))) return rc;
+  if (lse != nullptr && !aligned16(lse)) return FA_ERR_ALIGNMENT;
+  if (!isfinite(sm_scale)) return FA_ERR_SCALE;
+
+  fa::FwdArgs a{};
+  a.q = desc(q, q_st);
+  a.k = desc(k, k_st);
+  a.v = desc(v, v_st);
+  a.o = static_cast<f16 *>(o);
+  a.o_sb = o_st[0];
+  a.o_ss = o_st[1];
+  a.o_sh = o_st[2];
+  a.lse = lse;
+  a.B = s.B;
+  a.Sq = s.Sq;
+  a.Sk = s.Sk;
+  a.H = s.H;
+  a.grp = s.H / s.Hk;
+  a.off = s.Sk - s.Sq;
+  a.c = kernel_scale(sm_scale);
+  a.neg = sm_scale < 0.0f;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (s.D) {
+    case 32: return causal ? launch_fwd<32, true>(a, st) : launch_fwd<32, false>(a, st);
+    case 64: return causal ? launch_fwd<64, true>(a, st) : launch_fwd<64, false>(a, st);
+    default: return causal ? launch_fwd<128, true>(a, st) : launch_fwd<128, false>(a, st);
+  }
+}
+
+int run_pre(const void *o, const void *dout, float *delta, const Shape &s, const int64_t *o_st,
+            const int64_t *do_st, void *stream) {
+  int rc = check_shape(s);
+  if (rc) return rc;
+  if ((rc = check_q_like(o, o_st, s))) return rc;
+  if ((rc = check_q_like(dout, do_st, s))) return rc;
+  if (delta == nullptr) return FA_ERR_NULL_POINTER;
+  if (!aligned16(delta)) return FA_ERR_ALIGNMENT;
+  fa::PreArgs a{};
+  a.o = desc(o, o_st);
+  a.dout = desc(dout, do_st);
+  a.delta = delta;
+  a.B = s.B;
+  a.S = s.Sq;
+  a.H = s.H;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (s.D) {
+    case 32: return launch_pre<32>(a, st);
+    case 64: return launch_pre<64>(a, st);
+    default: return launch_pre<128>(a, st);
+  }
+}
+
+// Checks common to every backward step, then the kernel arguments; the
 // output pointers that a step does not write stay NULL.
-fa::BwdArgs bwd_args(const void *dout, const void *q, const void *k, const void *v,
-                     const float *lse, const float *delta, int B, int S, int H,
-                     const int64_t *do_st, const int64_t *q_st, const int64_t *k_st,
-                     const int64_t *v_st, float sm_scale) {
+int bwd_common(const void *dout, const void *q, const void *k, const void *v, const float *lse,
+               const float *delta, const Shape &s, const int64_t *do_st, const int64_t *q_st,
+               const int64_t *k_st, const int64_t *v_st, float sm_scale, fa::BwdArgs *out) {
+  int rc = check_shape(s);
+  if (rc) return rc;
+  if ((rc = check_q_like(dout, do_st, s))) return rc;
+  if ((rc = check_q_like(q, q_st, s))) return rc;
+  if ((rc = check_kv_like(k, k_st, s))) return rc;
+  if ((rc = check_kv_like(v, v_st, s))) return rc;
+  if (lse == nullptr || delta == nullptr) return FA_ERR_NULL_POINTER;
+  if (!aligned16(lse) || !aligned16(delta)) return FA_ERR_ALIGNMENT;
+  if (!isfinite(sm_scale)) return FA_ERR_SCALE;
   fa::BwdArgs a{};
   a.q = desc(q, q_st);
   a.k = desc(k, k_st);
@@ -183,35 +267,91 @@ fa::BwdArgs bwd_args(const void *dout, const void *q, const void *k, const void 
   a.dout = desc(dout, do_st);
   a.lse = lse;
   a.delta = delta;
-  a.B = B;
-  a.S = S;
-  a.H = H;
+  a.B = s.B;
+  a.Sq = s.Sq;
+  a.Sk = s.Sk;
+  a.H = s.H;
+  a.Hk = s.Hk;
+  a.grp = s.H / s.Hk;
+  a.off = s.Sk - s.Sq;
   a.c = kernel_scale(sm_scale);
   a.sm_scale = sm_scale;
   a.neg = sm_scale < 0.0f;
-  return a;
-}
-
-int check_bwd_inputs(const void *dout, const void *q, const void *k, const void *v,
-                     const float *lse, int B, int S, int H, int D,
-                     const int64_t *do_st, const int64_t *q_st, const int64_t *k_st,
-                     const int64_t *v_st, float sm_scale) {
-  int rc = check_sizes(B, S, H, D);
-  if (rc) return rc;
-  if ((rc = check_tensor(dout, do_st, B, S, H, D))) return rc;
-  if ((rc = check_tensor(q, q_st, B, S, H, D))) return rc;
-  if ((rc = check_tensor(k, k_st, B, S, H, D))) return rc;
-  if ((rc = check_tensor(v, v_st, B, S, H, D))) return rc;
-  if (lse == nullptr) return FA_ERR_NULL_POINTER;
-  if (!aligned16(lse)) return FA_ERR_ALIGNMENT;
-  if (!isfinite(sm_scale)) return FA_ERR_SCALE;
+  *out = a;
   return FA_OK;
 }
 
-size_t delta_bytes(int B, int S, int H) {
-  const size_t n = (size_t)B * (size_t)H * (size_t)S * sizeof(float);
+int run_dkdv(const void *dout, const void *q, const void *k, const void *v, const float *lse,
+             const float *delta, void *dk, void *dv, const Shape &s, const int64_t *do_st,
+             const int64_t *q_st, const int64_t *k_st, const int64_t *v_st, const int64_t *dk_st,
+             const int64_t *dv_st, float sm_scale, int causal, void *stream) {
+  fa::BwdArgs a;
+  int rc = bwd_common(dout, q, k, v, lse, delta, s, do_st, q_st, k_st, v_st, sm_scale, &a);
+  if (rc) return rc;
+  if ((rc = check_kv_like(dk, dk_st, s))) return rc;
+  if ((rc = check_kv_like(dv, dv_st, s))) return rc;
+  a.dk = static_cast<f16 *>(dk);
+  a.dv = static_cast<f16 *>(dv);
+  a.dk_sb = dk_st[0];
+  a.dk_ss = dk_st[1];
+  a.dk_sh = dk_st[2];
+  a.dv_sb = dv_st[0];
+  a.dv_ss = dv_st[1];
+  a.dv_sh = dv_st[2];
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return causal ? dispatch_dkdv<true>(s.D, a, st) : dispatch_dkdv<false>(s.D, a, st);
+}
+
+int run_dq(const void *dout, const void *q, const void *k, const void *v, const float *lse,
+           const float *delta, void *dq, const Shape &s, const int64_t *do_st, const int64_t *q_st,
+           const int64_t *k_st, const int64_t *v_st, const int64_t *dq_st, float sm_scale,
+           int causal, void *stream) {
+  fa::BwdArgs a;
+  int rc = bwd_common(dout, q, k, v, lse, delta, s, do_st, q_st, k_st, v_st, sm_scale, &a);
+  if (rc) return rc;
+  if ((rc = check_q_like(dq, dq_st, s))) return rc;
+  a.dq = static_cast<f16 *>(dq);
+  a.dq_sb = dq_st[0];
+  a.dq_ss = dq_st[1];
+  a.dq_sh = dq_st[2];
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return causal ? dispatch_dq<true>(s.D, a, st) : dispatch_dq<false>(s.D, a, st);
+}
+
+size_t delta_bytes(int B, int Sq, int H) {
+  const size_t n = (size_t)B * (size_t)H * (size_t)Sq * sizeof(float);
   return (n + 255) & ~(size_t)255;
 }
+
+int run_bwd(const void *dout, const void *q, const void *k, const void *v, const void *o,
+            const float *lse, void *dq, void *dk, void *dv, void *workspace,
+            size_t workspace_bytes, const Shape &s, const int64_t *do_st, const int64_t *q_st,
+            const int64_t *k_st, const int64_t *v_st, const int64_t *o_st, const int64_t *dq_st,
+            const int64_t *dk_st, const int64_t *dv_st, float sm_scale, int causal, void *stream) {
+  int rc = check_shape(s);
+  if (rc) return rc;
+  if ((rc = check_q_like(o, o_st, s))) return rc;
+  if ((rc = check_q_like(dq, dq_st, s))) return rc;
+  if ((rc = check_kv_like(dk, dk_st, s))) return rc;
+  if ((rc = check_kv_like(dv, dv_st, s))) return rc;
+  if (workspace == nullptr || workspace_bytes < delta_bytes(s.B, s.Sq, s.H))
+    return FA_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return FA_ERR_ALIGNMENT;
+  // Validate the inputs shared by the two main kernels before the first
+  // launch, so a bad call launches nothing.
+  fa::BwdArgs probe;
+  float *delta = static_cast<float *>(workspace);
+  if ((rc = bwd_common(dout, q, k, v, lse, delta, s, do_st, q_st, k_st, v_st, sm_scale, &probe)))
+    return rc;
+  if ((rc = run_pre(o, dout, delta, s, o_st, do_st, stream))) return rc;
+  if ((rc = run_dkdv(dout, q, k, v, lse, delta, dk, dv, s, do_st, q_st, k_st, v_st, dk_st, dv_st,
+                     sm_scale, causal, stream)))
+    return rc;
+  return run_dq(dout, q, k, v, lse, delta, dq, s, do_st, q_st, k_st, v_st, dq_st, sm_scale, causal,
+                stream);
+}
+
+Shape square(int B, int S, int H, int D) { return Shape{B, S, S, H, H, D}; }
 
 }  // namespace
 
@@ -224,7 +364,9 @@ const char *fa_strerror(int status) {
     case FA_OK: return "success";
     case FA_ERR_NULL_POINTER: return "a required pointer is NULL";
     case FA_ERR_HEAD_DIM: return "unsupported head_dim (supported: 32, 64, 128)";
-    case FA_ERR_SHAPE: return "B, S and H must be positive";
+    case FA_ERR_SHAPE:
+      return "B, sequence lengths and head counts must be positive, and the query head "
+             "count a multiple of the key/value head count";
     case FA_ERR_STRIDE:
       return "bad stride: the head_dim stride must be 1 and the other strides "
              "non-negative multiples of 8 elements";
@@ -242,64 +384,28 @@ int fa_fwd(const void *q, const void *k, const void *v, void *o, float *lse,
            const int64_t q_strides[4], const int64_t k_strides[4],
            const int64_t v_strides[4], const int64_t o_strides[4],
            float sm_scale, int causal, void *stream) {
-  int rc = check_sizes(B, S, H, D);
-  if (rc) return rc;
-  if ((rc = check_tensor(q, q_strides, B, S, H, D))) return rc;
-  if ((rc = check_tensor(k, k_strides, B, S, H, D))) return rc;
-  if ((rc = check_tensor(v, v_strides, B, S, H, D))) return rc;
-  if ((rc = check_tensor(o, o_strides, B, S, H, D))) return rc;
-  if (lse != nullptr && !aligned16(lse)) return FA_ERR_ALIGNMENT;
-  if (!isfinite(sm_scale)) return FA_ERR_SCALE;
+  return run_fwd(q, k, v, o, lse, square(B, S, H, D), q_strides, k_strides, v_strides, o_strides,
+                 sm_scale, causal, stream);
+}
 
-  fa::FwdArgs a{};
-  a.q = desc(q, q_strides);
-  a.k = desc(k, k_strides);
-  a.v = desc(v, v_strides);
-  a.o = static_cast<f16 *>(o);
-  a.o_sb = o_strides[0];
-  a.o_ss = o_strides[1];
-  a.o_sh = o_strides[2];
-  a.lse = lse;
-  a.B = B;
-  a.S = S;
-  a.H = H;
-  a.c = kernel_scale(sm_scale);
-  a.neg = sm_scale < 0.0f;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  switch (D) {
-    case 32: return causal ? launch_fwd<32, true>(a, st) : launch_fwd<32, false>(a, st);
-    case 64: return causal ? launch_fwd<64, true>(a, st) : launch_fwd<64, false>(a, st);
-    default: return causal ? launch_fwd<128, true>(a, st) : launch_fwd<128, false>(a, st);
-  }
+int fa_fwd_gqa(const void *q, const void *k, const void *v, void *o, float *lse,
+               int B, int Sq, int Sk, int H, int Hk, int D,
+               const int64_t q_strides[4], const int64_t k_strides[4],
+               const int64_t v_strides[4], const int64_t o_strides[4],
+               float sm_scale, int causal, void *stream) {
+  return run_fwd(q, k, v, o, lse, Shape{B, Sq, Sk, H, Hk, D}, q_strides, k_strides, v_strides,
+                 o_strides, sm_scale, causal, stream);
 }
 
 int fa_bwd_preprocess(const void *o, const void *dout, float *delta,
                       int B, int S, int H, int D,
                       const int64_t o_strides[4], const int64_t do_strides[4],
                       void *stream) {
-  int rc = check_sizes(B, S, H, D);
-  if (rc) return rc;
-  if ((rc = check_tensor(o, o_strides, B, S, H, D))) return rc;
-  if ((rc = check_tensor(dout, do_strides, B, S, H, D))) return rc;
-  if (delta == nullptr) return FA_ERR_NULL_POINTER;
-  if (!aligned16(delta)) return FA_ERR_ALIGNMENT;
-  fa::PreArgs a{};
-  a.o = desc(o, o_strides);
-  a.dout = desc(dout, do_strides);
-  a.delta = delta;
-  a.B = B;
-  a.S = S;
-  a.H = H;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  switch (D) {
-    case 32: return launch_pre<32>(a, st);
-    case 64: return launch_pre<64>(a, st);
-    default: return launch_pre<128>(a, st);
-  }
+  return run_pre(o, dout, delta, square(B, S, H, D), o_strides, do_strides, stream);
 }
 
 size_t fa_bwd_workspace_bytes(int B, int S, int H, int D) {
-  if (check_sizes(B, S, H, D) != FA_OK) return 0;
+  if (check_shape(square(B, S, H, D)) != FA_OK) return 0;
   return delta_bytes(B, S, H);
 }
 
@@ -313,24 +419,24 @@ int fa_bwd(const void *dout, const void *q, const void *k, const void *v,
            const int64_t o_strides[4], const int64_t dq_strides[4],
            const int64_t dk_strides[4], const int64_t dv_strides[4],
            float sm_scale, int causal, void *stream) {
-  int rc = check_bwd_inputs(dout, q, k, v, lse, B, S, H, D, do_strides, q_strides, k_strides,
-                            v_strides, sm_scale);
-  if (rc) return rc;
-  if ((rc = check_tensor(o, o_strides, B, S, H, D))) return rc;
-  if ((rc = check_tensor(dq, dq_strides, B, S, H, D))) return rc;
-  if ((rc = check_tensor(dk, dk_strides, B, S, H, D))) return rc;
-  if ((rc = check_tensor(dv, dv_strides, B, S, H, D))) return rc;
-  if (workspace == nullptr || workspace_bytes < delta_bytes(B, S, H)) return FA_ERR_WORKSPACE;
-  if (!aligned16(workspace)) return FA_ERR_ALIGNMENT;
+  return run_bwd(dout, q, k, v, o, lse, dq, dk, dv, workspace, workspace_bytes,
+                 square(B, S, H, D), do_strides, q_strides, k_strides, v_strides, o_strides,
+                 dq_strides, dk_strides, dv_strides, sm_scale, causal, stream);
+}
 
-  float *delta = static_cast<float *>(workspace);
-  rc = fa_bwd_preprocess(o, dout, delta, B, S, H, D, o_strides, do_strides, stream);
-  if (rc) return rc;
-  rc = fa_bwd_dkdv(dout, q, k, v, lse, delta, dk, dv, B, S, H, D, do_strides, q_strides,
-                   k_strides, v_strides, dk_strides, dv_strides, sm_scale, causal, stream);
-  if (rc) return rc;
-  return fa_bwd_dq(dout, q, k, v, lse, delta, dq, B, S, H, D, do_strides, q_strides, k_strides,
-                   v_strides, dq_strides, sm_scale, causal, stream);
+int fa_bwd_gqa(const void *dout, const void *q, const void *k, const void *v,
+               const void *o, const float *lse,
+               void *dq, void *dk, void *dv,
+               void *workspace, size_t workspace_bytes,
+               int B, int Sq, int Sk, int H, int Hk, int D,
+               const int64_t do_strides[4], const int64_t q_strides[4],
+               const int64_t k_strides[4], const int64_t v_strides[4],
+               const int64_t o_strides[4], const int64_t dq_strides[4],
+               const int64_t dk_strides[4], const int64_t dv_strides[4],
+               float sm_scale, int causal, void *stream) {
+  return run_bwd(dout, q, k, v, o, lse, dq, dk, dv, workspace, workspace_bytes,
+                 Shape{B, Sq, Sk, H, Hk, D}, do_strides, q_strides, k_strides, v_strides,
+                 o_strides, dq_strides, dk_strides, dv_strides, sm_scale, causal, stream);
 }
 
 int fa_bwd_dkdv(const void *dout, const void *q, const void *k, const void *v,
@@ -340,25 +446,8 @@ int fa_bwd_dkdv(const void *dout, const void *q, const void *k, const void *v,
                 const int64_t k_strides[4], const int64_t v_strides[4],
                 const int64_t dk_strides[4], const int64_t dv_strides[4],
                 float sm_scale, int causal, void *stream) {
-  int rc = check_bwd_inputs(dout, q, k, v, lse, B, S, H, D, do_strides, q_strides, k_strides,
-                            v_strides, sm_scale);
-  if (rc) return rc;
-  if ((rc = check_tensor(dk, dk_strides, B, S, H, D))) return rc;
-  if ((rc = check_tensor(dv, dv_strides, B, S, H, D))) return rc;
-  if (delta == nullptr) return FA_ERR_NULL_POINTER;
-  if (!aligned16(delta)) return FA_ERR_ALIGNMENT;
-  fa::BwdArgs a = bwd_args(dout, q, k, v, lse, delta, B, S, H, do_strides, q_strides, k_strides,
-                           v_strides, sm_scale);
-  a.dk = static_cast<f16 *>(dk);
-  a.dv = static_cast<f16 *>(dv);
-  a.dk_sb = dk_strides[0];
-  a.dk_ss = dk_strides[1];
-  a.dk_sh = dk_strides[2];
-  a.dv_sb = dv_strides[0];
-  a.dv_ss = dv_strides[1];
-  a.dv_sh = dv_strides[2];
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  return causal ? dispatch_dkdv<true>(D, a, st) : dispatch_dkdv<false>(D, a, st);
+  return run_dkdv(dout, q, k, v, lse, delta, dk, dv, square(B, S, H, D), do_strides, q_strides,
+                  k_strides, v_strides, dk_strides, dv_strides, sm_scale, causal, stream);
 }
 
 int fa_bwd_dq(const void *dout, const void *q, const void *k, const void *v,
@@ -368,20 +457,8 @@ int fa_bwd_dq(const void *dout, const void *q, const void *k, const void *v,
               const int64_t k_strides[4], const int64_t v_strides[4],
               const int64_t dq_strides[4],
               float sm_scale, int causal, void *stream) {
-  int rc = check_bwd_inputs(dout, q, k, v, lse, B, S, H, D, do_strides, q_strides, k_strides,
-                            v_strides, sm_scale);
-  if (rc) return rc;
-  if ((rc = check_tensor(dq, dq_strides, B, S, H, D))) return rc;
-  if (delta == nullptr) return FA_ERR_NULL_POINTER;
-  if (!aligned16(delta)) return FA_ERR_ALIGNMENT;
-  fa::BwdArgs a = bwd_args(dout, q, k, v, lse, delta, B, S, H, do_strides, q_strides, k_strides,
-                           v_strides, sm_scale);
-  a.dq = static_cast<f16 *>(dq);
-  a.dq_sb = dq_strides[0];
-  a.dq_ss = dq_strides[1];
-  a.dq_sh = dq_strides[2];
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  return causal ? dispatch_dq<true>(D, a, st) : dispatch_dq<false>(D, a, st);
+  return run_dq(dout, q, k, v, lse, delta, dq, square(B, S, H, D), do_strides, q_strides,
+                k_strides, v_strides, dq_strides, sm_scale, causal, stream);
 }
 
 }  // extern "C"

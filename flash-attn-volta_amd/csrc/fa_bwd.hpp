@@ -41,14 +41,16 @@
 namespace fa {
 
 struct BwdArgs {
-  TensorDesc q, k, v, dout;
-  const float *lse;     // (B, H, S) natural log
-  const float *delta;   // (B, H, S)
-  f16 *dq, *dk, *dv;
+  TensorDesc q, k, v, dout;   // q, dout: (B, Sq, H, D); k, v: (B, Sk, Hk, D)
+  const float *lse;     // (B, H, Sq) natural log
+  const float *delta;   // (B, H, Sq)
+  f16 *dq, *dk, *dv;    // dq: (B, Sq, H, D); dk, dv: (B, Sk, Hk, D)
   int64_t dq_sb, dq_ss, dq_sh;
   int64_t dk_sb, dk_ss, dk_sh;
   int64_t dv_sb, dv_ss, dv_sh;
-  int B, S, H;
+  int B, Sq, Sk, H, Hk;
+  int grp;              // query heads per key/value head (H / Hk)
+  int off;              // causal: query i sees keys j <= i + off (off = Sk - Sq)
   int n_blocks;         // query blocks (dQ) or key blocks (dK/dV)
   float c;              // |sm_scale| * log2(e), clamped away from 0
   float sm_scale;       // signed scale applied to dQ and dK
@@ -134,38 +136,6 @@ __device__ __forceinline__ float absmax16(const floatx16 &x) {
   return m;
 }
 
-// Row-major staging of a 64-row x D tile (rows r0.. of one (b,h)) into an LDS
-// slot with 32-row blocks in kperm order.  16-byte buffer loads; rows past S
-// read as zeros.
-template <int D, int NT, int RS>
-struct KpermStager {
-  static constexpr int CHUNKS = 64 * D / 8;
-  static constexpr int PER_T = (CHUNKS + NT - 1) / NT;
-  u32x4 r[PER_T];
-  int off[PER_T], lds[PER_T];
-
-  __device__ __forceinline__ void init(int tid, int64_t ss) {
-#pragma unroll
-    for (int i = 0; i < PER_T; ++i) {
-      const int idx = tid + i * NT;
-      const int row = idx / (D / 8), c8 = idx % (D / 8);
-      off[i] = row * (int)ss * 2 + 16 * c8;
-      lds[i] = kperm_row(row) * RS + 8 * c8;
-    }
-  }
-  __device__ __forceinline__ void load(const f16 *head, int64_t ss, int r0, int S, int tid) {
-    const __amdgpu_buffer_rsrc_t rs = rows_rsrc(head, ss, r0, S, D);
-#pragma unroll
-    for (int i = 0; i < PER_T; ++i)
-      if (CHUNKS % NT == 0 || tid + i * NT < CHUNKS) r[i] = buf_load16(rs, off[i]);
-  }
-  __device__ __forceinline__ void store(f16 *slot, int tid) const {
-#pragma unroll
-    for (int i = 0; i < PER_T; ++i)
-      if (CHUNKS % NT == 0 || tid + i * NT < CHUNKS) *(u32x4 *)(slot + lds[i]) = r[i];
-  }
-};
-
 // Store a D^T x 32 accumulator set (lane = row `row`, slots = columns) as
 // fp16 row `row` of a (.., D) tensor, scaled by `mul`.
 template <int D>
@@ -250,13 +220,13 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
   auto q_st = [&](auto stc) -> f16 * { return decltype(stc)::value ? s_q1 : s_q0; };
   auto do_st = [&](auto stc) -> f16 * { return decltype(stc)::value ? s_do1 : s_do0; };
 
-  const int S = a.S;
-  const int BH = a.B * a.H;
+  const int Sq = a.Sq, Sk = a.Sk, off = a.off;
+  const int BHk = a.B * a.Hk;
   const int bid = blockIdx.x;
-  const int bh = bid % BH;
+  const int bhk = bid % BHk;
   // Causal: low key blocks see the most queries; zigzag heavy/light.
-  const int kt = CAUSAL ? zigzag_rank(bid / BH, a.n_blocks) : bid / BH;
-  const int b = bh / a.H, h = bh % a.H;
+  const int kt = CAUSAL ? zigzag_rank(bid / BHk, a.n_blocks) : bid / BHk;
+  const int b = bhk / a.Hk, hk = bhk % a.Hk;
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int kg = SPLIT == 2 ? (w >> 1) : w;
   const int qh = SPLIT == 2 ? (w & 1) : 0;
@@ -265,10 +235,6 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
   const int wk0 = k0 + 32 * kg;
   const int key = wk0 + l32;
 
-  const f16 *qb = a.q.head(b, h);
-  const f16 *gb = a.dout.head(b, h);
-  const float *lse_b = a.lse + (int64_t)bh * S;
-  const float *dl_b = a.delta + (int64_t)bh * S;
 
   // K^T and V^T fragments (B operands): K[key][16c + 8g .. +7].  K is
   // pre-multiplied by +-ck = +-min(c, 1) and rounded to fp16 (as the
@@ -276,8 +242,8 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
   // ck * s directly; ck <= 1 keeps the product inside the fp16 range.  The
   // rest of c, cr = c / ck, is 1 unless |sm_scale| > ln 2.
   half8 kf[D / 16], vf[D / 16];
-  load_row_frags<D>(kf, a.k.head(b, h), a.k.ss, key, S, g);
-  load_row_frags<D>(vf, a.v.head(b, h), a.v.ss, key, S, g);
+  load_row_frags<D>(kf, a.k.head(b, hk), a.k.ss, key, Sk, g);
+  load_row_frags<D>(vf, a.v.head(b, hk), a.v.ss, key, Sk, g);
   const float ck = fminf(a.c, 1.0f);
   const float cr = a.c / ck;
   {
@@ -296,8 +262,14 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
   }
   DsScale sc;
 
-  const int m_begin = CAUSAL ? (k0 / BQ) * BQ : 0;
-  const int n_tiles = (S > m_begin) ? (S - m_begin + BQ - 1) / BQ : 0;
+  // Query tiles: for each of the grp query heads sharing this key/value
+  // head (their dK, dV contributions add up), the tiles from the first one
+  // that can see key k0 (query k0 - off, causal) to the end.  Flattened:
+  // tile t is tile t % nt_h of query head hk * grp + t / nt_h.
+  const int m_first = CAUSAL ? max(0, k0 - off) : 0;
+  const int m_begin = (m_first / BQ) * BQ;
+  const int nt_h = (Sq > m_begin) ? (Sq - m_begin + BQ - 1) / BQ : 0;
+  const int n_tiles = nt_h * a.grp;
 
   // Per-query rows staged beside each tile, laid out as MFMA accumulator
   // seeds: s_lse = -LSE * log2(e) / cr (-inf past S, so P = 0 there) and
@@ -309,15 +281,18 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
   const float lse_mul = -kLog2e / cr;
   float lse_r = 0.0f, dl_r = 0.0f;   // raw LSE / delta of row m0 + tid
   // Q and dO go straight to LDS stage `st`; LSE / delta through VGPRs.
-  auto load_tile = [&](int m0, auto stc) {
-    constexpr int st = decltype(stc)::value;
-    stq.load(q_st(stc), qb, a.q.ss, m0, S, w);
-    stg.load(do_st(stc), gb, a.dout.ss, m0, S, w);
+  auto tile_head = [&](int t) { return hk * a.grp + t / nt_h; };
+  auto tile_m0 = [&](int t) { return m_begin + (t % nt_h) * BQ; };
+  auto load_tile = [&](int t, auto stc) {
+    const int h = tile_head(t), m0 = tile_m0(t);
+    stq.load(q_st(stc), a.q.head(b, h), a.q.ss, m0, Sq, w);
+    stg.load(do_st(stc), a.dout.head(b, h), a.dout.ss, m0, Sq, w);
     if (tid < BQ) {
       const int m = m0 + tid;
-      // rows past S: +inf LSE, so the seed below is -inf and P = 0
-      lse_r = (m < S) ? lse_b[m] : kPosInf;
-      dl_r = (m < S) ? dl_b[m] : 0.0f;
+      const int64_t row = ((int64_t)b * a.H + h) * Sq + m;
+      // rows past Sq: +inf LSE, so the seed below is -inf and P = 0
+      lse_r = (m < Sq) ? a.lse[row] : kPosInf;
+      dl_r = (m < Sq) ? a.delta[row] : 0.0f;
     }
   };
   // Publishing a stage: its LSE / delta rows go to LDS, then every DMA of
@@ -351,7 +326,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
 
   __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): K/V fragments resident
   if (n_tiles > 0) {
-    load_tile(m_begin, std::integral_constant<int, 0>{});
+    load_tile(0, std::integral_constant<int, 0>{});
     store_tile(std::integral_constant<int, 0>{});
   }
   __syncthreads();
@@ -360,17 +335,17 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
   // is unrolled by two) so every LDS address is a base plus an immediate.
   auto tile_step = [&](auto stc, int t) {
     constexpr int st = decltype(stc)::value;
-    const int m0 = m_begin + t * BQ;
+    const int m0 = tile_m0(t);
     const bool more = t + 1 < n_tiles;
-    if (more) load_tile(m0 + BQ, std::integral_constant<int, st ^ 1>{});
+    if (more) load_tile(t + 1, std::integral_constant<int, st ^ 1>{});
 
 #pragma unroll
     for (int sb = 0; sb < NSUB; ++sb) {
       const int qs = NSUB * qh + sb;   // 32-query sub-block of the tile
       const int ms = m0 + 32 * qs;
       // whole sub-block above this wave's keys' diagonal: nothing visible
-      if (CAUSAL && ms + 31 < wk0) continue;
-      if (ms >= S) continue;
+      if (CAUSAL && ms + 31 + off < wk0) continue;
+      if (ms >= Sq) continue;
 
       // slot i <-> query ms + slot_row(i, g); lane <-> key.  Accumulator
       // seeds: slots 8hh + j hold rows 32qs + 16hh + 8g + j.
@@ -401,11 +376,11 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
       }
       // Invisible scores become -inf (P = 0) in one pass, taken only by
       // diagonal and ragged sub-blocks, so the softmax below is branch-free.
-      if ((CAUSAL && ms < wk0 + 31) || (ms + 31 >= S) || (wk0 + 31 >= S)) {
+      if ((CAUSAL && ms + off < wk0 + 31) || (ms + 31 >= Sq) || (wk0 + 31 >= Sk)) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int m = ms + slot_row(i, g);
-          const bool vis = m < S && key < S && (!CAUSAL || key <= m);
+          const bool vis = m < Sq && key < Sk && (!CAUSAL || key <= m + off);
           sacc[i] = vis ? sacc[i] : kNegInf;
         }
       }
@@ -469,9 +444,9 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
     if (qh == 1) return;
     dk_mul = a.sm_scale;
   }
-  if (key < S) {
-    store_row_fp16<D>(a.dk + b * a.dk_sb + h * a.dk_sh + (int64_t)key * a.dk_ss, dk, dk_mul, g);
-    store_row_fp16<D>(a.dv + b * a.dv_sb + h * a.dv_sh + (int64_t)key * a.dv_ss, dv, 1.0f, g);
+  if (key < Sk) {
+    store_row_fp16<D>(a.dk + b * a.dk_sb + hk * a.dk_sh + (int64_t)key * a.dk_ss, dk, dk_mul, g);
+    store_row_fp16<D>(a.dv + b * a.dv_sb + hk * a.dv_sh + (int64_t)key * a.dv_ss, dv, 1.0f, g);
   }
 }
 
@@ -504,13 +479,14 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
   auto k_st = [&](auto stc) -> f16 * { return decltype(stc)::value ? s_k1 : s_k0; };
   auto v_st = [&](auto stc) -> f16 * { return decltype(stc)::value ? s_v1 : s_v0; };
 
-  const int S = a.S;
+  const int Sq = a.Sq, Sk = a.Sk, off = a.off;
   const int BH = a.B * a.H;
   const int bid = blockIdx.x;
   const int bh = bid % BH;
   // Causal: late query blocks see the most keys; zigzag heavy/light.
   const int qt = CAUSAL ? a.n_blocks - 1 - zigzag_rank(bid / BH, a.n_blocks) : bid / BH;
   const int b = bh / a.H, h = bh % a.H;
+  const int hk = h / a.grp;
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int qg = SPLIT == 2 ? (w >> 1) : w;
   const int kh = SPLIT == 2 ? (w & 1) : 0;
@@ -519,19 +495,19 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
   const int wq0 = q0 + 32 * qg;
   const int qrow = wq0 + l32;
 
-  const f16 *kb = a.k.head(b, h);
-  const f16 *vb = a.v.head(b, h);
+  const f16 *kb = a.k.head(b, hk);
+  const f16 *vb = a.v.head(b, hk);
 
   half8 qf[D / 16], gf[D / 16];
-  load_row_frags<D>(qf, a.q.head(b, h), a.q.ss, qrow, S, g);
-  load_row_frags<D>(gf, a.dout.head(b, h), a.dout.ss, qrow, S, g);
+  load_row_frags<D>(qf, a.q.head(b, h), a.q.ss, qrow, Sq, g);
+  load_row_frags<D>(gf, a.dout.head(b, h), a.dout.ss, qrow, Sq, g);
   if (a.neg) {
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) qf[c] = neg8(qf[c]);
   }
-  const int qc = min(qrow, S - 1);
-  const float l2 = qrow < S ? a.lse[(int64_t)bh * S + qc] * kLog2e : kPosInf;
-  const float dl = qrow < S ? a.delta[(int64_t)bh * S + qc] : 0.0f;
+  const int qc = min(qrow, Sq - 1);
+  const float l2 = qrow < Sq ? a.lse[(int64_t)bh * Sq + qc] * kLog2e : kPosInf;
+  const float dl = qrow < Sq ? a.delta[(int64_t)bh * Sq + qc] : 0.0f;
 
   floatx16 dq[D / 32];
 #pragma unroll
@@ -539,9 +515,10 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
   DsScale sc;
   float shift = -l2;   // exponent offset: e - LSE * log2(e)
 
-  int kv_end = S;
-  if (CAUSAL) kv_end = min(S, q0 + BM);
-  const int n_tiles = (kv_end + BN - 1) / BN;
+  int kv_end = Sk;
+  if (CAUSAL) kv_end = min(Sk, q0 + BM + off);
+  // 0 when every query of the block precedes every key (causal, Sq > Sk)
+  const int n_tiles = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
   const float c = a.c;
 
   // K and V tiles go straight to LDS (fa_common.hpp DmaStager).
@@ -549,8 +526,8 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
   stk.init(w, lane, a.k.ss);
   stv.init(w, lane, a.v.ss);
   auto load_tile = [&](int n0, auto stc) {
-    stk.load(k_st(stc), kb, a.k.ss, n0, S, w);
-    stv.load(v_st(stc), vb, a.v.ss, n0, S, w);
+    stk.load(k_st(stc), kb, a.k.ss, n0, Sk, w);
+    stv.load(v_st(stc), vb, a.v.ss, n0, Sk, w);
   };
 
   // Per-lane LDS element offsets inside a stage (as in the dK/dV kernel):
@@ -570,7 +547,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
   }
 
   __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): Q/dO fragments, LSE, delta resident
-  load_tile(0, std::integral_constant<int, 0>{});
+  if (n_tiles > 0) load_tile(0, std::integral_constant<int, 0>{});
   __builtin_amdgcn_s_waitcnt(0x0f70);
   __syncthreads();
 
@@ -584,8 +561,8 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
     for (int sb = 0; sb < NSUB; ++sb) {
       const int ks = NSUB * kh + sb;   // 32-key sub-block of the tile
       const int ns = n0 + 32 * ks;
-      if (CAUSAL && ns > wq0 + 31) continue;
-      if (ns >= S) continue;
+      if (CAUSAL && ns > wq0 + 31 + off) continue;
+      if (ns >= Sk) continue;
       floatx16 sacc, dpacc;
       {
         const f16 *kr = k_st(stc) + 32 * ks * D;
@@ -599,11 +576,11 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
         }
       }
       // invisible scores -> -inf (P = 0), diagonal / ragged sub-blocks only
-      if ((CAUSAL && ns + 31 > wq0) || (ns + 31 >= S)) {
+      if ((CAUSAL && ns + 31 > wq0 + off) || (ns + 31 >= Sk)) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int n = ns + slot_row(i, g);
-          const bool vis = n < S && (!CAUSAL || n <= qrow);
+          const bool vis = n < Sk && (!CAUSAL || n <= qrow + off);
           sacc[i] = vis ? sacc[i] : kNegInf;
         }
       }
@@ -657,7 +634,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
     if (kh == 1) return;
     dq_mul = a.sm_scale;
   }
-  if (qrow < S)
+  if (qrow < Sq)
     store_row_fp16<D>(a.dq + b * a.dq_sb + h * a.dq_sh + (int64_t)qrow * a.dq_ss, dq, dq_mul, g);
 }
 

@@ -121,29 +121,6 @@ __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, int byte_o
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
 }
 
-// A-operand (32 x 16) fragment of X^T read from a row-major LDS tile X with
-// two ds_read_b64_tr_b16 transpose loads.  The lane receives
-//   X[row_lo + j][col0 + lane % 32]      for j = 0..3 (slots 0..3),
-//   X[row_hi + j - 4][col0 + lane % 32]  for j = 4..7 (slots 4..7),
-// where row_lo / row_hi are this lane group's (lane / 32) 4-row bases.
-// Transpose-load lane layout (measured on gfx950): in each 16-lane group,
-// source lane L addresses row L/4, columns 4*(L%4) .. +3 of a 4 x 16 block,
-// and lane i receives column i of the four rows.
-template <int STRIDE>
-__device__ __forceinline__ half8 load_tr8(const f16 *tile, int row_lo, int row_hi, int col0, int lane) {
-  const int l16 = lane & 15;
-  const int col = col0 + 16 * ((lane >> 4) & 1) + 4 * (l16 & 3);
-  typedef __fp16 h4 __attribute__((vector_size(8)));
-  const f16 *plo = tile + (row_lo + (l16 >> 2)) * STRIDE + col;
-  const f16 *phi = tile + (row_hi + (l16 >> 2)) * STRIDE + col;
-  h4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) h4 *)plo);
-  h4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) h4 *)phi);
-  half8 r;
-  r[0] = (f16)lo[0]; r[1] = (f16)lo[1]; r[2] = (f16)lo[2]; r[3] = (f16)lo[3];
-  r[4] = (f16)hi[0]; r[5] = (f16)hi[1]; r[6] = (f16)hi[2]; r[7] = (f16)hi[3];
-  return r;
-}
-
 // LDS row holding in-tile row r when 32-row blocks are stored in kperm order
 // (kperm swaps bits 2 and 3, so it is its own inverse).
 __device__ __forceinline__ int kperm_row(int r) { return (r & ~31) + kperm(r & 31); }
@@ -221,9 +198,14 @@ struct DmaStager {
   }
 };
 
-// Two ds_read_b64_tr_b16 at `p` and `p + hi` (elements): the A-operand
-// fragment whose slots 0..3 come from the 4-row block at p and 4..7 from the
-// block `hi` elements further (lane addresses precomputed by the caller).
+// A-operand (32 x 16) fragment of X^T from a row-major LDS tile X with two
+// ds_read_b64_tr_b16 transpose loads, at `p` and `p + hi` (elements).
+// Transpose-load lane layout (measured on gfx950): in each 16-lane group,
+// source lane L addresses row L/4, columns 4*(L%4) .. +3 of a 4 x 16 block,
+// and lane i receives column i of the four rows.  So with p = the lane's
+// address of (row_lo + L/4, col0 + 16*((lane/16)%2) + 4*(L%4)) the lane
+// receives X[row_lo + j][col0 + lane % 32] in slots j = 0..3, and from the
+// block `hi` elements further the slots 4..7 (callers precompute p).
 __device__ __forceinline__ half8 load_tr_pair(const f16 *p, int hi) {
   typedef __fp16 h4 __attribute__((vector_size(8)));
   h4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) h4 *)p);

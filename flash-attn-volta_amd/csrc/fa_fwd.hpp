@@ -31,7 +31,7 @@
 //     well inside fp16, and the final O and LSE use the same max, so the
 //     result is exact either way;
 //   * the tile loads use raw buffer descriptors whose extent ends at row
-//     S-1, so rows past the end read as zeros without any branch (they only
+//     Sk-1, so rows past the end read as zeros without any branch (they only
 //     ever meet -inf scores); the Q row index is clamped (never stored).
 #pragma once
 
@@ -42,11 +42,13 @@ namespace fa {
 constexpr float kRescaleLog2 = 8.0f;
 
 struct FwdArgs {
-  TensorDesc q, k, v;
-  f16 *o;
+  TensorDesc q, k, v;  // q: (B, Sq, H, D); k, v: (B, Sk, Hk, D)
+  f16 *o;              // (B, Sq, H, D)
   int64_t o_sb, o_ss, o_sh;
-  float *lse;          // (B, H, S) or nullptr
-  int B, S, H;
+  float *lse;          // (B, H, Sq) or nullptr
+  int B, Sq, Sk, H;
+  int grp;             // query heads per key/value head (H / Hk)
+  int off;             // causal: query i sees keys j <= i + off (off = Sk - Sq)
   int n_qtiles;
   float c;             // |sm_scale| * log2(e), clamped away from 0
   int neg;             // 1 when sm_scale < 0: Q is negated on load
@@ -96,7 +98,7 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   auto k_sl = [&](auto sc) -> f16 * { return decltype(sc)::value ? sk1 : sk0; };
   auto v_sl = [&](auto sc) -> f16 * { return decltype(sc)::value ? sv1 : sv0; };
 
-  const int S = a.S;
+  const int Sq = a.Sq, Sk = a.Sk, off = a.off;
   const int BH = a.B * a.H;
   const int bid = blockIdx.x;
   const int bh = bid % BH;
@@ -105,6 +107,7 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   // share its L2.
   const int qt = CAUSAL ? a.n_qtiles - 1 - zigzag_rank(bid / BH, a.n_qtiles) : bid / BH;
   const int b = bh / a.H, h = bh % a.H;
+  const int hk = h / a.grp;       // key/value head of this query head
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = wave_id();
   const int qg = KSPLIT == 2 ? (w >> 1) : w;
@@ -115,20 +118,21 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   const int qrow = wq0 + l32;     // query owned by this lane
 
   const f16 *qb = a.q.head(b, h);
-  const f16 *kb = a.k.head(b, h);
-  const f16 *vb = a.v.head(b, h);
+  const f16 *kb = a.k.head(b, hk);
+  const f16 *vb = a.v.head(b, hk);
 
-  int kv_end = S;
-  if (CAUSAL) kv_end = min(S, q0 + BM);
-  const int n_tiles = (kv_end + BN - 1) / BN;   // >= 1
+  int kv_end = Sk;
+  if (CAUSAL) kv_end = min(Sk, q0 + BM + off);
+  // 0 when every query of the block precedes every key (causal, Sq > Sk)
+  const int n_tiles = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
 
   // ---- K and V tiles go straight to LDS (fa_common.hpp DmaStager): both
-  // in kperm row order, chunks swizzled; rows past S read as zeros.
+  // in kperm row order, chunks swizzled; rows past Sk read as zeros.
   DmaStager<D> stk, stv;
   stk.init(w, lane, a.k.ss);
   stv.init(w, lane, a.v.ss);
-  auto load_k = [&](int n0, auto sc) { stk.load(k_sl(sc), kb, a.k.ss, n0, S, w); };
-  auto load_v = [&](int n0, auto sc) { stv.load(v_sl(sc), vb, a.v.ss, n0, S, w); };
+  auto load_k = [&](int n0, auto sc) { stk.load(k_sl(sc), kb, a.k.ss, n0, Sk, w); };
+  auto load_v = [&](int n0, auto sc) { stv.load(v_sl(sc), vb, a.v.ss, n0, Sk, w); };
 
   // Per-lane LDS element offsets inside a slot: K rows l32 (A operand of
   // S^T = K Q^T), chunk 2cc + g; V^T transpose reads of rows 4g + (l16 >> 2)
@@ -148,9 +152,9 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
 
   // Sub-block sb (32 keys) of this wave in the tile at n0 starts at key
   // n0 + 32 * (NSUB * kh + sb); it is dead when it lies entirely above the
-  // wave's causal diagonal.
+  // wave's causal diagonal (the last key its last query sees is wq0+31+off).
   auto sub_key = [&](int n0, int sb) { return n0 + 32 * (NSUB * kh + sb); };
-  auto dead = [&](int n0, int sb) { return CAUSAL && sub_key(n0, sb) > wq0 + 31; };
+  auto dead = [&](int n0, int sb) { return CAUSAL && sub_key(n0, sb) > wq0 + 31 + off; };
 
   // ---- S^T = K Q^T for this wave's sub-blocks of a tile
   half8 qf[D / 16];
@@ -170,11 +174,13 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   using C0 = std::integral_constant<int, 0>;
   using C1 = std::integral_constant<int, 1>;
   // ---- prologue: K(0), V(0) -> slot 0, K(1) -> K slot 1
-  load_k(0, C0{});
-  load_v(0, C0{});
+  if (n_tiles > 0) {
+    load_k(0, C0{});
+    load_v(0, C0{});
+  }
   if (n_tiles > 1) load_k(BN, C1{});
   {
-    const int qr = min(qrow, S - 1);
+    const int qr = min(qrow, Sq - 1);
     const f16 *qp = qb + (int64_t)qr * a.q.ss + 8 * g;
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) qf[c] = *(const half8 *)(qp + 16 * c);
@@ -193,7 +199,7 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   // tile, which would wait for the next tile's S MFMAs right after issuing
   // them): tile t's scores live in s_a when t is even, s_b when odd.
   floatx16 s_a[NSUB], s_b[NSUB];
-  qk(C0{}, 0, s_a);
+  if (n_tiles > 0) qk(C0{}, 0, s_a);
   // K slot 0 is refilled with K(2) at the start of the first iteration
   __syncthreads();
 
@@ -223,11 +229,11 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int sb = 0; sb < NSUB; ++sb) {
         const int ns = sub_key(n0, sb);
-        if ((CAUSAL && ns + 31 > wq0) || (ns + 31 >= S)) {
+        if ((CAUSAL && ns + 31 > wq0 + off) || (ns + 31 >= Sk)) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const int key = ns + slot_row(i, g);
-            const bool vis = key < S && (!CAUSAL || key <= qrow);
+            const bool vis = key < Sk && (!CAUSAL || key <= qrow + off);
             s_cur[sb][i] = vis ? s_cur[sb][i] : kNegInf;
           }
         }
@@ -319,7 +325,7 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   // ---- epilogue: O = acc / l, LSE = (m + log2 l) * ln2
   const float l_tot = l_run + xor32(l_run);
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  if (qrow < S) {
+  if (qrow < Sq) {
     f16 *orow = a.o + b * a.o_sb + h * a.o_sh + (int64_t)qrow * a.o_ss;
 #pragma unroll
     for (int d = 0; d < D / 32; ++d) {
@@ -333,7 +339,7 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
     }
     if (a.lse != nullptr && g == 0) {
       const float lse = l_tot > 0.0f ? (m_run + fast_log2(l_tot)) * kLn2 : kPosInf;
-      a.lse[(int64_t)bh * S + qrow] = lse;
+      a.lse[(int64_t)bh * Sq + qrow] = lse;
     }
   }
 }

@@ -14,16 +14,25 @@ Public API:
                         causal=False, sm_scale=None)     -> (dq, dk, dv)
 
 q, k, v, out: (batch, seq, n_heads, head_dim) fp16; lse: (B, H, N) fp32.
+
+Beyond the reference (its wrapper requires q, k, v of one shape):
+    flash_attn_forward_gqa / flash_attn_backward_gqa / flash_attn_gqa
+        grouped-query and multi-query attention, k and v (B, Sk, Hk, D)
+        with H a multiple of Hk, and Sq != Sk with a bottom-right causal
+        mask (KV-cache prefill continuation).
 """
 
-from .forward import flash_attn_forward, flash_attn_volta
-from .backward import flash_attn_backward
-from .autograd import flash_attn
+from .forward import flash_attn_forward, flash_attn_forward_gqa, flash_attn_volta
+from .backward import flash_attn_backward, flash_attn_backward_gqa
+from .autograd import flash_attn, flash_attn_gqa
 
 __all__ = [
     "flash_attn_forward",
     "flash_attn_volta",
     "flash_attn_backward",
     "flash_attn",
+    "flash_attn_forward_gqa",
+    "flash_attn_backward_gqa",
+    "flash_attn_gqa",
 ]
-__version__ = "0.2.0"
+__version__ = "0.3.0"

@@ -14,7 +14,7 @@ import threading
 LIB_NAME = "libfa_mi355x.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # status codes (enum fa_status)
 FA_OK = 0
@@ -33,9 +33,11 @@ EXPORTED_SYMBOLS = (
     "fa_abi_version",
     "fa_strerror",
     "fa_fwd",
+    "fa_fwd_gqa",
     "fa_bwd_preprocess",
     "fa_bwd_workspace_bytes",
     "fa_bwd",
+    "fa_bwd_gqa",
     "fa_bwd_dkdv",
     "fa_bwd_dq",
 )
@@ -69,6 +71,10 @@ def _declare(lib):
     lib.fa_fwd.argtypes = [_vp, _vp, _vp, _vp, _vp, _ci, _ci, _ci, _ci,
                            _i64x4, _i64x4, _i64x4, _i64x4,
                            ctypes.c_float, _ci, _vp]
+    lib.fa_fwd_gqa.restype = _ci
+    lib.fa_fwd_gqa.argtypes = [_vp, _vp, _vp, _vp, _vp, _ci, _ci, _ci, _ci, _ci, _ci,
+                               _i64x4, _i64x4, _i64x4, _i64x4,
+                               ctypes.c_float, _ci, _vp]
     lib.fa_bwd_preprocess.restype = _ci
     lib.fa_bwd_preprocess.argtypes = [_vp, _vp, _vp, _ci, _ci, _ci, _ci, _i64x4, _i64x4, _vp]
     lib.fa_bwd_workspace_bytes.restype = ctypes.c_size_t
@@ -81,6 +87,14 @@ def _declare(lib):
                            _i64x4, _i64x4, _i64x4, _i64x4,
                            _i64x4, _i64x4, _i64x4, _i64x4,
                            ctypes.c_float, _ci, _vp]
+    lib.fa_bwd_gqa.restype = _ci
+    lib.fa_bwd_gqa.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp,
+                               _vp, _vp, _vp,
+                               _vp, ctypes.c_size_t,
+                               _ci, _ci, _ci, _ci, _ci, _ci,
+                               _i64x4, _i64x4, _i64x4, _i64x4,
+                               _i64x4, _i64x4, _i64x4, _i64x4,
+                               ctypes.c_float, _ci, _vp]
     lib.fa_bwd_dkdv.restype = _ci
     lib.fa_bwd_dkdv.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                 _ci, _ci, _ci, _ci,

@@ -14,8 +14,8 @@ import math
 import torch
 
 from . import _capi
-from .forward import (NATIVE_HEAD_DIMS, SUPPORTED_HEAD_DIMS, _kernel_ready, _on_device, _pad_d,
-                      _require, _stream_ptr, kernel_strides)
+from .forward import (NATIVE_HEAD_DIMS, SUPPORTED_HEAD_DIMS, _check_gqa, _kernel_ready, _on_device,
+                      _pad_d, _require, _stream_ptr, kernel_strides)
 
 
 def flash_attn_backward(
@@ -52,36 +52,79 @@ def flash_attn_backward(
 
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(D)
+    return _backward(do, q, k, v, o, lse, causal, sm_scale, gqa=False)
 
+
+def _backward(do, q, k, v, o, lse, causal, sm_scale, gqa):
+    D = q.shape[-1]
     if D not in NATIVE_HEAD_DIMS:
         dq, dk, dv = _run_bwd(_pad_d(do, 32), _pad_d(q, 32), _pad_d(k, 32), _pad_d(v, 32),
-                              _pad_d(o, 32), lse, causal, sm_scale)
+                              _pad_d(o, 32), lse, causal, sm_scale, gqa)
         return dq[..., :D].contiguous(), dk[..., :D].contiguous(), dv[..., :D].contiguous()
-    return _run_bwd(do, q, k, v, o, lse, causal, sm_scale)
+    return _run_bwd(do, q, k, v, o, lse, causal, sm_scale, gqa)
 
 
-def _run_bwd(do, q, k, v, o, lse, causal, sm_scale):
+def _run_bwd(do, q, k, v, o, lse, causal, sm_scale, gqa):
     lib = _capi.load()
     B, N, H, D = q.shape
+    Sk, Hk = k.shape[1], k.shape[2]
     do, q, k, v, o = (_kernel_ready(t) for t in (do, q, k, v, o))
     lse = lse.contiguous()
     dq = torch.empty((B, N, H, D), dtype=torch.float16, device=q.device)
-    dk = torch.empty_like(dq)
-    dv = torch.empty_like(dq)
-    if dq.numel() == 0:
+    dk = torch.empty((B, Sk, Hk, D), dtype=torch.float16, device=q.device)
+    dv = torch.empty_like(dk)
+    if dq.numel() == 0 or dk.numel() == 0:
+        # nothing attends to anything: every gradient is zero
+        for t in (dq, dk, dv):
+            t.zero_()
         return dq, dk, dv
     ws_bytes = lib.fa_bwd_workspace_bytes(B, N, H, D)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
-    sg = kernel_strides(dq)
+    sq_, sk_ = kernel_strides(dq), kernel_strides(dk)
+    st = (kernel_strides(do), kernel_strides(q), kernel_strides(k), kernel_strides(v),
+          kernel_strides(o), sq_, sk_, sk_)
     with _on_device(q.device):
-        rc = lib.fa_bwd(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-                        lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-                        ws.data_ptr(), ws_bytes, B, N, H, D,
-                        kernel_strides(do), kernel_strides(q), kernel_strides(k), kernel_strides(v),
-                        kernel_strides(o), sg, sg, sg,
-                        float(sm_scale), int(bool(causal)), _stream_ptr(q.device))
-    _capi.check(rc, "fa_bwd")
+        if gqa:
+            rc = lib.fa_bwd_gqa(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                o.data_ptr(), lse.data_ptr(), dq.data_ptr(), dk.data_ptr(),
+                                dv.data_ptr(), ws.data_ptr(), ws_bytes, B, N, Sk, H, Hk, D, *st,
+                                float(sm_scale), int(bool(causal)), _stream_ptr(q.device))
+        else:
+            rc = lib.fa_bwd(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                            lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                            ws.data_ptr(), ws_bytes, B, N, H, D, *st,
+                            float(sm_scale), int(bool(causal)), _stream_ptr(q.device))
+    _capi.check(rc, "fa_bwd_gqa" if gqa else "fa_bwd")
     return dq, dk, dv
+
+
+def flash_attn_backward_gqa(
+    do: torch.Tensor,
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    o: torch.Tensor,
+    lse: torch.Tensor,
+    causal: bool = False,
+    sm_scale: float | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Backward of ``flash_attn_forward_gqa`` (no counterpart in the
+    reference).  do, q, o: (B, Sq, H, D); k, v: (B, Sk, Hk, D); lse:
+    (B, H, Sq).  Returns dq (B, Sq, H, D) and dk, dv (B, Sk, Hk, D), the
+    latter summed over the query heads that share each key/value head."""
+    _require(q.is_cuda and k.is_cuda and v.is_cuda and o.is_cuda and do.is_cuda,
+             "tensors must be on CUDA")
+    _require(q.dtype == torch.float16 == k.dtype == v.dtype == o.dtype == do.dtype, "fp16 only")
+    _require(lse.dtype == torch.float32, "lse must be fp32")
+    _check_gqa(q, k, v)
+    _require(q.shape == o.shape == do.shape, "q, o and do shapes differ")
+    B, N, H, D = q.shape
+    _require(D in SUPPORTED_HEAD_DIMS, f"unsupported head_dim {D}")
+    _require(tuple(lse.shape) == (B, H, N), f"lse shape {tuple(lse.shape)} expected ({B},{H},{N})")
+    _require(lse.is_cuda and lse.device == q.device, "lse must be on the same device")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    return _backward(do, q, k, v, o, lse, causal, sm_scale, gqa=True)
 
 
 def bwd_preprocess(o: torch.Tensor, do: torch.Tensor) -> torch.Tensor:

@@ -123,35 +123,94 @@ def flash_attn_forward(
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(D)
 
+    return _forward(q, k, v, causal, sm_scale, return_softmax_lse, gqa=False)
+
+
+def _forward(q, k, v, causal, sm_scale, return_softmax_lse, gqa):
+    D = q.shape[-1]
     if D not in NATIVE_HEAD_DIMS:
         out, lse = _run_fwd(_pad_d(q, 32), _pad_d(k, 32), _pad_d(v, 32), causal, sm_scale,
-                            return_softmax_lse)
+                            return_softmax_lse, gqa)
         out = out[..., :D].contiguous()
     else:
-        out, lse = _run_fwd(q, k, v, causal, sm_scale, return_softmax_lse)
+        out, lse = _run_fwd(q, k, v, causal, sm_scale, return_softmax_lse, gqa)
     if return_softmax_lse:
         return out, lse
     return out
 
 
-def _run_fwd(q, k, v, causal, sm_scale, write_lse):
+def _run_fwd(q, k, v, causal, sm_scale, write_lse, gqa):
     lib = _capi.load()
     B, N, H, D = q.shape
+    Sk, Hk = k.shape[1], k.shape[2]
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     out = torch.empty((B, N, H, D), dtype=torch.float16, device=q.device)
     lse = torch.empty((B, H, N), dtype=torch.float32, device=q.device) if write_lse else None
-    if out.numel() == 0:
+    if out.numel() == 0 or Sk == 0:
+        # no query, or no key: every row sees nothing (O = 0, LSE = +inf)
+        out.zero_()
         if lse is not None:
             lse.fill_(float("inf"))
         return out, lse
+    st = (kernel_strides(q), kernel_strides(k), kernel_strides(v), kernel_strides(out))
+    lse_ptr = lse.data_ptr() if lse is not None else None
     with _on_device(q.device):
-        rc = lib.fa_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-                        lse.data_ptr() if lse is not None else None,
-                        B, N, H, D,
-                        kernel_strides(q), kernel_strides(k), kernel_strides(v), kernel_strides(out),
-                        float(sm_scale), int(bool(causal)), _stream_ptr(q.device))
-    _capi.check(rc, "fa_fwd")
+        if gqa:
+            rc = lib.fa_fwd_gqa(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse_ptr,
+                                B, N, Sk, H, Hk, D, *st,
+                                float(sm_scale), int(bool(causal)), _stream_ptr(q.device))
+        else:
+            rc = lib.fa_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse_ptr,
+                            B, N, H, D, *st,
+                            float(sm_scale), int(bool(causal)), _stream_ptr(q.device))
+    _capi.check(rc, "fa_fwd_gqa" if gqa else "fa_fwd")
     return out, lse
+
+
+def _check_gqa(q, k, v):
+    """Shape rules of the grouped-query entry points: q (B, Sq, H, D),
+    k and v (B, Sk, Hk, D) with H a multiple of Hk."""
+    _require(q.dim() == 4 and k.dim() == 4 and v.dim() == 4,
+             f"expected 4-D (B, N, H, D) tensors, got {tuple(q.shape)} {tuple(k.shape)} {tuple(v.shape)}")
+    _require(k.shape == v.shape, f"k and v shapes differ: {tuple(k.shape)} {tuple(v.shape)}")
+    _require(q.shape[0] == k.shape[0], f"batch mismatch {q.shape[0]} vs {k.shape[0]}")
+    _require(q.shape[3] == k.shape[3], f"head_dim mismatch {q.shape[3]} vs {k.shape[3]}")
+    H, Hk = q.shape[2], k.shape[2]
+    _require(Hk > 0 and H % Hk == 0,
+             f"query heads ({H}) must be a multiple of key/value heads ({Hk})")
+
+
+def flash_attn_forward_gqa(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    causal: bool = False,
+    sm_scale: float | None = None,
+    return_softmax_lse: bool = False,
+):
+    """Grouped-query / multi-query attention forward with independent query
+    and key lengths (no counterpart in the reference; it removes the
+    repeat_kv copy and the KV-cache fallback of the reference's HF patch,
+    flash_attn_volta/patch_hf.py:145-162, 186-188).
+
+    Args:
+        q: (B, Sq, H, D) fp16 on the GPU; k, v: (B, Sk, Hk, D) fp16 with H a
+            multiple of Hk.  Query head h uses key/value head h // (H // Hk),
+            the head order of HuggingFace's ``repeat_kv``.
+        causal: bottom-right aligned mask: query i sees key j iff
+            j <= i + Sk - Sq (a query with no visible key gets 0 output and
+            +inf LSE).  With Sq == Sk it is the usual causal mask.
+        sm_scale, return_softmax_lse: as in ``flash_attn_forward``.
+    """
+    _require(q.is_cuda and k.is_cuda and v.is_cuda, "tensors must be on CUDA")
+    _require(q.dtype == torch.float16 == k.dtype == v.dtype, "fp16 only")
+    _require(q.device == k.device == v.device, "q, k, v must be on one device")
+    _check_gqa(q, k, v)
+    D = q.shape[3]
+    _require(D in SUPPORTED_HEAD_DIMS, f"unsupported head_dim {D} (allowed: 16,32,64,128)")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    return _forward(q, k, v, causal, sm_scale, return_softmax_lse, gqa=True)
 
 
 # Public alias (reference: triton_fa.py:401)

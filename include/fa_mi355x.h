@@ -28,13 +28,14 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 1
+#define FA_ABI_VERSION 2
 
 enum fa_status {
   FA_OK = 0,
   FA_ERR_NULL_POINTER = -1,   /* a required pointer is NULL                 */
   FA_ERR_HEAD_DIM = -2,       /* D not in {32, 64, 128}                     */
-  FA_ERR_SHAPE = -3,          /* B, S or H <= 0                             */
+  FA_ERR_SHAPE = -3,          /* B, a sequence length or a head count <= 0,
+                                 or H not a multiple of Hk                  */
   FA_ERR_STRIDE = -4,         /* D stride != 1, or a stride not a multiple
                                  of 8 elements (16-byte vector access)      */
   FA_ERR_ALIGNMENT = -5,      /* a base pointer not 16-byte aligned         */
@@ -68,6 +69,29 @@ int fa_fwd(const void *q, const void *k, const void *v, void *o, float *lse,
            float sm_scale, int causal, void *stream);
 
 /*
+ * Grouped-query / multi-query attention with separate query and key
+ * lengths: q, o are (B, Sq, H, D); k, v are (B, Sk, Hk, D) with H a
+ * multiple of Hk, and query head h attends with key/value head
+ * h / (H / Hk) (the head order of HuggingFace's repeat_kv); lse is
+ * (B, H, Sq).  `causal` aligns the mask to the bottom right: query i sees
+ * key j iff j <= i + (Sk - Sq), so the last query sees every key (the
+ * KV-cache / chunked-prefill convention); a query that sees no key gets
+ * o = 0 and lse = +inf.  With Sq == Sk and Hk == H it is fa_fwd.
+ *
+ * No counterpart in the reference kernels, whose wrapper asserts equal
+ * q/k/v shapes (flash_attn_volta/triton_fa.py:315); it replaces the
+ * repeat_kv expansion of K/V the reference's HuggingFace patch does before
+ * calling them (flash_attn_volta/patch_hf.py:186-188, 470-471) and that
+ * patch's fallback to the original attention when a KV cache makes
+ * q_len != kv_len (patch_hf.py:145-162).
+ */
+int fa_fwd_gqa(const void *q, const void *k, const void *v, void *o, float *lse,
+               int B, int Sq, int Sk, int H, int Hk, int D,
+               const int64_t q_strides[4], const int64_t k_strides[4],
+               const int64_t v_strides[4], const int64_t o_strides[4],
+               float sm_scale, int causal, void *stream);
+
+/*
  * Backward pre-pass: delta[b,h,s] = sum_d o[b,s,h,d] * do[b,s,h,d] in fp32.
  * Replaces the torch expression at flash_attn_volta/triton_fa_bwd.py:649-650.
  */
@@ -99,6 +123,28 @@ int fa_bwd(const void *dout, const void *q, const void *k, const void *v,
            const int64_t o_strides[4], const int64_t dq_strides[4],
            const int64_t dk_strides[4], const int64_t dv_strides[4],
            float sm_scale, int causal, void *stream);
+
+/*
+ * Backward of fa_fwd_gqa: dq is (B, Sq, H, D), dk and dv are (B, Sk, Hk, D)
+ * and hold the sums over the H / Hk query heads that share each key/value
+ * head (computed in the kernel, in a fixed order: still bit-reproducible).
+ * The workspace is fa_bwd_workspace_bytes(B, Sq, H, D).  Same masking
+ * convention as fa_fwd_gqa; with Sq == Sk and Hk == H it is fa_bwd.
+ *
+ * No counterpart in the reference kernels (see fa_fwd_gqa); it replaces
+ * autograd through the reference patch's repeat_kv
+ * (flash_attn_volta/patch_hf.py:186-188, 470-471).
+ */
+int fa_bwd_gqa(const void *dout, const void *q, const void *k, const void *v,
+               const void *o, const float *lse,
+               void *dq, void *dk, void *dv,
+               void *workspace, size_t workspace_bytes,
+               int B, int Sq, int Sk, int H, int Hk, int D,
+               const int64_t do_strides[4], const int64_t q_strides[4],
+               const int64_t k_strides[4], const int64_t v_strides[4],
+               const int64_t o_strides[4], const int64_t dq_strides[4],
+               const int64_t dk_strides[4], const int64_t dv_strides[4],
+               float sm_scale, int causal, void *stream);
 
 /*
  * The two main backward kernels as separate steps (fa_bwd runs

@@ -22,6 +22,13 @@ It restates, from the mathematics, what the reference computes:
 * ``attention_ref_fp32`` -- the reference's float32 eager CPU path
   (ref.py:9-36) restated in torch; this is the CPU baseline bench.py times.
 * ``make_inputs`` -- the seeded fp16 inputs every test and bench uses.
+* ``attention_fwd_gqa`` / ``attention_bwd_gqa`` / ``make_inputs_gqa`` --
+  the same mathematics for grouped-query attention with separate query and
+  key lengths (q (B,Sq,H,D), k and v (B,Sk,Hk,D), query head h reading
+  key/value head h // (H // Hk), the head order of the repeat_kv the
+  reference's HF patch applies, patch_hf.py:186-188), causal mask aligned
+  bottom-right (query i sees keys j <= i + Sk - Sq).  The reference kernels
+  have no such mode (triton_fa.py:315 asserts equal shapes).
 
 How each function is pinned (tests/test_oracle.py):
   attention_fwd : golden vectors written by torch's float64
@@ -32,6 +39,14 @@ How each function is pinned (tests/test_oracle.py):
   attention_bwd : golden vectors from torch float64 autograd, the C brute
                   force, and central finite differences of attention_fwd.
   attention_ref_fp32 : agreement with attention_fwd to fp32 rounding.
+  attention_fwd_gqa / attention_bwd_gqa : golden vectors from torch's
+                  float64 SDPA (enable_gqa, explicit bottom-right mask) and
+                  autograd; reduction identities to the pinned square
+                  functions (GQA == attention over repeat_kv-expanded K/V
+                  with dK/dV summed over each group; Sq < Sk == the last Sq
+                  rows of a square causal problem; Sq > Sk == empty rows
+                  then a square causal problem); planted head-mapping and
+                  mask-alignment mistakes that these checks catch.
 """
 from __future__ import annotations
 
@@ -41,7 +56,8 @@ from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 
-__all__ = ["make_inputs", "attention_fwd", "attention_bwd", "attention_ref_fp32"]
+__all__ = ["make_inputs", "attention_fwd", "attention_bwd", "attention_ref_fp32",
+           "make_inputs_gqa", "attention_fwd_gqa", "attention_bwd_gqa"]
 
 
 def make_inputs(B: int, S: int, H: int, D: int, seed: int = 0, scale: float = 1.0,
@@ -71,6 +87,23 @@ def make_inputs(B: int, S: int, H: int, D: int, seed: int = 0, scale: float = 1.
     return q, k, v, do
 
 
+def make_inputs_gqa(B: int, Sq: int, Sk: int, H: int, Hk: int, D: int, seed: int = 0,
+                    scale: float = 1.0):
+    """Seeded fp16 inputs for the grouped-query functions: q (B,Sq,H,D),
+    k and v (B,Sk,Hk,D) from ``Generator('cpu').manual_seed(seed)`` (randn
+    fp32 -> fp16, times ``scale``), dO (B,Sq,H,D) from seed + 1."""
+    import torch
+    gen = torch.Generator("cpu").manual_seed(seed)
+    q = torch.randn((B, Sq, H, D), generator=gen, dtype=torch.float32).half()
+    k = torch.randn((B, Sk, Hk, D), generator=gen, dtype=torch.float32).half()
+    v = torch.randn((B, Sk, Hk, D), generator=gen, dtype=torch.float32).half()
+    gen2 = torch.Generator("cpu").manual_seed(seed + 1)
+    do = torch.randn((B, Sq, H, D), generator=gen2, dtype=torch.float32).half()
+    if scale != 1.0:
+        q, k, v, do = q * scale, k * scale, v * scale, do * scale
+    return q, k, v, do
+
+
 def _np64(x) -> np.ndarray:
     if hasattr(x, "detach"):
         x = x.detach().cpu().double().numpy()
@@ -80,28 +113,32 @@ def _np64(x) -> np.ndarray:
 _UPPER = {}
 
 
-def _upper(n: int) -> np.ndarray:
-    """Boolean strict upper triangle (j > i) of an n x n score matrix."""
-    m = _UPPER.get(n)
+def _upper(n: int, nk: int | None = None, off: int = 0) -> np.ndarray:
+    """Boolean mask of the causally hidden scores (j > i + off) of an
+    n x nk score matrix; n x n with off = 0 is the strict upper triangle."""
+    nk = n if nk is None else nk
+    key = (n, nk, off)
+    m = _UPPER.get(key)
     if m is None:
-        m = np.triu(np.ones((n, n), dtype=bool), k=1)
+        m = np.triu(np.ones((n, nk), dtype=bool), k=1 + off)
         _UPPER.clear()
-        _UPPER[n] = m
+        _UPPER[key] = m
     return m
 
 
-def _scores(qh, kh, sm_scale, causal):
-    """sm_scale * q k^T for one (b, h), with the causal strict upper
-    triangle set to -inf (ref.py:25-31)."""
+def _scores(qh, kh, sm_scale, causal, off: int = 0):
+    """sm_scale * q k^T for one (b, h), with the causally hidden scores
+    (key j > query i + off; off = 0 is ref.py:25-31's strict upper
+    triangle) set to -inf."""
     s = qh @ kh.T
     s *= sm_scale
     if causal:
-        np.putmask(s, _upper(s.shape[0]), -np.inf)
+        np.putmask(s, _upper(s.shape[0], s.shape[1], off), -np.inf)
     return s
 
 
-def _fwd_head(qh, kh, vh, sm_scale, causal):
-    s = _scores(qh, kh, sm_scale, causal)
+def _fwd_head(qh, kh, vh, sm_scale, causal, off: int = 0):
+    s = _scores(qh, kh, sm_scale, causal, off)
     m = s.max(axis=1, keepdims=True)
     empty = ~np.isfinite(m[:, 0])
     m_safe = np.where(np.isfinite(m), m, 0.0)
@@ -144,8 +181,8 @@ def attention_fwd(q, k, v, causal: bool = False, sm_scale: float | None = None):
     return o, lse
 
 
-def _bwd_head(qh, kh, vh, doh, oh, sm_scale, causal):
-    s = _scores(qh, kh, sm_scale, causal)
+def _bwd_head(qh, kh, vh, doh, oh, sm_scale, causal, off: int = 0):
+    s = _scores(qh, kh, sm_scale, causal, off)
     m = s.max(axis=1, keepdims=True)
     m = np.where(np.isfinite(m), m, 0.0)
     s -= m
@@ -184,6 +221,56 @@ def attention_bwd(do, q, k, v, causal: bool = False, sm_scale: float | None = No
                                             o[b, :, h], sm_scale, causal), B, H)
     for (b, h), (gq, gk, gv, dl) in zip([(b, h) for b in range(B) for h in range(H)], res):
         dq[b, :, h], dk[b, :, h], dv[b, :, h], delta[b, h] = gq, gk, gv, dl
+    return dq, dk, dv, delta
+
+
+def attention_fwd_gqa(q, k, v, causal: bool = False, sm_scale: float | None = None):
+    """float64 grouped-query attention: q (B,Sq,H,D), k and v (B,Sk,Hk,D).
+    Query head h reads key/value head h // (H // Hk); causal hides key j
+    from query i when j > i + Sk - Sq.  Returns (o (B,Sq,H,D),
+    lse (B,H,Sq)); a row with no visible key has o = 0, lse = +inf."""
+    q, k, v = _np64(q), _np64(k), _np64(v)
+    B, Sq, H, D = q.shape
+    Sk, Hk = k.shape[1], k.shape[2]
+    grp = H // Hk
+    off = Sk - Sq
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    o = np.zeros((B, Sq, H, D))
+    lse = np.zeros((B, H, Sq))
+    res = _map_heads(lambda b, h: _fwd_head(q[b, :, h], k[b, :, h // grp], v[b, :, h // grp],
+                                            sm_scale, causal, off), B, H)
+    for (b, h), (oh, lh) in zip([(b, h) for b in range(B) for h in range(H)], res):
+        o[b, :, h] = oh
+        lse[b, h] = lh
+    return o, lse
+
+
+def attention_bwd_gqa(do, q, k, v, causal: bool = False, sm_scale: float | None = None, o=None):
+    """float64 gradients of attention_fwd_gqa's L = <O, dO>.  Returns
+    (dq (B,Sq,H,D), dk, dv (B,Sk,Hk,D) summed over each key/value head's
+    query heads, delta (B,H,Sq)); ``o`` as in attention_bwd."""
+    do, q, k, v = _np64(do), _np64(q), _np64(k), _np64(v)
+    B, Sq, H, D = q.shape
+    Sk, Hk = k.shape[1], k.shape[2]
+    grp = H // Hk
+    off = Sk - Sq
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    if o is None:
+        o, _ = attention_fwd_gqa(q, k, v, causal, sm_scale)
+    o = _np64(o)
+    dq = np.zeros_like(q)
+    dk = np.zeros_like(k)
+    dv = np.zeros_like(v)
+    delta = np.zeros((B, H, Sq))
+    res = _map_heads(lambda b, h: _bwd_head(q[b, :, h], k[b, :, h // grp], v[b, :, h // grp],
+                                            do[b, :, h], o[b, :, h], sm_scale, causal, off), B, H)
+    for (b, h), (gq, gk, gv, dl) in zip([(b, h) for b in range(B) for h in range(H)], res):
+        dq[b, :, h] = gq
+        dk[b, :, h // grp] += gk
+        dv[b, :, h // grp] += gv
+        delta[b, h] = dl
     return dq, dk, dv, delta
 
 

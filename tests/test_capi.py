@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.fa_abi_version() == _capi.ABI_VERSION == 1
+    assert lib.fa_abi_version() == _capi.ABI_VERSION == 2
 
 
 def test_strerror_covers_every_code(lib):
@@ -113,6 +113,41 @@ def test_preprocess_validation(lib):
     assert lib.fa_bwd_preprocess(P, P, BAD, 1, 64, 1, 64, s, s, None) == _capi.FA_ERR_ALIGNMENT
     assert lib.fa_bwd_preprocess(P, None, P, 1, 64, 1, 64, s, s, None) == _capi.FA_ERR_NULL_POINTER
     assert lib.fa_bwd_preprocess(P, P, P, 1, 64, 1, 40, s, s, None) == _capi.FA_ERR_HEAD_DIM
+
+
+def _fwd_gqa(lib, B=1, Sq=100, Sk=300, H=8, Hk=2, D=64, q=P, k=P, v=P, o=P, lse=None,
+             kst=None, scale=0.125):
+    sq = _st(B, Sq, H, D)
+    sk = kst or _st(B, Sk, Hk, D)
+    return lib.fa_fwd_gqa(q, k, v, o, lse, B, Sq, Sk, H, Hk, D, sq, sk, sk, sq, scale, 1, None)
+
+
+def test_fwd_gqa_validation(lib):
+    assert _fwd_gqa(lib, H=8, Hk=3) == _capi.FA_ERR_SHAPE        # H not a multiple of Hk
+    assert _fwd_gqa(lib, Hk=0) == _capi.FA_ERR_SHAPE
+    assert _fwd_gqa(lib, Sk=0) == _capi.FA_ERR_SHAPE
+    assert _fwd_gqa(lib, Sq=0) == _capi.FA_ERR_SHAPE
+    assert _fwd_gqa(lib, D=80) == _capi.FA_ERR_HEAD_DIM
+    assert _fwd_gqa(lib, v=None) == _capi.FA_ERR_NULL_POINTER
+    assert _fwd_gqa(lib, k=BAD) == _capi.FA_ERR_ALIGNMENT
+    assert _fwd_gqa(lib, kst=(ctypes.c_int64 * 4)(300 * 128, 128, 60, 1)) == _capi.FA_ERR_STRIDE
+    assert _fwd_gqa(lib, scale=float("nan")) == _capi.FA_ERR_SCALE
+    assert _fwd_gqa(lib, Sk=(1 << 30) + 1) == _capi.FA_ERR_TOO_LARGE
+
+
+def test_bwd_gqa_validation(lib):
+    B, Sq, Sk, H, Hk, D = 1, 64, 192, 4, 1, 64
+    sq, sk = _st(B, Sq, H, D), _st(B, Sk, Hk, D)
+    ws = lib.fa_bwd_workspace_bytes(B, Sq, H, D)
+
+    def call(ws_ptr=P, ws_bytes=ws, Hk_=Hk, dk=P):
+        return lib.fa_bwd_gqa(P, P, P, P, P, P, P, dk, P, ws_ptr, ws_bytes, B, Sq, Sk, H, Hk_, D,
+                              sq, sq, sk, sk, sq, sq, sk, sk, 0.125, 1, None)
+    assert call(ws_bytes=ws - 4) == _capi.FA_ERR_WORKSPACE
+    assert call(ws_ptr=None) == _capi.FA_ERR_WORKSPACE
+    assert call(Hk_=3) == _capi.FA_ERR_SHAPE
+    assert call(dk=None) == _capi.FA_ERR_NULL_POINTER
+    assert call(dk=BAD) == _capi.FA_ERR_ALIGNMENT
 
 
 def test_missing_library_fails_loudly(tmp_path):

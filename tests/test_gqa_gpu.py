@@ -1,0 +1,165 @@
+"""Grouped-query attention and Sq != Sk on the GPU: flash_attn_forward_gqa /
+flash_attn_backward_gqa / flash_attn_gqa (fa_fwd_gqa / fa_bwd_gqa via the C
+ABI) against the float64 oracle (attention_fwd_gqa / attention_bwd_gqa) on
+identical seeded fp16 inputs.  Tolerance: max-abs 1e-2 on O, LSE and every
+gradient, as for the square entry points.
+
+Cases: GQA and MQA groups at equal lengths; fewer queries than keys
+(prefill continuation, single-token decode) and more queries than keys
+(rows that see no key: O = 0, LSE = +inf, zero gradient); ragged lengths;
+D = 16/32/64/128; grids large enough for the unsplit kernels; HF-layout
+strided inputs; determinism; equivalence with the square entry points when
+Hk == H and Sq == Sk, and with attention over repeat_kv-expanded K/V.
+"""
+from __future__ import annotations
+
+import functools
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import TOL, default_scale, max_abs, report
+from oracle import attention as orc
+
+pytestmark = pytest.mark.gpu
+
+
+@functools.lru_cache(maxsize=2)
+def _oracle(B, Sq, Sk, H, Hk, D, causal, seed):
+    q, k, v, do = orc.make_inputs_gqa(B, Sq, Sk, H, Hk, D, seed=seed)
+    sc = default_scale(D, None)
+    o, lse = orc.attention_fwd_gqa(q, k, v, causal, sc)
+    dq, dk, dv, _ = orc.attention_bwd_gqa(do, q, k, v, causal, sc, o=o)
+    return (q, k, v, do), (o, lse, dq, dk, dv)
+
+
+def _lse_err(lse, ref):
+    """max-abs over finite entries; +inf (row with no visible key) must match
+    exactly."""
+    a = lse.detach().double().cpu().numpy()
+    inf_ref = np.isinf(ref)
+    assert np.array_equal(np.isinf(a), inf_ref), "rows with no visible key differ"
+    return float(np.max(np.abs(a[~inf_ref] - ref[~inf_ref]))) if (~inf_ref).any() else 0.0
+
+
+def _run(q, k, v, do, causal):
+    from flash_attn_volta import flash_attn_backward_gqa, flash_attn_forward_gqa
+    qd, kd, vd, dod = (t.cuda() for t in (q, k, v, do))
+    out, lse = flash_attn_forward_gqa(qd, kd, vd, causal=causal, return_softmax_lse=True)
+    dq, dk, dv = flash_attn_backward_gqa(dod, qd, kd, vd, out, lse, causal=causal)
+    torch.cuda.synchronize()
+    return out, lse, dq, dk, dv
+
+
+CASES = [
+    # (B, Sq, Sk, H, Hk, D, causal)
+    (2, 300, 300, 8, 2, 64, True),
+    (2, 300, 300, 8, 2, 64, False),
+    (1, 1024, 1024, 16, 4, 128, True),
+    (1, 257, 257, 6, 1, 32, True),            # MQA
+    (1, 100, 900, 8, 2, 64, True),            # prefill continuation
+    (1, 100, 900, 8, 2, 64, False),
+    (2, 1, 513, 4, 4, 128, True),             # single-token decode
+    (1, 3, 1000, 8, 1, 64, True),
+    (1, 64, 4096, 8, 8, 64, True),
+    (1, 500, 130, 4, 2, 64, True),            # rows with no visible key
+    (1, 500, 130, 4, 2, 64, False),
+    (2, 77, 191, 6, 3, 32, True),             # ragged
+    (1, 129, 65, 2, 1, 128, True),
+    (1, 200, 333, 4, 2, 16, True),            # D = 16 (zero-padded to 32)
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[
+    f"B{c[0]}_q{c[1]}_k{c[2]}_H{c[3]}_Hk{c[4]}_D{c[5]}_{'c' if c[6] else 'n'}" for c in CASES])
+def test_gqa_parity(case):
+    B, Sq, Sk, H, Hk, D, causal = case
+    print(f"[case] gqa {case}", flush=True)
+    (q, k, v, do), (o, lse, dq, dk, dv) = _oracle(B, Sq, Sk, H, Hk, D, causal, 31)
+    out, glse, gq, gk, gv = _run(q, k, v, do, causal)
+    assert out.shape == (B, Sq, H, D) and gk.shape == (B, Sk, Hk, D) and gv.shape == gk.shape
+    errs = dict(out=max_abs(out, o), lse=_lse_err(glse, lse), dq=max_abs(gq, dq),
+                dk=max_abs(gk, dk), dv=max_abs(gv, dv))
+    report(f"gqa {Sq}x{Sk} {H}/{Hk}", **errs)
+    for key, e in errs.items():
+        assert e < TOL, f"{case} {key} max-abs {e:.3e} >= {TOL}"
+
+
+# Grids large enough for the unsplit (one wave per 32 rows) kernels.
+@pytest.mark.parametrize("case", [(4, 1000, 1000, 32, 8, 64, True), (4, 520, 777, 32, 4, 128, False),
+                                  (8, 300, 700, 32, 16, 32, True)])
+def test_gqa_large_grid_variant(case):
+    B, Sq, Sk, H, Hk, D, causal = case
+    print(f"[case] gqa large-grid {case}", flush=True)
+    (q, k, v, do), (o, lse, dq, dk, dv) = _oracle(B, Sq, Sk, H, Hk, D, causal, 32)
+    out, glse, gq, gk, gv = _run(q, k, v, do, causal)
+    errs = dict(out=max_abs(out, o), lse=_lse_err(glse, lse), dq=max_abs(gq, dq),
+                dk=max_abs(gk, dk), dv=max_abs(gv, dv))
+    report(f"gqa-large {Sq}x{Sk}", **errs)
+    for key, e in errs.items():
+        assert e < TOL, f"{case} {key} max-abs {e:.3e} >= {TOL}"
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_gqa_with_equal_heads_and_lengths_is_the_square_path(causal):
+    """Hk == H, Sq == Sk: the grouped entry points give bit-identical results
+    to flash_attn_forward / flash_attn_backward."""
+    from flash_attn_volta import (flash_attn_backward, flash_attn_backward_gqa, flash_attn_forward,
+                                  flash_attn_forward_gqa)
+    q, k, v, do = (t.cuda() for t in orc.make_inputs(2, 333, 4, 64, seed=33))
+    o1, l1 = flash_attn_forward(q, k, v, causal=causal, return_softmax_lse=True)
+    o2, l2 = flash_attn_forward_gqa(q, k, v, causal=causal, return_softmax_lse=True)
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+    g1 = flash_attn_backward(do, q, k, v, o1, l1, causal=causal)
+    g2 = flash_attn_backward_gqa(do, q, k, v, o1, l1, causal=causal)
+    for a, b in zip(g1, g2):
+        assert torch.equal(a, b)
+
+
+def test_gqa_forward_equals_repeated_heads_bitwise():
+    """Each query head reads its key/value head in place: the forward is
+    bit-identical to the square kernel on repeat_kv-expanded K/V."""
+    from flash_attn_volta import flash_attn_forward, flash_attn_forward_gqa
+    q, k, v, _ = (t.cuda() for t in orc.make_inputs_gqa(1, 400, 400, 8, 2, 64, seed=34))
+    kr, vr = (t.repeat_interleave(4, dim=2).contiguous() for t in (k, v))
+    for causal in (False, True):
+        a, la = flash_attn_forward_gqa(q, k, v, causal=causal, return_softmax_lse=True)
+        b, lb = flash_attn_forward(q, kr, vr, causal=causal, return_softmax_lse=True)
+        assert torch.equal(a, b) and torch.equal(la, lb)
+
+
+def test_gqa_autograd_and_strided_inputs():
+    """flash_attn_gqa through autograd on (B, H, S, D).transpose(1, 2) views
+    (the HuggingFace layout) matches contiguous inputs bit for bit, and is
+    deterministic run to run."""
+    from flash_attn_volta import flash_attn_gqa
+    q, k, v, do = orc.make_inputs_gqa(2, 190, 450, 6, 2, 64, seed=35)
+
+    def run(strided):
+        ts = []
+        for t in (q, k, v):
+            t = t.cuda()
+            if strided:
+                t = t.permute(0, 2, 1, 3).contiguous().transpose(1, 2)
+            ts.append(t.requires_grad_())
+        out = flash_attn_gqa(*ts, causal=True)
+        out.backward(do.cuda())
+        return [out.detach()] + [t.grad for t in ts]
+
+    a, b, c = run(False), run(True), run(False)
+    for x, y, z in zip(a, b, c):
+        assert torch.equal(x, y) and torch.equal(x, z)
+
+
+def test_gqa_argument_errors():
+    from flash_attn_volta import flash_attn_forward_gqa
+    from flash_attn_volta.forward import FlashAttnArgumentError
+    q = torch.zeros(1, 8, 6, 64, dtype=torch.float16, device="cuda")
+    k = torch.zeros(1, 8, 4, 64, dtype=torch.float16, device="cuda")
+    with pytest.raises(FlashAttnArgumentError):
+        flash_attn_forward_gqa(q, k, k)                      # 6 % 4 != 0
+    with pytest.raises(FlashAttnArgumentError):
+        flash_attn_forward_gqa(q, k[..., :32], k[..., :32])  # head_dim mismatch
+    with pytest.raises(FlashAttnArgumentError):
+        flash_attn_forward_gqa(q, k[:, :, :2], k[:, :, :3])  # k / v differ
