@@ -19,14 +19,18 @@ of its config whose ``_attn_implementation`` names it.  Unpatching restores
 the module's own config object.  Projections, QK-norm, RoPE, caches and the
 output projection stay HuggingFace's own code for every family.
 
-The fast path is taken under the reference's conditions (:68-75, :145-162,
-:443-452): self-attention with q_len == kv_len (prefill, or training; a KV
-cache with content gives kv_len > q_len), no ``output_attentions``, no
-attention dropout, no sliding window narrower than the sequence, and an
-attention mask that is absent (the module is causal) or causal-only.
-Otherwise the module's original attention implementation runs unchanged.
-GQA/MQA key/value heads are expanded to the query heads, as the
-reference's ``repeat_kv`` calls do (:186-188, :470-471).
+The fast path is taken under the reference's conditions (:68-75,
+:443-452): self-attention, no ``output_attentions``, no attention dropout,
+no sliding window narrower than the sequence, and an attention mask that
+is absent (the module is causal) or causal-only.  Two of the reference's
+restrictions are lifted by the grouped-query kernels (flash_attn_gqa):
+GQA/MQA key/value heads are read in place instead of being expanded with
+repeat_kv (:186-188, :470-471), and a KV cache with content
+(kv_len > q_len: decode steps, chunked prefill) no longer falls back
+(:145-162) when its mask is the bottom-right-aligned causal mask (query i
+sees cache positions j <= i + kv_len - q_len), as a dynamic cache gives.
+Anything else runs the module's original attention implementation
+unchanged.
 """
 from __future__ import annotations
 
@@ -36,7 +40,7 @@ from typing import Optional, Tuple
 
 import torch
 
-from .autograd import flash_attn
+from .autograd import flash_attn, flash_attn_gqa
 
 ATTN_IMPLEMENTATION = "flash_attn_volta"
 
@@ -70,6 +74,27 @@ def _is_causal_only_mask(mask: torch.Tensor, q_len: int) -> bool:
     return True
 
 
+def _is_bottom_right_causal_mask(mask: torch.Tensor, q_len: int, kv_len: int) -> bool:
+    """True if ``mask`` (4-D, (.., q_len, kv_len)) lets query i see exactly
+    the keys j <= i + kv_len - q_len: the causal mask of q_len new tokens
+    appended to a cache of kv_len - q_len.  Float masks: visible entries
+    |m| <= 1e-3, hidden <= -1; bool masks: True = attend."""
+    if mask is None or mask.dim() != 4:
+        return False
+    if mask.size(-2) != q_len or mask.size(-1) != kv_len or kv_len < q_len:
+        return False
+    i = torch.arange(q_len, device=mask.device)[:, None]
+    j = torch.arange(kv_len, device=mask.device)[None, :]
+    vis = j <= i + (kv_len - q_len)
+    if mask.dtype == torch.bool:
+        return bool(mask[..., vis].all()) and not bool(mask[..., ~vis].any())
+    if (mask[..., vis].abs() > 1e-3).any():
+        return False
+    if (mask[..., ~vis] > -1.0).any():
+        return False
+    return True
+
+
 def _original_interface(module):
     """The attention function the module would use unpatched."""
     from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
@@ -97,15 +122,19 @@ def fast_path_causal(module, q_len: int, kv_len: int, head_dim: int,
     """Decide whether an attention call may run on the flash kernel.
 
     Returns None to fall back to the module's original implementation, else
-    the causal flag to run the kernel with.  Fallbacks mirror the reference
-    (patch_hf.py:68-75, :145-162, :443-452): a KV cache with content
-    (kv_len != q_len), output_attentions, cross-attention, a head mask, a
-    mask that is not causal-only; plus what the kernel does not implement
-    here: attention dropout, a sliding window narrower than the sequence,
-    head dims outside {16, 32, 64, 128}.
+    the causal flag to run the kernel with (bottom-right aligned when
+    kv_len > q_len).  Fallbacks mirror the reference (patch_hf.py:68-75,
+    :443-452): output_attentions, cross-attention, a head mask, a mask that
+    is not causal-only; plus what the kernel does not implement here:
+    attention dropout, a sliding window narrower than the sequence, head
+    dims outside {16, 32, 64, 128}.  A KV cache with content (kv_len >
+    q_len, where the reference always falls back, :145-162) runs on the
+    kernel when the module is causal and the mask is the bottom-right
+    causal mask, or absent for a single new token; a cache whose mask hides
+    more (a static cache's unused tail, padding) falls back.
     """
     causal = bool(getattr(module, "is_causal", True))
-    if q_len != kv_len or kwargs.get("output_attentions", False):
+    if kwargs.get("output_attentions", False):
         return None
     if getattr(module, "is_cross_attention", False) or kwargs.get("head_mask") is not None:
         return None
@@ -115,6 +144,12 @@ def fast_path_causal(module, q_len: int, kv_len: int, head_dim: int,
         return None
     if head_dim not in (16, 32, 64, 128):
         return None
+    if q_len != kv_len:
+        if not causal or kv_len < q_len:
+            return None
+        if attention_mask is None:
+            return True if q_len == 1 else None
+        return True if _is_bottom_right_causal_mask(attention_mask, q_len, kv_len) else None
     if attention_mask is not None:
         if not (causal and _is_causal_only_mask(attention_mask, q_len)):
             return None
@@ -142,16 +177,17 @@ def flash_attn_volta_attention(
                                            dropout=dropout, scaling=scaling,
                                            sliding_window=sliding_window, **kwargs)
 
-    n_rep = query.shape[1] // key.shape[1]
-    key = _expand_kv(key, n_rep)
-    value = _expand_kv(value, n_rep)
     out_dtype = query.dtype
     q = query.transpose(1, 2).to(torch.float16)
     k = key.transpose(1, 2).to(torch.float16)
     v = value.transpose(1, 2).to(torch.float16)
     if scaling is None:
         scaling = query.shape[-1] ** -0.5
-    out = flash_attn(q, k, v, causal=causal, sm_scale=float(scaling))
+    if q.shape == k.shape:
+        out = flash_attn(q, k, v, causal=causal, sm_scale=float(scaling))
+    else:
+        # grouped K/V heads and/or a cache: read in place, no repeat_kv copy
+        out = flash_attn_gqa(q, k, v, causal=causal, sm_scale=float(scaling))
     return out.to(out_dtype), None
 
 

@@ -98,6 +98,27 @@ def test_causal_only_mask_rule():
     assert not patch_hf._is_causal_only_mask(torch.ones(1, 1, n, n, dtype=torch.bool), n)
 
 
+def _bottom_right_bool(q, kv):
+    i = torch.arange(q)[:, None]
+    j = torch.arange(kv)[None, :]
+    return (j <= i + (kv - q)).expand(2, 1, q, kv).clone()
+
+
+def _bottom_right_float(q, kv):
+    m = torch.zeros(2, 1, q, kv)
+    return m.masked_fill(~_bottom_right_bool(q, kv), torch.finfo(torch.float32).min)
+
+
+def test_bottom_right_mask_rule():
+    r = patch_hf._is_bottom_right_causal_mask
+    assert r(_bottom_right_bool(5, 12), 5, 12) and r(_bottom_right_float(5, 12), 5, 12)
+    assert r(_bottom_right_bool(7, 7), 7, 7)
+    top_left = torch.ones(2, 1, 5, 12, dtype=torch.bool).tril()
+    assert not r(top_left, 5, 12)
+    assert not r(_bottom_right_bool(5, 12), 5, 13)
+    assert not r(None, 5, 12)
+
+
 class _Mod:
     is_causal = True
 
@@ -112,7 +133,16 @@ def test_fast_path_decisions():
     assert f(m, n, n, 64, None, 0.0, None, {}) is True
     assert f(m, n, n, 64, _float_causal(n), 0.0, None, {}) is True
     assert f(_Enc(), n, n, 64, None, 0.0, None, {}) is False       # non-causal module, no mask
-    assert f(m, 1, n, 64, None, 0.0, None, {}) is None             # KV cache with content
+    assert f(m, 1, n, 64, None, 0.0, None, {}) is True             # decode step: sees the cache
+    assert f(m, 4, n, 64, None, 0.0, None, {}) is None             # chunk without a mask
+    assert f(m, 4, n, 64, _bottom_right_bool(4, n), 0.0, None, {}) is True   # chunked prefill
+    assert f(m, 4, n, 64, _bottom_right_float(4, n), 0.0, None, {}) is True
+    static = _bottom_right_bool(4, n)
+    static[..., -1] = False                                          # unused cache slot hidden
+    assert f(m, 4, n, 64, static, 0.0, None, {}) is None
+    assert f(m, 4, n, 64, _bottom_right_bool(4, n)[..., :n - 1], 0.0, None, {}) is None
+    assert f(_Enc(), 1, n, 64, None, 0.0, None, {}) is None         # non-causal with a cache
+    assert f(m, n, 4, 64, None, 0.0, None, {}) is None             # more queries than keys
     assert f(m, n, n, 64, None, 0.0, None, {"output_attentions": True}) is None
     assert f(m, n, n, 64, None, 0.1, None, {}) is None             # attention dropout
     assert f(m, n, n, 64, None, 0.0, 8, {}) is None                # narrow sliding window

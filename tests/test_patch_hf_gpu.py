@@ -125,54 +125,103 @@ def test_tiny_models_match_fp32_attention(family, make, names, patch):
         assert c >= 0.99 and rel <= 0.1
 
 
+def _count_kernel_calls(monkeypatch):
+    """Count calls of the two kernel entry points patch_hf uses."""
+    import flash_attn_volta.patch_hf as ph
+    calls = {"square": 0, "gqa": 0}
+    real_sq, real_gqa = ph.flash_attn, ph.flash_attn_gqa
+
+    def sq(*a, **k):
+        calls["square"] += 1
+        return real_sq(*a, **k)
+
+    def gqa(*a, **k):
+        calls["gqa"] += 1
+        return real_gqa(*a, **k)
+
+    monkeypatch.setattr(ph, "flash_attn", sq)
+    monkeypatch.setattr(ph, "flash_attn_gqa", gqa)
+    return calls
+
+
 def test_patched_fast_path_actually_runs(monkeypatch):
-    """The patched model must call the kernel, not fall back."""
+    """The patched model must call the kernel, not fall back: MHA through
+    flash_attn, GQA through flash_attn_gqa (no repeat_kv copy)."""
     import flash_attn_volta.patch_hf as ph
-    calls = {"n": 0}
-    real = ph.flash_attn
-
-    def counting(*a, **k):
-        calls["n"] += 1
-        return real(*a, **k)
-
-    monkeypatch.setattr(ph, "flash_attn", counting)
-    model = hf_models.tiny_llama().half().cuda()
-    ph.patch_llama(model)
+    calls = _count_kernel_calls(monkeypatch)
+    mha = hf_models.tiny_llama(gqa=False).half().cuda()
+    ph.patch_llama(mha)
     with torch.no_grad():
-        model(hf_models.token_ids(64, device="cuda"))
-    assert calls["n"] == 2
+        mha(hf_models.token_ids(64, device="cuda"))
+    assert calls == {"square": 2, "gqa": 0}
+    gqa = hf_models.tiny_llama(gqa=True).half().cuda()
+    ph.patch_llama(gqa)
+    with torch.no_grad():
+        gqa(hf_models.token_ids(64, device="cuda"))
+    assert calls == {"square": 2, "gqa": 2}
 
 
-def test_generation_with_kv_cache_falls_back_after_prefill(monkeypatch):
-    """Prefill runs on the kernel; decode steps (KV cache with content,
-    q_len != kv_len) fall back to the original attention
-    (reference patch_hf.py:145-162).  The prefill logits match the unpatched
-    model and the first greedy token agrees."""
+def _greedy_logits(model, ids, steps):
+    """Prefill `ids`, then `steps` decode steps feeding the given next
+    tokens (teacher forcing with ids[:, -steps:] appended); returns the list
+    of per-step last-position logits."""
+    out = []
+    with torch.no_grad():
+        r = model(ids[:, :-steps], use_cache=True)
+        out.append(r.logits[:, -1].float())
+        past = r.past_key_values
+        for t in range(steps):
+            tok = ids[:, ids.shape[1] - steps + t:ids.shape[1] - steps + t + 1]
+            r = model(tok, past_key_values=past, use_cache=True)
+            past = r.past_key_values
+            out.append(r.logits[:, -1].float())
+    return out
+
+
+def test_decode_with_kv_cache_runs_on_the_kernel(monkeypatch):
+    """Decode steps (q_len = 1 against a cache with content) run on
+    flash_attn_gqa instead of falling back (the reference falls back,
+    patch_hf.py:145-162), and every step's logits match the unpatched
+    model's."""
     import flash_attn_volta.patch_hf as ph
-    calls = {"n": 0}
-    real = ph.flash_attn
-
-    def counting(*a, **k):
-        calls["n"] += 1
-        return real(*a, **k)
-
-    monkeypatch.setattr(ph, "flash_attn", counting)
+    calls = _count_kernel_calls(monkeypatch)
     ref = hf_models.tiny_llama(gqa=True).half().cuda()
     ours = hf_models.tiny_llama(gqa=True).half().cuda()
     ours.load_state_dict(ref.state_dict())
     ph.patch_llama(ours)
-    ids = hf_models.token_ids(40, device="cuda", seed=3)
+    ids = hf_models.token_ids(48, device="cuda", seed=3)
+    la = _greedy_logits(ref, ids, 8)
+    lb = _greedy_logits(ours, ids, 8)
+    assert calls["gqa"] == 2 * 9            # 2 layers x (prefill + 8 decode steps)
+    for a, b in zip(la, lb):
+        assert _cos(a, b) >= 0.999 and (a - b).abs().max().item() <= 0.1
+    gen = ours.generate(ids[:, :40], max_new_tokens=8, do_sample=False)
+    ref_gen = ref.generate(ids[:, :40], max_new_tokens=8, do_sample=False)
+    agree = (gen == ref_gen).float().mean().item()
+    print(f"[patch_hf] greedy generation agreement {agree:.3f}", flush=True)
+    assert gen.shape == ref_gen.shape and agree >= 0.95
+
+
+def test_chunked_prefill_runs_on_the_kernel(monkeypatch):
+    """A second prefill chunk (q_len = 16 against a 40-token cache, whose mask
+    is the bottom-right causal mask) runs on the kernel and matches the
+    unpatched model's logits for the same positions of a one-shot forward."""
+    import flash_attn_volta.patch_hf as ph
+    calls = _count_kernel_calls(monkeypatch)
+    ref = hf_models.tiny_llama(gqa=True).half().cuda()
+    ours = hf_models.tiny_llama(gqa=True).half().cuda()
+    ours.load_state_dict(ref.state_dict())
+    ph.patch_llama(ours)
+    ids = hf_models.token_ids(40, device="cuda", seed=4)
     with torch.no_grad():
-        la = ref(ids).logits.float()
-        lb = ours(ids).logits.float()
-    assert calls["n"] == 2
-    assert _cos(la, lb) >= 0.999 and (la - lb).abs().max().item() <= 0.1
-    calls["n"] = 0
-    out = ours.generate(ids, max_new_tokens=8, do_sample=False)
-    assert out.shape[1] == 48
-    assert calls["n"] == 2          # prefill only: 2 layers x 1 call
-    assert out[0, 40].item() == la[0, -1].argmax().item() or \
-        (la[0, -1].topk(2).values.diff().abs().item() < 1e-2)
+        full = ref(ids).logits.float()
+        r = ours(ids[:, :24], use_cache=True)
+        calls["gqa"] = 0
+        r2 = ours(ids[:, 24:], past_key_values=r.past_key_values, use_cache=True)
+    assert calls["gqa"] == 2
+    chunk = r2.logits.float()
+    assert _cos(chunk, full[:, 24:]) >= 0.999
+    assert (chunk - full[:, 24:]).abs().max().item() <= 0.1
 
 
 def test_config5_llama_training_step():
