@@ -188,23 +188,32 @@ __device__ __forceinline__ void merge_pair(float *buf, bool writer, floatx16 (&a
 
 // ---------------------------------------------------------------------------
 // dK / dV: workgroup = 4 waves.  SPLIT = 1: wave w owns 32 keys (BK = 128)
-// and both 32-query halves of every 64-query tile.  SPLIT = 2: wave w owns
-// key group kg = w / 2 (BK = 64) and query half qh = w % 2 of every tile;
-// the two query halves of a key group merge their dK / dV partial sums
-// through LDS at the end.  The split doubles the waves in flight for grids
-// too small to fill the GPU (the launcher decides).  Query tiles of
-// BQ = 64 rows stream through double-buffered LDS as Q and dO (kperm row
-// order) plus LSE and delta.
+// and both 32-query sub-blocks of every 64-query tile.  SPLIT = 2: wave w
+// owns key group kg = w / 2 (BK = 64) and query half qh = w % 2 of every
+// tile; the two query halves of a key group merge their dK / dV partial
+// sums through LDS at the end.  The split doubles the waves in flight for
+// grids too small to fill the GPU (the launcher decides).  Query tiles of
+// BQ rows stream through double-buffered LDS as Q and dO (kperm row order)
+// plus LSE and delta.  With SPLIT = 2 and D <= 64 (EARLY_S) tiles are 128
+// queries, so each wave again has two 32-query sub-blocks, and both
+// sub-blocks' S and dP MFMAs are issued before the first sub-block's
+// softmax: the matrix cores work on the second sub-block while the wave's
+// VALU works on the first.  Otherwise (D = 128: no registers for two score
+// sets) tiles are 64 queries.
 template <int D, int SPLIT>
 struct DkdvTile {
   static_assert(SPLIT == 1 || SPLIT == 2, "split is 1 or 2");
   static constexpr int NKG = 4 / SPLIT;    // key groups of 32 per workgroup
-  static constexpr int NSUB = 2 / SPLIT;   // 32-query sub-blocks per wave per tile
+  // issue all S / dP MFMAs of a tile first (measured: helps the split
+  // variant, costs ~1 % unsplit, where two waves per SIMD already overlap)
+  static constexpr bool EARLY_S = D <= 64 && SPLIT == 2;
+  // 32-query sub-blocks per wave per tile (64-query tiles unless EARLY_S)
+  static constexpr int NSUB = EARLY_S ? 2 : 2 / SPLIT;
   static constexpr int BK = 32 * NKG;
-  static constexpr int BQ = 64;
+  static constexpr int BQ = 32 * NSUB * SPLIT;   // queries per tile
   static constexpr int NT = 256;
   static constexpr int LDS_TILE = BQ * D;   // swizzled, unpadded (fa_common.hpp)
-  static_assert(64 * (D / 2) * 4 * 2 <= 2 * LDS_TILE * 2, "merge buffers must fit in a tile ring");
+  static_assert(64 * (D / 2) * 4 <= LDS_TILE * 2, "a merge buffer must fit in one stage");
 };
 
 template <int D, bool CAUSAL, int SPLIT>
@@ -275,7 +284,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
   // seeds: s_lse = -LSE * log2(e) / cr (-inf past S, so P = 0 there) and
   // s_dl = -delta.  Seeding the S and dP MFMAs with them yields
   // ck * s - LSE' and dP - delta with no per-score VALU work.
-  DmaStager<D> stq, stg;
+  DmaStager<D, BQ> stq, stg;
   stq.init(w, lane, a.q.ss);
   stg.init(w, lane, a.dout.ss);
   const float lse_mul = -kLog2e / cr;
@@ -339,17 +348,19 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
     const bool more = t + 1 < n_tiles;
     if (more) load_tile(t + 1, std::integral_constant<int, st ^ 1>{});
 
-#pragma unroll
-    for (int sb = 0; sb < NSUB; ++sb) {
-      const int qs = NSUB * qh + sb;   // 32-query sub-block of the tile
-      const int ms = m0 + 32 * qs;
-      // whole sub-block above this wave's keys' diagonal: nothing visible
-      if (CAUSAL && ms + 31 + off < wk0) continue;
-      if (ms >= Sq) continue;
-
-      // slot i <-> query ms + slot_row(i, g); lane <-> key.  Accumulator
-      // seeds: slots 8hh + j hold rows 32qs + 16hh + 8g + j.
-      floatx16 sacc, dpacc;
+    // 32-query sub-block sb of this wave: queries m0 + 32 * (NSUB*qh + sb)
+    auto sub_m = [&](int sb) { return m0 + 32 * (NSUB * qh + sb); };
+    // live: not entirely above this wave's keys' diagonal, not past Sq
+    auto live = [&](int sb) {
+      const int ms = sub_m(sb);
+      return !(CAUSAL && ms + 31 + off < wk0) && ms < Sq;
+    };
+    // S = c_k Q K^T - LSE' and dP = dO V^T - delta for sub-block sb: the
+    // accumulators start from the LDS seeds (slots 8hh + j hold rows
+    // 32qs + 16hh + 8g + j; slot i <-> query ms + slot_row(i, g), lane <->
+    // key).
+    auto s_dp = [&](int sb, floatx16 &sacc, floatx16 &dpacc) {
+      const int qs = NSUB * qh + sb;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const int r = 32 * qs + 16 * hh + 8 * g;
@@ -365,15 +376,18 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
           dpacc[8 * hh + 4 + j] = d_hi[j];
         }
       }
-      {
-        const f16 *qr = q_st(stc) + 32 * qs * D;
-        const f16 *gr = do_st(stc) + 32 * qs * D;
+      const f16 *qr = q_st(stc) + 32 * qs * D;
+      const f16 *gr = do_st(stc) + 32 * qs * D;
 #pragma unroll
-        for (int cc = 0; cc < D / 16; ++cc) {
-          sacc = mfma32(*(const half8 *)(qr + a_off[cc]), kf[cc], sacc);
-          dpacc = mfma32(*(const half8 *)(gr + a_off[cc]), vf[cc], dpacc);
-        }
+      for (int cc = 0; cc < D / 16; ++cc) {
+        sacc = mfma32(*(const half8 *)(qr + a_off[cc]), kf[cc], sacc);
+        dpacc = mfma32(*(const half8 *)(gr + a_off[cc]), vf[cc], dpacc);
       }
+    };
+    // Softmax-gradient of sub-block sb and its dV / dK MFMAs.
+    auto grad = [&](int sb, floatx16 &sacc, const floatx16 &dpacc) {
+      const int qs = NSUB * qh + sb;
+      const int ms = sub_m(sb);
       // Invisible scores become -inf (P = 0) in one pass, taken only by
       // diagonal and ragged sub-blocks, so the softmax below is branch-free.
       if ((CAUSAL && ms + off < wk0 + 31) || (ms + 31 >= Sq) || (wk0 + 31 >= Sk)) {
@@ -421,6 +435,24 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
           dv[d] = mfma32(load_tr_pair(do_st(stc) + rb + t_off[d], 8 * D), pf[hh], dv[d]);
           dk[d] = mfma32(load_tr_pair(q_st(stc) + rb + t_off[d], 8 * D), dsf[hh], dk[d]);
         }
+      }
+    };
+
+    if constexpr (T::EARLY_S) {
+      floatx16 sacc[NSUB], dpacc[NSUB];
+#pragma unroll
+      for (int sb = 0; sb < NSUB; ++sb)
+        if (live(sb)) s_dp(sb, sacc[sb], dpacc[sb]);
+#pragma unroll
+      for (int sb = 0; sb < NSUB; ++sb)
+        if (live(sb)) grad(sb, sacc[sb], dpacc[sb]);
+    } else {
+#pragma unroll
+      for (int sb = 0; sb < NSUB; ++sb) {
+        if (!live(sb)) continue;
+        floatx16 sacc, dpacc;
+        s_dp(sb, sacc, dpacc);
+        grad(sb, sacc, dpacc);
       }
     }
 

@@ -174,12 +174,14 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, const void 
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void *)lds, 16, voff, 0, 0, 0);
 }
 
-// Loads one 64-row tile (rows r0 .. r0+63 of a (b, h) head, zeros past S)
-// into a swizzled LDS slot: 64*D*2 bytes = D/8 wave instructions of 1 KiB,
-// D/32 per wave of a 4-wave workgroup.  No VGPRs hold tile data.
-template <int D>
+// Loads one ROWS-row tile (rows r0 .. r0+ROWS-1 of a (b, h) head, zeros
+// past S) into a swizzled LDS slot: ROWS*D*2 bytes = ROWS*D/512 wave
+// instructions of 1 KiB, ROWS*D/2048 per wave of a 4-wave workgroup.  No
+// VGPRs hold tile data.
+template <int D, int ROWS = 64>
 struct DmaStager {
-  static constexpr int PER_WAVE = D / 32;
+  static constexpr int PER_WAVE = ROWS * D / 2048;
+  static_assert(PER_WAVE >= 1, "tile smaller than one DMA instruction per wave");
   int off[PER_WAVE];   // global byte offset of this lane's chunk, relative to row r0
 
   __device__ __forceinline__ void init(int w, int lane, int64_t ss) {
