@@ -484,11 +484,13 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
 
 // ---------------------------------------------------------------------------
 // dQ: workgroup = 4 waves.  SPLIT = 1: wave w owns 32 queries (BM = 128)
-// and both 32-key halves of every 64-key tile.  SPLIT = 2: wave w owns query
-// group qg = w / 2 (BM = 64) and key half kh = w % 2 of every tile; the two
-// key halves of a query group merge their dQ partial sums through LDS at
-// the end.  Key tiles of BN = 64 rows stream through double-buffered LDS as
-// K and V (kperm row order).
+// and both 32-key sub-blocks of every 64-key tile.  SPLIT = 2: wave w owns
+// query group qg = w / 2 (BM = 64) and key half kh = w % 2 of every tile;
+// the two key halves of a query group merge their dQ partial sums through
+// LDS at the end.  Key tiles of BN = 64 rows stream through double-buffered
+// LDS as K and V (kperm row order).  (The dK/dV kernel's 128-row tiles with
+// early S/dP issue measured 12 % slower here: the second score set costs
+// the third wave per SIMD.)
 template <int D, int SPLIT>
 struct DqTile {
   static_assert(SPLIT == 1 || SPLIT == 2, "split is 1 or 2");
@@ -546,6 +548,10 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
   for (int d = 0; d < D / 32; ++d) dq[d] = floatx16{};
   DsScale sc;
   float shift = -l2;   // exponent offset: e - LSE * log2(e)
+  // dP^T MFMAs start from -delta (the lane's query), so they yield dP - delta
+  floatx16 dl_seed;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) dl_seed[i] = -dl;
 
   int kv_end = Sk;
   if (CAUSAL) kv_end = min(Sk, q0 + BM + off);
@@ -554,7 +560,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
   const float c = a.c;
 
   // K and V tiles go straight to LDS (fa_common.hpp DmaStager).
-  DmaStager<D> stk, stv;
+  DmaStager<D, BN> stk, stv;
   stk.init(w, lane, a.k.ss);
   stv.init(w, lane, a.v.ss);
   auto load_tile = [&](int n0, auto stc) {
@@ -589,24 +595,28 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
     const bool more = t + 1 < n_tiles;
     if (more) load_tile(n0 + BN, std::integral_constant<int, st ^ 1>{});
 
+    // 32-key sub-block sb of this wave: keys n0 + 32 * (NSUB*kh + sb)
+    auto sub_n = [&](int sb) { return n0 + 32 * (NSUB * kh + sb); };
+    auto live = [&](int sb) {
+      const int ns = sub_n(sb);
+      return !(CAUSAL && ns > wq0 + 31 + off) && ns < Sk;
+    };
+    // S^T = K Q^T and dP^T = V dO^T for sub-block sb
+    auto s_dp = [&](int sb, floatx16 &sacc, floatx16 &dpacc) {
+      const int ks = NSUB * kh + sb;
+      const f16 *kr = k_st(stc) + 32 * ks * D;
+      const f16 *vr = v_st(stc) + 32 * ks * D;
+      sacc = mfma32(*(const half8 *)(kr + a_off[0]), qf[0], floatx16{});
+      dpacc = mfma32(*(const half8 *)(vr + a_off[0]), gf[0], dl_seed);
 #pragma unroll
-    for (int sb = 0; sb < NSUB; ++sb) {
-      const int ks = NSUB * kh + sb;   // 32-key sub-block of the tile
-      const int ns = n0 + 32 * ks;
-      if (CAUSAL && ns > wq0 + 31 + off) continue;
-      if (ns >= Sk) continue;
-      floatx16 sacc, dpacc;
-      {
-        const f16 *kr = k_st(stc) + 32 * ks * D;
-        const f16 *vr = v_st(stc) + 32 * ks * D;
-        sacc = mfma32(*(const half8 *)(kr + a_off[0]), qf[0], floatx16{});
-        dpacc = mfma32(*(const half8 *)(vr + a_off[0]), gf[0], floatx16{});
-#pragma unroll
-        for (int cc = 1; cc < D / 16; ++cc) {
-          sacc = mfma32(*(const half8 *)(kr + a_off[cc]), qf[cc], sacc);
-          dpacc = mfma32(*(const half8 *)(vr + a_off[cc]), gf[cc], dpacc);
-        }
+      for (int cc = 1; cc < D / 16; ++cc) {
+        sacc = mfma32(*(const half8 *)(kr + a_off[cc]), qf[cc], sacc);
+        dpacc = mfma32(*(const half8 *)(vr + a_off[cc]), gf[cc], dpacc);
       }
+    };
+    auto grad = [&](int sb, floatx16 &sacc, const floatx16 &dpacc) {
+      const int ks = NSUB * kh + sb;
+      const int ns = sub_n(sb);
       // invisible scores -> -inf (P = 0), diagonal / ragged sub-blocks only
       if ((CAUSAL && ns + 31 > wq0 + off) || (ns + 31 >= Sk)) {
 #pragma unroll
@@ -622,7 +632,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const float p = fast_exp2(__builtin_fmaf(sacc[i], c, shift));
-        ds[i] = p * (dpacc[i] - dl);
+        ds[i] = p * dpacc[i];
       }
       const float m = absmax16(ds);
       {
@@ -648,6 +658,14 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
         for (int d = 0; d < D / 32; ++d)
           dq[d] = mfma32(load_tr_pair(k_st(stc) + rb + t_off[d], 8 * D), dsf[hh], dq[d]);
       }
+    };
+
+#pragma unroll
+    for (int sb = 0; sb < NSUB; ++sb) {
+      if (!live(sb)) continue;
+      floatx16 sacc, dpacc;
+      s_dp(sb, sacc, dpacc);
+      grad(sb, sacc, dpacc);
     }
 
     if (more) __builtin_amdgcn_s_waitcnt(0x0f70);   // this wave's DMAs of the next stage
