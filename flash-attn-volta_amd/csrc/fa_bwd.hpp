@@ -391,12 +391,14 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
       // Invisible scores become -inf (P = 0) in one pass, taken only by
       // diagonal and ragged sub-blocks, so the softmax below is branch-free.
       if ((CAUSAL && ms + off < wk0 + 31) || (ms + 31 >= Sq) || (wk0 + 31 >= Sk)) {
+        // query ms + slot_row(i, g) sees this lane's key iff
+        // lo <= slot_row(i, 0) < hi (nothing when the key is past Sk)
+        const int base = ms + 8 * g;
+        const int hi = key < Sk ? Sq - base : -(1 << 30);
+        const int lo = CAUSAL ? key - off - base : -(1 << 30);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int m = ms + slot_row(i, g);
-          const bool vis = m < Sq && key < Sk && (!CAUSAL || key <= m + off);
-          sacc[i] = vis ? sacc[i] : kNegInf;
-        }
+        for (int i = 0; i < 16; ++i)
+          sacc[i] = (slot_row(i, 0) >= lo && slot_row(i, 0) < hi) ? sacc[i] : kNegInf;
       }
       if (cr != 1.0f) {
 #pragma unroll
@@ -619,12 +621,12 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
       const int ns = sub_n(sb);
       // invisible scores -> -inf (P = 0), diagonal / ragged sub-blocks only
       if ((CAUSAL && ns + 31 > wq0 + off) || (ns + 31 >= Sk)) {
+        // key ns + slot_row(i, g) is visible iff slot_row(i, 0) <= lim
+        int lim = Sk - 1;
+        if (CAUSAL) lim = min(lim, qrow + off);
+        lim -= ns + 8 * g;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int n = ns + slot_row(i, g);
-          const bool vis = n < Sk && (!CAUSAL || n <= qrow + off);
-          sacc[i] = vis ? sacc[i] : kNegInf;
-        }
+        for (int i = 0; i < 16; ++i) sacc[i] = slot_row(i, 0) <= lim ? sacc[i] : kNegInf;
       }
       // The lane's dS scale 2^e rides in the exponent: P * 2^e =
       // exp2(c s - LSE' + e), so ds below is already dS * 2^e.
