@@ -413,7 +413,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
       // adaptive power-of-two scale of this key's dS column
       const float mk = absmax16(ds);
       {
-        const float f = sc.update(fmaxf(mk, __shfl_xor(mk, 32, 64)));
+        const float f = sc.update(max_xor32(mk));
         if (__any(f != 1.0f)) {
 #pragma unroll
           for (int d = 0; d < D / 32; ++d)
@@ -638,7 +638,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
       }
       const float m = absmax16(ds);
       {
-        const float f = sc.update_scaled(fmaxf(m, __shfl_xor(m, 32, 64)));
+        const float f = sc.update_scaled(max_xor32(m));
         if (__any(f != 1.0f)) {
           shift = (float)sc.e - l2;
 #pragma unroll

@@ -75,6 +75,15 @@ __device__ __forceinline__ float xor32(float x) {
   return __shfl_xor(x, 32, 64);
 }
 
+// max(x, value of lane ^ 32) without an LDS round trip.  v_permlane32_swap
+// exchanges the upper half of its first operand with the lower half of its
+// second; with both operands x, each lane ends up holding {own, partner} in
+// some order.
+__device__ __forceinline__ float max_xor32(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(x, fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])));
+}
+
 // Sum of the two fp16 values of `p` accumulated into fp32 `acc`
 // (v_dot2_f32_f16 against (1, 1)).
 __device__ __forceinline__ float dot2_acc(half2 p, float acc) {

@@ -67,14 +67,6 @@ struct FwdTile {
   static_assert(64 * (D / 2) * 4 <= LDS_TILE * 2, "a merge buffer must fit in one K slot");
 };
 
-// max(x, value of lane ^ 32).  v_permlane32_swap exchanges the upper half of
-// its first operand with the lower half of its second; with both operands x,
-// each lane ends up holding {own, partner} in some order.
-__device__ __forceinline__ float max_xor32(float x) {
-  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(x, fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])));
-}
-
 // Workgroup = 4 waves.  KSPLIT = 1: each wave owns 32 queries (BM = 128)
 // and both 32-key halves of every 64-key tile.  KSPLIT = 2: wave w owns
 // query group qg = w / 2 (BM = 64) and key half kh = w % 2 of every tile;
