@@ -127,10 +127,10 @@ def kernel_times(q, k, v, do, steps, warmup):
         # name, fn, kernel symbol prefix (the last template argument, the
         # in-workgroup split, is chosen by the launcher from the grid size),
         # algorithmic dense FLOPs per launch, algorithmic HBM bytes
-        ("fwd", fwd, f"fa_fwd_kernel<{D}, {cb}, ", 2 * base, 4 * io),
-        ("bwd_preprocess", pre, f"fa_bwd_preprocess_kernel<{D}>", 2.0 * B * H * S * D, 2 * io + rows),
-        ("bwd_dkdv", dkdv, f"fa_bwd_dkdv_kernel<{D}, {cb}, ", 4 * base, 6 * io + 2 * rows),
-        ("bwd_dq", dqk, f"fa_bwd_dq_kernel<{D}, {cb}, ", 3 * base, 5 * io + 2 * rows),
+        ("fwd", fwd, f"fa_fwd_kernel<_Float16, {D}, {cb}, ", 2 * base, 4 * io),
+        ("bwd_preprocess", pre, f"fa_bwd_preprocess_kernel<_Float16, {D}>", 2.0 * B * H * S * D, 2 * io + rows),
+        ("bwd_dkdv", dkdv, f"fa_bwd_dkdv_kernel<_Float16, {D}, {cb}, ", 4 * base, 6 * io + 2 * rows),
+        ("bwd_dq", dqk, f"fa_bwd_dq_kernel<_Float16, {D}, {cb}, ", 3 * base, 5 * io + 2 * rows),
     ]
     res = {}
     for name, fn, sym, flops, nbytes in table:

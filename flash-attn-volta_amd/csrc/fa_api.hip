@@ -23,9 +23,11 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 // (B, Sk, Hk, D); query head h uses key/value head h / (H / Hk).
 struct Shape {
   int B, Sq, Sk, H, Hk, D;
+  int dtype;   // FA_DTYPE_F16 or FA_DTYPE_BF16
 };
 
 int check_shape(const Shape &s) {
+  if (s.dtype != FA_DTYPE_F16 && s.dtype != FA_DTYPE_BF16) return FA_ERR_DTYPE;
   if (s.B <= 0 || s.Sq <= 0 || s.Sk <= 0 || s.H <= 0 || s.Hk <= 0) return FA_ERR_SHAPE;
   if (s.H % s.Hk != 0) return FA_ERR_SHAPE;
   if (s.D != 32 && s.D != 64 && s.D != 128) return FA_ERR_HEAD_DIM;
@@ -103,88 +105,87 @@ bool row_split(int rows, int64_t heads, bool causal) {
   return wgs < (int64_t)(causal ? 4 : 2) * device_cus();
 }
 
-template <int D, bool CAUSAL, int KSPLIT>
+template <typename E, int D, bool CAUSAL, int KSPLIT>
 int launch_fwd_split(const fa::FwdArgs &args, hipStream_t stream) {
   using T = fa::FwdTile<D, KSPLIT>;
   fa::FwdArgs a = args;
   a.n_qtiles = (a.Sq + T::BM - 1) / T::BM;
   const int64_t grid = (int64_t)a.n_qtiles * a.B * a.H;
   if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
-  hipLaunchKernelGGL((fa::fa_fwd_kernel<D, CAUSAL, KSPLIT>), dim3((unsigned)grid), dim3(T::NT), 0,
+  hipLaunchKernelGGL((fa::fa_fwd_kernel<E, D, CAUSAL, KSPLIT>), dim3((unsigned)grid), dim3(T::NT), 0,
                      stream, a);
   return launch_status();
 }
 
-template <int D, bool CAUSAL>
+template <typename E, int D, bool CAUSAL>
 int launch_fwd(const fa::FwdArgs &a, hipStream_t stream) {
-  return row_split(a.Sq, (int64_t)a.B * a.H, CAUSAL) ? launch_fwd_split<D, CAUSAL, 2>(a, stream)
-                                                     : launch_fwd_split<D, CAUSAL, 1>(a, stream);
+  return row_split(a.Sq, (int64_t)a.B * a.H, CAUSAL) ? launch_fwd_split<E, D, CAUSAL, 2>(a, stream)
+                                                     : launch_fwd_split<E, D, CAUSAL, 1>(a, stream);
 }
 
-template <int D>
+template <typename E, int D>
 int launch_pre(const fa::PreArgs &a, hipStream_t stream) {
   constexpr int RPB = 256 / (D / 8);
   const int64_t rows = (int64_t)a.B * a.H * a.S;
   const int64_t grid = (rows + RPB - 1) / RPB;
   if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
-  hipLaunchKernelGGL((fa::fa_bwd_preprocess_kernel<D>), dim3((unsigned)grid), dim3(256), 0,
+  hipLaunchKernelGGL((fa::fa_bwd_preprocess_kernel<E, D>), dim3((unsigned)grid), dim3(256), 0,
                      stream, a);
   return launch_status();
 }
 
-template <int D, bool CAUSAL, int SPLIT>
+template <typename E, int D, bool CAUSAL, int SPLIT>
 int launch_dkdv_split(const fa::BwdArgs &args, hipStream_t stream) {
   using T = fa::DkdvTile<D, SPLIT>;
   fa::BwdArgs a = args;
   a.n_blocks = (a.Sk + T::BK - 1) / T::BK;
   const int64_t grid = (int64_t)a.n_blocks * a.B * a.Hk;
   if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
-  hipLaunchKernelGGL((fa::fa_bwd_dkdv_kernel<D, CAUSAL, SPLIT>), dim3((unsigned)grid), dim3(T::NT),
+  hipLaunchKernelGGL((fa::fa_bwd_dkdv_kernel<E, D, CAUSAL, SPLIT>), dim3((unsigned)grid), dim3(T::NT),
                      0, stream, a);
   return launch_status();
 }
 
-template <int D, bool CAUSAL, int SPLIT>
+template <typename E, int D, bool CAUSAL, int SPLIT>
 int launch_dq_split(const fa::BwdArgs &args, hipStream_t stream) {
   using T = fa::DqTile<D, SPLIT>;
   fa::BwdArgs a = args;
   a.n_blocks = (a.Sq + T::BM - 1) / T::BM;
   const int64_t grid = (int64_t)a.n_blocks * a.B * a.H;
   if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
-  hipLaunchKernelGGL((fa::fa_bwd_dq_kernel<D, CAUSAL, SPLIT>), dim3((unsigned)grid), dim3(T::NT), 0,
+  hipLaunchKernelGGL((fa::fa_bwd_dq_kernel<E, D, CAUSAL, SPLIT>), dim3((unsigned)grid), dim3(T::NT), 0,
                      stream, a);
   return launch_status();
 }
 
-template <int D, bool CAUSAL>
+template <typename E, int D, bool CAUSAL>
 int launch_dkdv(const fa::BwdArgs &a, hipStream_t stream) {
-  return row_split(a.Sk, (int64_t)a.B * a.Hk, CAUSAL) ? launch_dkdv_split<D, CAUSAL, 2>(a, stream)
-                                                      : launch_dkdv_split<D, CAUSAL, 1>(a, stream);
+  return row_split(a.Sk, (int64_t)a.B * a.Hk, CAUSAL) ? launch_dkdv_split<E, D, CAUSAL, 2>(a, stream)
+                                                      : launch_dkdv_split<E, D, CAUSAL, 1>(a, stream);
 }
 
-template <int D, bool CAUSAL>
+template <typename E, int D, bool CAUSAL>
 int launch_dq(const fa::BwdArgs &a, hipStream_t stream) {
-  return row_split(a.Sq, (int64_t)a.B * a.H, CAUSAL) ? launch_dq_split<D, CAUSAL, 2>(a, stream)
-                                                     : launch_dq_split<D, CAUSAL, 1>(a, stream);
+  return row_split(a.Sq, (int64_t)a.B * a.H, CAUSAL) ? launch_dq_split<E, D, CAUSAL, 2>(a, stream)
+                                                     : launch_dq_split<E, D, CAUSAL, 1>(a, stream);
 }
 
-template <bool CAUSAL>
-int dispatch_dkdv(int D, const fa::BwdArgs &a, hipStream_t st) {
-  switch (D) {
-    case 32: return launch_dkdv<32, CAUSAL>(a, st);
-    case 64: return launch_dkdv<64, CAUSAL>(a, st);
-    default: return launch_dkdv<128, CAUSAL>(a, st);
-  }
-}
-
-template <bool CAUSAL>
-int dispatch_dq(int D, const fa::BwdArgs &a, hipStream_t st) {
-  switch (D) {
-    case 32: return launch_dq<32, CAUSAL>(a, st);
-    case 64: return launch_dq<64, CAUSAL>(a, st);
-    default: return launch_dq<128, CAUSAL>(a, st);
-  }
-}
+// (dtype, D, causal) -> one instantiation of launcher L<E, D, CAUSAL>.
+#define FA_DISPATCH(L, s, causal, a, st)                                              \
+  do {                                                                                \
+    if ((s).dtype == FA_DTYPE_BF16) {                                                 \
+      switch ((s).D) {                                                                \
+        case 32: return causal ? L<fa::bf16, 32, true>(a, st) : L<fa::bf16, 32, false>(a, st);   \
+        case 64: return causal ? L<fa::bf16, 64, true>(a, st) : L<fa::bf16, 64, false>(a, st);   \
+        default: return causal ? L<fa::bf16, 128, true>(a, st) : L<fa::bf16, 128, false>(a, st); \
+      }                                                                               \
+    }                                                                                 \
+    switch ((s).D) {                                                                  \
+      case 32: return causal ? L<fa::f16, 32, true>(a, st) : L<fa::f16, 32, false>(a, st);       \
+      case 64: return causal ? L<fa::f16, 64, true>(a, st) : L<fa::f16, 64, false>(a, st);       \
+      default: return causal ? L<fa::f16, 128, true>(a, st) : L<fa::f16, 128, false>(a, st);     \
+    }                                                                                 \
+  } while (0)
 
 int run_fwd(const void *q, const void *k, const void *v, void *o, float *lse, const Shape &s,
             const int64_t *q_st, const int64_t *k_st, const int64_t *v_st, const int64_t *o_st,
@@ -216,11 +217,7 @@ int run_fwd(const void *q, const void *k, const void *v, void *o, float *lse, co
   a.c = kernel_scale(sm_scale);
   a.neg = sm_scale < 0.0f;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  switch (s.D) {
-    case 32: return causal ? launch_fwd<32, true>(a, st) : launch_fwd<32, false>(a, st);
-    case 64: return causal ? launch_fwd<64, true>(a, st) : launch_fwd<64, false>(a, st);
-    default: return causal ? launch_fwd<128, true>(a, st) : launch_fwd<128, false>(a, st);
-  }
+  FA_DISPATCH(launch_fwd, s, causal, a, st);
 }
 
 int run_pre(const void *o, const void *dout, float *delta, const Shape &s, const int64_t *o_st,
@@ -239,10 +236,11 @@ int run_pre(const void *o, const void *dout, float *delta, const Shape &s, const
   a.S = s.Sq;
   a.H = s.H;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool bf = s.dtype == FA_DTYPE_BF16;
   switch (s.D) {
-    case 32: return launch_pre<32>(a, st);
-    case 64: return launch_pre<64>(a, st);
-    default: return launch_pre<128>(a, st);
+    case 32: return bf ? launch_pre<fa::bf16, 32>(a, st) : launch_pre<fa::f16, 32>(a, st);
+    case 64: return bf ? launch_pre<fa::bf16, 64>(a, st) : launch_pre<fa::f16, 64>(a, st);
+    default: return bf ? launch_pre<fa::bf16, 128>(a, st) : launch_pre<fa::f16, 128>(a, st);
   }
 }
 
@@ -299,7 +297,7 @@ int run_dkdv(const void *dout, const void *q, const void *k, const void *v, cons
   a.dv_ss = dv_st[1];
   a.dv_sh = dv_st[2];
   hipStream_t st = static_cast<hipStream_t>(stream);
-  return causal ? dispatch_dkdv<true>(s.D, a, st) : dispatch_dkdv<false>(s.D, a, st);
+  FA_DISPATCH(launch_dkdv, s, causal, a, st);
 }
 
 int run_dq(const void *dout, const void *q, const void *k, const void *v, const float *lse,
@@ -315,7 +313,7 @@ int run_dq(const void *dout, const void *q, const void *k, const void *v, const 
   a.dq_ss = dq_st[1];
   a.dq_sh = dq_st[2];
   hipStream_t st = static_cast<hipStream_t>(stream);
-  return causal ? dispatch_dq<true>(s.D, a, st) : dispatch_dq<false>(s.D, a, st);
+  FA_DISPATCH(launch_dq, s, causal, a, st);
 }
 
 size_t delta_bytes(int B, int Sq, int H) {
@@ -351,7 +349,7 @@ int run_bwd(const void *dout, const void *q, const void *k, const void *v, const
                 stream);
 }
 
-Shape square(int B, int S, int H, int D) { return Shape{B, S, S, H, H, D}; }
+Shape square(int B, int S, int H, int D) { return Shape{B, S, S, H, H, D, FA_DTYPE_F16}; }
 
 }  // namespace
 
@@ -375,6 +373,7 @@ const char *fa_strerror(int status) {
     case FA_ERR_WORKSPACE: return "workspace is NULL or smaller than fa_bwd_workspace_bytes()";
     case FA_ERR_TOO_LARGE: return "sizes exceed the kernel's index or grid limits";
     case FA_ERR_LAUNCH: return "the HIP runtime rejected a kernel launch";
+    case FA_ERR_DTYPE: return "unsupported dtype (supported: FA_DTYPE_F16, FA_DTYPE_BF16)";
     default: return "unknown status code";
   }
 }
@@ -392,8 +391,8 @@ int fa_fwd_gqa(const void *q, const void *k, const void *v, void *o, float *lse,
                int B, int Sq, int Sk, int H, int Hk, int D,
                const int64_t q_strides[4], const int64_t k_strides[4],
                const int64_t v_strides[4], const int64_t o_strides[4],
-               float sm_scale, int causal, void *stream) {
-  return run_fwd(q, k, v, o, lse, Shape{B, Sq, Sk, H, Hk, D}, q_strides, k_strides, v_strides,
+               float sm_scale, int causal, int dtype, void *stream) {
+  return run_fwd(q, k, v, o, lse, Shape{B, Sq, Sk, H, Hk, D, dtype}, q_strides, k_strides, v_strides,
                  o_strides, sm_scale, causal, stream);
 }
 
@@ -433,9 +432,9 @@ int fa_bwd_gqa(const void *dout, const void *q, const void *k, const void *v,
                const int64_t k_strides[4], const int64_t v_strides[4],
                const int64_t o_strides[4], const int64_t dq_strides[4],
                const int64_t dk_strides[4], const int64_t dv_strides[4],
-               float sm_scale, int causal, void *stream) {
+               float sm_scale, int causal, int dtype, void *stream) {
   return run_bwd(dout, q, k, v, o, lse, dq, dk, dv, workspace, workspace_bytes,
-                 Shape{B, Sq, Sk, H, Hk, D}, do_strides, q_strides, k_strides, v_strides,
+                 Shape{B, Sq, Sk, H, Hk, D, dtype}, do_strides, q_strides, k_strides, v_strides,
                  o_strides, dq_strides, dk_strides, dv_strides, sm_scale, causal, stream);
 }
 

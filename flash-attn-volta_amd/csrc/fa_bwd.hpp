@@ -23,17 +23,18 @@
 // is staged row-major (kperm row order) with 16-byte buffer loads; the
 // transposed operands (Q^T, dO^T, K^T) come from ds_read_b64_tr_b16.
 //
-// dS scaling.  dS is rounded to fp16 for the MFMAs.  Its magnitude follows
-// the upstream gradient and can sit far below the fp16 normal range (a
-// loss averaged over thousands of tokens gives |dS| ~ 1e-9 deep in a
-// network), where fp16 would flush it to zero.  Each lane therefore keeps
-// a running power-of-two scale 2^e for its output row (a key in dK, a query
-// in dQ), chosen from the largest |dS| it has produced so that scaled values
-// stay in [2^10, 2^15]: dS * 2^e is rounded to fp16, the fp32 accumulator is
-// rescaled exactly (by a power of two) whenever e changes, and the result is
-// divided by 2^e at the end.  Scaling by powers of two changes no rounding
-// in the normal range, never overflows fp16, and depends only on the lane's
-// own data, so results stay deterministic.
+// dS scaling.  dS is rounded to the element type (fp16 or bf16) for the
+// MFMAs.  Its magnitude follows the upstream gradient and can sit far below
+// the fp16 normal range (a loss averaged over thousands of tokens gives
+// |dS| ~ 1e-9 deep in a network), where fp16 would flush it to zero.  Each
+// lane therefore keeps a running power-of-two scale 2^e for its output row
+// (a key in dK, a query in dQ), chosen from the largest |dS| it has
+// produced so that scaled values stay in [2^10, 2^15]: dS * 2^e is rounded,
+// the fp32 accumulator is rescaled exactly (by a power of two) whenever e
+// changes, and the result is divided by 2^e at the end.  Scaling by powers
+// of two changes no rounding in the normal range, never overflows, and
+// depends only on the lane's own data, so results stay deterministic (bf16,
+// with fp32's exponent range, does not need it but loses nothing by it).
 #pragma once
 
 #include "fa_common.hpp"
@@ -67,7 +68,7 @@ struct PreArgs {
 // delta[b,h,s] = sum_d O * dO.  Each group of D/8 lanes reduces one row from
 // 16-byte loads; rows are enumerated in (b, h, s) order so delta writes are
 // contiguous.
-template <int D>
+template <typename E, int D>
 __global__ __launch_bounds__(256) void fa_bwd_preprocess_kernel(PreArgs a) {
   constexpr int LPR = D / 8;               // lanes per row
   constexpr int RPB = 256 / LPR;           // rows per block
@@ -80,8 +81,8 @@ __global__ __launch_bounds__(256) void fa_bwd_preprocess_kernel(PreArgs a) {
     const int s = (int)(row % a.S);
     const int64_t bh = row / a.S;
     const int h = (int)(bh % a.H), b = (int)(bh / a.H);
-    const half8 ov = *(const half8 *)(a.o.head(b, h) + (int64_t)s * a.o.ss + 8 * part);
-    const half8 gv = *(const half8 *)(a.dout.head(b, h) + (int64_t)s * a.dout.ss + 8 * part);
+    const vec8<E> ov = ld8<E>(a.o.head(b, h) + (int64_t)s * a.o.ss + 8 * part);
+    const vec8<E> gv = ld8<E>(a.dout.head(b, h) + (int64_t)s * a.dout.ss + 8 * part);
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc = __builtin_fmaf((float)ov[j], (float)gv[j], acc);
   }
@@ -137,28 +138,28 @@ __device__ __forceinline__ float absmax16(const floatx16 &x) {
 }
 
 // Store a D^T x 32 accumulator set (lane = row `row`, slots = columns) as
-// fp16 row `row` of a (.., D) tensor, scaled by `mul`.
-template <int D>
-__device__ __forceinline__ void store_row_fp16(f16 *dst, const floatx16 (&acc)[D / 32], float mul, int g) {
+// row `row` of a (.., D) tensor of element type E, scaled by `mul`.
+template <typename E, int D>
+__device__ __forceinline__ void store_row(f16 *dst, const floatx16 (&acc)[D / 32], float mul, int g) {
 #pragma unroll
   for (int d = 0; d < D / 32; ++d) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      half4 v4;
+      vec4<E> v4;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) v4[j] = (f16)(acc[d][4 * r + j] * mul);
-      *(half4 *)(dst + 32 * d + c_row(4 * r, g)) = v4;
+      for (int j = 0; j < 4; ++j) v4[j] = (E)(acc[d][4 * r + j] * mul);
+      *(vec4<E> *)(dst + 32 * d + c_row(4 * r, g)) = v4;
     }
   }
 }
 
 // Load a lane's D/16 B-operand fragments of row `row` (clamped to S-1).
-template <int D>
-__device__ __forceinline__ void load_row_frags(half8 (&f)[D / 16], const f16 *head, int64_t ss,
+template <typename E, int D>
+__device__ __forceinline__ void load_row_frags(vec8<E> (&f)[D / 16], const f16 *head, int64_t ss,
                                                int row, int S, int g) {
   const f16 *p = head + (int64_t)min(row, S - 1) * ss + 8 * g;
 #pragma unroll
-  for (int c = 0; c < D / 16; ++c) f[c] = *(const half8 *)(p + 16 * c);
+  for (int c = 0; c < D / 16; ++c) f[c] = ld8<E>(p + 16 * c);
 }
 
 // ---------------------------------------------------------------------------
@@ -216,7 +217,7 @@ struct DkdvTile {
   static_assert(64 * (D / 2) * 4 <= LDS_TILE * 2, "a merge buffer must fit in one stage");
 };
 
-template <int D, bool CAUSAL, int SPLIT>
+template <typename E, int D, bool CAUSAL, int SPLIT>
 __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
   using T = DkdvTile<D, SPLIT>;
   constexpr int BK = T::BK, BQ = T::BQ, NSUB = T::NSUB;
@@ -244,23 +245,24 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
   const int wk0 = k0 + 32 * kg;
   const int key = wk0 + l32;
 
-
-  // K^T and V^T fragments (B operands): K[key][16c + 8g .. +7].  K is
-  // pre-multiplied by +-ck = +-min(c, 1) and rounded to fp16 (as the
+  // K^T and V^T fragments (B operands): K[key][16c + 8g .. +7].  For fp16,
+  // K is pre-multiplied by +-ck = +-min(c, 1) and rounded to fp16 (as the
   // reference pre-scales K^T, triton_fa_bwd.py:355), so the S MFMAs produce
   // ck * s directly; ck <= 1 keeps the product inside the fp16 range.  The
-  // rest of c, cr = c / ck, is 1 unless |sm_scale| > ln 2.
-  half8 kf[D / 16], vf[D / 16];
-  load_row_frags<D>(kf, a.k.head(b, hk), a.k.ss, key, Sk, g);
-  load_row_frags<D>(vf, a.v.head(b, hk), a.v.ss, key, Sk, g);
-  const float ck = fminf(a.c, 1.0f);
+  // rest of c, cr = c / ck, is 1 unless |sm_scale| > ln 2.  bf16 keeps K
+  // unscaled (ck = 1: a second bf16 rounding would cost 8-bit accuracy),
+  // only its sign follows sm_scale.
+  vec8<E> kf[D / 16], vf[D / 16];
+  load_row_frags<E, D>(kf, a.k.head(b, hk), a.k.ss, key, Sk, g);
+  load_row_frags<E, D>(vf, a.v.head(b, hk), a.v.ss, key, Sk, g);
+  const float ck = std::is_same<E, f16>::value ? fminf(a.c, 1.0f) : 1.0f;
   const float cr = a.c / ck;
   {
     const float kmul = a.neg ? -ck : ck;
 #pragma unroll
     for (int c = 0; c < D / 16; ++c)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) kf[c][j] = (f16)((float)kf[c][j] * kmul);
+      for (int j = 0; j < 8; ++j) kf[c][j] = (E)((float)kf[c][j] * kmul);
   }
 
   floatx16 dk[D / 32], dv[D / 32];
@@ -380,8 +382,8 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
       const f16 *gr = do_st(stc) + 32 * qs * D;
 #pragma unroll
       for (int cc = 0; cc < D / 16; ++cc) {
-        sacc = mfma32(*(const half8 *)(qr + a_off[cc]), kf[cc], sacc);
-        dpacc = mfma32(*(const half8 *)(gr + a_off[cc]), vf[cc], dpacc);
+        sacc = mfma32(ld8<E>(qr + a_off[cc]), kf[cc], sacc);
+        dpacc = mfma32(ld8<E>(gr + a_off[cc]), vf[cc], dpacc);
       }
     };
     // Softmax-gradient of sub-block sb and its dV / dK MFMAs.
@@ -421,11 +423,11 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
             for (int i = 0; i < 16; ++i) dk[d][i] *= f;
         }
       }
-      half8 pf[2], dsf[2];
+      vec8<E> pf[2], dsf[2];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        pf[i >> 3][i & 7] = (f16)p[i];
-        dsf[i >> 3][i & 7] = (f16)(ds[i] * sc.mul);
+        pf[i >> 3][i & 7] = (E)p[i];
+        dsf[i >> 3][i & 7] = (E)(ds[i] * sc.mul);
       }
       // dV^T += dO^T P ; dK^T += Q^T dS   (k = queries ms + 16hh + 8g ..)
 #pragma unroll
@@ -434,8 +436,8 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
         const int rb = (32 * qs + 16 * hh) * D;
 #pragma unroll
         for (int d = 0; d < D / 32; ++d) {
-          dv[d] = mfma32(load_tr_pair(do_st(stc) + rb + t_off[d], 8 * D), pf[hh], dv[d]);
-          dk[d] = mfma32(load_tr_pair(q_st(stc) + rb + t_off[d], 8 * D), dsf[hh], dk[d]);
+          dv[d] = mfma32(load_tr_pair<E>(do_st(stc) + rb + t_off[d], 8 * D), pf[hh], dv[d]);
+          dk[d] = mfma32(load_tr_pair<E>(q_st(stc) + rb + t_off[d], 8 * D), dsf[hh], dk[d]);
         }
       }
     };
@@ -479,8 +481,8 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
     dk_mul = a.sm_scale;
   }
   if (key < Sk) {
-    store_row_fp16<D>(a.dk + b * a.dk_sb + hk * a.dk_sh + (int64_t)key * a.dk_ss, dk, dk_mul, g);
-    store_row_fp16<D>(a.dv + b * a.dv_sb + hk * a.dv_sh + (int64_t)key * a.dv_ss, dv, 1.0f, g);
+    store_row<E, D>(a.dk + b * a.dk_sb + hk * a.dk_sh + (int64_t)key * a.dk_ss, dk, dk_mul, g);
+    store_row<E, D>(a.dv + b * a.dv_sb + hk * a.dv_sh + (int64_t)key * a.dv_ss, dv, 1.0f, g);
   }
 }
 
@@ -505,7 +507,7 @@ struct DqTile {
   static_assert(64 * (D / 2) * 4 <= LDS_TILE * 2, "a merge buffer must fit in one K stage");
 };
 
-template <int D, bool CAUSAL, int SPLIT>
+template <typename E, int D, bool CAUSAL, int SPLIT>
 __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
   using T = DqTile<D, SPLIT>;
   constexpr int BM = T::BM, BN = T::BN, NSUB = T::NSUB;
@@ -534,9 +536,9 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
   const f16 *kb = a.k.head(b, hk);
   const f16 *vb = a.v.head(b, hk);
 
-  half8 qf[D / 16], gf[D / 16];
-  load_row_frags<D>(qf, a.q.head(b, h), a.q.ss, qrow, Sq, g);
-  load_row_frags<D>(gf, a.dout.head(b, h), a.dout.ss, qrow, Sq, g);
+  vec8<E> qf[D / 16], gf[D / 16];
+  load_row_frags<E, D>(qf, a.q.head(b, h), a.q.ss, qrow, Sq, g);
+  load_row_frags<E, D>(gf, a.dout.head(b, h), a.dout.ss, qrow, Sq, g);
   if (a.neg) {
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) qf[c] = neg8(qf[c]);
@@ -608,12 +610,12 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
       const int ks = NSUB * kh + sb;
       const f16 *kr = k_st(stc) + 32 * ks * D;
       const f16 *vr = v_st(stc) + 32 * ks * D;
-      sacc = mfma32(*(const half8 *)(kr + a_off[0]), qf[0], floatx16{});
-      dpacc = mfma32(*(const half8 *)(vr + a_off[0]), gf[0], dl_seed);
+      sacc = mfma32(ld8<E>(kr + a_off[0]), qf[0], floatx16{});
+      dpacc = mfma32(ld8<E>(vr + a_off[0]), gf[0], dl_seed);
 #pragma unroll
       for (int cc = 1; cc < D / 16; ++cc) {
-        sacc = mfma32(*(const half8 *)(kr + a_off[cc]), qf[cc], sacc);
-        dpacc = mfma32(*(const half8 *)(vr + a_off[cc]), gf[cc], dpacc);
+        sacc = mfma32(ld8<E>(kr + a_off[cc]), qf[cc], sacc);
+        dpacc = mfma32(ld8<E>(vr + a_off[cc]), gf[cc], dpacc);
       }
     };
     auto grad = [&](int sb, floatx16 &sacc, const floatx16 &dpacc) {
@@ -649,16 +651,16 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
           for (int i = 0; i < 16; ++i) ds[i] *= f;
         }
       }
-      half8 dsf[2];
+      vec8<E> dsf[2];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) dsf[i >> 3][i & 7] = (f16)ds[i];
+      for (int i = 0; i < 16; ++i) dsf[i >> 3][i & 7] = (E)ds[i];
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         // kperm rows 32ks + 16hh + 4g + (0..3) and +8: this 8-key slice
         const int rb = (32 * ks + 16 * hh) * D;
 #pragma unroll
         for (int d = 0; d < D / 32; ++d)
-          dq[d] = mfma32(load_tr_pair(k_st(stc) + rb + t_off[d], 8 * D), dsf[hh], dq[d]);
+          dq[d] = mfma32(load_tr_pair<E>(k_st(stc) + rb + t_off[d], 8 * D), dsf[hh], dq[d]);
       }
     };
 
@@ -687,7 +689,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
     dq_mul = a.sm_scale;
   }
   if (qrow < Sq)
-    store_row_fp16<D>(a.dq + b * a.dq_sb + h * a.dq_sh + (int64_t)qrow * a.dq_ss, dq, dq_mul, g);
+    store_row<E, D>(a.dq + b * a.dq_sb + h * a.dq_sh + (int64_t)qrow * a.dq_ss, dq, dq_mul, g);
 }
 
 }  // namespace fa

@@ -1,7 +1,11 @@
 // fa_common.hpp -- shared device helpers for the gfx950 FlashAttention kernels.
 //
-// Everything here is written for CDNA4 wave64 and the 32x32x16 fp16 MFMA
-// (v_mfma_f32_32x32x16_f16, 8 passes, 32768 FLOP per wave instruction).
+// Everything here is written for CDNA4 wave64 and the 32x32x16 16-bit MFMAs
+// (v_mfma_f32_32x32x16_f16 / _bf16, 8 passes, 32768 FLOP per wave
+// instruction).  Kernels are templated on the element type E (fp16 or
+// bf16); pointers, LDS tiles and DMA staging carry raw 16-bit values typed
+// `f16`, and only the fragments fed to the MFMAs and conversions are typed
+// E.
 //
 // MFMA fragment conventions used by every kernel (lane = 0..63,
 // l32 = lane % 32, g = lane / 32):
@@ -28,9 +32,13 @@
 namespace fa {
 
 typedef _Float16 f16;
+typedef __bf16 bf16;
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half2 __attribute__((ext_vector_type(2)));
+template <typename E> using vec8 = E __attribute__((ext_vector_type(8)));
+template <typename E> using vec4 = E __attribute__((ext_vector_type(4)));
+template <typename E> using vec2 = E __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx2 __attribute__((ext_vector_type(2)));
@@ -42,8 +50,12 @@ constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kNegInf = -__builtin_inff();
 constexpr float kPosInf = __builtin_inff();
 
-__device__ __forceinline__ floatx16 mfma32(half8 a, half8 b, floatx16 c) {
+__device__ __forceinline__ floatx16 mfma32(vec8<f16> a, vec8<f16> b, floatx16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ floatx16 mfma32(vec8<bf16> a, vec8<bf16> b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
 // Key (or query) index, inside a 32-block, of result slot i for lane group g.
@@ -84,8 +96,13 @@ __device__ __forceinline__ float max_xor32(float x) {
   return fmaxf(x, fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])));
 }
 
-// Sum of the two fp16 values of `p` accumulated into fp32 `acc`
-// (v_dot2_f32_f16 against (1, 1)).
+// Sum of the two 16-bit values of `p` accumulated into fp32 `acc`
+// (v_dot2_f32_f16 / v_dot2_f32_bf16 against (1, 1)).
+__device__ __forceinline__ float dot2_acc(vec2<bf16> p, float acc) {
+  const vec2<bf16> ones = {(bf16)1.0f, (bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(p, ones, acc, false);
+}
+
 __device__ __forceinline__ float dot2_acc(half2 p, float acc) {
   const half2 ones = {(f16)1.0f, (f16)1.0f};
   return __builtin_amdgcn_fdot2(p, ones, acc, false);
@@ -100,10 +117,11 @@ __device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
 }
 
 // Flip the sign of 8 packed fp16 values (exact).
-__device__ __forceinline__ half8 neg8(half8 x) {
+template <typename V>
+__device__ __forceinline__ V neg8(V x) {
   u32x4 u = __builtin_bit_cast(u32x4, x);
-  u ^= 0x80008000u;
-  return __builtin_bit_cast(half8, u);
+  u ^= 0x80008000u;   // flip the sign bit of each 16-bit value (fp16 and bf16 alike)
+  return __builtin_bit_cast(V, u);
 }
 
 // Buffer resource over rows [n0, S) of one (b, h) of a (B, S, H, D) tensor
@@ -217,14 +235,22 @@ struct DmaStager {
 // address of (row_lo + L/4, col0 + 16*((lane/16)%2) + 4*(L%4)) the lane
 // receives X[row_lo + j][col0 + lane % 32] in slots j = 0..3, and from the
 // block `hi` elements further the slots 4..7 (callers precompute p).
-__device__ __forceinline__ half8 load_tr_pair(const f16 *p, int hi) {
+// The transpose read moves 16-bit values without interpreting them, so one
+// fp16-typed read serves both element types (the result is bit-cast).
+template <typename E>
+__device__ __forceinline__ vec8<E> load_tr_pair(const f16 *p, int hi) {
   typedef __fp16 h4 __attribute__((vector_size(8)));
   h4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) h4 *)p);
   h4 up = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) h4 *)(p + hi));
-  half8 r;
-  r[0] = (f16)lo[0]; r[1] = (f16)lo[1]; r[2] = (f16)lo[2]; r[3] = (f16)lo[3];
-  r[4] = (f16)up[0]; r[5] = (f16)up[1]; r[6] = (f16)up[2]; r[7] = (f16)up[3];
-  return r;
+  const u32x2 a = __builtin_bit_cast(u32x2, lo), b = __builtin_bit_cast(u32x2, up);
+  const u32x4 r = {a[0], a[1], b[0], b[1]};
+  return __builtin_bit_cast(vec8<E>, r);
+}
+
+// 8 consecutive 16-bit values at p (16-byte aligned), as an E vector.
+template <typename E>
+__device__ __forceinline__ vec8<E> ld8(const f16 *p) {
+  return *reinterpret_cast<const vec8<E> *>(p);
 }
 
 // Kernel arguments shared by the forward and backward launches. Strides are

@@ -1,8 +1,8 @@
 // fa_fwd.hpp -- forward FlashAttention kernel for gfx950.
 //
 // Computes, for one (query tile, batch*head), O = softmax(c * Q K^T) V with an
-// online (streaming) softmax over key tiles, fp16 MFMA with fp32 accumulation,
-// and the natural-log row LSE.  Behaviour follows the reference forward
+// online (streaming) softmax over key tiles, fp16 or bf16 (E) MFMA with fp32
+// accumulation, and the natural-log row LSE.  Behaviour follows the reference forward
 // (flash_attn_volta/triton_fa.py:63-159): causal tiles above the diagonal are
 // skipped (:110-117), masked scores are -inf (:123-126), O = acc / l
 // (:146-150) and LSE = m + ln(l), +inf when a row saw no key (:152-159).
@@ -23,7 +23,7 @@
 //   * a lane owns one query row: the running max / sum and the O^T
 //     accumulator column live in that lane, the only cross-lane step is one
 //     v_permlane32_swap per key half for the row max;
-//   * probabilities are rounded to fp16 once and the row sum accumulates
+//   * probabilities are rounded to E once and the row sum accumulates
 //     those rounded values (v_dot2_f32_f16), so numerator and denominator
 //     see the same weights;
 //   * the accumulator is rescaled only when a row max grows by more than
@@ -77,7 +77,7 @@ struct FwdTile {
 // flight: it pays when the grid is too small to fill the GPU, and for
 // causal attention, whose last query tile walks every key tile.  The
 // launcher picks KSPLIT from the grid size.
-template <int D, bool CAUSAL, int KSPLIT>
+template <typename E, int D, bool CAUSAL, int KSPLIT>
 __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   using T = FwdTile<D, KSPLIT>;
   constexpr int NSUB = T::NSUB;
@@ -149,16 +149,16 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   auto dead = [&](int n0, int sb) { return CAUSAL && sub_key(n0, sb) > wq0 + 31 + off; };
 
   // ---- S^T = K Q^T for this wave's sub-blocks of a tile
-  half8 qf[D / 16];
+  vec8<E> qf[D / 16];
   auto qk = [&](auto sc, int n0, floatx16 (&s)[NSUB]) {
 #pragma unroll
     for (int sb = 0; sb < NSUB; ++sb) {
       // dead sub-blocks are skipped; the diagonal mask overwrites them
       if (dead(n0, sb)) continue;
       const f16 *kr = k_sl(sc) + 32 * (NSUB * kh + sb) * D;
-      floatx16 acc = mfma32(*(const half8 *)(kr + a_off[0]), qf[0], floatx16{});
+      floatx16 acc = mfma32(ld8<E>(kr + a_off[0]), qf[0], floatx16{});
 #pragma unroll
-      for (int cc = 1; cc < D / 16; ++cc) acc = mfma32(*(const half8 *)(kr + a_off[cc]), qf[cc], acc);
+      for (int cc = 1; cc < D / 16; ++cc) acc = mfma32(ld8<E>(kr + a_off[cc]), qf[cc], acc);
       s[sb] = acc;
     }
   };
@@ -175,7 +175,7 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
     const int qr = min(qrow, Sq - 1);
     const f16 *qp = qb + (int64_t)qr * a.q.ss + 8 * g;
 #pragma unroll
-    for (int c = 0; c < D / 16; ++c) qf[c] = *(const half8 *)(qp + 16 * c);
+    for (int c = 0; c < D / 16; ++c) qf[c] = ld8<E>(qp + 16 * c);
     if (a.neg) {
 #pragma unroll
       for (int c = 0; c < D / 16; ++c) qf[c] = neg8(qf[c]);
@@ -251,19 +251,19 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
       }
       const float neg_m = (m_run == kNegInf) ? 0.0f : -m_run;
 
-      // ---- P = exp2(c*s - m) rounded to fp16; O^T += V^T P^T
+      // ---- P = exp2(c*s - m) rounded to E; O^T += V^T P^T
 #pragma unroll
       for (int sb = 0; sb < NSUB; ++sb) {
         if (dead(n0, sb)) continue;
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
-          half8 pf;
+          vec8<E> pf;
 #pragma unroll
           for (int j = 0; j < 8; j += 2) {
-            half2 pr = __builtin_convertvector(
+            vec2<E> pr = __builtin_convertvector(
                 (floatx2){fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + j], c, neg_m)),
                           fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + j + 1], c, neg_m))},
-                half2);
+                vec2<E>);
             l_run = dot2_acc(pr, l_run);
             pf[j] = pr[0];
             pf[j + 1] = pr[1];
@@ -272,7 +272,7 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
           const int rb = (32 * (NSUB * kh + sb) + 16 * hh) * D;
 #pragma unroll
           for (int d = 0; d < D / 32; ++d)
-            oacc[d] = mfma32(load_tr_pair(v_sl(CP{}) + rb + t_off[d], 8 * D), pf, oacc[d]);
+            oacc[d] = mfma32(load_tr_pair<E>(v_sl(CP{}) + rb + t_off[d], 8 * D), pf, oacc[d]);
         }
       }
     }
@@ -323,10 +323,10 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
     for (int d = 0; d < D / 32; ++d) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        half4 v4;
+        vec4<E> v4;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v4[j] = (f16)(oacc[d][4 * r + j] * inv);
-        *(half4 *)(orow + 32 * d + c_row(4 * r, g)) = v4;
+        for (int j = 0; j < 4; ++j) v4[j] = (E)(oacc[d][4 * r + j] * inv);
+        *(vec4<E> *)(orow + 32 * d + c_row(4 * r, g)) = v4;
       }
     }
     if (a.lse != nullptr && g == 0) {

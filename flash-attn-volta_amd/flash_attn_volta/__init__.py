@@ -18,8 +18,8 @@ q, k, v, out: (batch, seq, n_heads, head_dim) fp16; lse: (B, H, N) fp32.
 Beyond the reference (its wrapper requires q, k, v of one shape):
     flash_attn_forward_gqa / flash_attn_backward_gqa / flash_attn_gqa
         grouped-query and multi-query attention, k and v (B, Sk, Hk, D)
-        with H a multiple of Hk, and Sq != Sk with a bottom-right causal
-        mask (KV-cache prefill continuation).
+        with H a multiple of Hk, Sq != Sk with a bottom-right causal
+        mask (KV-cache prefill continuation), and bf16 as well as fp16.
 """
 
 from .forward import flash_attn_forward, flash_attn_forward_gqa, flash_attn_volta

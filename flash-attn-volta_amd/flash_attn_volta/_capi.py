@@ -14,7 +14,7 @@ import threading
 LIB_NAME = "libfa_mi355x.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # status codes (enum fa_status)
 FA_OK = 0
@@ -27,6 +27,11 @@ FA_ERR_SCALE = -6
 FA_ERR_WORKSPACE = -7
 FA_ERR_TOO_LARGE = -8
 FA_ERR_LAUNCH = -9
+FA_ERR_DTYPE = -10
+
+# element types (enum fa_dtype)
+FA_DTYPE_F16 = 0
+FA_DTYPE_BF16 = 1
 
 # Every symbol include/fa_mi355x.h declares.
 EXPORTED_SYMBOLS = (
@@ -74,7 +79,7 @@ def _declare(lib):
     lib.fa_fwd_gqa.restype = _ci
     lib.fa_fwd_gqa.argtypes = [_vp, _vp, _vp, _vp, _vp, _ci, _ci, _ci, _ci, _ci, _ci,
                                _i64x4, _i64x4, _i64x4, _i64x4,
-                               ctypes.c_float, _ci, _vp]
+                               ctypes.c_float, _ci, _ci, _vp]
     lib.fa_bwd_preprocess.restype = _ci
     lib.fa_bwd_preprocess.argtypes = [_vp, _vp, _vp, _ci, _ci, _ci, _ci, _i64x4, _i64x4, _vp]
     lib.fa_bwd_workspace_bytes.restype = ctypes.c_size_t
@@ -94,7 +99,7 @@ def _declare(lib):
                                _ci, _ci, _ci, _ci, _ci, _ci,
                                _i64x4, _i64x4, _i64x4, _i64x4,
                                _i64x4, _i64x4, _i64x4, _i64x4,
-                               ctypes.c_float, _ci, _vp]
+                               ctypes.c_float, _ci, _ci, _vp]
     lib.fa_bwd_dkdv.restype = _ci
     lib.fa_bwd_dkdv.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                 _ci, _ci, _ci, _ci,

@@ -80,7 +80,7 @@ class _FlashAttnGqaFn(torch.autograd.Function):
 def flash_attn_gqa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                    causal: bool = False, sm_scale: float | None = None) -> torch.Tensor:
     """Autograd-aware grouped-query attention (no counterpart in the
-    reference): q (B, Sq, H, D), k and v (B, Sk, Hk, D) fp16 with H a
-    multiple of Hk; causal masks bottom-right aligned (query i sees keys
-    j <= i + Sk - Sq).  Returns (B, Sq, H, D) fp16."""
+    reference): q (B, Sq, H, D), k and v (B, Sk, Hk, D), fp16 or bf16, with H
+    a multiple of Hk; causal masks bottom-right aligned (query i sees keys
+    j <= i + Sk - Sq).  Returns (B, Sq, H, D) in the input dtype."""
     return _FlashAttnGqaFn.apply(q, k, v, causal, sm_scale)

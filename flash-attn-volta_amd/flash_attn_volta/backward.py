@@ -14,8 +14,8 @@ import math
 import torch
 
 from . import _capi
-from .forward import (NATIVE_HEAD_DIMS, SUPPORTED_HEAD_DIMS, _check_gqa, _kernel_ready, _on_device,
-                      _pad_d, _require, _stream_ptr, kernel_strides)
+from .forward import (_DTYPES, NATIVE_HEAD_DIMS, SUPPORTED_HEAD_DIMS, _check_gqa, _kernel_ready,
+                      _on_device, _pad_d, _require, _stream_ptr, kernel_strides)
 
 
 def flash_attn_backward(
@@ -70,8 +70,8 @@ def _run_bwd(do, q, k, v, o, lse, causal, sm_scale, gqa):
     Sk, Hk = k.shape[1], k.shape[2]
     do, q, k, v, o = (_kernel_ready(t) for t in (do, q, k, v, o))
     lse = lse.contiguous()
-    dq = torch.empty((B, N, H, D), dtype=torch.float16, device=q.device)
-    dk = torch.empty((B, Sk, Hk, D), dtype=torch.float16, device=q.device)
+    dq = torch.empty((B, N, H, D), dtype=q.dtype, device=q.device)
+    dk = torch.empty((B, Sk, Hk, D), dtype=q.dtype, device=q.device)
     dv = torch.empty_like(dk)
     if dq.numel() == 0 or dk.numel() == 0:
         # nothing attends to anything: every gradient is zero
@@ -88,7 +88,8 @@ def _run_bwd(do, q, k, v, o, lse, causal, sm_scale, gqa):
             rc = lib.fa_bwd_gqa(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
                                 o.data_ptr(), lse.data_ptr(), dq.data_ptr(), dk.data_ptr(),
                                 dv.data_ptr(), ws.data_ptr(), ws_bytes, B, N, Sk, H, Hk, D, *st,
-                                float(sm_scale), int(bool(causal)), _stream_ptr(q.device))
+                                float(sm_scale), int(bool(causal)), _DTYPES[q.dtype],
+                                _stream_ptr(q.device))
         else:
             rc = lib.fa_bwd(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                             lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
@@ -111,10 +112,12 @@ def flash_attn_backward_gqa(
     """Backward of ``flash_attn_forward_gqa`` (no counterpart in the
     reference).  do, q, o: (B, Sq, H, D); k, v: (B, Sk, Hk, D); lse:
     (B, H, Sq).  Returns dq (B, Sq, H, D) and dk, dv (B, Sk, Hk, D), the
-    latter summed over the query heads that share each key/value head."""
+    latter summed over the query heads that share each key/value head.
+    fp16 or bf16 (every tensor alike, gradients in the same dtype)."""
     _require(q.is_cuda and k.is_cuda and v.is_cuda and o.is_cuda and do.is_cuda,
              "tensors must be on CUDA")
-    _require(q.dtype == torch.float16 == k.dtype == v.dtype == o.dtype == do.dtype, "fp16 only")
+    _require(q.dtype in _DTYPES and q.dtype == k.dtype == v.dtype == o.dtype == do.dtype,
+             "fp16 or bf16 only, all alike")
     _require(lse.dtype == torch.float32, "lse must be fp32")
     _check_gqa(q, k, v)
     _require(q.shape == o.shape == do.shape, "q, o and do shapes differ")

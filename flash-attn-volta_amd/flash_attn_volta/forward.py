@@ -139,12 +139,15 @@ def _forward(q, k, v, causal, sm_scale, return_softmax_lse, gqa):
     return out
 
 
+_DTYPES = {torch.float16: _capi.FA_DTYPE_F16, torch.bfloat16: _capi.FA_DTYPE_BF16}
+
+
 def _run_fwd(q, k, v, causal, sm_scale, write_lse, gqa):
     lib = _capi.load()
     B, N, H, D = q.shape
     Sk, Hk = k.shape[1], k.shape[2]
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
-    out = torch.empty((B, N, H, D), dtype=torch.float16, device=q.device)
+    out = torch.empty((B, N, H, D), dtype=q.dtype, device=q.device)
     lse = torch.empty((B, H, N), dtype=torch.float32, device=q.device) if write_lse else None
     if out.numel() == 0 or Sk == 0:
         # no query, or no key: every row sees nothing (O = 0, LSE = +inf)
@@ -158,7 +161,8 @@ def _run_fwd(q, k, v, causal, sm_scale, write_lse, gqa):
         if gqa:
             rc = lib.fa_fwd_gqa(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse_ptr,
                                 B, N, Sk, H, Hk, D, *st,
-                                float(sm_scale), int(bool(causal)), _stream_ptr(q.device))
+                                float(sm_scale), int(bool(causal)), _DTYPES[q.dtype],
+                                _stream_ptr(q.device))
         else:
             rc = lib.fa_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse_ptr,
                             B, N, H, D, *st,
@@ -194,16 +198,18 @@ def flash_attn_forward_gqa(
     flash_attn_volta/patch_hf.py:145-162, 186-188).
 
     Args:
-        q: (B, Sq, H, D) fp16 on the GPU; k, v: (B, Sk, Hk, D) fp16 with H a
-            multiple of Hk.  Query head h uses key/value head h // (H // Hk),
-            the head order of HuggingFace's ``repeat_kv``.
+        q: (B, Sq, H, D) on the GPU; k, v: (B, Sk, Hk, D) with H a multiple
+            of Hk.  Query head h uses key/value head h // (H // Hk), the head
+            order of HuggingFace's ``repeat_kv``.  fp16 or bf16 (all three
+            alike; the output has the same dtype, accumulation is fp32).
         causal: bottom-right aligned mask: query i sees key j iff
             j <= i + Sk - Sq (a query with no visible key gets 0 output and
             +inf LSE).  With Sq == Sk it is the usual causal mask.
         sm_scale, return_softmax_lse: as in ``flash_attn_forward``.
     """
     _require(q.is_cuda and k.is_cuda and v.is_cuda, "tensors must be on CUDA")
-    _require(q.dtype == torch.float16 == k.dtype == v.dtype, "fp16 only")
+    _require(q.dtype in _DTYPES and q.dtype == k.dtype == v.dtype,
+             f"fp16 or bf16 only, all alike (got {q.dtype}, {k.dtype}, {v.dtype})")
     _require(q.device == k.device == v.device, "q, k, v must be on one device")
     _check_gqa(q, k, v)
     D = q.shape[3]

@@ -178,15 +178,18 @@ def flash_attn_volta_attention(
                                            sliding_window=sliding_window, **kwargs)
 
     out_dtype = query.dtype
-    q = query.transpose(1, 2).to(torch.float16)
-    k = key.transpose(1, 2).to(torch.float16)
-    v = value.transpose(1, 2).to(torch.float16)
+    # bf16 models stay in bf16 (their activations may not fit fp16); the
+    # rest run in fp16 like the reference (patch_hf.py:473-475)
+    kdt = torch.bfloat16 if out_dtype == torch.bfloat16 else torch.float16
+    q = query.transpose(1, 2).to(kdt)
+    k = key.transpose(1, 2).to(kdt)
+    v = value.transpose(1, 2).to(kdt)
     if scaling is None:
         scaling = query.shape[-1] ** -0.5
-    if q.shape == k.shape:
+    if q.shape == k.shape and kdt == torch.float16:
         out = flash_attn(q, k, v, causal=causal, sm_scale=float(scaling))
     else:
-        # grouped K/V heads and/or a cache: read in place, no repeat_kv copy
+        # grouped K/V heads, a cache or bf16: read in place, no repeat_kv copy
         out = flash_attn_gqa(q, k, v, causal=causal, sm_scale=float(scaling))
     return out.to(out_dtype), None
 

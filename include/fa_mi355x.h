@@ -8,7 +8,8 @@
  * output and the backward workspace.
  *
  * Tensor convention (same as the Python API this library backs):
- *   q, k, v, o, do, dq, dk, dv : (B, S, H, D) fp16 (IEEE binary16), any
+ *   q, k, v, o, do, dq, dk, dv : (B, S, H, D) fp16 (IEEE binary16; bf16 too
+ *                                 in fa_fwd_gqa / fa_bwd_gqa), any
  *                                 strides with the D stride equal to 1;
  *   lse, delta                 : (B, H, S) fp32, contiguous.
  * Strides are in elements and given per tensor as {b, s, h, d}.
@@ -28,7 +29,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 2
+#define FA_ABI_VERSION 3
 
 enum fa_status {
   FA_OK = 0,
@@ -43,7 +44,15 @@ enum fa_status {
   FA_ERR_WORKSPACE = -7,      /* workspace NULL or smaller than required    */
   FA_ERR_TOO_LARGE = -8,      /* sizes whose element offsets overflow int64
                                  or whose grid exceeds the launch limits    */
-  FA_ERR_LAUNCH = -9          /* the HIP runtime rejected a kernel launch   */
+  FA_ERR_LAUNCH = -9,         /* the HIP runtime rejected a kernel launch   */
+  FA_ERR_DTYPE = -10          /* dtype not one of enum fa_dtype             */
+};
+
+/* Element type of the 16-bit tensors (fa_fwd_gqa / fa_bwd_gqa; the other
+ * entry points are fp16, like the reference). */
+enum fa_dtype {
+  FA_DTYPE_F16 = 0,           /* IEEE binary16                              */
+  FA_DTYPE_BF16 = 1           /* bfloat16                                   */
 };
 
 /* Version of this ABI (FA_ABI_VERSION of the build). */
@@ -76,7 +85,9 @@ int fa_fwd(const void *q, const void *k, const void *v, void *o, float *lse,
  * (B, H, Sq).  `causal` aligns the mask to the bottom right: query i sees
  * key j iff j <= i + (Sk - Sq), so the last query sees every key (the
  * KV-cache / chunked-prefill convention); a query that sees no key gets
- * o = 0 and lse = +inf.  With Sq == Sk and Hk == H it is fa_fwd.
+ * o = 0 and lse = +inf.  `dtype` (enum fa_dtype) is the element type of
+ * q, k, v and o; accumulation is fp32 either way.  With Sq == Sk, Hk == H
+ * and FA_DTYPE_F16 it is fa_fwd.
  *
  * No counterpart in the reference kernels, whose wrapper asserts equal
  * q/k/v shapes (flash_attn_volta/triton_fa.py:315); it replaces the
@@ -89,7 +100,7 @@ int fa_fwd_gqa(const void *q, const void *k, const void *v, void *o, float *lse,
                int B, int Sq, int Sk, int H, int Hk, int D,
                const int64_t q_strides[4], const int64_t k_strides[4],
                const int64_t v_strides[4], const int64_t o_strides[4],
-               float sm_scale, int causal, void *stream);
+               float sm_scale, int causal, int dtype, void *stream);
 
 /*
  * Backward pre-pass: delta[b,h,s] = sum_d o[b,s,h,d] * do[b,s,h,d] in fp32.
@@ -128,8 +139,10 @@ int fa_bwd(const void *dout, const void *q, const void *k, const void *v,
  * Backward of fa_fwd_gqa: dq is (B, Sq, H, D), dk and dv are (B, Sk, Hk, D)
  * and hold the sums over the H / Hk query heads that share each key/value
  * head (computed in the kernel, in a fixed order: still bit-reproducible).
- * The workspace is fa_bwd_workspace_bytes(B, Sq, H, D).  Same masking
- * convention as fa_fwd_gqa; with Sq == Sk and Hk == H it is fa_bwd.
+ * The workspace is fa_bwd_workspace_bytes(B, Sq, H, D).  Same masking and
+ * dtype convention as fa_fwd_gqa (every 16-bit tensor, inputs and
+ * gradients, has element type `dtype`); with Sq == Sk, Hk == H and
+ * FA_DTYPE_F16 it is fa_bwd.
  *
  * No counterpart in the reference kernels (see fa_fwd_gqa); it replaces
  * autograd through the reference patch's repeat_kv
@@ -144,7 +157,7 @@ int fa_bwd_gqa(const void *dout, const void *q, const void *k, const void *v,
                const int64_t k_strides[4], const int64_t v_strides[4],
                const int64_t o_strides[4], const int64_t dq_strides[4],
                const int64_t dk_strides[4], const int64_t dv_strides[4],
-               float sm_scale, int causal, void *stream);
+               float sm_scale, int causal, int dtype, void *stream);
 
 /*
  * The two main backward kernels as separate steps (fa_bwd runs

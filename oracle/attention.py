@@ -88,17 +88,19 @@ def make_inputs(B: int, S: int, H: int, D: int, seed: int = 0, scale: float = 1.
 
 
 def make_inputs_gqa(B: int, Sq: int, Sk: int, H: int, Hk: int, D: int, seed: int = 0,
-                    scale: float = 1.0):
-    """Seeded fp16 inputs for the grouped-query functions: q (B,Sq,H,D),
+                    scale: float = 1.0, dtype=None):
+    """Seeded 16-bit inputs for the grouped-query functions: q (B,Sq,H,D),
     k and v (B,Sk,Hk,D) from ``Generator('cpu').manual_seed(seed)`` (randn
-    fp32 -> fp16, times ``scale``), dO (B,Sq,H,D) from seed + 1."""
+    fp32 -> ``dtype``, fp16 by default, times ``scale``), dO (B,Sq,H,D) from
+    seed + 1."""
     import torch
+    dtype = torch.float16 if dtype is None else dtype
     gen = torch.Generator("cpu").manual_seed(seed)
-    q = torch.randn((B, Sq, H, D), generator=gen, dtype=torch.float32).half()
-    k = torch.randn((B, Sk, Hk, D), generator=gen, dtype=torch.float32).half()
-    v = torch.randn((B, Sk, Hk, D), generator=gen, dtype=torch.float32).half()
+    q = torch.randn((B, Sq, H, D), generator=gen, dtype=torch.float32).to(dtype)
+    k = torch.randn((B, Sk, Hk, D), generator=gen, dtype=torch.float32).to(dtype)
+    v = torch.randn((B, Sk, Hk, D), generator=gen, dtype=torch.float32).to(dtype)
     gen2 = torch.Generator("cpu").manual_seed(seed + 1)
-    do = torch.randn((B, Sq, H, D), generator=gen2, dtype=torch.float32).half()
+    do = torch.randn((B, Sq, H, D), generator=gen2, dtype=torch.float32).to(dtype)
     if scale != 1.0:
         q, k, v, do = q * scale, k * scale, v * scale, do * scale
     return q, k, v, do

@@ -46,11 +46,11 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.fa_abi_version() == _capi.ABI_VERSION == 2
+    assert lib.fa_abi_version() == _capi.ABI_VERSION == 3
 
 
 def test_strerror_covers_every_code(lib):
-    codes = [0, -1, -2, -3, -4, -5, -6, -7, -8, -9]
+    codes = [0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10]
     msgs = [lib.fa_strerror(c).decode() for c in codes]
     assert len(set(msgs)) == len(codes)
     assert "unknown" in lib.fa_strerror(-1234).decode()
@@ -116,10 +116,11 @@ def test_preprocess_validation(lib):
 
 
 def _fwd_gqa(lib, B=1, Sq=100, Sk=300, H=8, Hk=2, D=64, q=P, k=P, v=P, o=P, lse=None,
-             kst=None, scale=0.125):
+             kst=None, scale=0.125, dtype=_capi.FA_DTYPE_F16):
     sq = _st(B, Sq, H, D)
     sk = kst or _st(B, Sk, Hk, D)
-    return lib.fa_fwd_gqa(q, k, v, o, lse, B, Sq, Sk, H, Hk, D, sq, sk, sk, sq, scale, 1, None)
+    return lib.fa_fwd_gqa(q, k, v, o, lse, B, Sq, Sk, H, Hk, D, sq, sk, sk, sq, scale, 1, dtype,
+                          None)
 
 
 def test_fwd_gqa_validation(lib):
@@ -133,6 +134,8 @@ def test_fwd_gqa_validation(lib):
     assert _fwd_gqa(lib, kst=(ctypes.c_int64 * 4)(300 * 128, 128, 60, 1)) == _capi.FA_ERR_STRIDE
     assert _fwd_gqa(lib, scale=float("nan")) == _capi.FA_ERR_SCALE
     assert _fwd_gqa(lib, Sk=(1 << 30) + 1) == _capi.FA_ERR_TOO_LARGE
+    assert _fwd_gqa(lib, dtype=2) == _capi.FA_ERR_DTYPE
+    assert _fwd_gqa(lib, dtype=-1) == _capi.FA_ERR_DTYPE
 
 
 def test_bwd_gqa_validation(lib):
@@ -142,7 +145,7 @@ def test_bwd_gqa_validation(lib):
 
     def call(ws_ptr=P, ws_bytes=ws, Hk_=Hk, dk=P):
         return lib.fa_bwd_gqa(P, P, P, P, P, P, P, dk, P, ws_ptr, ws_bytes, B, Sq, Sk, H, Hk_, D,
-                              sq, sq, sk, sk, sq, sq, sk, sk, 0.125, 1, None)
+                              sq, sq, sk, sk, sq, sq, sk, sk, 0.125, 1, _capi.FA_DTYPE_BF16, None)
     assert call(ws_bytes=ws - 4) == _capi.FA_ERR_WORKSPACE
     assert call(ws_ptr=None) == _capi.FA_ERR_WORKSPACE
     assert call(Hk_=3) == _capi.FA_ERR_SHAPE

@@ -1,8 +1,9 @@
-"""Grouped-query attention and Sq != Sk on the GPU: flash_attn_forward_gqa /
-flash_attn_backward_gqa / flash_attn_gqa (fa_fwd_gqa / fa_bwd_gqa via the C
-ABI) against the float64 oracle (attention_fwd_gqa / attention_bwd_gqa) on
-identical seeded fp16 inputs.  Tolerance: max-abs 1e-2 on O, LSE and every
-gradient, as for the square entry points.
+"""Grouped-query attention, Sq != Sk and bf16 on the GPU:
+flash_attn_forward_gqa / flash_attn_backward_gqa / flash_attn_gqa
+(fa_fwd_gqa / fa_bwd_gqa via the C ABI) against the float64 oracle
+(attention_fwd_gqa / attention_bwd_gqa) on identical seeded 16-bit inputs.
+Tolerance: max-abs 1e-2 on O, LSE and every gradient for fp16, as for the
+square entry points; 4e-2 for bf16 (see BF16_TOL).
 
 Cases: GQA and MQA groups at equal lengths; fewer queries than keys
 (prefill continuation, single-token decode) and more queries than keys
@@ -26,8 +27,8 @@ pytestmark = pytest.mark.gpu
 
 
 @functools.lru_cache(maxsize=2)
-def _oracle(B, Sq, Sk, H, Hk, D, causal, seed):
-    q, k, v, do = orc.make_inputs_gqa(B, Sq, Sk, H, Hk, D, seed=seed)
+def _oracle(B, Sq, Sk, H, Hk, D, causal, seed, dtype=torch.float16):
+    q, k, v, do = orc.make_inputs_gqa(B, Sq, Sk, H, Hk, D, seed=seed, dtype=dtype)
     sc = default_scale(D, None)
     o, lse = orc.attention_fwd_gqa(q, k, v, causal, sc)
     dq, dk, dv, _ = orc.attention_bwd_gqa(do, q, k, v, causal, sc, o=o)
@@ -152,6 +153,56 @@ def test_gqa_autograd_and_strided_inputs():
         assert torch.equal(x, y) and torch.equal(x, z)
 
 
+# bf16: max-abs 4e-2, four times the fp16 bar (bf16 keeps 2 fewer mantissa
+# bits, so its rounding of the inputs, of P and dS, and of the outputs is 4x
+# coarser).  The oracle sees the same bf16 inputs.
+BF16_TOL = 4e-2
+BF16_CASES = [
+    (2, 300, 300, 8, 2, 64, True),
+    (1, 1024, 1024, 8, 8, 128, True),
+    (1, 100, 900, 8, 2, 64, False),
+    (1, 500, 130, 4, 2, 64, True),
+    (2, 77, 191, 6, 3, 32, True),
+    (1, 200, 333, 4, 2, 16, False),
+    (1, 4096, 4096, 16, 16, 64, True),        # the C4a shape
+]
+
+
+@pytest.mark.parametrize("case", BF16_CASES, ids=[
+    f"bf16_B{c[0]}_q{c[1]}_k{c[2]}_H{c[3]}_Hk{c[4]}_D{c[5]}_{'c' if c[6] else 'n'}" for c in BF16_CASES])
+def test_gqa_bf16_parity(case):
+    B, Sq, Sk, H, Hk, D, causal = case
+    print(f"[case] gqa bf16 {case}", flush=True)
+    (q, k, v, do), (o, lse, dq, dk, dv) = _oracle(B, Sq, Sk, H, Hk, D, causal, 36, torch.bfloat16)
+    out, glse, gq, gk, gv = _run(q, k, v, do, causal)
+    assert out.dtype == gq.dtype == gk.dtype == gv.dtype == torch.bfloat16
+    errs = dict(out=max_abs(out, o), lse=_lse_err(glse, lse), dq=max_abs(gq, dq),
+                dk=max_abs(gk, dk), dv=max_abs(gv, dv))
+    report(f"bf16 {Sq}x{Sk} {H}/{Hk} D{D}", **errs)
+    for key, e in errs.items():
+        assert e < BF16_TOL, f"{case} {key} max-abs {e:.3e} >= {BF16_TOL}"
+
+
+def test_gqa_bf16_negative_and_large_scale():
+    """bf16 keeps K unscaled in the dK/dV recompute, so |sm_scale| > ln 2
+    and negative scales take the general exponent path."""
+    from flash_attn_volta import flash_attn_backward_gqa, flash_attn_forward_gqa
+    B, Sq, Sk, H, Hk, D = 1, 200, 260, 4, 2, 64
+    q, k, v, do = orc.make_inputs_gqa(B, Sq, Sk, H, Hk, D, seed=37, scale=0.25, dtype=torch.bfloat16)
+    for scale in (-0.125, 0.9):
+        o, lse = orc.attention_fwd_gqa(q, k, v, True, scale)
+        dq, dk, dv, _ = orc.attention_bwd_gqa(do, q, k, v, True, scale, o=o)
+        qd, kd, vd, dod = (t.cuda() for t in (q, k, v, do))
+        out, glse = flash_attn_forward_gqa(qd, kd, vd, causal=True, sm_scale=scale,
+                                           return_softmax_lse=True)
+        gq, gk, gv = flash_attn_backward_gqa(dod, qd, kd, vd, out, glse, causal=True, sm_scale=scale)
+        errs = dict(out=max_abs(out, o), lse=_lse_err(glse, lse), dq=max_abs(gq, dq),
+                    dk=max_abs(gk, dk), dv=max_abs(gv, dv))
+        report(f"bf16 scale {scale}", **errs)
+        for key, e in errs.items():
+            assert e < BF16_TOL, f"scale {scale} {key} max-abs {e:.3e}"
+
+
 def test_gqa_argument_errors():
     from flash_attn_volta import flash_attn_forward_gqa
     from flash_attn_volta.forward import FlashAttnArgumentError
@@ -163,3 +214,7 @@ def test_gqa_argument_errors():
         flash_attn_forward_gqa(q, k[..., :32], k[..., :32])  # head_dim mismatch
     with pytest.raises(FlashAttnArgumentError):
         flash_attn_forward_gqa(q, k[:, :, :2], k[:, :, :3])  # k / v differ
+    with pytest.raises(FlashAttnArgumentError):
+        flash_attn_forward_gqa(q.bfloat16(), k[:, :, :2], k[:, :, :2])   # mixed dtypes
+    with pytest.raises(FlashAttnArgumentError):
+        flash_attn_forward_gqa(q.float(), k[:, :, :2].float(), k[:, :, :2].float())

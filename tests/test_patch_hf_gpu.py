@@ -224,6 +224,34 @@ def test_chunked_prefill_runs_on_the_kernel(monkeypatch):
     assert (chunk - full[:, 24:]).abs().max().item() <= 0.1
 
 
+def test_bf16_model_runs_in_bf16(monkeypatch):
+    """A bf16 model's attention runs on the bf16 kernels (not cast to fp16)
+    and matches the same bf16 model with fp32 attention."""
+    import flash_attn_volta.patch_hf as ph
+    calls = _count_kernel_calls(monkeypatch)
+    seen = []
+    real = ph.flash_attn_gqa
+
+    def spy(q, k, v, **kw):
+        seen.append(q.dtype)
+        return real(q, k, v, **kw)
+
+    monkeypatch.setattr(ph, "flash_attn_gqa", spy)
+    ref = hf_models.tiny_llama(gqa=True).to(torch.bfloat16).cuda()
+    ours = hf_models.tiny_llama(gqa=True).to(torch.bfloat16).cuda()
+    ours.load_state_dict(ref.state_dict())
+    _route_fp32(ref, patch_hf._LLAMA_NAMES)
+    assert ph.patch_llama(ours) == 2
+    ids = hf_models.token_ids(200, device="cuda", seed=5)
+    with torch.no_grad():
+        la = ref(ids).logits.float()
+        lb = ours(ids).logits.float()
+    assert seen == [torch.bfloat16, torch.bfloat16] and calls["square"] == 0
+    print(f"[patch_hf] bf16 llama: logits max-abs {(la - lb).abs().max().item():.3e} "
+          f"cos {_cos(la, lb):.6f}", flush=True)
+    assert _cos(la, lb) >= 0.999 and (la - lb).abs().max().item() <= 0.25
+
+
 def test_config5_llama_training_step():
     """16 layers, hidden 2048, 16 heads x 128, SwiGLU 5632,
     RMSNorm, RoPE theta 10000, vocab 32000, N(0, 0.02) init, fp16; one
