@@ -64,6 +64,9 @@ def _backward(do, q, k, v, o, lse, causal, sm_scale, gqa):
     return _run_bwd(do, q, k, v, o, lse, causal, sm_scale, gqa)
 
 
+_WS_BYTES = {}
+
+
 def _run_bwd(do, q, k, v, o, lse, causal, sm_scale, gqa):
     lib = _capi.load()
     B, N, H, D = q.shape
@@ -71,14 +74,16 @@ def _run_bwd(do, q, k, v, o, lse, causal, sm_scale, gqa):
     do, q, k, v, o = (_kernel_ready(t) for t in (do, q, k, v, o))
     lse = lse.contiguous()
     dq = torch.empty((B, N, H, D), dtype=q.dtype, device=q.device)
-    dk = torch.empty((B, Sk, Hk, D), dtype=q.dtype, device=q.device)
-    dv = torch.empty_like(dk)
+    dk, dv = torch.empty((2, B, Sk, Hk, D), dtype=q.dtype, device=q.device).unbind(0)
     if dq.numel() == 0 or dk.numel() == 0:
         # nothing attends to anything: every gradient is zero
         for t in (dq, dk, dv):
             t.zero_()
         return dq, dk, dv
-    ws_bytes = lib.fa_bwd_workspace_bytes(B, N, H, D)
+    key = (B, N, H, D)
+    ws_bytes = _WS_BYTES.get(key)
+    if ws_bytes is None:
+        ws_bytes = _WS_BYTES[key] = lib.fa_bwd_workspace_bytes(B, N, H, D)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
     sq_, sk_ = kernel_strides(dq), kernel_strides(dk)
     st = (kernel_strides(do), kernel_strides(q), kernel_strides(k), kernel_strides(v),

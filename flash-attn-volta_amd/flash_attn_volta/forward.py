@@ -38,6 +38,8 @@ def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
     """Return ``t`` if the kernel can read it in place (unit D stride,
     16-byte aligned base, other strides multiples of 8 elements), else a
     contiguous copy."""
+    if t.is_contiguous() and t.data_ptr() % 16 == 0:
+        return t            # D is a multiple of 8, so every stride is too
     ok = t.stride(3) == 1 and t.data_ptr() % 16 == 0
     if ok:
         for dim in range(3):
@@ -64,7 +66,14 @@ def kernel_strides(t: torch.Tensor):
     return arr
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream_ptr(device: torch.device) -> int:
+    """hipStream_t of the device's current stream (the raw query skips
+    building a Stream object; same value)."""
+    if _RAW_STREAM is not None:
+        return _RAW_STREAM(device.index)
     return torch.cuda.current_stream(device).cuda_stream
 
 
