@@ -212,12 +212,103 @@ def cpu_baseline(max_seconds=30.0):
     }
 
 
+# BASELINE.json configs for --configs: (name, B, S, H, D, causal, sm_scale,
+# input scale, fwd+bwd timed?).  C1 is the forward-only config; "C5-layer" is
+# one layer of the config-5 Llama attention.
+CONFIG_TABLE = [
+    ("C1", 2, 1024, 8, 64, False, None, 1.0, False),
+    ("C2", 4, 512, 4, 32, True, None, 1.0, True),
+    ("C3", 1, 2048, 16, 64, True, 0.125, 1.0, True),
+    ("C4a-causal", 1, 4096, 16, 64, True, None, 0.5, True),
+    ("C4a-noncausal", 1, 4096, 16, 64, False, None, 0.5, True),
+    ("C4b-causal", 1, 4096, 8, 128, True, None, 0.5, True),
+    ("C4b-noncausal", 1, 4096, 8, 128, False, None, 0.5, True),
+    ("C5-layer", 1, 4096, 16, 128, True, None, 1.0, True),
+]
+
+
+def cpu_time(fn, max_seconds):
+    """1 warmup, then the median of up to 3 timed calls within ~max_seconds."""
+    t0 = time.perf_counter()
+    fn()
+    first = time.perf_counter() - t0
+    n = max(1, min(3, int(max_seconds // max(first, 1e-3))))
+    ts = []
+    for _ in range(n):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts), n
+
+
+def run_configs(steps, warmup, with_cpu):
+    """Every BASELINE config: GPU forward and fwd+bwd (autograd) on the HIP
+    kernels, and the CPU baseline (fp32 eager path, all host threads) for the
+    same inputs.  One JSON line per config, then a markdown table."""
+    import torch
+    from flash_attn_volta import flash_attn, flash_attn_forward
+    from oracle.attention import attention_ref_fp32
+    threads = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
+    torch.set_num_threads(threads)
+    rows = []
+    for name, b, s, h, d, causal, sc, in_scale, with_bwd in CONFIG_TABLE:
+        g = torch.Generator(device="cpu").manual_seed(0)
+        qc, kc, vc = (torch.randn((b, s, h, d), generator=g).half() * in_scale for _ in range(3))
+        doc = torch.randn((b, s, h, d), generator=torch.Generator(device="cpu").manual_seed(1)).half()
+        q, k, v, do = (t.cuda() for t in (qc, kc, vc, doc))
+        qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
+        flops = fwd_flops(b, s, h, d)
+        _, t_f = time_loop(lambda: flash_attn_forward(q, k, v, causal=causal, sm_scale=sc), steps, warmup)
+
+        def gpu_fb():
+            qg.grad = kg.grad = vg.grad = None
+            flash_attn(qg, kg, vg, causal=causal, sm_scale=sc).backward(do)
+        t_fb = time_loop(gpu_fb, steps, warmup)[1] if with_bwd else None
+        row = {"config": name, "shape": [b, s, h, d], "causal": causal,
+               "gpu_fwd_us": round(t_f * 1e6, 2), "gpu_fwd_tflops": round(flops / t_f / 1e12, 2),
+               "gpu_fwd_pct_peak": round(100 * flops / t_f / 1e12 / PEAK_FP16_TFLOPS, 2)}
+        if with_bwd:
+            row.update({"gpu_fwd_bwd_us": round(t_fb * 1e6, 2),
+                        "gpu_fwd_bwd_tflops": round(5 * flops / t_fb / 1e12, 2),
+                        "gpu_fwd_bwd_pct_peak": round(100 * 5 * flops / t_fb / 1e12 / PEAK_FP16_TFLOPS, 2)})
+        if with_cpu:
+            with torch.no_grad():
+                t_cf, n_f = cpu_time(lambda: attention_ref_fp32(qc, kc, vc, causal=causal, sm_scale=sc), 10.0)
+            row.update({"cpu_fwd_tflops": round(flops / t_cf / 1e12, 4), "cpu_threads": torch.get_num_threads()})
+            if with_bwd:
+                qs, ks, vs = (t.clone().requires_grad_() for t in (qc, kc, vc))
+
+                def cpu_fb():
+                    qs.grad = ks.grad = vs.grad = None
+                    attention_ref_fp32(qs, ks, vs, causal=causal, sm_scale=sc).backward(doc)
+                t_cfb, _ = cpu_time(cpu_fb, 10.0)
+                row["cpu_fwd_bwd_tflops"] = round(5 * flops / t_cfb / 1e12, 4)
+        rows.append(row)
+        print(json.dumps(row), flush=True)
+    hdr = ("| config | shape | GPU fwd us | GPU fwd TFLOP/s (% peak) | GPU fwd+bwd us | "
+           "GPU fwd+bwd TFLOP/s (% peak) | CPU fwd TFLOP/s | CPU fwd+bwd TFLOP/s |")
+    print(hdr)
+    print("|---|---|---:|---:|---:|---:|---:|---:|")
+    for r in rows:
+        fb = (f"{r['gpu_fwd_bwd_us']} | {r['gpu_fwd_bwd_tflops']} ({r['gpu_fwd_bwd_pct_peak']} %)"
+              if "gpu_fwd_bwd_us" in r else "n/a | n/a")
+        print(f"| {r['config']} | {tuple(r['shape'])}{' causal' if r['causal'] else ''} | "
+              f"{r['gpu_fwd_us']} | {r['gpu_fwd_tflops']} ({r['gpu_fwd_pct_peak']} %) | {fb} | "
+              f"{r.get('cpu_fwd_tflops', '-')} | {r.get('cpu_fwd_bwd_tflops', '-')} |")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--configs", action="store_true",
+                    help="instead of the benchmark line, time every BASELINE config (GPU "
+                         "fwd and fwd+bwd, plus the CPU baseline unless --no-cpu) and print "
+                         "a table")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run 10 plain device copies of MIB MiB "
                          "(a kernel of known HBM traffic, to scale rocprofv3 FETCH_SIZE / "
@@ -240,6 +331,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         log(f"[bench] copy calibration: 10 x {n} bytes read + {n} bytes written")
+        return
+    if args.configs:
+        torch.cuda.set_device(0)
+        run_configs(args.steps, args.warmup, not args.no_cpu)
         return
     from flash_attn_volta import flash_attn, flash_attn_forward
     dev = torch.device("cuda:0")
