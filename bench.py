@@ -299,6 +299,156 @@ def run_configs(steps, warmup, with_cpu):
               f"{r.get('cpu_fwd_tflops', '-')} | {r.get('cpu_fwd_bwd_tflops', '-')} |")
 
 
+# Fused-prologue workloads: (name, B, S, H, Hk, D, qk_norm, dtype name)
+ROPE_TABLE = [
+    ("C5-llama", 1, 4096, 16, 16, 128, False, "fp16"),
+    ("C5-qwen3", 1, 4096, 16, 8, 128, True, "bf16"),
+]
+
+
+def rope_bytes(b, s, h, hk, d, norm, tables_b=1):
+    """Algorithmic HBM bytes of the fused prologue's forward and backward
+    launches: each q/k element read and written once (16-bit), the forward
+    inputs read again by a normed backward, the cos/sin tables once, and the
+    backward's fp32 dw partials written and read."""
+    elems = b * s * (h + hk) * d
+    tables = 2 * tables_b * s * d * 2
+    fwd = 2 * elems * 2 + tables
+    bwd = 2 * elems * 2 + tables
+    if norm:
+        rows = b * s * max(h, hk)
+        nblk = min(-(-rows // (4096 // d)), 1024)
+        bwd += elems * 2 + 2 * (2 * nblk * d * 4)
+    return fwd, bwd
+
+
+def rope_kernel_times(q, k, cos, sin, wq, wk, gq, gk, eps, steps, warmup):
+    """Average HIP-event time per call of fa_rope_qk_fwd and fa_rope_qk_bwd
+    (the backward including its dw reduction), launched back to back through
+    the C ABI with prepared arguments, so the host issues faster than the
+    GPU drains."""
+    import torch
+    from flash_attn_volta import _capi
+    from flash_attn_volta.forward import _DTYPES, kernel_strides
+    lib = _capi.load()
+    b, s, h, d = q.shape
+    hk = k.shape[2]
+    qo, ko, dq, dk = (torch.empty_like(t) for t in (q, k, q, k))
+    dwq = torch.empty(d, dtype=torch.float32, device=q.device) if wq is not None else None
+    dwk = torch.empty(d, dtype=torch.float32, device=q.device) if wk is not None else None
+    ws = torch.empty(lib.fa_rope_qk_workspace_bytes(b, s, h, hk, d), dtype=torch.uint8,
+                     device=q.device)
+    cs = (ctypes.c_int64 * 2)(0, d)
+    ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    stream = torch.cuda.current_stream().cuda_stream
+    dt = _DTYPES[q.dtype]
+    fa = (ptr(q), ptr(k), ptr(qo), ptr(ko), ptr(cos), ptr(sin), ptr(wq), ptr(wk), eps,
+          b, s, h, hk, d, kernel_strides(q), kernel_strides(k), kernel_strides(qo),
+          kernel_strides(ko), cs, dt, stream)
+    ba = (ptr(gq), ptr(gk), ptr(q), ptr(k), ptr(cos), ptr(sin), ptr(wq), ptr(wk), eps,
+          ptr(dq), ptr(dk), ptr(dwq), ptr(dwk), ptr(ws), ws.numel(), b, s, h, hk, d,
+          kernel_strides(gq), kernel_strides(gk), kernel_strides(q), kernel_strides(k),
+          kernel_strides(dq), kernel_strides(dk), cs, dt, stream)
+    out = []
+    for fn, a in ((lib.fa_rope_qk_fwd, fa), (lib.fa_rope_qk_bwd, ba)):
+        _capi.check(fn(*a), "rope kernel timing")
+        out.append(time_loop(lambda: fn(*a), steps, warmup)[1])
+    return out
+
+
+def run_rope(steps, warmup):
+    """The fused QK-norm + rotary prologue against transformers' eager
+    prologue (Qwen3RMSNorm + apply_rotary_pos_emb, as the reference's patch
+    calls them) at the config-5 layer shape: kernel times and HBM roofline
+    of fa_rope_qk_fwd / fa_rope_qk_bwd, and fwd / fwd+bwd of both prologues
+    through autograd, next to the attention fwd+bwd of the same layer."""
+    import torch
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm, apply_rotary_pos_emb
+    from flash_attn_volta import apply_rotary_qk, flash_attn_gqa
+    rows = []
+    for name, b, s, h, hk, d, norm, dt in ROPE_TABLE:
+        dtype = torch.float16 if dt == "fp16" else torch.bfloat16
+        g = torch.Generator(device="cpu").manual_seed(0)
+        q, gq = (torch.randn((b, s, h, d), generator=g).to(dtype).cuda() for _ in range(2))
+        k, gk = (torch.randn((b, s, hk, d), generator=g).to(dtype).cuda() for _ in range(2))
+        # rotary tables as transformers' default rotary embedding builds them
+        inv = 1.0 / (10000.0 ** (torch.arange(0, d, 2, dtype=torch.int64).float() / d))
+        freqs = torch.arange(s).float()[:, None] * inv
+        emb = torch.cat((freqs, freqs), dim=-1)[None]
+        cos, sin = emb.cos().to(dtype).cuda(), emb.sin().to(dtype).cuda()
+        wq = wk = None
+        if norm:
+            wq, wk = ((1.0 + 0.25 * torch.randn(d, generator=g)).to(dtype).cuda() for _ in range(2))
+        eps = 1e-6
+        t_kf, t_kb = rope_kernel_times(q, k, cos, sin, wq, wk, gq, gk, eps, steps, warmup)
+        by_f, by_b = rope_bytes(b, s, h, hk, d, norm)
+
+        qg, kg = q.clone().requires_grad_(), k.clone().requires_grad_()
+        wqg = torch.nn.Parameter(wq.clone()) if norm else None
+        wkg = torch.nn.Parameter(wk.clone()) if norm else None
+        nq = nk = None
+        if norm:
+            nq, nk = Qwen3RMSNorm(d, eps=eps).cuda().to(dtype), Qwen3RMSNorm(d, eps=eps).cuda().to(dtype)
+            with torch.no_grad():
+                nq.weight.copy_(wq)
+                nk.weight.copy_(wk)
+
+        def fused_fb():
+            qg.grad = kg.grad = None
+            qo, ko = apply_rotary_qk(qg, kg, cos, sin, wqg, wkg, eps)
+            torch.autograd.backward((qo, ko), (gq, gk))
+
+        def hf_prologue(qx, kx):
+            if norm:
+                qx, kx = nq(qx), nk(kx)
+            return apply_rotary_pos_emb(qx.transpose(1, 2), kx.transpose(1, 2), cos, sin)
+
+        def hf_fb():
+            qg.grad = kg.grad = None
+            qo, ko = hf_prologue(qg, kg)
+            torch.autograd.backward((qo, ko), (gq.transpose(1, 2), gk.transpose(1, 2)))
+
+        with torch.no_grad():
+            _, t_ff = time_loop(lambda: apply_rotary_qk(q, k, cos, sin, wq, wk, eps), steps, warmup)
+            _, t_hf = time_loop(lambda: hf_prologue(q, k), steps, warmup)
+        _, t_ffb = time_loop(fused_fb, steps, warmup)
+        _, t_hfb = time_loop(hf_fb, steps, warmup)
+        v = torch.randn_like(k)
+        qa, ka, va = (t.clone().requires_grad_() for t in (q, k, v))
+        do = torch.randn_like(q)
+
+        def attn_fb():
+            qa.grad = ka.grad = va.grad = None
+            flash_attn_gqa(qa, ka, va, causal=True).backward(do)
+        _, t_att = time_loop(attn_fb, steps, warmup)
+        row = {"workload": name, "shape": [b, s, h, hk, d], "qk_norm": norm, "dtype": dt,
+               "kernel_fwd_us": round(t_kf * 1e6, 2),
+               "kernel_fwd_gbs": round(by_f / t_kf / 1e9, 1),
+               "kernel_fwd_frac_hbm": round(by_f / t_kf / 1e9 / PEAK_HBM_GBS, 4),
+               "kernel_bwd_us": round(t_kb * 1e6, 2),
+               "kernel_bwd_gbs": round(by_b / t_kb / 1e9, 1),
+               "kernel_bwd_frac_hbm": round(by_b / t_kb / 1e9 / PEAK_HBM_GBS, 4),
+               "algorithmic_bytes": {"fwd": by_f, "bwd": by_b},
+               "fused_fwd_us": round(t_ff * 1e6, 2), "transformers_fwd_us": round(t_hf * 1e6, 2),
+               "fused_fwd_bwd_us": round(t_ffb * 1e6, 2),
+               "transformers_fwd_bwd_us": round(t_hfb * 1e6, 2),
+               "speedup_fwd_bwd": round(t_hfb / t_ffb, 2),
+               "attention_fwd_bwd_us": round(t_att * 1e6, 2)}
+        rows.append(row)
+        print(json.dumps(row), flush=True)
+    print("| workload | shape (B,S,H,Hk,D) | kernel fwd us (GB/s, % of 8 TB/s) | kernel bwd us "
+          "(GB/s, %) | fused fwd+bwd us | transformers fwd+bwd us | speed-up | attention "
+          "fwd+bwd us |")
+    print("|---|---|---:|---:|---:|---:|---:|---:|")
+    for r in rows:
+        print(f"| {r['workload']} ({r['dtype']}{', qk-norm' if r['qk_norm'] else ''}) | "
+              f"{tuple(r['shape'])} | {r['kernel_fwd_us']} ({r['kernel_fwd_gbs']}, "
+              f"{100 * r['kernel_fwd_frac_hbm']:.1f} %) | {r['kernel_bwd_us']} ({r['kernel_bwd_gbs']}, "
+              f"{100 * r['kernel_bwd_frac_hbm']:.1f} %) | {r['fused_fwd_bwd_us']} | "
+              f"{r['transformers_fwd_bwd_us']} | {r['speedup_fwd_bwd']}x | "
+              f"{r['attention_fwd_bwd_us']} |")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -309,6 +459,9 @@ def main():
                     help="instead of the benchmark line, time every BASELINE config (GPU "
                          "fwd and fwd+bwd, plus the CPU baseline unless --no-cpu) and print "
                          "a table")
+    ap.add_argument("--rope", action="store_true",
+                    help="instead of the benchmark line, time the fused QK-norm + rotary "
+                         "prologue against transformers' eager one and print a table")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run 10 plain device copies of MIB MiB "
                          "(a kernel of known HBM traffic, to scale rocprofv3 FETCH_SIZE / "
@@ -335,6 +488,10 @@ def main():
     if args.configs:
         torch.cuda.set_device(0)
         run_configs(args.steps, args.warmup, not args.no_cpu)
+        return
+    if args.rope:
+        torch.cuda.set_device(0)
+        run_rope(args.steps, args.warmup)
         return
     from flash_attn_volta import flash_attn, flash_attn_forward
     dev = torch.device("cuda:0")

@@ -12,6 +12,7 @@
 #include "../../include/fa_mi355x.h"
 #include "fa_bwd.hpp"
 #include "fa_fwd.hpp"
+#include "fa_rope.hpp"
 
 namespace {
 
@@ -351,6 +352,211 @@ int run_bwd(const void *dout, const void *q, const void *k, const void *v, const
 
 Shape square(int B, int S, int H, int D) { return Shape{B, S, S, H, H, D, FA_DTYPE_F16}; }
 
+// ---------------------------------------------------------------------------
+// QK-norm + rotary prologue
+
+struct RopeShape {
+  int B, S, H, Hk, D, dtype;
+};
+
+int check_rope_shape(const RopeShape &s) {
+  if (s.dtype != FA_DTYPE_F16 && s.dtype != FA_DTYPE_BF16) return FA_ERR_DTYPE;
+  if (s.B <= 0 || s.S <= 0 || s.H <= 0 || s.Hk <= 0) return FA_ERR_SHAPE;
+  if (s.D != 16 && s.D != 32 && s.D != 64 && s.D != 128) return FA_ERR_HEAD_DIM;
+  // Rows of the larger side, B * S * H, index a grid-stride loop in int64
+  // and the grid's x dimension in 32 bits.
+  if ((double)s.B * s.S * (s.H > s.Hk ? s.H : s.Hk) > 1.0e15) return FA_ERR_TOO_LARGE;
+  return FA_OK;
+}
+
+// Rows per 256-thread workgroup pass (a row takes D/16 lanes).
+int64_t rope_rows_per_block(int D) { return fa::kRopeThreads / (D / 16); }
+
+int64_t rope_rows(const RopeShape &s) {
+  return (int64_t)s.B * s.S * (s.H > s.Hk ? s.H : s.Hk);
+}
+
+// Workgroups per side.  With a norm the backward writes one dw partial per
+// workgroup, so its grid is capped (grid-stride beyond); everything else
+// covers the rows in one pass.
+constexpr int64_t kRopeNormBlocks = 1024;
+
+int64_t rope_blocks(const RopeShape &s, bool capped) {
+  const int64_t rpb = rope_rows_per_block(s.D);
+  const int64_t need = (rope_rows(s) + rpb - 1) / rpb;
+  // (a launch's x extent in work-items must stay below 2^32)
+  const int64_t cap = capped ? kRopeNormBlocks : ((int64_t)1 << 22);
+  return need < cap ? need : cap;
+}
+
+size_t rope_partial_bytes(const RopeShape &s) {
+  return (size_t)rope_blocks(s, true) * (size_t)s.D * sizeof(float);
+}
+
+int check_rope_table(const void *cos, const void *sin, const int64_t *cs_st) {
+  if (cos == nullptr || sin == nullptr || cs_st == nullptr) return FA_ERR_NULL_POINTER;
+  if (!aligned16(cos) || !aligned16(sin)) return FA_ERR_ALIGNMENT;
+  for (int i = 0; i < 2; ++i) {
+    if (cs_st[i] < 0 || (cs_st[i] & 7) != 0) return FA_ERR_STRIDE;
+  }
+  return FA_OK;
+}
+
+int check_rope_eps(const void *wq, const void *wk, float eps) {
+  if (wq != nullptr && !aligned16(wq)) return FA_ERR_ALIGNMENT;
+  if (wk != nullptr && !aligned16(wk)) return FA_ERR_ALIGNMENT;
+  if ((wq != nullptr || wk != nullptr) && !(isfinite(eps) && eps >= 0.0f)) return FA_ERR_EPS;
+  return FA_OK;
+}
+
+void rope_strides(const int64_t *st, int64_t &b, int64_t &s, int64_t &h) {
+  b = st[0];
+  s = st[1];
+  h = st[2];
+}
+
+template <typename E, int D>
+int launch_rope_fwd(const fa::RopeArgs &a, int64_t blocks, hipStream_t st) {
+  hipLaunchKernelGGL((fa::fa_rope_fwd_kernel<E, D>), dim3((unsigned)blocks, 2), dim3(fa::kRopeThreads),
+                     0, st, a);
+  return launch_status();
+}
+
+template <typename E, int D>
+int launch_rope_bwd(const fa::RopeArgs &a, int64_t blocks, float *dwq, float *dwk,
+                    hipStream_t st) {
+  hipLaunchKernelGGL((fa::fa_rope_bwd_kernel<E, D>), dim3((unsigned)blocks, 2), dim3(fa::kRopeThreads),
+                     0, st, a);
+  int rc = launch_status();
+  if (rc || (a.side[0].w == nullptr && a.side[1].w == nullptr)) return rc;
+  hipLaunchKernelGGL(fa::fa_rope_dw_reduce_kernel<D>, dim3(D / 16, 2), dim3(fa::kRopeReduceThreads), 0, st,
+                     a.side[0].partial, a.side[1].partial, dwq, dwk, (int)blocks);
+  return launch_status();
+}
+
+// (dtype, D) -> one instantiation of launcher L<E, D>.
+#define FA_ROPE_DISPATCH(L, s, ...)                                           \
+  do {                                                                        \
+    if ((s).dtype == FA_DTYPE_BF16) {                                         \
+      switch ((s).D) {                                                        \
+        case 16: return L<fa::bf16, 16>(__VA_ARGS__);                         \
+        case 32: return L<fa::bf16, 32>(__VA_ARGS__);                         \
+        case 64: return L<fa::bf16, 64>(__VA_ARGS__);                         \
+        default: return L<fa::bf16, 128>(__VA_ARGS__);                        \
+      }                                                                       \
+    }                                                                         \
+    switch ((s).D) {                                                          \
+      case 16: return L<fa::f16, 16>(__VA_ARGS__);                            \
+      case 32: return L<fa::f16, 32>(__VA_ARGS__);                            \
+      case 64: return L<fa::f16, 64>(__VA_ARGS__);                            \
+      default: return L<fa::f16, 128>(__VA_ARGS__);                           \
+    }                                                                         \
+  } while (0)
+
+int run_rope_fwd(const void *q, const void *k, void *q_out, void *k_out, const void *cos,
+                 const void *sin, const void *wq, const void *wk, float eps, const RopeShape &s,
+                 const int64_t *q_st, const int64_t *k_st, const int64_t *qo_st,
+                 const int64_t *ko_st, const int64_t *cs_st, void *stream) {
+  int rc = check_rope_shape(s);
+  if (rc) return rc;
+  if ((rc = check_tensor(q, q_st, s.B, s.S, s.H, s.D))) return rc;
+  if ((rc = check_tensor(k, k_st, s.B, s.S, s.Hk, s.D))) return rc;
+  if ((rc = check_tensor(q_out, qo_st, s.B, s.S, s.H, s.D))) return rc;
+  if ((rc = check_tensor(k_out, ko_st, s.B, s.S, s.Hk, s.D))) return rc;
+  if ((rc = check_rope_table(cos, sin, cs_st))) return rc;
+  if ((rc = check_rope_eps(wq, wk, eps))) return rc;
+
+  fa::RopeArgs a{};
+  const void *x[2] = {q, k};
+  void *y[2] = {q_out, k_out};
+  const void *w[2] = {wq, wk};
+  const int64_t *xs[2] = {q_st, k_st}, *ys[2] = {qo_st, ko_st};
+  const int heads[2] = {s.H, s.Hk};
+  for (int i = 0; i < 2; ++i) {
+    fa::RopeSide &t = a.side[i];
+    t.x = static_cast<const f16 *>(x[i]);
+    t.y = static_cast<f16 *>(y[i]);
+    t.w = static_cast<const f16 *>(w[i]);
+    rope_strides(xs[i], t.xb, t.xs, t.xh);
+    rope_strides(ys[i], t.yb, t.ys, t.yh);
+    t.heads = heads[i];
+    t.rows = (int64_t)s.B * s.S * heads[i];
+  }
+  a.cos = static_cast<const f16 *>(cos);
+  a.sin = static_cast<const f16 *>(sin);
+  a.cb = cs_st[0];
+  a.cs = cs_st[1];
+  a.S = s.S;
+  a.eps = eps;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t blocks = rope_blocks(s, false);
+  FA_ROPE_DISPATCH(launch_rope_fwd, s, a, blocks, st);
+}
+
+int run_rope_bwd(const void *dq_out, const void *dk_out, const void *q, const void *k,
+                 const void *cos, const void *sin, const void *wq, const void *wk, float eps,
+                 void *dq, void *dk, float *dwq, float *dwk, void *workspace,
+                 size_t workspace_bytes, const RopeShape &s, const int64_t *dqo_st,
+                 const int64_t *dko_st, const int64_t *q_st, const int64_t *k_st,
+                 const int64_t *dq_st, const int64_t *dk_st, const int64_t *cs_st, void *stream) {
+  int rc = check_rope_shape(s);
+  if (rc) return rc;
+  if ((rc = check_tensor(dq_out, dqo_st, s.B, s.S, s.H, s.D))) return rc;
+  if ((rc = check_tensor(dk_out, dko_st, s.B, s.S, s.Hk, s.D))) return rc;
+  if ((rc = check_tensor(dq, dq_st, s.B, s.S, s.H, s.D))) return rc;
+  if ((rc = check_tensor(dk, dk_st, s.B, s.S, s.Hk, s.D))) return rc;
+  if ((rc = check_rope_table(cos, sin, cs_st))) return rc;
+  if ((rc = check_rope_eps(wq, wk, eps))) return rc;
+  const bool norm = wq != nullptr || wk != nullptr;
+  // The forward's inputs and the dw outputs matter only for a normed side.
+  if (wq != nullptr) {
+    if ((rc = check_tensor(q, q_st, s.B, s.S, s.H, s.D))) return rc;
+    if (dwq == nullptr) return FA_ERR_NULL_POINTER;
+    if (!aligned16(dwq)) return FA_ERR_ALIGNMENT;
+  }
+  if (wk != nullptr) {
+    if ((rc = check_tensor(k, k_st, s.B, s.S, s.Hk, s.D))) return rc;
+    if (dwk == nullptr) return FA_ERR_NULL_POINTER;
+    if (!aligned16(dwk)) return FA_ERR_ALIGNMENT;
+  }
+  if (norm) {
+    if (workspace == nullptr || workspace_bytes < 2 * rope_partial_bytes(s)) return FA_ERR_WORKSPACE;
+    if (!aligned16(workspace)) return FA_ERR_ALIGNMENT;
+  }
+
+  fa::RopeArgs a{};
+  const void *x[2] = {q, k}, *g[2] = {dq_out, dk_out};
+  void *y[2] = {dq, dk};
+  const void *w[2] = {wq, wk};
+  const int64_t *xs[2] = {q_st, k_st}, *gs[2] = {dqo_st, dko_st}, *ys[2] = {dq_st, dk_st};
+  const int heads[2] = {s.H, s.Hk};
+  for (int i = 0; i < 2; ++i) {
+    fa::RopeSide &t = a.side[i];
+    t.g = static_cast<const f16 *>(g[i]);
+    t.y = static_cast<f16 *>(y[i]);
+    t.w = static_cast<const f16 *>(w[i]);
+    rope_strides(gs[i], t.gb, t.gs, t.gh);
+    rope_strides(ys[i], t.yb, t.ys, t.yh);
+    if (t.w != nullptr) {
+      t.x = static_cast<const f16 *>(x[i]);
+      rope_strides(xs[i], t.xb, t.xs, t.xh);
+      t.partial = reinterpret_cast<float *>(static_cast<char *>(workspace) +
+                                            (size_t)i * rope_partial_bytes(s));
+    }
+    t.heads = heads[i];
+    t.rows = (int64_t)s.B * s.S * heads[i];
+  }
+  a.cos = static_cast<const f16 *>(cos);
+  a.sin = static_cast<const f16 *>(sin);
+  a.cb = cs_st[0];
+  a.cs = cs_st[1];
+  a.S = s.S;
+  a.eps = eps;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t blocks = rope_blocks(s, norm);
+  FA_ROPE_DISPATCH(launch_rope_bwd, s, a, blocks, dwq, dwk, st);
+}
+
 }  // namespace
 
 extern "C" {
@@ -374,6 +580,7 @@ const char *fa_strerror(int status) {
     case FA_ERR_TOO_LARGE: return "sizes exceed the kernel's index or grid limits";
     case FA_ERR_LAUNCH: return "the HIP runtime rejected a kernel launch";
     case FA_ERR_DTYPE: return "unsupported dtype (supported: FA_DTYPE_F16, FA_DTYPE_BF16)";
+    case FA_ERR_EPS: return "norm eps is negative or not finite";
     default: return "unknown status code";
   }
 }
@@ -458,6 +665,40 @@ int fa_bwd_dq(const void *dout, const void *q, const void *k, const void *v,
               float sm_scale, int causal, void *stream) {
   return run_dq(dout, q, k, v, lse, delta, dq, square(B, S, H, D), do_strides, q_strides,
                 k_strides, v_strides, dq_strides, sm_scale, causal, stream);
+}
+
+size_t fa_rope_qk_workspace_bytes(int B, int S, int H, int Hk, int D) {
+  const RopeShape s{B, S, H, Hk, D, FA_DTYPE_F16};
+  if (check_rope_shape(s) != FA_OK) return 0;
+  return 2 * rope_partial_bytes(s);
+}
+
+int fa_rope_qk_fwd(const void *q, const void *k, void *q_out, void *k_out,
+                   const void *cos, const void *sin,
+                   const void *q_norm_weight, const void *k_norm_weight, float eps,
+                   int B, int S, int H, int Hk, int D,
+                   const int64_t q_strides[4], const int64_t k_strides[4],
+                   const int64_t q_out_strides[4], const int64_t k_out_strides[4],
+                   const int64_t cs_strides[2], int dtype, void *stream) {
+  return run_rope_fwd(q, k, q_out, k_out, cos, sin, q_norm_weight, k_norm_weight, eps,
+                      RopeShape{B, S, H, Hk, D, dtype}, q_strides, k_strides, q_out_strides,
+                      k_out_strides, cs_strides, stream);
+}
+
+int fa_rope_qk_bwd(const void *dq_out, const void *dk_out, const void *q, const void *k,
+                   const void *cos, const void *sin,
+                   const void *q_norm_weight, const void *k_norm_weight, float eps,
+                   void *dq, void *dk, float *dq_norm_weight, float *dk_norm_weight,
+                   void *workspace, size_t workspace_bytes,
+                   int B, int S, int H, int Hk, int D,
+                   const int64_t dq_out_strides[4], const int64_t dk_out_strides[4],
+                   const int64_t q_strides[4], const int64_t k_strides[4],
+                   const int64_t dq_strides[4], const int64_t dk_strides[4],
+                   const int64_t cs_strides[2], int dtype, void *stream) {
+  return run_rope_bwd(dq_out, dk_out, q, k, cos, sin, q_norm_weight, k_norm_weight, eps, dq, dk,
+                      dq_norm_weight, dk_norm_weight, workspace, workspace_bytes,
+                      RopeShape{B, S, H, Hk, D, dtype}, dq_out_strides, dk_out_strides, q_strides,
+                      k_strides, dq_strides, dk_strides, cs_strides, stream);
 }
 
 }  // extern "C"

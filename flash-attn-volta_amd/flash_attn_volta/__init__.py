@@ -20,11 +20,16 @@ Beyond the reference (its wrapper requires q, k, v of one shape):
         grouped-query and multi-query attention, k and v (B, Sk, Hk, D)
         with H a multiple of Hk, Sq != Sk with a bottom-right causal
         mask (KV-cache prefill continuation), and bf16 as well as fp16.
+    apply_rotary_qk / rope_qk_forward / rope_qk_backward
+        the attention prologue fused into one pass: optional per-head
+        RMSNorm (Qwen3's q_norm / k_norm) and rotary position embedding
+        of q and k.
 """
 
 from .forward import flash_attn_forward, flash_attn_forward_gqa, flash_attn_volta
 from .backward import flash_attn_backward, flash_attn_backward_gqa
 from .autograd import flash_attn, flash_attn_gqa
+from .rope import apply_rotary_qk, rope_qk_backward, rope_qk_forward
 
 __all__ = [
     "flash_attn_forward",
@@ -34,5 +39,8 @@ __all__ = [
     "flash_attn_forward_gqa",
     "flash_attn_backward_gqa",
     "flash_attn_gqa",
+    "apply_rotary_qk",
+    "rope_qk_forward",
+    "rope_qk_backward",
 ]
-__version__ = "0.3.0"
+__version__ = "0.4.0"

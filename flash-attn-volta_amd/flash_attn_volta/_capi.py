@@ -14,7 +14,7 @@ import threading
 LIB_NAME = "libfa_mi355x.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # status codes (enum fa_status)
 FA_OK = 0
@@ -28,6 +28,7 @@ FA_ERR_WORKSPACE = -7
 FA_ERR_TOO_LARGE = -8
 FA_ERR_LAUNCH = -9
 FA_ERR_DTYPE = -10
+FA_ERR_EPS = -11
 
 # element types (enum fa_dtype)
 FA_DTYPE_F16 = 0
@@ -45,6 +46,9 @@ EXPORTED_SYMBOLS = (
     "fa_bwd_gqa",
     "fa_bwd_dkdv",
     "fa_bwd_dq",
+    "fa_rope_qk_fwd",
+    "fa_rope_qk_workspace_bytes",
+    "fa_rope_qk_bwd",
 )
 
 _lock = threading.Lock()
@@ -110,6 +114,19 @@ def _declare(lib):
                               _ci, _ci, _ci, _ci,
                               _i64x4, _i64x4, _i64x4, _i64x4, _i64x4,
                               ctypes.c_float, _ci, _vp]
+    _i64x2 = ctypes.POINTER(ctypes.c_int64)
+    lib.fa_rope_qk_fwd.restype = _ci
+    lib.fa_rope_qk_fwd.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_float,
+                                   _ci, _ci, _ci, _ci, _ci,
+                                   _i64x4, _i64x4, _i64x4, _i64x4, _i64x2, _ci, _vp]
+    lib.fa_rope_qk_workspace_bytes.restype = ctypes.c_size_t
+    lib.fa_rope_qk_workspace_bytes.argtypes = [_ci, _ci, _ci, _ci, _ci]
+    lib.fa_rope_qk_bwd.restype = _ci
+    lib.fa_rope_qk_bwd.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_float,
+                                   _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t,
+                                   _ci, _ci, _ci, _ci, _ci,
+                                   _i64x4, _i64x4, _i64x4, _i64x4, _i64x4, _i64x4,
+                                   _i64x2, _ci, _vp]
 
 
 def load(path: str | None = None):

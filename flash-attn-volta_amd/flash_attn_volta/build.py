@@ -16,7 +16,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG_DIR)                  # flash-attn-volta_amd/
 CSRC = os.path.join(ROOT, "csrc")
 SOURCES = [os.path.join(CSRC, "fa_api.hip")]
-HEADERS = [os.path.join(CSRC, f) for f in ("fa_common.hpp", "fa_fwd.hpp", "fa_bwd.hpp")]
+HEADERS = [os.path.join(CSRC, f) for f in ("fa_common.hpp", "fa_fwd.hpp", "fa_bwd.hpp", "fa_rope.hpp")]
 OUT = os.path.join(PKG_DIR, "libfa_mi355x.so")
 
 HIPCC_FLAGS = [

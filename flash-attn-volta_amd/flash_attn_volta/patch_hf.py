@@ -31,16 +31,30 @@ repeat_kv (:186-188, :470-471), and a KV cache with content
 sees cache positions j <= i + kv_len - q_len), as a dynamic cache gives.
 Anything else runs the module's original attention implementation
 unchanged.
+
+For the Llama, Qwen2 and Qwen3 families the patch also replaces the
+module's forward (the reference does the same for transformers 4.44,
+patch_hf.py:164-198, 284-313, 425-480) so that the attention prologue --
+Qwen3's q_norm / k_norm and the rotary embedding, which transformers runs as
+some ten elementwise kernels per tensor and direction -- is one fused
+kernel (apply_rotary_qk) that also writes q and k in the (B, S, H, D)
+layout the attention kernels read.  The projections, cache update and
+output projection are the module's own layers, called as transformers
+calls them.  A module whose prologue is not the standard one (another norm
+type, partial rotary tables, CPU tensors) runs its original forward.
+``fuse_rope=False`` keeps transformers' own prologue.
 """
 from __future__ import annotations
 
 import copy
 import sys
+import types
 from typing import Optional, Tuple
 
 import torch
 
 from .autograd import flash_attn, flash_attn_gqa
+from .rope import ROPE_HEAD_DIMS, apply_rotary_qk
 
 ATTN_IMPLEMENTATION = "flash_attn_volta"
 
@@ -194,6 +208,85 @@ def flash_attn_volta_attention(
     return out.to(out_dtype), None
 
 
+# Norm modules that compute weight * x / sqrt(mean(x^2) + eps) over the last
+# dimension (transformers' Qwen3RMSNorm and its identical siblings).
+_RMSNORM_NAMES = {"Qwen3RMSNorm", "Qwen2RMSNorm", "LlamaRMSNorm"}
+
+
+def _qk_norm(module, name: str, D: int):
+    """(weight, eps) of the module's q_norm / k_norm; (None, None) when it
+    has none; raises LookupError for a norm the fused kernel does not
+    implement."""
+    m = getattr(module, name, None)
+    if m is None or isinstance(m, torch.nn.Identity):
+        return None, None
+    w = getattr(m, "weight", None)
+    eps = getattr(m, "variance_epsilon", None)
+    if type(m).__name__ not in _RMSNORM_NAMES or w is None or tuple(w.shape) != (D,) or eps is None:
+        raise LookupError(name)
+    return w, float(eps)
+
+
+def fused_prologue_args(module, hidden_states: torch.Tensor, position_embeddings):
+    """The arguments of apply_rotary_qk for this call, ``(cos, sin, q_norm
+    weight, k_norm weight, eps)``, or None when the prologue must run as
+    transformers writes it: CPU or non-16-bit activations, a head dim the
+    kernel lacks, rotary tables that are not (B or 1, S, head_dim) (partial
+    rotary), tables that require grad, or a QK-norm of another kind."""
+    if not hidden_states.is_cuda or hidden_states.dtype not in (torch.float16, torch.bfloat16):
+        return None
+    D = getattr(module, "head_dim", None)
+    if D not in ROPE_HEAD_DIMS or hidden_states.dim() != 3:
+        return None
+    if not isinstance(position_embeddings, (tuple, list)) or len(position_embeddings) != 2:
+        return None
+    cos, sin = position_embeddings
+    if not (isinstance(cos, torch.Tensor) and isinstance(sin, torch.Tensor)):
+        return None
+    B, S = hidden_states.shape[:2]
+    if cos.shape != sin.shape or cos.dim() != 3 or tuple(cos.shape[1:]) != (S, D) \
+            or cos.shape[0] not in (1, B) or cos.requires_grad or sin.requires_grad:
+        return None
+    try:
+        wq, eq = _qk_norm(module, "q_norm", D)
+        wk, ek = _qk_norm(module, "k_norm", D)
+    except LookupError:
+        return None
+    if eq is not None and ek is not None and eq != ek:
+        return None
+    eps = eq if eq is not None else (ek if ek is not None else 1e-6)
+    return cos, sin, wq, wk, eps
+
+
+def _fused_forward(self, hidden_states: torch.Tensor, position_embeddings=None,
+                   attention_mask: Optional[torch.Tensor] = None, past_key_values=None, **kwargs):
+    """transformers 5.x Llama / Qwen2 / Qwen3 attention forward with the
+    q/k prologue fused (same arguments and results as the module's own)."""
+    args = fused_prologue_args(self, hidden_states, position_embeddings)
+    if args is None:
+        return self._orig_forward(hidden_states, position_embeddings=position_embeddings,
+                                  attention_mask=attention_mask, past_key_values=past_key_values,
+                                  **kwargs)
+    cos, sin, wq, wk, eps = args
+    input_shape = hidden_states.shape[:-1]
+    hidden_shape = (*input_shape, -1, self.head_dim)
+    q = self.q_proj(hidden_states).view(hidden_shape)          # (B, S, H, D)
+    k = self.k_proj(hidden_states).view(hidden_shape)
+    v = self.v_proj(hidden_states).view(hidden_shape)
+    q, k = apply_rotary_qk(q, k, cos, sin, wq, wk, eps)
+    query_states, key_states, value_states = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+    if past_key_values is not None:
+        key_states, value_states = past_key_values.update(key_states, value_states, self.layer_idx)
+    if "sliding_window" in self.__dict__ or hasattr(type(self), "sliding_window"):
+        kwargs.setdefault("sliding_window", self.sliding_window)
+    attn_output, attn_weights = flash_attn_volta_attention(
+        self, query_states, key_states, value_states, attention_mask,
+        dropout=0.0 if not self.training else self.attention_dropout,
+        scaling=self.scaling, **kwargs)
+    attn_output = attn_output.reshape(*input_shape, -1).contiguous()
+    return self.o_proj(attn_output), attn_weights
+
+
 _registered = False
 
 
@@ -206,7 +299,7 @@ def _register() -> None:
     _registered = True
 
 
-def _patch(model: torch.nn.Module, names) -> int:
+def _patch(model: torch.nn.Module, names, fuse_rope: bool = False) -> int:
     _register()
     n = 0
     for mod in model.modules():
@@ -222,6 +315,9 @@ def _patch(model: torch.nn.Module, names) -> int:
             routed._attn_implementation_internal = ATTN_IMPLEMENTATION
             mod.config = routed
             mod._orig_forward = mod.forward
+            if fuse_rope and all(hasattr(mod, a) for a in ("q_proj", "k_proj", "v_proj",
+                                                           "o_proj", "head_dim")):
+                mod.forward = types.MethodType(_fused_forward, mod)
         n += 1
     return n
 
@@ -235,6 +331,7 @@ def _unpatch(model: torch.nn.Module, names) -> int:
             del mod._fav_orig_impl
             if "_orig_forward" in mod.__dict__:
                 del mod._orig_forward
+            mod.__dict__.pop("forward", None)
             n += 1
     return n
 
@@ -248,33 +345,36 @@ def unpatch_gpt2(model: torch.nn.Module) -> int:
     return _unpatch(model, _GPT2_NAMES)
 
 
-def patch_qwen2(model: torch.nn.Module) -> int:
-    """Patch every Qwen2 attention block on ``model``. Returns count patched."""
-    return _patch(model, _QWEN2_NAMES)
+def patch_qwen2(model: torch.nn.Module, fuse_rope: bool = True) -> int:
+    """Patch every Qwen2 attention block on ``model``. Returns count patched.
+    ``fuse_rope``: run the rotary prologue as one fused kernel."""
+    return _patch(model, _QWEN2_NAMES, fuse_rope)
 
 
 def unpatch_qwen2(model: torch.nn.Module) -> int:
     return _unpatch(model, _QWEN2_NAMES)
 
 
-def patch_qwen3(model: torch.nn.Module) -> int:
-    """Patch every Qwen3 attention block (QK-norm is HuggingFace's own code,
-    applied before the routed attention call). Returns count patched; 0 when
-    the installed transformers has no Qwen3."""
+def patch_qwen3(model: torch.nn.Module, fuse_rope: bool = True) -> int:
+    """Patch every Qwen3 attention block. Returns count patched; 0 when the
+    installed transformers has no Qwen3.  ``fuse_rope``: run QK-norm and the
+    rotary embedding as one fused kernel (else transformers' own modules,
+    applied before the routed attention call)."""
     try:
         from transformers.models.qwen3 import modeling_qwen3  # noqa: F401
     except ImportError:
         return 0
-    return _patch(model, _QWEN3_NAMES)
+    return _patch(model, _QWEN3_NAMES, fuse_rope)
 
 
 def unpatch_qwen3(model: torch.nn.Module) -> int:
     return _unpatch(model, _QWEN3_NAMES)
 
 
-def patch_llama(model: torch.nn.Module) -> int:
-    """Patch every Llama attention block on ``model``. Returns count patched."""
-    return _patch(model, _LLAMA_NAMES)
+def patch_llama(model: torch.nn.Module, fuse_rope: bool = True) -> int:
+    """Patch every Llama attention block on ``model``. Returns count patched.
+    ``fuse_rope``: run the rotary prologue as one fused kernel."""
+    return _patch(model, _LLAMA_NAMES, fuse_rope)
 
 
 def unpatch_llama(model: torch.nn.Module) -> int:
@@ -322,8 +422,9 @@ def _linear_attn_family(model: torch.nn.Module) -> Optional[str]:
     return None
 
 
-def patch_model(model: torch.nn.Module) -> Tuple[str, int]:
+def patch_model(model: torch.nn.Module, fuse_rope: bool = True) -> Tuple[str, int]:
     """Detect the model family and patch it. Returns ``(family, n_patched)``.
+    ``fuse_rope`` is passed to the Llama / Qwen2 / Qwen3 patches.
 
     Raises ``RuntimeError`` for linear-attention / state-space models, for
     which softmax attention would be mathematically wrong, and
@@ -340,9 +441,9 @@ def patch_model(model: torch.nn.Module) -> Tuple[str, int]:
     if "GPT2" in cls or any(type(m).__name__ in _GPT2_NAMES for m in mods):
         return "gpt2", patch_gpt2(model)
     if "Qwen3" in cls or any(_is_qwen3_attention(m) for m in mods):
-        return "qwen3", patch_qwen3(model)
+        return "qwen3", patch_qwen3(model, fuse_rope)
     if "Qwen2" in cls or any(_is_qwen2_attention(m) for m in mods):
-        return "qwen2", patch_qwen2(model)
+        return "qwen2", patch_qwen2(model, fuse_rope)
     if "Llama" in cls or any(_is_llama_attention(m) for m in mods):
-        return "llama", patch_llama(model)
+        return "llama", patch_llama(model, fuse_rope)
     raise ValueError(f"no patch known for model class {cls}")

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 3
+#define FA_ABI_VERSION 4
 
 enum fa_status {
   FA_OK = 0,
@@ -45,7 +45,8 @@ enum fa_status {
   FA_ERR_TOO_LARGE = -8,      /* sizes whose element offsets overflow int64
                                  or whose grid exceeds the launch limits    */
   FA_ERR_LAUNCH = -9,         /* the HIP runtime rejected a kernel launch   */
-  FA_ERR_DTYPE = -10          /* dtype not one of enum fa_dtype             */
+  FA_ERR_DTYPE = -10,         /* dtype not one of enum fa_dtype             */
+  FA_ERR_EPS = -11            /* norm eps negative or not finite            */
 };
 
 /* Element type of the 16-bit tensors (fa_fwd_gqa / fa_bwd_gqa; the other
@@ -184,6 +185,60 @@ int fa_bwd_dq(const void *dout, const void *q, const void *k, const void *v,
               const int64_t k_strides[4], const int64_t v_strides[4],
               const int64_t dq_strides[4],
               float sm_scale, int causal, void *stream);
+
+/*
+ * Fused attention prologue for q and k: optional per-head RMSNorm (QK-norm)
+ * followed by rotary position embedding in the rotate-half form.  For each
+ * row x (one (b, s, head) of D elements) of q and of k:
+ *
+ *   y = w * x / sqrt(mean(x^2) + eps)      when that side's norm weight w
+ *   y = x                                  is given, else
+ *   out[d]       = y[d] cos[d]         - y[d + D/2] sin[d]        (d < D/2)
+ *   out[d + D/2] = y[d + D/2] cos[d + D/2] + y[d] sin[d + D/2]
+ *
+ * computed in fp32 and rounded once.  q, q_out: (B, S, H, D); k, k_out:
+ * (B, S, Hk, D), strides {b, s, h, d} as for the attention calls; cos, sin:
+ * (B or 1, S, D) tables of the same dtype with element strides
+ * cs_strides = {b, s} (d stride 1; b stride 0 shares one table across the
+ * batch); q_norm_weight / k_norm_weight: (D) of the same dtype, or NULL for
+ * no norm on that side; eps is used only with a weight.  D in {16, 32, 64,
+ * 128}; dtype is FA_DTYPE_F16 or FA_DTYPE_BF16.
+ *
+ * Replaces the prologue the reference leaves to transformers before its
+ * attention call: Qwen3's q_norm / k_norm then apply_rotary_pos_emb
+ * (flash_attn_volta/patch_hf.py:291-303), and apply_rotary_pos_emb alone
+ * for Qwen2 / Llama (patch_hf.py:177, :462).  The reference lists the fused
+ * QK-norm as not landed (PERF.md:99-104).
+ */
+int fa_rope_qk_fwd(const void *q, const void *k, void *q_out, void *k_out,
+                   const void *cos, const void *sin,
+                   const void *q_norm_weight, const void *k_norm_weight, float eps,
+                   int B, int S, int H, int Hk, int D,
+                   const int64_t q_strides[4], const int64_t k_strides[4],
+                   const int64_t q_out_strides[4], const int64_t k_out_strides[4],
+                   const int64_t cs_strides[2], int dtype, void *stream);
+
+/* Bytes of workspace fa_rope_qk_bwd needs when a norm weight is given (0 for
+ * an invalid shape).  Depends only on the sizes. */
+size_t fa_rope_qk_workspace_bytes(int B, int S, int H, int Hk, int D);
+
+/*
+ * Backward of fa_rope_qk_fwd: from the gradients of q_out / k_out, the
+ * gradients of q / k, and for a normed side the gradient of its weight,
+ * (D) fp32, reduced in a fixed order (reproducible).  q / k (the forward's
+ * inputs), dq_norm_weight / dk_norm_weight and the workspace are read only
+ * for a side with a norm weight and may be NULL otherwise.
+ */
+int fa_rope_qk_bwd(const void *dq_out, const void *dk_out, const void *q, const void *k,
+                   const void *cos, const void *sin,
+                   const void *q_norm_weight, const void *k_norm_weight, float eps,
+                   void *dq, void *dk, float *dq_norm_weight, float *dk_norm_weight,
+                   void *workspace, size_t workspace_bytes,
+                   int B, int S, int H, int Hk, int D,
+                   const int64_t dq_out_strides[4], const int64_t dk_out_strides[4],
+                   const int64_t q_strides[4], const int64_t k_strides[4],
+                   const int64_t dq_strides[4], const int64_t dk_strides[4],
+                   const int64_t cs_strides[2], int dtype, void *stream);
 
 #ifdef __cplusplus
 }

@@ -46,11 +46,11 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.fa_abi_version() == _capi.ABI_VERSION == 3
+    assert lib.fa_abi_version() == _capi.ABI_VERSION == 4
 
 
 def test_strerror_covers_every_code(lib):
-    codes = [0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10]
+    codes = [0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10, -11]
     msgs = [lib.fa_strerror(c).decode() for c in codes]
     assert len(set(msgs)) == len(codes)
     assert "unknown" in lib.fa_strerror(-1234).decode()
@@ -156,3 +156,55 @@ def test_bwd_gqa_validation(lib):
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(_capi.LibraryNotBuilt):
         _capi.load(str(tmp_path / "nope.so"))
+
+
+def _rope_fwd(lib, B=2, S=64, H=4, Hk=2, D=64, q=P, k=P, qo=P, ko=P, cos=P, sin=P, wq=None,
+              wk=None, eps=1e-6, qst=None, cs=(64 * 64, 64), dtype=_capi.FA_DTYPE_F16):
+    sq = qst or _st(B, S, H, D)
+    sk = _st(B, S, Hk, D)
+    return lib.fa_rope_qk_fwd(q, k, qo, ko, cos, sin, wq, wk, eps, B, S, H, Hk, D, sq, sk, sq, sk,
+                              (ctypes.c_int64 * 2)(*cs), dtype, None)
+
+
+def test_rope_fwd_validation(lib):
+    assert _rope_fwd(lib, D=48) == _capi.FA_ERR_HEAD_DIM
+    assert _rope_fwd(lib, D=256) == _capi.FA_ERR_HEAD_DIM
+    assert _rope_fwd(lib, B=0) == _capi.FA_ERR_SHAPE
+    assert _rope_fwd(lib, Hk=0) == _capi.FA_ERR_SHAPE
+    assert _rope_fwd(lib, S=-3) == _capi.FA_ERR_SHAPE
+    assert _rope_fwd(lib, dtype=2) == _capi.FA_ERR_DTYPE
+    assert _rope_fwd(lib, q=None) == _capi.FA_ERR_NULL_POINTER
+    assert _rope_fwd(lib, ko=None) == _capi.FA_ERR_NULL_POINTER
+    assert _rope_fwd(lib, sin=None) == _capi.FA_ERR_NULL_POINTER
+    assert _rope_fwd(lib, k=BAD) == _capi.FA_ERR_ALIGNMENT
+    assert _rope_fwd(lib, cos=BAD) == _capi.FA_ERR_ALIGNMENT
+    assert _rope_fwd(lib, wq=BAD) == _capi.FA_ERR_ALIGNMENT
+    assert _rope_fwd(lib, cs=(64 * 64, 60)) == _capi.FA_ERR_STRIDE
+    assert _rope_fwd(lib, cs=(-8, 64)) == _capi.FA_ERR_STRIDE
+    assert _rope_fwd(lib, qst=(ctypes.c_int64 * 4)(64 * 256, 256, 64, 2)) == _capi.FA_ERR_STRIDE
+    assert _rope_fwd(lib, wq=P, eps=-1e-6) == _capi.FA_ERR_EPS
+    assert _rope_fwd(lib, wk=P, eps=float("nan")) == _capi.FA_ERR_EPS
+    assert _rope_fwd(lib, wk=P, eps=float("inf")) == _capi.FA_ERR_EPS
+
+
+def test_rope_bwd_validation(lib):
+    B, S, H, Hk, D = 1, 128, 8, 2, 128
+    sq, sk = _st(B, S, H, D), _st(B, S, Hk, D)
+    cs = (ctypes.c_int64 * 2)(0, D)
+    ws = lib.fa_rope_qk_workspace_bytes(B, S, H, Hk, D)
+    assert ws > 0 and ws % 16 == 0
+    assert lib.fa_rope_qk_workspace_bytes(B, S, H, Hk, 96) == 0
+    assert lib.fa_rope_qk_workspace_bytes(0, S, H, Hk, D) == 0
+
+    def call(q=P, wq=P, dwq=P, ws_ptr=P, ws_bytes=ws, dq=P, eps=1e-6):
+        return lib.fa_rope_qk_bwd(P, P, q, P, P, P, wq, None, eps, dq, P, dwq, None, ws_ptr,
+                                  ws_bytes, B, S, H, Hk, D, sq, sk, sq, sk, sq, sk, cs,
+                                  _capi.FA_DTYPE_BF16, None)
+    assert call(ws_bytes=ws - 4) == _capi.FA_ERR_WORKSPACE
+    assert call(ws_ptr=None) == _capi.FA_ERR_WORKSPACE
+    assert call(ws_ptr=BAD) == _capi.FA_ERR_ALIGNMENT
+    assert call(q=None) == _capi.FA_ERR_NULL_POINTER        # a normed side needs its input
+    assert call(dwq=None) == _capi.FA_ERR_NULL_POINTER      # ... and its weight-gradient output
+    assert call(dq=None) == _capi.FA_ERR_NULL_POINTER
+    assert call(dq=BAD) == _capi.FA_ERR_ALIGNMENT
+    assert call(eps=-1.0) == _capi.FA_ERR_EPS

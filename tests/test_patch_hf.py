@@ -160,3 +160,76 @@ def test_expand_kv_matches_transformers_repeat_kv():
     x = torch.randn(2, 3, 5, 8)
     assert torch.equal(patch_hf._expand_kv(x, 4), repeat_kv(x, 4))
     assert patch_hf._expand_kv(x, 1) is x
+
+
+@pytest.mark.parametrize("family,make,names,patch,unpatch", [
+    ("llama", hf_models.tiny_llama, patch_hf._LLAMA_NAMES, patch_hf.patch_llama, patch_hf.unpatch_llama),
+    ("qwen2", hf_models.tiny_qwen2, patch_hf._QWEN2_NAMES, patch_hf.patch_qwen2, patch_hf.unpatch_qwen2),
+    ("qwen3", hf_models.tiny_qwen3, patch_hf._QWEN3_NAMES, patch_hf.patch_qwen3, patch_hf.unpatch_qwen3),
+])
+def test_fused_prologue_forward_is_installed_and_removed(family, make, names, patch, unpatch):
+    model = make()
+    assert patch(model, fuse_rope=False) == 2
+    assert all("forward" not in m.__dict__ for m in _attn_modules(model, names))
+    unpatch(model)
+    assert patch(model) == 2                     # fused by default
+    mods = _attn_modules(model, names)
+    assert all(m.forward.__func__ is patch_hf._fused_forward for m in mods)
+    ids = hf_models.token_ids(16)
+    with torch.no_grad():                        # CPU: falls back to the module's own forward
+        out = model(ids).logits
+    assert unpatch(model) == 2
+    assert all("forward" not in m.__dict__ for m in mods)
+    with torch.no_grad():
+        assert torch.equal(model(ids).logits, out)
+
+
+def test_gpt2_gets_no_fused_prologue():
+    model = hf_models.tiny_gpt2()
+    patch_hf.patch_gpt2(model)
+    assert all("forward" not in m.__dict__
+               for m in _attn_modules(model, patch_hf._GPT2_NAMES))
+
+
+class _FakeHidden:
+    """Stands in for a GPU activation tensor in the prologue decision."""
+
+    def __init__(self, B, S, hidden, dtype=torch.float16, cuda=True):
+        self.shape = (B, S, hidden)
+        self.dtype = dtype
+        self.is_cuda = cuda
+
+    def dim(self):
+        return 3
+
+
+def test_fused_prologue_decisions():
+    qwen3 = _attn_modules(hf_models.tiny_qwen3(), patch_hf._QWEN3_NAMES)[0]
+    llama = _attn_modules(hf_models.tiny_llama(), patch_hf._LLAMA_NAMES)[0]
+    D3, DL = qwen3.head_dim, llama.head_dim
+    B, S = 2, 7
+    h = _FakeHidden(B, S, 128)
+    t3 = (torch.ones(B, S, D3), torch.zeros(B, S, D3))
+    args = patch_hf.fused_prologue_args(qwen3, h, t3)
+    assert args is not None
+    cos, sin, wq, wk, eps = args
+    assert wq is qwen3.q_norm.weight and wk is qwen3.k_norm.weight
+    assert eps == qwen3.q_norm.variance_epsilon
+    la = patch_hf.fused_prologue_args(llama, h, (torch.ones(1, S, DL), torch.zeros(1, S, DL)))
+    assert la is not None and la[2] is None and la[3] is None
+    # fall back to transformers' own prologue:
+    assert patch_hf.fused_prologue_args(qwen3, _FakeHidden(B, S, 128, cuda=False), t3) is None
+    assert patch_hf.fused_prologue_args(qwen3, _FakeHidden(B, S, 128, torch.float32), t3) is None
+    half = (torch.ones(B, S, D3 // 2), torch.zeros(B, S, D3 // 2))      # partial rotary
+    assert patch_hf.fused_prologue_args(qwen3, h, half) is None
+    assert patch_hf.fused_prologue_args(qwen3, h, (t3[0][:, :3], t3[1][:, :3])) is None
+    assert patch_hf.fused_prologue_args(qwen3, h, (torch.ones(3, S, D3), torch.zeros(3, S, D3))) is None
+    assert patch_hf.fused_prologue_args(qwen3, h, (t3[0].requires_grad_(True), t3[1])) is None
+    assert patch_hf.fused_prologue_args(qwen3, h, None) is None
+    other = hf_models.tiny_qwen3()
+    m = _attn_modules(other, patch_hf._QWEN3_NAMES)[0]
+    m.q_norm = torch.nn.LayerNorm(D3)                                   # another norm kind
+    assert patch_hf.fused_prologue_args(m, h, (torch.ones(B, S, D3), torch.zeros(B, S, D3))) is None
+    m2 = _attn_modules(hf_models.tiny_qwen3(), patch_hf._QWEN3_NAMES)[0]
+    m2.k_norm.variance_epsilon = 1e-5                                   # eps differ
+    assert patch_hf.fused_prologue_args(m2, h, (torch.ones(B, S, D3), torch.zeros(B, S, D3))) is None

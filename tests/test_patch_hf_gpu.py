@@ -80,6 +80,9 @@ def _grads(model, names):
         m = qs[i]
         w = m.q_proj.weight if hasattr(m, "q_proj") else m.c_attn.weight
         out[f"attn{i}"] = w.grad
+        for nm in ("q_norm", "k_norm"):
+            if hasattr(m, nm):
+                out[f"{nm}{i}"] = getattr(m, nm).weight.grad
     return out
 
 
@@ -100,14 +103,22 @@ FAMILIES = [
 ]
 
 
-@pytest.mark.parametrize("family,make,names,patch", FAMILIES, ids=[f[0] for f in FAMILIES])
-def test_tiny_models_match_fp32_attention(family, make, names, patch):
-    print(f"[case] patch_hf {family}", flush=True)
+CASES = [f + (True,) for f in FAMILIES] + [f + (False,) for f in FAMILIES if f[0] != "gpt2"]
+
+
+@pytest.mark.parametrize("family,make,names,patch,fuse", CASES,
+                         ids=[f"{c[0]}{'' if c[4] else '-hf_prologue'}" for c in CASES])
+def test_tiny_models_match_fp32_attention(family, make, names, patch, fuse):
+    """Patched model (kernel attention; for Llama / Qwen2 / Qwen3 with the
+    fused QK-norm + rotary prologue unless fuse is False) against the
+    unpatched model with fp32 attention; the gradients checked include
+    Qwen3's q_norm / k_norm weights."""
+    print(f"[case] patch_hf {family} fuse_rope={fuse}", flush=True)
     ref = make().half().cuda().train()
     ours = make().half().cuda().train()
     ours.load_state_dict(ref.state_dict())
     _route_fp32(ref, names)
-    assert patch(ours) == 2
+    assert (patch(ours) if family == "gpt2" else patch(ours, fuse_rope=fuse)) == 2
     ids = hf_models.token_ids(300, vocab=512, batch=2, seed=1, device="cuda")
     lr, loss_r = _step(ref, ids)
     lo, loss_o = _step(ours, ids)
@@ -159,6 +170,32 @@ def test_patched_fast_path_actually_runs(monkeypatch):
     with torch.no_grad():
         gqa(hf_models.token_ids(64, device="cuda"))
     assert calls == {"square": 2, "gqa": 2}
+
+
+@pytest.mark.parametrize("family,make,names,patch", FAMILIES[:3], ids=[f[0] for f in FAMILIES[:3]])
+def test_fused_prologue_actually_runs(monkeypatch, family, make, names, patch):
+    """Llama / Qwen2 / Qwen3: one fused prologue call per layer and forward,
+    with Qwen3's norm weights passed in; none with fuse_rope=False."""
+    import flash_attn_volta.patch_hf as ph
+    seen = []
+    real = ph.apply_rotary_qk
+
+    def spy(q, k, cos, sin, wq=None, wk=None, eps=1e-6):
+        seen.append((wq is not None, wk is not None))
+        return real(q, k, cos, sin, wq, wk, eps)
+
+    monkeypatch.setattr(ph, "apply_rotary_qk", spy)
+    model = make().half().cuda()
+    patch(model)
+    with torch.no_grad():
+        model(hf_models.token_ids(64, device="cuda"))
+    normed = family == "qwen3"
+    assert seen == [(normed, normed)] * 2
+    ph.unpatch_llama(model), ph.unpatch_qwen2(model), ph.unpatch_qwen3(model)
+    patch(model, fuse_rope=False)
+    with torch.no_grad():
+        model(hf_models.token_ids(64, device="cuda"))
+    assert len(seen) == 2
 
 
 def _greedy_logits(model, ids, steps):
@@ -252,21 +289,39 @@ def test_bf16_model_runs_in_bf16(monkeypatch):
     assert _cos(la, lb) >= 0.999 and (la - lb).abs().max().item() <= 0.25
 
 
-def test_config5_llama_training_step():
+def _rope_fp32_once(q, k, cos, sin, wq=None, wk=None, eps=1e-6):
+    """The fused prologue's rounding model in eager torch: norm and rotation
+    in fp32, one rounding to the input dtype (autograd through torch ops)."""
+    def side(x, w):
+        xf = x.float()
+        if w is not None:
+            xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * w.float()
+        c, s = cos.float()[:, :, None], sin.float()[:, :, None]
+        h = xf.shape[-1] // 2
+        rot = torch.cat((-xf[..., h:], xf[..., :h]), -1)
+        return (xf * c + rot * s).to(x.dtype).contiguous()
+    return side(q, wq), side(k, wk)
+
+
+def test_config5_llama_training_step(monkeypatch):
     """16 layers, hidden 2048, 16 heads x 128, SwiGLU 5632,
     RMSNorm, RoPE theta 10000, vocab 32000, N(0, 0.02) init, fp16; one
     training step (causal LM loss, fwd + bwd) at B=1, S=4096.
 
-    Three runs on identical weights and ids: attention on the HIP kernels,
-    fp32 eager attention (the reference), and float64 eager attention (a
-    control that is exact up to rounding).  In fp16 training at random init
-    the deep-layer gradients are ~1e-6, stored as fp16 subnormals, so even
-    the two exact attentions disagree on deep q_proj gradients (cos ~0.988):
-    that is the noise floor.  The kernel must sit at that floor for every
-    layer -- no further from the fp32 reference than the float64 control is
-    (cosine within 3e-3) -- and match loss, logits and lm_head gradients.
+    Runs on identical weights and ids: the reference (transformers' own
+    prologue, fp32 eager attention); the patch without and with the fused
+    rotary prologue (attention on the HIP kernels); and two exact-attention
+    controls (float64 eager attention), one with transformers' prologue and
+    one with the fused prologue's rounding model (fp32, rounded once).  In
+    fp16 training at random init the deep-layer gradients are ~1e-6, stored
+    as fp16 subnormals, so even an exact attention disagrees with the
+    reference on deep q_proj gradients (cos ~0.99): that is the noise floor.
+    Each patched run must sit at the floor of its control -- no further from
+    the reference than the float64 control with the same prologue (cosine
+    within 3e-3) -- and match loss, logits and lm_head gradients.
     """
     from transformers import LlamaConfig, LlamaForCausalLM
+    import flash_attn_volta.patch_hf as ph
     print("[case] config5 llama training step", flush=True)
     cfg = LlamaConfig(vocab_size=32000, hidden_size=2048, intermediate_size=5632,
                       num_hidden_layers=16, num_attention_heads=16, num_key_value_heads=16,
@@ -287,23 +342,34 @@ def test_config5_llama_training_step():
         for m in mods:
             m.config = model.config
 
+    assert patch_hf.patch_llama(model, fuse_rope=False) == 16
+    plain = run()
+    patch_hf.unpatch_llama(model)
     assert patch_hf.patch_llama(model) == 16
-    lo, loss_o, head_o, qo = run()
+    fused = run()
+    with monkeypatch.context() as mp:
+        # the fused forward with an exact attention and an eager prologue of
+        # the same rounding model
+        mp.setattr(ph, "apply_rotary_qk", _rope_fp32_once)
+        mp.setattr(ph, "flash_attn_volta_attention", _make_eager(torch.float64))
+        ctrl_fused = run()
     patch_hf.unpatch_llama(model)
     _route_fp32(model, names)
     lr, loss_r, head_r, qr = run()
     unroute()
     _route_attention(model, names, FP64_CTRL, _make_eager(torch.float64))
-    _, loss_c, _, qc = run()
+    ctrl_plain = run()
     unroute()
 
-    print(f"[config5] loss flash {loss_o:.6f}  fp32-attention {loss_r:.6f}  fp64-attention {loss_c:.6f}",
-          flush=True)
-    assert math.isfinite(loss_o) and abs(loss_o - loss_r) <= 1e-4 * abs(loss_r)
-    assert _cos(lo, lr) >= 0.999 and (lo - lr).abs().max().item() <= 0.1
-    assert _cos(head_o, head_r) >= 0.999
-    for i in range(len(mods)):
-        c_ours, c_ctrl = _cos(qo[i], qr[i]), _cos(qc[i], qr[i])
-        print(f"[config5] layer {i:2d} q_proj grad cos vs fp32: flash {c_ours:.5f}  fp64 control {c_ctrl:.5f}",
-              flush=True)
-        assert c_ours >= c_ctrl - 3e-3
+    print(f"[config5] loss reference {loss_r:.6f}  flash {plain[1]:.6f}  flash+fused-rope "
+          f"{fused[1]:.6f}  fp64 controls {ctrl_plain[1]:.6f} / {ctrl_fused[1]:.6f}", flush=True)
+    for label, (lo, loss_o, head_o, qo), (_, _, _, qc) in (("flash", plain, ctrl_plain),
+                                                          ("flash+fused-rope", fused, ctrl_fused)):
+        assert math.isfinite(loss_o) and abs(loss_o - loss_r) <= 1e-4 * abs(loss_r)
+        assert _cos(lo, lr) >= 0.999 and (lo - lr).abs().max().item() <= 0.1
+        assert _cos(head_o, head_r) >= 0.999
+        for i in range(len(mods)):
+            c_ours, c_ctrl = _cos(qo[i], qr[i]), _cos(qc[i], qr[i])
+            print(f"[config5] {label:16s} layer {i:2d} q_proj grad cos vs reference: {c_ours:.5f}  "
+                  f"fp64 control {c_ctrl:.5f}", flush=True)
+            assert c_ours >= c_ctrl - 3e-3
