@@ -449,6 +449,61 @@ def run_rope(steps, warmup):
               f"{r['attention_fwd_bwd_us']} |")
 
 
+# Decode workloads (one new token, or a few, against a KV cache), fp16,
+# causal: (B, Sq, Sk, H, Hk, D)
+DECODE_TABLE = [
+    (1, 1, 4096, 32, 8, 128),
+    (1, 1, 32768, 32, 8, 128),
+    (1, 1, 131072, 64, 8, 128),
+    (8, 1, 8192, 32, 8, 128),
+    (4, 4, 8192, 32, 8, 128),
+    (1, 1, 8192, 32, 32, 128),
+    (1, 1, 4096, 16, 16, 64),
+]
+
+
+def run_decode(steps, warmup):
+    """Decode-step attention: fa_fwd_splitkv (keys split over workgroups,
+    partials merged by LSE) against the unsplit fa_fwd_gqa on the same
+    inputs, by HIP events around back-to-back C-ABI launches.  Algorithmic
+    bytes = K and V read once + Q read + O written (+ LSE); HBM-bound."""
+    import torch
+    from flash_attn_volta import _capi
+    from flash_attn_volta.forward import kernel_strides
+    lib = _capi.load()
+    rows = []
+    for (b, sq, sk, h, hk, d) in DECODE_TABLE:
+        g = torch.Generator(device="cpu").manual_seed(0)
+        q = torch.randn((b, sq, h, d), generator=g).half().cuda()
+        k, v = (torch.randn((b, sk, hk, d), generator=g).half().cuda() for _ in range(2))
+        o = torch.empty_like(q)
+        lse = torch.empty((b, h, sq), dtype=torch.float32, device="cuda")
+        st = [kernel_strides(t) for t in (q, k, v, o)]
+        stream = torch.cuda.current_stream().cuda_stream
+        nb = lib.fa_fwd_splitkv_workspace_bytes(b, sq, sk, h, hk, d)
+        ws = torch.empty(max(nb, 256), dtype=torch.uint8, device="cuda")
+        common = (b, sq, sk, h, hk, d, *st, d ** -0.5, 1, _capi.FA_DTYPE_F16, stream)
+        ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr())
+        unsplit = lambda: lib.fa_fwd_gqa(*ptrs, *common)  # noqa: E731
+        split = lambda: lib.fa_fwd_splitkv(*ptrs, ws.data_ptr(), ws.numel(), *common)  # noqa: E731
+        _capi.check(split(), "fa_fwd_splitkv")
+        t_u = time_loop(unsplit, steps, warmup)[1]
+        t_s = time_loop(split, steps, warmup)[1]
+        by = 2 * b * sk * hk * d * 2 + 2 * b * sq * h * d * 2 + b * h * sq * 4
+        row = {"shape": [b, sq, sk, h, hk, d], "workspace_bytes": nb,
+               "unsplit_us": round(t_u * 1e6, 2), "splitkv_us": round(t_s * 1e6, 2),
+               "algorithmic_bytes": by, "splitkv_gbs": round(by / t_s / 1e9, 1),
+               "splitkv_frac_hbm": round(by / t_s / 1e9 / PEAK_HBM_GBS, 4),
+               "speedup": round(t_u / t_s, 2)}
+        rows.append(row)
+        print(json.dumps(row), flush=True)
+    print("| (B, Sq, Sk, H, Hk, D) | unsplit us | split-KV us | split-KV GB/s (% of 8 TB/s) | speed-up |")
+    print("|---|---:|---:|---:|---:|")
+    for r in rows:
+        print(f"| {tuple(r['shape'])} | {r['unsplit_us']} | {r['splitkv_us']} | {r['splitkv_gbs']} "
+              f"({100 * r['splitkv_frac_hbm']:.1f} %) | {r['speedup']}x |")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -462,6 +517,9 @@ def main():
     ap.add_argument("--rope", action="store_true",
                     help="instead of the benchmark line, time the fused QK-norm + rotary "
                          "prologue against transformers' eager one and print a table")
+    ap.add_argument("--decode", action="store_true",
+                    help="instead of the benchmark line, time decode-step attention "
+                         "(split-KV against the unsplit kernel) and print a table")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run 10 plain device copies of MIB MiB "
                          "(a kernel of known HBM traffic, to scale rocprofv3 FETCH_SIZE / "
@@ -488,6 +546,10 @@ def main():
     if args.configs:
         torch.cuda.set_device(0)
         run_configs(args.steps, args.warmup, not args.no_cpu)
+        return
+    if args.decode:
+        torch.cuda.set_device(0)
+        run_decode(args.steps, args.warmup)
         return
     if args.rope:
         torch.cuda.set_device(0)

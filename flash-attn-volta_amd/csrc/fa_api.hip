@@ -188,9 +188,80 @@ int launch_dq(const fa::BwdArgs &a, hipStream_t stream) {
     }                                                                                 \
   } while (0)
 
-int run_fwd(const void *q, const void *k, const void *v, void *o, float *lse, const Shape &s,
-            const int64_t *q_st, const int64_t *k_st, const int64_t *v_st, const int64_t *o_st,
-            float sm_scale, int causal, void *stream) {
+// ---------------------------------------------------------------------------
+// Split-KV forward (decode: a short query block against a long cache)
+
+struct SplitPlan {
+  int n_splits;   // 0: the split path does not apply
+  int kv_split;   // keys per split, a multiple of the 64-key tile
+};
+
+// Split when one packed 64-row tile holds a key/value head's whole group of
+// query rows (grp * Sq <= 64), the regular grid would leave the GPU
+// under-filled, and there are enough keys: about 4 workgroups per CU, at
+// least 128 keys per split.
+SplitPlan splitkv_plan(const Shape &s) {
+  const SplitPlan none{0, 0};
+  const int64_t grp = s.H / s.Hk;
+  if (grp * s.Sq > 64 || s.Sk < 256) return none;
+  const int64_t cus = device_cus();
+  const int64_t regular = (int64_t)((s.Sq + 63) / 64) * s.B * s.H;
+  if (regular >= 2 * cus) return none;
+  const int64_t heads = (int64_t)s.B * s.Hk;
+  int64_t n = (4 * cus + heads - 1) / heads;
+  const int64_t max_n = (s.Sk + 127) / 128;
+  if (n > max_n) n = max_n;
+  if (n < 2) return none;
+  const int64_t kv = ((s.Sk + n - 1) / n + 63) / 64 * 64;
+  n = (s.Sk + kv - 1) / kv;
+  if (n < 2 || n > 65535) return none;
+  return SplitPlan{(int)n, (int)kv};
+}
+
+// Workspace: part_o (n_splits, B, H, Sq, D) fp32, then part_lse (n_splits, B, H, Sq) fp32.
+size_t splitkv_rows(const Shape &s, const SplitPlan &p) {
+  return (size_t)p.n_splits * (size_t)s.B * (size_t)s.H * (size_t)s.Sq;
+}
+
+size_t splitkv_bytes(const Shape &s, const SplitPlan &p) {
+  if (p.n_splits == 0) return 0;
+  const size_t n = splitkv_rows(s, p) * (size_t)(s.D + 1) * sizeof(float);
+  return (n + 255) & ~(size_t)255;
+}
+
+struct SplitLaunch {
+  fa::FwdArgs f;
+  fa::CombineArgs c;
+  int n_splits;
+};
+
+template <typename E, int D, bool CAUSAL>
+int launch_fwd_splitkv(const SplitLaunch &L, hipStream_t stream) {
+  using T = fa::FwdTile<D, 2>;
+  fa::FwdArgs a = L.f;
+  a.n_qtiles = (a.grp * a.Sq + T::BM - 1) / T::BM;
+  const int64_t gx = (int64_t)a.n_qtiles * a.B * (a.H / a.grp);
+  if (gx > 0x7fffffff) return FA_ERR_TOO_LARGE;
+  hipLaunchKernelGGL((fa::fa_fwd_kernel<E, D, CAUSAL, 2, true>), dim3((unsigned)gx, L.n_splits),
+                     dim3(T::NT), 0, stream, a);
+  int rc = launch_status();
+  if (rc) return rc;
+  const int64_t rows = (int64_t)a.B * a.H * a.Sq;
+  fa::CombineArgs c = L.c;
+  constexpr int SLOTS = 256 / (D / 8);
+  c.zgroups = 1;
+  while (c.zgroups < SLOTS && c.zgroups < L.n_splits) c.zgroups *= 2;
+  const int64_t rpb = SLOTS / c.zgroups;
+  const int64_t gc = (rows + rpb - 1) / rpb;
+  if (gc > 0x7fffffff) return FA_ERR_TOO_LARGE;
+  hipLaunchKernelGGL((fa::fa_fwd_combine_kernel<E, D>), dim3((unsigned)gc), dim3(256), 0, stream,
+                     c);
+  return launch_status();
+}
+
+int check_fwd(const void *q, const void *k, const void *v, void *o, float *lse, const Shape &s,
+              const int64_t *q_st, const int64_t *k_st, const int64_t *v_st, const int64_t *o_st,
+              float sm_scale) {
   int rc = check_shape(s);
   if (rc) return rc;
   if ((rc = check_q_like(q, q_st, s))) return rc;
@@ -199,7 +270,12 @@ int run_fwd(const void *q, const void *k, const void *v, void *o, float *lse, co
   if ((rc = check_q_like(o, o_st, s))) return rc;
   if (lse != nullptr && !aligned16(lse)) return FA_ERR_ALIGNMENT;
   if (!isfinite(sm_scale)) return FA_ERR_SCALE;
+  return FA_OK;
+}
 
+fa::FwdArgs fwd_args(const void *q, const void *k, const void *v, void *o, float *lse,
+                     const Shape &s, const int64_t *q_st, const int64_t *k_st,
+                     const int64_t *v_st, const int64_t *o_st, float sm_scale) {
   fa::FwdArgs a{};
   a.q = desc(q, q_st);
   a.k = desc(k, k_st);
@@ -217,8 +293,49 @@ int run_fwd(const void *q, const void *k, const void *v, void *o, float *lse, co
   a.off = s.Sk - s.Sq;
   a.c = kernel_scale(sm_scale);
   a.neg = sm_scale < 0.0f;
+  return a;
+}
+
+int run_fwd(const void *q, const void *k, const void *v, void *o, float *lse, const Shape &s,
+            const int64_t *q_st, const int64_t *k_st, const int64_t *v_st, const int64_t *o_st,
+            float sm_scale, int causal, void *stream) {
+  int rc = check_fwd(q, k, v, o, lse, s, q_st, k_st, v_st, o_st, sm_scale);
+  if (rc) return rc;
+  const fa::FwdArgs a = fwd_args(q, k, v, o, lse, s, q_st, k_st, v_st, o_st, sm_scale);
   hipStream_t st = static_cast<hipStream_t>(stream);
   FA_DISPATCH(launch_fwd, s, causal, a, st);
+}
+
+int run_fwd_splitkv(const void *q, const void *k, const void *v, void *o, float *lse,
+                    void *workspace, size_t workspace_bytes, const Shape &s, const int64_t *q_st,
+                    const int64_t *k_st, const int64_t *v_st, const int64_t *o_st, float sm_scale,
+                    int causal, void *stream) {
+  int rc = check_fwd(q, k, v, o, lse, s, q_st, k_st, v_st, o_st, sm_scale);
+  if (rc) return rc;
+  const SplitPlan plan = splitkv_plan(s);
+  if (plan.n_splits == 0)
+    return run_fwd(q, k, v, o, lse, s, q_st, k_st, v_st, o_st, sm_scale, causal, stream);
+  if (workspace == nullptr || workspace_bytes < splitkv_bytes(s, plan)) return FA_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return FA_ERR_ALIGNMENT;
+  SplitLaunch L{};
+  L.f = fwd_args(q, k, v, o, lse, s, q_st, k_st, v_st, o_st, sm_scale);
+  L.f.kv_split = plan.kv_split;
+  L.f.part_o = static_cast<float *>(workspace);
+  L.f.part_lse = L.f.part_o + splitkv_rows(s, plan) * (size_t)s.D;
+  L.c.part_o = L.f.part_o;
+  L.c.part_lse = L.f.part_lse;
+  L.c.o = static_cast<f16 *>(o);
+  L.c.o_sb = o_st[0];
+  L.c.o_ss = o_st[1];
+  L.c.o_sh = o_st[2];
+  L.c.lse = lse;
+  L.c.B = s.B;
+  L.c.Sq = s.Sq;
+  L.c.H = s.H;
+  L.c.n_splits = plan.n_splits;
+  L.n_splits = plan.n_splits;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  FA_DISPATCH(launch_fwd_splitkv, s, causal, L, st);
 }
 
 int run_pre(const void *o, const void *dout, float *delta, const Shape &s, const int64_t *o_st,
@@ -601,6 +718,23 @@ int fa_fwd_gqa(const void *q, const void *k, const void *v, void *o, float *lse,
                float sm_scale, int causal, int dtype, void *stream) {
   return run_fwd(q, k, v, o, lse, Shape{B, Sq, Sk, H, Hk, D, dtype}, q_strides, k_strides, v_strides,
                  o_strides, sm_scale, causal, stream);
+}
+
+size_t fa_fwd_splitkv_workspace_bytes(int B, int Sq, int Sk, int H, int Hk, int D) {
+  const Shape s{B, Sq, Sk, H, Hk, D, FA_DTYPE_F16};
+  if (check_shape(s) != FA_OK) return 0;
+  return splitkv_bytes(s, splitkv_plan(s));
+}
+
+int fa_fwd_splitkv(const void *q, const void *k, const void *v, void *o, float *lse,
+                   void *workspace, size_t workspace_bytes,
+                   int B, int Sq, int Sk, int H, int Hk, int D,
+                   const int64_t q_strides[4], const int64_t k_strides[4],
+                   const int64_t v_strides[4], const int64_t o_strides[4],
+                   float sm_scale, int causal, int dtype, void *stream) {
+  return run_fwd_splitkv(q, k, v, o, lse, workspace, workspace_bytes,
+                         Shape{B, Sq, Sk, H, Hk, D, dtype}, q_strides, k_strides, v_strides,
+                         o_strides, sm_scale, causal, stream);
 }
 
 int fa_bwd_preprocess(const void *o, const void *dout, float *delta,

@@ -52,6 +52,10 @@ struct FwdArgs {
   int n_qtiles;
   float c;             // |sm_scale| * log2(e), clamped away from 0
   int neg;             // 1 when sm_scale < 0: Q is negated on load
+  // split-KV mode only (fa_fwd_kernel<..., SPLITKV = true>):
+  int kv_split;        // keys per split, a multiple of the 64-key tile
+  float *part_o;       // (n_splits, B, H, Sq, D) fp32: each split's normalised O
+  float *part_lse;     // (n_splits, B, H, Sq) fp32: each split's LSE in log2 units
 };
 
 template <int D, int KSPLIT>
@@ -77,7 +81,14 @@ struct FwdTile {
 // flight: it pays when the grid is too small to fill the GPU, and for
 // causal attention, whose last query tile walks every key tile.  The
 // launcher picks KSPLIT from the grid size.
-template <typename E, int D, bool CAUSAL, int KSPLIT>
+//
+// SPLITKV (decode against a long cache): the rows of a tile are the
+// (query position, query head) pairs of one key/value head's group, row
+// r = position * grp + head-in-group, so the group's heads share each K/V
+// tile; blockIdx.y selects a range of kv_split keys, and the workgroup
+// writes its rows' normalised O and log2-domain LSE over that range to
+// part_o / part_lse, which fa_fwd_combine_kernel merges.
+template <typename E, int D, bool CAUSAL, int KSPLIT, bool SPLITKV = false>
 __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   using T = FwdTile<D, KSPLIT>;
   constexpr int NSUB = T::NSUB;
@@ -90,31 +101,47 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   auto k_sl = [&](auto sc) -> f16 * { return decltype(sc)::value ? sk1 : sk0; };
   auto v_sl = [&](auto sc) -> f16 * { return decltype(sc)::value ? sv1 : sv0; };
 
-  const int Sq = a.Sq, Sk = a.Sk, off = a.off;
-  const int BH = a.B * a.H;
+  const int Sq = a.Sq;
+  const int grp = a.grp;
+  // (b, h) pairs, or (b, key/value head) pairs in split-KV mode
+  const int BH = SPLITKV ? a.B * (a.H / grp) : a.B * a.H;
   const int bid = blockIdx.x;
   const int bh = bid % BH;
   // Causal: zigzag heavy/light query tiles (heavy = late tiles); workgroups
   // of one (b, h) are BH apart, so with BH % 8 == 0 they land on one XCD and
   // share its L2.
-  const int qt = CAUSAL ? a.n_qtiles - 1 - zigzag_rank(bid / BH, a.n_qtiles) : bid / BH;
-  const int b = bh / a.H, h = bh % a.H;
-  const int hk = h / a.grp;       // key/value head of this query head
+  const int qt = (CAUSAL && !SPLITKV) ? a.n_qtiles - 1 - zigzag_rank(bid / BH, a.n_qtiles)
+                                      : bid / BH;
+  const int hx = SPLITKV ? a.H / grp : a.H;
+  const int b = bh / hx;
+  const int h = SPLITKV ? 0 : bh % hx;               // SPLITKV: the head is per lane
+  const int hk = SPLITKV ? bh % hx : h / grp;        // key/value head
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = wave_id();
   const int qg = KSPLIT == 2 ? (w >> 1) : w;
   const int kh = KSPLIT == 2 ? (w & 1) : 0;
   const int g = lane >> 5, l32 = lane & 31;
   const int q0 = qt * BM;
-  const int wq0 = q0 + 32 * qg;   // first query of this wave
-  const int qrow = wq0 + l32;     // query owned by this lane
+  const int wq0 = q0 + 32 * qg;   // first row of this wave
+  const int qrow = wq0 + l32;     // row owned by this lane
+  const int nrows = SPLITKV ? grp * Sq : Sq;
+  // Query positions for the causal mask: the lane's, the wave's first and
+  // last, the block's last (rows are positions, or position * grp + head).
+  const int qpos = SPLITKV ? qrow / grp : qrow;
+  const int wpos_lo = SPLITKV ? wq0 / grp : wq0;
+  const int wpos_hi = SPLITKV ? (wq0 + 31) / grp : wq0 + 31;
+  const int bpos_hi = SPLITKV ? min((q0 + BM - 1) / grp, Sq - 1) : q0 + BM - 1;
 
-  const f16 *qb = a.q.head(b, h);
-  const f16 *kb = a.k.head(b, hk);
-  const f16 *vb = a.v.head(b, hk);
+  // Key range of this workgroup: all keys, or split blockIdx.y's
+  const int kbase = SPLITKV ? (int)blockIdx.y * a.kv_split : 0;
+  const int Sk = SPLITKV ? min(a.kv_split, a.Sk - kbase) : a.Sk;
+  const int off = a.off - kbase;   // key j (relative) is visible to position i iff j <= i + off
+
+  const f16 *kb = a.k.head(b, hk) + (int64_t)kbase * a.k.ss;
+  const f16 *vb = a.v.head(b, hk) + (int64_t)kbase * a.v.ss;
 
   int kv_end = Sk;
-  if (CAUSAL) kv_end = min(Sk, q0 + BM + off);
+  if (CAUSAL) kv_end = min(Sk, bpos_hi + 1 + off);
   // 0 when every query of the block precedes every key (causal, Sq > Sk)
   const int n_tiles = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
 
@@ -146,7 +173,7 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   // n0 + 32 * (NSUB * kh + sb); it is dead when it lies entirely above the
   // wave's causal diagonal (the last key its last query sees is wq0+31+off).
   auto sub_key = [&](int n0, int sb) { return n0 + 32 * (NSUB * kh + sb); };
-  auto dead = [&](int n0, int sb) { return CAUSAL && sub_key(n0, sb) > wq0 + 31 + off; };
+  auto dead = [&](int n0, int sb) { return CAUSAL && sub_key(n0, sb) > wpos_hi + off; };
 
   // ---- S^T = K Q^T for this wave's sub-blocks of a tile
   vec8<E> qf[D / 16];
@@ -172,8 +199,9 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   }
   if (n_tiles > 1) load_k(BN, C1{});
   {
-    const int qr = min(qrow, Sq - 1);
-    const f16 *qp = qb + (int64_t)qr * a.q.ss + 8 * g;
+    const int qr = min(qrow, nrows - 1);
+    const f16 *qp = (SPLITKV ? a.q.head(b, hk * grp + qr % grp) + (int64_t)(qr / grp) * a.q.ss
+                             : a.q.head(b, h) + (int64_t)qr * a.q.ss) + 8 * g;
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) qf[c] = ld8<E>(qp + 16 * c);
     if (a.neg) {
@@ -221,11 +249,11 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int sb = 0; sb < NSUB; ++sb) {
         const int ns = sub_key(n0, sb);
-        if ((CAUSAL && ns + 31 > wq0 + off) || (ns + 31 >= Sk)) {
+        if ((CAUSAL && ns + 31 > wpos_lo + off) || (ns + 31 >= Sk)) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const int key = ns + slot_row(i, g);
-            const bool vis = key < Sk && (!CAUSAL || key <= qrow + off);
+            const bool vis = key < Sk && (!CAUSAL || key <= qpos + off);
             s_cur[sb][i] = vis ? s_cur[sb][i] : kNegInf;
           }
         }
@@ -317,6 +345,26 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   // ---- epilogue: O = acc / l, LSE = (m + log2 l) * ln2
   const float l_tot = l_run + xor32(l_run);
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  if (SPLITKV) {
+    // this split's normalised O and log2-domain LSE (-inf: no visible key)
+    if (qrow < nrows) {
+      const int hq = hk * grp + qrow % grp;
+      const int64_t prow = (((int64_t)blockIdx.y * a.B + b) * a.H + hq) * Sq + qrow / grp;
+      float *po = a.part_o + prow * D;
+#pragma unroll
+      for (int d = 0; d < D / 32; ++d) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          floatx4 v4;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) v4[j] = oacc[d][4 * r + j] * inv;
+          *(floatx4 *)(po + 32 * d + c_row(4 * r, g)) = v4;
+        }
+      }
+      if (g == 0) a.part_lse[prow] = l_tot > 0.0f ? m_run + fast_log2(l_tot) : kNegInf;
+    }
+    return;
+  }
   if (qrow < Sq) {
     f16 *orow = a.o + b * a.o_sb + h * a.o_sh + (int64_t)qrow * a.o_ss;
 #pragma unroll
@@ -334,6 +382,94 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
       a.lse[(int64_t)bh * Sq + qrow] = lse;
     }
   }
+}
+
+// ---- merge of the split-KV partials: per row (b, h, position)
+//   m = max_z lse_z,  w_z = 2^(lse_z - m),  O = sum_z w_z O_z / sum_z w_z,
+//   LSE = (m + log2 sum_z w_z) ln 2  (+inf and O = 0 when no split saw a key).
+// A row's D values belong to D/8 lanes (8 fp32 each) and its splits to
+// `zgroups` lane groups (split z to group z % zgroups), each merging its
+// splits online with a running maximum; the groups then merge through LDS
+// in group order.  Every sum has a fixed order (reproducible results).
+struct CombineArgs {
+  const float *part_o, *part_lse;   // as written by fa_fwd_kernel<..., SPLITKV>
+  f16 *o;
+  int64_t o_sb, o_ss, o_sh;
+  float *lse;                       // (B, H, Sq) or nullptr
+  int B, Sq, H, n_splits;
+  int zgroups;                      // power of two, at most 256 / (D / 8)
+};
+
+template <typename E, int D>
+__global__ __launch_bounds__(256) void fa_fwd_combine_kernel(CombineArgs a) {
+  constexpr int LPR = D / 8;
+  constexpr int SLOTS = 256 / LPR;   // (row, split group) pairs per workgroup
+  __shared__ float s_m[SLOTS], s_sum[SLOTS];
+  __shared__ __attribute__((aligned(16))) float s_acc[SLOTS][D];
+  const int zn = a.zgroups;
+  const int rpb = SLOTS / zn;
+  const int slot = threadIdx.x / LPR, j = threadIdx.x % LPR;
+  const int rloc = slot / zn, zg = slot % zn;
+  const int64_t rows = (int64_t)a.B * a.H * a.Sq;
+  const int64_t row = (int64_t)blockIdx.x * rpb + rloc;
+  const bool valid = row < rows;
+
+  float m = kNegInf, sum = 0.0f;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (valid) {
+#pragma unroll 4
+    for (int z = zg; z < a.n_splits; z += zn) {
+      const float lz = a.part_lse[z * rows + row];
+      const floatx4 *src = (const floatx4 *)(a.part_o + (z * rows + row) * D + 8 * j);
+      const floatx4 x0 = src[0], x1 = src[1];
+      if (lz == kNegInf) continue;   // no visible key in this split
+      if (lz > m) {
+        const float sc = fast_exp2(m - lz);   // 0 while m is -inf
+        sum *= sc;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] *= sc;
+        m = lz;
+      }
+      const float wz = fast_exp2(lz - m);
+      sum += wz;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[i] += wz * x0[i];
+        acc[4 + i] += wz * x1[i];
+      }
+    }
+  }
+  if (j == 0) {
+    s_m[slot] = m;
+    s_sum[slot] = sum;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s_acc[slot][8 * j + i] = acc[i];
+  __syncthreads();
+  if (zg != 0 || !valid) return;
+
+  float mt = kNegInf;
+  for (int k = 0; k < zn; ++k) mt = fmaxf(mt, s_m[slot + k]);
+  float tot = 0.0f;
+  float o8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (mt != kNegInf) {
+    for (int k = 0; k < zn; ++k) {
+      const float mk = s_m[slot + k];
+      const float sc = mk == kNegInf ? 0.0f : fast_exp2(mk - mt);
+      tot += sc * s_sum[slot + k];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o8[i] += sc * s_acc[slot + k][8 * j + i];
+    }
+  }
+  const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
+  const int s = (int)(row % a.Sq);
+  const int64_t bh = row / a.Sq;
+  const int hh = (int)(bh % a.H), b = (int)(bh / a.H);
+  vec8<E> out;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) out[i] = (E)(o8[i] * inv);
+  *(vec8<E> *)(a.o + b * a.o_sb + s * a.o_ss + hh * a.o_sh + 8 * j) = out;
+  if (a.lse != nullptr && j == 0) a.lse[row] = tot > 0.0f ? (mt + fast_log2(tot)) * kLn2 : kPosInf;
 }
 
 }  // namespace fa

@@ -14,7 +14,7 @@ import threading
 LIB_NAME = "libfa_mi355x.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # status codes (enum fa_status)
 FA_OK = 0
@@ -40,6 +40,8 @@ EXPORTED_SYMBOLS = (
     "fa_strerror",
     "fa_fwd",
     "fa_fwd_gqa",
+    "fa_fwd_splitkv",
+    "fa_fwd_splitkv_workspace_bytes",
     "fa_bwd_preprocess",
     "fa_bwd_workspace_bytes",
     "fa_bwd",
@@ -84,6 +86,13 @@ def _declare(lib):
     lib.fa_fwd_gqa.argtypes = [_vp, _vp, _vp, _vp, _vp, _ci, _ci, _ci, _ci, _ci, _ci,
                                _i64x4, _i64x4, _i64x4, _i64x4,
                                ctypes.c_float, _ci, _ci, _vp]
+    lib.fa_fwd_splitkv.restype = _ci
+    lib.fa_fwd_splitkv.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t,
+                                   _ci, _ci, _ci, _ci, _ci, _ci,
+                                   _i64x4, _i64x4, _i64x4, _i64x4,
+                                   ctypes.c_float, _ci, _ci, _vp]
+    lib.fa_fwd_splitkv_workspace_bytes.restype = ctypes.c_size_t
+    lib.fa_fwd_splitkv_workspace_bytes.argtypes = [_ci, _ci, _ci, _ci, _ci, _ci]
     lib.fa_bwd_preprocess.restype = _ci
     lib.fa_bwd_preprocess.argtypes = [_vp, _vp, _vp, _ci, _ci, _ci, _ci, _i64x4, _i64x4, _vp]
     lib.fa_bwd_workspace_bytes.restype = ctypes.c_size_t

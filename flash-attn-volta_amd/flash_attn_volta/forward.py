@@ -167,6 +167,15 @@ def _run_fwd(q, k, v, causal, sm_scale, write_lse, gqa):
     st = (kernel_strides(q), kernel_strides(k), kernel_strides(v), kernel_strides(out))
     lse_ptr = lse.data_ptr() if lse is not None else None
     with _on_device(q.device):
+        ws = _splitkv_workspace(lib, B, N, Sk, H, Hk, D, q.device) if gqa else None
+        if ws is not None:
+            # short query block against long keys (decode): split the keys
+            rc = lib.fa_fwd_splitkv(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                    lse_ptr, ws.data_ptr(), ws.numel(), B, N, Sk, H, Hk, D, *st,
+                                    float(sm_scale), int(bool(causal)), _DTYPES[q.dtype],
+                                    _stream_ptr(q.device))
+            _capi.check(rc, "fa_fwd_splitkv")
+            return out, lse
         if gqa:
             rc = lib.fa_fwd_gqa(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse_ptr,
                                 B, N, Sk, H, Hk, D, *st,
@@ -178,6 +187,24 @@ def _run_fwd(q, k, v, causal, sm_scale, write_lse, gqa):
                             float(sm_scale), int(bool(causal)), _stream_ptr(q.device))
     _capi.check(rc, "fa_fwd_gqa" if gqa else "fa_fwd")
     return out, lse
+
+
+_SPLITKV_BYTES = {}
+
+
+def _splitkv_workspace(lib, B, Sq, Sk, H, Hk, D, device):
+    """Workspace tensor for fa_fwd_splitkv when the library would split the
+    keys for these sizes on this device (decode-like shapes), else None.
+    Only short query blocks can qualify, so longer ones skip the query."""
+    if (H // Hk) * Sq > 64:
+        return None
+    key = (B, Sq, Sk, H, Hk, D, device.index)
+    nbytes = _SPLITKV_BYTES.get(key)
+    if nbytes is None:
+        nbytes = _SPLITKV_BYTES[key] = int(lib.fa_fwd_splitkv_workspace_bytes(B, Sq, Sk, H, Hk, D))
+    if nbytes == 0:
+        return None
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
 
 
 def _check_gqa(q, k, v):

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 4
+#define FA_ABI_VERSION 5
 
 enum fa_status {
   FA_OK = 0,
@@ -102,6 +102,33 @@ int fa_fwd_gqa(const void *q, const void *k, const void *v, void *o, float *lse,
                const int64_t q_strides[4], const int64_t k_strides[4],
                const int64_t v_strides[4], const int64_t o_strides[4],
                float sm_scale, int causal, int dtype, void *stream);
+
+/*
+ * fa_fwd_gqa for a short block of queries against a long key sequence
+ * (decode and speculative-decode steps with a KV cache), given a
+ * workspace: when every key/value head's group of query rows fits one
+ * 64-row tile (H / Hk * Sq <= 64), the regular grid would leave the GPU
+ * under-filled and Sk >= 256, the keys are split into ranges processed by
+ * separate workgroups, each key/value head's query heads share every K/V
+ * tile, and a second kernel merges the ranges through their log-sum-exps;
+ * otherwise it is exactly fa_fwd_gqa (the workspace is not touched).
+ * Same arguments and results as fa_fwd_gqa (to fp32 rounding of the merge).
+ *
+ * No counterpart in the reference, whose HF patch falls back to eager
+ * attention whenever a KV cache has content (flash_attn_volta/patch_hf.py:
+ * 145-162).
+ */
+int fa_fwd_splitkv(const void *q, const void *k, const void *v, void *o, float *lse,
+                   void *workspace, size_t workspace_bytes,
+                   int B, int Sq, int Sk, int H, int Hk, int D,
+                   const int64_t q_strides[4], const int64_t k_strides[4],
+                   const int64_t v_strides[4], const int64_t o_strides[4],
+                   float sm_scale, int causal, int dtype, void *stream);
+
+/* Workspace bytes fa_fwd_splitkv needs for these sizes on the current
+ * device (its compute-unit count sets the split), 0 when it would not split
+ * (or for invalid sizes). */
+size_t fa_fwd_splitkv_workspace_bytes(int B, int Sq, int Sk, int H, int Hk, int D);
 
 /*
  * Backward pre-pass: delta[b,h,s] = sum_d o[b,s,h,d] * do[b,s,h,d] in fp32.

@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.fa_abi_version() == _capi.ABI_VERSION == 4
+    assert lib.fa_abi_version() == _capi.ABI_VERSION == 5
 
 
 def test_strerror_covers_every_code(lib):
@@ -208,3 +208,30 @@ def test_rope_bwd_validation(lib):
     assert call(dq=None) == _capi.FA_ERR_NULL_POINTER
     assert call(dq=BAD) == _capi.FA_ERR_ALIGNMENT
     assert call(eps=-1.0) == _capi.FA_ERR_EPS
+
+
+def test_splitkv_plan_and_validation(lib):
+    """fa_fwd_splitkv: the workspace query (on the CPU the library assumes
+    MI355X's 256 compute units) is non-zero exactly for decode-like sizes,
+    and a splitting call rejects a missing or short workspace before any
+    HIP call."""
+    ws = lib.fa_fwd_splitkv_workspace_bytes
+    assert ws(1, 1, 4096, 32, 8, 128) > 0            # decode, GQA group of 4
+    assert ws(1, 8, 4096, 64, 8, 128) > 0            # 8 query rows x group of 8 = 64
+    assert ws(1, 9, 4096, 64, 8, 128) == 0           # 72 rows: no single tile
+    assert ws(1, 4096, 4096, 16, 16, 64) == 0        # prefill fills the GPU
+    assert ws(1, 1, 128, 32, 8, 128) == 0            # too few keys
+    assert ws(64, 1, 4096, 32, 32, 128) == 0         # regular grid already full
+    assert ws(1, 1, 4096, 30, 8, 128) == 0           # invalid (H % Hk)
+    n = ws(1, 1, 4096, 32, 8, 128)
+    assert n % 256 == 0 and n >= 2 * 32 * (128 + 1) * 4
+    sq, sk = _st(1, 1, 32, 128), _st(1, 4096, 8, 128)
+
+    def call(w=P, nb=n, Sk=4096):
+        return lib.fa_fwd_splitkv(P, P, P, P, None, w, nb, 1, 1, Sk, 32, 8, 128, sq, sk, sk, sq,
+                                  0.1, 1, _capi.FA_DTYPE_F16, None)
+    assert call(w=None) == _capi.FA_ERR_WORKSPACE
+    assert call(nb=n - 16) == _capi.FA_ERR_WORKSPACE
+    assert call(w=BAD) == _capi.FA_ERR_ALIGNMENT
+    assert lib.fa_fwd_splitkv(P, P, P, P, None, P, n, 1, 1, 4096, 32, 8, 96, sq, sk, sk, sq,
+                              0.1, 1, 0, None) == _capi.FA_ERR_HEAD_DIM
