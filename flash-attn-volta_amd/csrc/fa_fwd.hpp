@@ -22,14 +22,17 @@
 //   * the wave's Q fragment stays in registers for the whole sweep;
 //   * a lane owns one query row: the running max / sum and the O^T
 //     accumulator column live in that lane, the only cross-lane step is one
-//     v_permlane32_swap per key half for the row max;
+//     v_permlane32_swap per key half when a row max is taken;
 //   * probabilities are rounded to E once and the row sum accumulates
 //     those rounded values (v_dot2_f32_f16), so numerator and denominator
 //     see the same weights;
-//   * the accumulator is rescaled only when a row max grows by more than
-//     kRescaleLog2 (in log2 units): the stale max keeps p <= 2^kRescaleLog2,
-//     well inside fp16, and the final O and LSE use the same max, so the
-//     result is exact either way;
+//   * most tiles take no row max at all: probabilities are computed against
+//     the running max, and the lane's sum of them (an upper bound of each,
+//     since p >= 0) proves them inside fp16 when it is <= kFastSum; only
+//     the first tile with a visible key and tiles whose scores outgrow the
+//     running max by more than log2 kFastSum take the max, rescale and
+//     recompute.  The final O and LSE use the same max, so the result is
+//     exact either way;
 //   * the tile loads use raw buffer descriptors whose extent ends at row
 //     Sk-1, so rows past the end read as zeros without any branch (they only
 //     ever meet -inf scores); the Q row index is clamped (never stored).
@@ -39,7 +42,9 @@
 
 namespace fa {
 
-constexpr float kRescaleLog2 = 8.0f;
+// Bound on a lane's per-tile sum of probabilities taken against a stale
+// running max (so every probability is <= 2^15, inside fp16's range).
+constexpr float kFastSum = 32768.0f;
 
 struct FwdArgs {
   TensorDesc q, k, v;  // q: (B, Sq, H, D); k, v: (B, Sk, Hk, D)
@@ -226,7 +231,7 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   floatx16 oacc[D / 32];
 #pragma unroll
   for (int d = 0; d < D / 32; ++d) oacc[d] = floatx16{};
-  float m_run = kNegInf;   // running max of c*s (log2 units), stale by <= kRescaleLog2
+  float m_run = kNegInf;   // running max of c*s (log2 units), stale by <= log2 kFastSum
   float l_run = 0.0f;      // this lane's share of the running sum
   const float c = a.c;
 
@@ -259,48 +264,68 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
         }
       }
 
-      // ---- row max over this wave's keys of the tile and lazy rescale
-      float mx = s_cur[0][0];
+      // ---- P = exp2(c*s - m) rounded to E, against the running max m.
+      // p >= 0, so the lane's sum of its rounded p bounds each of them: a
+      // sum <= kFastSum proves every p inside E's range, and the tile needs
+      // no row max.  Otherwise (the first tile with a visible key, or a
+      // score grown past m by more than log2 kFastSum) the wave takes the
+      // row max, rescales and recomputes.
+      vec8<E> pf[NSUB][2];
+      float l_tile = 0.0f;
+      auto probs = [&](float neg_m) {
+        l_tile = 0.0f;
 #pragma unroll
-      for (int sb = 0; sb < NSUB; ++sb)
+        for (int sb = 0; sb < NSUB; ++sb) {
+          if (dead(n0, sb)) continue;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s_cur[sb][i]);
-      mx = max_xor32(mx);
-      const float m_new = fmaxf(m_run, mx * c);
-      const bool grow = m_new > m_run + kRescaleLog2;
-      if (__any(grow)) {
-        const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f;
+          for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) {
+              vec2<E> pr = __builtin_convertvector(
+                  (floatx2){fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + j], c, neg_m)),
+                            fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + j + 1], c, neg_m))},
+                  vec2<E>);
+              l_tile = dot2_acc(pr, l_tile);
+              pf[sb][hh][j] = pr[0];
+              pf[sb][hh][j + 1] = pr[1];
+            }
+          }
+        }
+      };
+      probs(-m_run);
+      const bool slow = m_run == kNegInf || !(l_tile <= kFastSum);
+      if (__any(slow)) {
+        float mx = s_cur[0][0];
+#pragma unroll
+        for (int sb = 0; sb < NSUB; ++sb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s_cur[sb][i]);
+        mx = max_xor32(mx);
+        const float m_new = fmaxf(m_run, mx * c);
+        const bool grow = m_new > m_run;
+        const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f;   // 0 from -inf
         m_run = grow ? m_new : m_run;
         l_run *= alpha;
 #pragma unroll
         for (int d = 0; d < D / 32; ++d)
 #pragma unroll
           for (int i = 0; i < 16; ++i) oacc[d][i] *= alpha;
+        probs(m_run == kNegInf ? 0.0f : -m_run);
       }
-      const float neg_m = (m_run == kNegInf) ? 0.0f : -m_run;
+      l_run += l_tile;
 
-      // ---- P = exp2(c*s - m) rounded to E; O^T += V^T P^T
+      // ---- O^T += V^T P^T
 #pragma unroll
       for (int sb = 0; sb < NSUB; ++sb) {
         if (dead(n0, sb)) continue;
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
-          vec8<E> pf;
-#pragma unroll
-          for (int j = 0; j < 8; j += 2) {
-            vec2<E> pr = __builtin_convertvector(
-                (floatx2){fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + j], c, neg_m)),
-                          fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + j + 1], c, neg_m))},
-                vec2<E>);
-            l_run = dot2_acc(pr, l_run);
-            pf[j] = pr[0];
-            pf[j + 1] = pr[1];
-          }
           // kperm rows 32 * (sub-block) + 16hh + 4g (+8): keys 16hh + 8g + 0..7
           const int rb = (32 * (NSUB * kh + sb) + 16 * hh) * D;
 #pragma unroll
           for (int d = 0; d < D / 32; ++d)
-            oacc[d] = mfma32(load_tr_pair<E>(v_sl(CP{}) + rb + t_off[d], 8 * D), pf, oacc[d]);
+            oacc[d] = mfma32(load_tr_pair<E>(v_sl(CP{}) + rb + t_off[d], 8 * D), pf[sb][hh],
+                             oacc[d]);
         }
       }
     }
