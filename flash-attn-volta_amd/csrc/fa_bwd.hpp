@@ -27,14 +27,18 @@
 // MFMAs.  Its magnitude follows the upstream gradient and can sit far below
 // the fp16 normal range (a loss averaged over thousands of tokens gives
 // |dS| ~ 1e-9 deep in a network), where fp16 would flush it to zero.  Each
-// lane therefore keeps a running power-of-two scale 2^e for its output row
-// (a key in dK, a query in dQ), chosen from the largest |dS| it has
-// produced so that scaled values stay in [2^10, 2^15]: dS * 2^e is rounded,
-// the fp32 accumulator is rescaled exactly (by a power of two) whenever e
-// changes, and the result is divided by 2^e at the end.  Scaling by powers
-// of two changes no rounding in the normal range, never overflows, and
-// depends only on the lane's own data, so results stay deterministic (bf16,
-// with fp32's exponent range, does not need it but loses nothing by it).
+// lane therefore scales its output row's dS by a power of two 2^e and
+// divides the result by 2^e at the end.  In dK (lane = key, summing over
+// queries) e is a running scale chosen from the largest |dS| the lane has
+// produced, so that scaled values stay in [2^10, 2^15], with the fp32
+// accumulator rescaled exactly whenever e changes.  In dQ (lane = query) e
+// is fixed per query before the sweep, from the query's dO row: dO and
+// delta are scaled so that the row's largest |dO| lies in [2^-4, 2^-3),
+// which bounds |dS * 2^e| by 2^-2 D max|V| and needs no per-tile checks.
+// Scaling by powers of two changes no rounding in the normal range and
+// depends only on the lane's own data, so results stay deterministic
+// (bf16, with fp32's exponent range, does not need it but loses nothing by
+// it).
 #pragma once
 
 #include "fa_common.hpp"
@@ -92,7 +96,7 @@ __global__ __launch_bounds__(256) void fa_bwd_preprocess_kernel(PreArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Running power-of-two scale of one lane's dS column (see the header).
+// Running power-of-two scale of one dK lane's dS column (see the header).
 struct DsScale {
   int e = 0;
   float mul = 1.0f;   // 2^e
@@ -105,21 +109,6 @@ struct DsScale {
     if (m > 0.0f && (sm > 32768.0f || sm < 1024.0f)) {
       // m = f * 2^x, f in [0.5, 1): new e puts m * 2^e in [2^13, 2^14)
       int en = 14 - __builtin_amdgcn_frexp_expf(m);
-      en = en > 100 ? 100 : (en < -100 ? -100 : en);
-      const float f = __builtin_amdgcn_ldexpf(1.0f, en - e);
-      e = en;
-      mul = __builtin_amdgcn_ldexpf(1.0f, en);
-      return f;
-    }
-    return 1.0f;
-  }
-
-  // Same update when `m` is the largest |dS * 2^e| (values already scaled
-  // by the current mul): rescales to keep them in [2^10, 2^15].
-  __device__ __forceinline__ float update_scaled(float m) {
-    if (m > 0.0f && (m > 32768.0f || m < 1024.0f)) {
-      // m = f * 2^x, f in [0.5, 1): the unscaled max is m * 2^-e
-      int en = 14 - (__builtin_amdgcn_frexp_expf(m) - e);
       en = en > 100 ? 100 : (en < -100 ? -100 : en);
       const float f = __builtin_amdgcn_ldexpf(1.0f, en - e);
       e = en;
@@ -547,15 +536,38 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
   const float l2 = qrow < Sq ? a.lse[(int64_t)bh * Sq + qc] * kLog2e : kPosInf;
   const float dl = qrow < Sq ? a.delta[(int64_t)bh * Sq + qc] : 0.0f;
 
+  // Power-of-two scale 2^e of this query's dS, fixed for the whole sweep:
+  // the lane's dO row is scaled so that its largest |value| lies in
+  // [2^-4, 2^-3) (exact: a power of two that cannot overflow), and delta
+  // with it, so the MFMAs below produce dS * 2^e directly.  Then
+  // |dS * 2^e| <= P (|dO' . V| + |delta'|) <= 2^-2 D max|V|, far inside
+  // fp16 for any sane V, while dO ~ 1e-6 (fp16 subnormals) still yields dS
+  // well above fp16's subnormal range.  dQ is unscaled at the store.
+  float gm = 0.0f;
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) gm = fmaxf(gm, fabsf((float)gf[c][j]));
+  gm = max_xor32(gm);   // the row's other half is in lane ^ 32
+  int ge = 0;
+  if (gm > 0.0f && gm < kPosInf) {
+    ge = -3 - __builtin_amdgcn_frexp_expf(gm);
+    ge = ge > 126 ? 126 : (ge < -126 ? -126 : ge);
+  }
+  const float gmul = __builtin_amdgcn_ldexpf(1.0f, ge);
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) gf[c][j] = (E)((float)gf[c][j] * gmul);
+
   floatx16 dq[D / 32];
 #pragma unroll
   for (int d = 0; d < D / 32; ++d) dq[d] = floatx16{};
-  DsScale sc;
-  float shift = -l2;   // exponent offset: e - LSE * log2(e)
+  const float shift = -l2;   // P = exp2(c s - LSE * log2(e))
   // dP^T MFMAs start from -delta (the lane's query), so they yield dP - delta
   floatx16 dl_seed;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) dl_seed[i] = -dl;
+  for (int i = 0; i < 16; ++i) dl_seed[i] = -dl * gmul;
 
   int kv_end = Sk;
   if (CAUSAL) kv_end = min(Sk, q0 + BM + off);
@@ -630,26 +642,12 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) sacc[i] = slot_row(i, 0) <= lim ? sacc[i] : kNegInf;
       }
-      // The lane's dS scale 2^e rides in the exponent: P * 2^e =
-      // exp2(c s - LSE' + e), so ds below is already dS * 2^e.
+      // dpacc holds (dP - delta) * 2^e, so ds is dS * 2^e
       floatx16 ds;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const float p = fast_exp2(__builtin_fmaf(sacc[i], c, shift));
         ds[i] = p * dpacc[i];
-      }
-      const float m = absmax16(ds);
-      {
-        const float f = sc.update_scaled(max_xor32(m));
-        if (__any(f != 1.0f)) {
-          shift = (float)sc.e - l2;
-#pragma unroll
-          for (int d = 0; d < D / 32; ++d)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) dq[d][i] *= f;
-#pragma unroll
-          for (int i = 0; i < 16; ++i) ds[i] *= f;
-        }
       }
       vec8<E> dsf[2];
 #pragma unroll
@@ -681,12 +679,12 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
     if (t + 1 < n_tiles) tile_step(std::integral_constant<int, 1>{}, t + 1);
   }
 
-  float dq_mul = a.sm_scale / sc.mul;
+  const float dq_mul = a.sm_scale / gmul;
   if (SPLIT == 2) {
-    // the loop's last barrier ordered every tile read before these writes
-    merge_pair<D>(reinterpret_cast<float *>(qg ? s_k1 : s_k0), kh == 1, dq, sc, lane);
+    // the loop's last barrier ordered every tile read before these writes;
+    // both key halves of a query carry the same scale
+    merge_pair<D>(reinterpret_cast<float *>(qg ? s_k1 : s_k0), kh == 1, dq, DsScale{}, lane);
     if (kh == 1) return;
-    dq_mul = a.sm_scale;
   }
   if (qrow < Sq)
     store_row<E, D>(a.dq + b * a.dq_sb + h * a.dq_sh + (int64_t)qrow * a.dq_ss, dq, dq_mul, g);
