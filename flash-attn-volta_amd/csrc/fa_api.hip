@@ -418,14 +418,21 @@ int run_dkdv(const void *dout, const void *q, const void *k, const void *v, cons
   FA_DISPATCH(launch_dkdv, s, causal, a, st);
 }
 
+// dQ; with `o` given (the full backward), the kernel also computes delta
+// from O and dO and writes it to `delta` instead of reading it.
 int run_dq(const void *dout, const void *q, const void *k, const void *v, const float *lse,
            const float *delta, void *dq, const Shape &s, const int64_t *do_st, const int64_t *q_st,
            const int64_t *k_st, const int64_t *v_st, const int64_t *dq_st, float sm_scale,
-           int causal, void *stream) {
+           int causal, void *stream, const void *o = nullptr, const int64_t *o_st = nullptr) {
   fa::BwdArgs a;
   int rc = bwd_common(dout, q, k, v, lse, delta, s, do_st, q_st, k_st, v_st, sm_scale, &a);
   if (rc) return rc;
   if ((rc = check_q_like(dq, dq_st, s))) return rc;
+  if (o != nullptr) {
+    if ((rc = check_q_like(o, o_st, s))) return rc;
+    a.o = desc(o, o_st);
+    a.delta_out = const_cast<float *>(delta);
+  }
   a.dq = static_cast<f16 *>(dq);
   a.dq_sb = dq_st[0];
   a.dq_ss = dq_st[1];
@@ -459,12 +466,13 @@ int run_bwd(const void *dout, const void *q, const void *k, const void *v, const
   float *delta = static_cast<float *>(workspace);
   if ((rc = bwd_common(dout, q, k, v, lse, delta, s, do_st, q_st, k_st, v_st, sm_scale, &probe)))
     return rc;
-  if ((rc = run_pre(o, dout, delta, s, o_st, do_st, stream))) return rc;
-  if ((rc = run_dkdv(dout, q, k, v, lse, delta, dk, dv, s, do_st, q_st, k_st, v_st, dk_st, dv_st,
-                     sm_scale, causal, stream)))
+  // dQ first: it computes delta (the pre-pass, folded in) for the dK/dV
+  // kernel, which runs after it on the same stream.
+  if ((rc = run_dq(dout, q, k, v, lse, delta, dq, s, do_st, q_st, k_st, v_st, dq_st, sm_scale,
+                   causal, stream, o, o_st)))
     return rc;
-  return run_dq(dout, q, k, v, lse, delta, dq, s, do_st, q_st, k_st, v_st, dq_st, sm_scale, causal,
-                stream);
+  return run_dkdv(dout, q, k, v, lse, delta, dk, dv, s, do_st, q_st, k_st, v_st, dk_st, dv_st,
+                  sm_scale, causal, stream);
 }
 
 Shape square(int B, int S, int H, int D) { return Shape{B, S, S, H, H, D, FA_DTYPE_F16}; }

@@ -49,6 +49,10 @@ struct BwdArgs {
   TensorDesc q, k, v, dout;   // q, dout: (B, Sq, H, D); k, v: (B, Sk, Hk, D)
   const float *lse;     // (B, H, Sq) natural log
   const float *delta;   // (B, H, Sq)
+  // dQ kernel only: when non-NULL, delta is not read but computed from O
+  // and dO and written here (the pre-pass folded into the dQ kernel)
+  float *delta_out;
+  TensorDesc o;         // (B, Sq, H, D), read when delta_out is set
   f16 *dq, *dk, *dv;    // dq: (B, Sq, H, D); dk, dv: (B, Sk, Hk, D)
   int64_t dq_sb, dq_ss, dq_sh;
   int64_t dk_sb, dk_ss, dk_sh;
@@ -534,7 +538,23 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
   }
   const int qc = min(qrow, Sq - 1);
   const float l2 = qrow < Sq ? a.lse[(int64_t)bh * Sq + qc] * kLog2e : kPosInf;
-  const float dl = qrow < Sq ? a.delta[(int64_t)bh * Sq + qc] : 0.0f;
+  float dl;
+  if (a.delta_out != nullptr) {
+    // delta = rowsum(O * dO) from the lane's half row and its lane ^ 32
+    // partner's (the pre-pass, folded in); the dK/dV kernel reads it later
+    vec8<E> of[D / 16];
+    load_row_frags<E, D>(of, a.o.head(b, h), a.o.ss, qrow, Sq, g);
+    float acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc = __builtin_fmaf((float)of[c][j], (float)gf[c][j], acc);
+    acc += xor32(acc);
+    dl = qrow < Sq ? acc : 0.0f;
+    if (qrow < Sq && g == 0 && kh == 0) a.delta_out[(int64_t)bh * Sq + qrow] = dl;
+  } else {
+    dl = qrow < Sq ? a.delta[(int64_t)bh * Sq + qc] : 0.0f;
+  }
 
   // Power-of-two scale 2^e of this query's dS, fixed for the whole sweep:
   // the lane's dO row is scaled so that its largest |value| lies in

@@ -144,9 +144,11 @@ size_t fa_bwd_workspace_bytes(int B, int S, int H, int D);
 
 /*
  * Backward attention: (dq, dk, dv) of L = <o, dout> with o = fa_fwd(q,k,v),
- * given the forward's `lse`. Runs fa_bwd_preprocess into the workspace,
- * then fa_bwd_dkdv (one workgroup per key block) and fa_bwd_dq (one
- * workgroup per query block). No atomics: results are bit-reproducible.
+ * given the forward's `lse`. Two launches: the dQ kernel (one workgroup
+ * per query block), which also computes delta = rowsum(o * dout) -- what
+ * fa_bwd_preprocess computes -- into the workspace, then the dK/dV kernel
+ * (one workgroup per key block), which reads it. No atomics: results are
+ * bit-reproducible.
  *
  * Replaces flash_attn_volta/triton_fa_bwd.py:587-700 (flash_attn_backward
  * and _run_bwd_kernels, launching _fa_bwd_dq_kernel_* and
