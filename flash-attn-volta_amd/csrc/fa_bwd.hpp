@@ -108,18 +108,19 @@ struct DsScale {
   // `m` = largest unscaled |dS| of the current block over this lane and its
   // lane^32 partner (same output row).  Returns the factor by which the
   // lane's accumulator must be multiplied (1 when e is unchanged).
+  // Straight-line selects (no per-lane branch, so no exec-mask juggling in
+  // the loop that calls it).
   __device__ __forceinline__ float update(float m) {
     const float sm = m * mul;
-    if (m > 0.0f && (sm > 32768.0f || sm < 1024.0f)) {
-      // m = f * 2^x, f in [0.5, 1): new e puts m * 2^e in [2^13, 2^14)
-      int en = 14 - __builtin_amdgcn_frexp_expf(m);
-      en = en > 100 ? 100 : (en < -100 ? -100 : en);
-      const float f = __builtin_amdgcn_ldexpf(1.0f, en - e);
-      e = en;
-      mul = __builtin_amdgcn_ldexpf(1.0f, en);
-      return f;
-    }
-    return 1.0f;
+    const bool need = m > 0.0f && (sm > 32768.0f || sm < 1024.0f);
+    // m = f * 2^x, f in [0.5, 1): new e puts m * 2^e in [2^13, 2^14)
+    int en = 14 - __builtin_amdgcn_frexp_expf(m);
+    en = en > 100 ? 100 : (en < -100 ? -100 : en);
+    en = need ? en : e;
+    const float f = __builtin_amdgcn_ldexpf(1.0f, en - e);
+    e = en;
+    mul = __builtin_amdgcn_ldexpf(1.0f, en);
+    return f;
   }
 };
 
