@@ -95,15 +95,20 @@ int device_cus() {
 }
 
 // Split each tile's rows across two waves when the grid of 128-row
-// workgroups would leave the GPU under-filled (fewer than 2 per CU; 4 for
-// causal, whose light blocks finish early and leave the heavy blocks' long
-// sweeps as the critical path).  Used by the forward and both backward
-// kernels (the split is over keys in the forward and dQ, over queries in
-// dK/dV); `rows` is the length of the blocked dimension, `heads` the
-// number of (b, head) pairs the grid covers.
-bool row_split(int rows, int64_t heads, bool causal) {
+// workgroups would leave the GPU under-filled: fewer than one round of the
+// resident workgroup slots (`per_cu` per CU), two rounds for causal, whose
+// light blocks finish early and leave the heavy blocks' long sweeps as the
+// critical path.  Used by the forward and both backward kernels (the split
+// is over keys in the forward and dQ, over queries in dK/dV); `rows` is
+// the length of the blocked dimension, `heads` the number of (b, head)
+// pairs the grid covers.  per_cu = 2 for the kernels that run two
+// workgroups per CU; 1 for D = 128 dK/dV, whose registers allow one
+// (measured: unsplit is 11 % faster at (1,4096,8,128) non-causal and 4 %
+// at (1,4096,16,128) causal, split stays 19 % faster at (1,4096,8,128)
+// causal).
+bool row_split(int rows, int64_t heads, bool causal, int per_cu = 2) {
   const int64_t wgs = (int64_t)((rows + 127) / 128) * heads;
-  return wgs < (int64_t)(causal ? 4 : 2) * device_cus();
+  return wgs < (int64_t)(causal ? 2 : 1) * per_cu * device_cus();
 }
 
 template <typename E, int D, bool CAUSAL, int KSPLIT>
@@ -161,8 +166,9 @@ int launch_dq_split(const fa::BwdArgs &args, hipStream_t stream) {
 
 template <typename E, int D, bool CAUSAL>
 int launch_dkdv(const fa::BwdArgs &a, hipStream_t stream) {
-  return row_split(a.Sk, (int64_t)a.B * a.Hk, CAUSAL) ? launch_dkdv_split<E, D, CAUSAL, 2>(a, stream)
-                                                      : launch_dkdv_split<E, D, CAUSAL, 1>(a, stream);
+  return row_split(a.Sk, (int64_t)a.B * a.Hk, CAUSAL, D >= 128 ? 1 : 2)
+             ? launch_dkdv_split<E, D, CAUSAL, 2>(a, stream)
+             : launch_dkdv_split<E, D, CAUSAL, 1>(a, stream);
 }
 
 template <typename E, int D, bool CAUSAL>
