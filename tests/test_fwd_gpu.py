@@ -154,3 +154,25 @@ def test_forward_large_grid_variant(shape, causal):
     out, lse = _run(q, k, v, causal, None)
     assert max_abs(out, o_ref) < TOL
     assert max_abs(lse, lse_ref) < TOL
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_forward_scores_growing_along_the_keys(causal):
+    """Scores that grow steadily along the keys (K rows scaled by a ramp,
+    aligned with Q): each query's running max is outgrown by ~4 (log2
+    units) per 64-key tile and ~70 over the sweep, so the forward's rare
+    path (take the row max, rescale O, recompute the tile) runs every few
+    tiles instead of once; O and LSE must still match the oracle."""
+    B, S, H, D = 1, 1024, 2, 64
+    g = torch.Generator("cpu").manual_seed(40)
+    u = torch.randn(D, generator=g)
+    u = u / u.norm()
+    ramp = torch.linspace(0.25, 6.0, S).view(1, S, 1, 1)
+    q = (8.0 * u + 0.3 * torch.randn(B, S, H, D, generator=g)).half()
+    k = (8.0 * ramp * u + 0.3 * torch.randn(B, S, H, D, generator=g)).half()
+    v = torch.randn(B, S, H, D, generator=g).half()
+    o, lse = orc.attention_fwd(q, k, v, causal, default_scale(D, None))
+    out, lse_g = _run(q, k, v, causal, None)
+    errs = dict(out=max_abs(out, o), lse=max_abs(lse_g, lse))
+    report(f"fwd growing-scores c={int(causal)}", **errs)
+    assert errs["out"] <= TOL and errs["lse"] <= TOL
