@@ -204,8 +204,9 @@ struct SplitPlan {
 
 // Split when one packed 64-row tile holds a key/value head's whole group of
 // query rows (grp * Sq <= 64), the regular grid would leave the GPU
-// under-filled, and there are enough keys: about 4 workgroups per CU, at
-// least 128 keys per split.
+// under-filled, and there are enough keys: about 2 workgroups per CU, at
+// least 128 keys per split (measured against 4 and 8 per CU and a 64- or
+// 256-key minimum: equal or faster on every decode shape of bench.py).
 SplitPlan splitkv_plan(const Shape &s) {
   const SplitPlan none{0, 0};
   const int64_t grp = s.H / s.Hk;
@@ -214,7 +215,7 @@ SplitPlan splitkv_plan(const Shape &s) {
   const int64_t regular = (int64_t)((s.Sq + 63) / 64) * s.B * s.H;
   if (regular >= 2 * cus) return none;
   const int64_t heads = (int64_t)s.B * s.Hk;
-  int64_t n = (4 * cus + heads - 1) / heads;
+  int64_t n = (2 * cus + heads - 1) / heads;
   const int64_t max_n = (s.Sk + 127) / 128;
   if (n > max_n) n = max_n;
   if (n < 2) return none;
