@@ -495,9 +495,8 @@ int check_rope_shape(const RopeShape &s) {
   if (s.dtype != FA_DTYPE_F16 && s.dtype != FA_DTYPE_BF16) return FA_ERR_DTYPE;
   if (s.B <= 0 || s.S <= 0 || s.H <= 0 || s.Hk <= 0) return FA_ERR_SHAPE;
   if (s.D != 16 && s.D != 32 && s.D != 64 && s.D != 128) return FA_ERR_HEAD_DIM;
-  // Rows of the larger side, B * S * H, index a grid-stride loop in int64
-  // and the grid's x dimension in 32 bits.
-  if ((double)s.B * s.S * (s.H > s.Hk ? s.H : s.Hk) > 1.0e15) return FA_ERR_TOO_LARGE;
+  // Rows of the larger side, B * S * H, are indexed in 32 bits.
+  if ((double)s.B * s.S * (s.H > s.Hk ? s.H : s.Hk) > 2147483647.0) return FA_ERR_TOO_LARGE;
   return FA_OK;
 }
 

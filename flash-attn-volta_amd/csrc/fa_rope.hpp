@@ -60,6 +60,7 @@ struct RopeArgs {
 };
 
 constexpr int kRopeThreads = 256;
+constexpr int kRopeUnroll = 1;   // rows per lane per pass (2 measured mixed: -9..+6 %)
 
 template <typename E>
 __device__ __forceinline__ void to_f32(u32x4 raw, float *f) {
@@ -93,17 +94,20 @@ __device__ __forceinline__ float row_sum(float v) {
 }
 
 // Row index -> element offsets of that row (chunk 0) in a (B, S, heads, D)
-// tensor with strides (sb, ss, sh), and of its cos/sin row.
+// tensor with strides (sb, ss, sh), and of its cos/sin row.  Row indices
+// are 32-bit (the launcher rejects more than 2^31 - 1 rows per side):
+// 64-bit division by the runtime head count and length would cost several
+// times the VALU work of the row itself.
 struct RowPos {
-  int64_t b, s, h;
-  __device__ __forceinline__ RowPos(int64_t row, int heads, int S) {
+  uint32_t b, s, h;
+  __device__ __forceinline__ RowPos(uint32_t row, uint32_t heads, uint32_t S) {
     h = row % heads;
-    const int64_t bs = row / heads;
+    const uint32_t bs = row / heads;
     s = bs % S;
     b = bs / S;
   }
   __device__ __forceinline__ int64_t off(int64_t sb, int64_t ss, int64_t sh) const {
-    return b * sb + s * ss + h * sh;
+    return (int64_t)b * sb + (int64_t)s * ss + (int64_t)h * sh;
   }
 };
 
@@ -111,6 +115,7 @@ template <typename E, int D, bool NORM>
 __device__ __forceinline__ void rope_fwd_side(const RopeArgs &a, const RopeSide &t) {
   constexpr int LPR = D / 16;                 // lanes per row
   constexpr int RPB = kRopeThreads / LPR;     // rows per workgroup per pass
+  constexpr int U = kRopeUnroll;              // rows per lane per pass
   const int tid = threadIdx.x;
   const int j = tid % LPR;
   float wl[8], wh[8];
@@ -118,48 +123,61 @@ __device__ __forceinline__ void rope_fwd_side(const RopeArgs &a, const RopeSide 
     to_f32<E>(ld16(t.w + 8 * j), wl);
     to_f32<E>(ld16(t.w + D / 2 + 8 * j), wh);
   }
-  for (int64_t row0 = (int64_t)blockIdx.x * RPB; row0 < t.rows; row0 += (int64_t)gridDim.x * RPB) {
-    const int64_t row = row0 + tid / LPR;
-    const bool valid = row < t.rows;          // uniform over the LPR lanes of a row
-    const RowPos p(valid ? row : 0, t.heads, a.S);
-    const f16 *xp = t.x + p.off(t.xb, t.xs, t.xh) + 8 * j;
-    const int64_t co = p.b * a.cb + p.s * a.cs + 8 * j;
-    u32x4 rxl = {0, 0, 0, 0}, rxh = {0, 0, 0, 0};
-    if (valid) {
-      rxl = ld16(xp);
-      rxh = ld16(xp + D / 2);
-    }
-    const u32x4 rcl = ld16(a.cos + co), rch = ld16(a.cos + co + D / 2);
-    const u32x4 rsl = ld16(a.sin + co), rsh = ld16(a.sin + co + D / 2);
-    float xl[8], xh[8], cl[8], ch[8], sl[8], sh[8];
-    to_f32<E>(rxl, xl);
-    to_f32<E>(rxh, xh);
-    to_f32<E>(rcl, cl);
-    to_f32<E>(rch, ch);
-    to_f32<E>(rsl, sl);
-    to_f32<E>(rsh, sh);
-    if (NORM) {
-      float ss = 0.0f;
+  for (int64_t row0 = (int64_t)blockIdx.x * RPB * U; row0 < t.rows;
+       row0 += (int64_t)gridDim.x * RPB * U) {
+    // all loads of the pass first (U rows per lane in flight), then the math
+    u32x4 rx[U][2], rc[U][2], rs[U][2];
+    int64_t yo[U];
+    bool valid[U];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ss += xl[i] * xl[i] + xh[i] * xh[i];
-      ss = row_sum<LPR>(ss);
-      const float r = rsqrtf(ss * (1.0f / D) + a.eps);
+    for (int u = 0; u < U; ++u) {
+      const int64_t row = row0 + u * RPB + tid / LPR;
+      valid[u] = row < t.rows;                // uniform over the LPR lanes of a row
+      const RowPos p(valid[u] ? (uint32_t)row : 0u, (uint32_t)t.heads, (uint32_t)a.S);
+      const f16 *xp = t.x + p.off(t.xb, t.xs, t.xh) + 8 * j;
+      const int64_t co = (int64_t)p.b * a.cb + (int64_t)p.s * a.cs + 8 * j;
+      yo[u] = p.off(t.yb, t.ys, t.yh) + 8 * j;
+      rx[u][0] = rx[u][1] = u32x4{0, 0, 0, 0};
+      if (valid[u]) {
+        rx[u][0] = ld16(xp);
+        rx[u][1] = ld16(xp + D / 2);
+      }
+      rc[u][0] = ld16(a.cos + co);
+      rc[u][1] = ld16(a.cos + co + D / 2);
+      rs[u][0] = ld16(a.sin + co);
+      rs[u][1] = ld16(a.sin + co + D / 2);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float xl[8], xh[8], cl[8], ch[8], sl[8], sh[8];
+      to_f32<E>(rx[u][0], xl);
+      to_f32<E>(rx[u][1], xh);
+      to_f32<E>(rc[u][0], cl);
+      to_f32<E>(rc[u][1], ch);
+      to_f32<E>(rs[u][0], sl);
+      to_f32<E>(rs[u][1], sh);
+      if (NORM) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss += xl[i] * xl[i] + xh[i] * xh[i];
+        ss = row_sum<LPR>(ss);
+        const float r = rsqrtf(ss * (1.0f / D) + a.eps);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          xl[i] = xl[i] * r * wl[i];
+          xh[i] = xh[i] * r * wh[i];
+        }
+      }
+      float ol[8], oh[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        xl[i] = xl[i] * r * wl[i];
-        xh[i] = xh[i] * r * wh[i];
+        ol[i] = xl[i] * cl[i] - xh[i] * sl[i];
+        oh[i] = xh[i] * ch[i] + xl[i] * sh[i];
       }
-    }
-    float ol[8], oh[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      ol[i] = xl[i] * cl[i] - xh[i] * sl[i];
-      oh[i] = xh[i] * ch[i] + xl[i] * sh[i];
-    }
-    if (valid) {
-      f16 *yp = t.y + p.off(t.yb, t.ys, t.yh) + 8 * j;
-      st16(yp, from_f32<E>(ol));
-      st16(yp + D / 2, from_f32<E>(oh));
+      if (valid[u]) {
+        st16(t.y + yo[u], from_f32<E>(ol));
+        st16(t.y + yo[u] + D / 2, from_f32<E>(oh));
+      }
     }
   }
 }
@@ -189,9 +207,9 @@ __device__ __forceinline__ void rope_bwd_side(const RopeArgs &a, const RopeSide 
   for (int64_t row0 = (int64_t)blockIdx.x * RPB; row0 < t.rows; row0 += (int64_t)gridDim.x * RPB) {
     const int64_t row = row0 + tid / LPR;
     const bool valid = row < t.rows;
-    const RowPos p(valid ? row : 0, t.heads, a.S);
+    const RowPos p(valid ? (uint32_t)row : 0u, (uint32_t)t.heads, (uint32_t)a.S);
     const f16 *gp = t.g + p.off(t.gb, t.gs, t.gh) + 8 * j;
-    const int64_t co = p.b * a.cb + p.s * a.cs + 8 * j;
+    const int64_t co = (int64_t)p.b * a.cb + (int64_t)p.s * a.cs + 8 * j;
     u32x4 rgl = {0, 0, 0, 0}, rgh = {0, 0, 0, 0}, rxl = {0, 0, 0, 0}, rxh = {0, 0, 0, 0};
     if (valid) {
       rgl = ld16(gp);

@@ -185,6 +185,7 @@ def test_rope_fwd_validation(lib):
     assert _rope_fwd(lib, wq=P, eps=-1e-6) == _capi.FA_ERR_EPS
     assert _rope_fwd(lib, wk=P, eps=float("nan")) == _capi.FA_ERR_EPS
     assert _rope_fwd(lib, wk=P, eps=float("inf")) == _capi.FA_ERR_EPS
+    assert _rope_fwd(lib, B=1, S=1 << 20, H=4096, Hk=8) == _capi.FA_ERR_TOO_LARGE   # 2^32 rows
 
 
 def test_rope_bwd_validation(lib):
