@@ -9,6 +9,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "../../include/fa_mi355x.h"
 #include "fa_bwd.hpp"
 #include "fa_fwd.hpp"
@@ -81,17 +83,19 @@ int launch_status() {
 }
 
 // Compute units of the current device (cached per device; 256 on MI355X).
+// The cache is atomic: entry points may be called from several host
+// threads at once (they all store the same value).
 int device_cus() {
-  static int cache[64] = {0};
+  static std::atomic<int> cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int n = 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
       n = 256;
-    cache[dev] = n;
+    cache[dev].store(n, std::memory_order_relaxed);
   }
-  return cache[dev];
+  return n;
 }
 
 // Split each tile's rows across two waves when the grid of 128-row
