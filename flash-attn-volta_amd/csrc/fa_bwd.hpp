@@ -112,7 +112,8 @@ struct DsScale {
   // the loop that calls it).
   __device__ __forceinline__ float update(float m) {
     const float sm = m * mul;
-    const bool need = m > 0.0f && (sm > 32768.0f || sm < 1024.0f);
+    // bitwise, not short-circuit: && / || would become branches again
+    const bool need = (m > 0.0f) & ((sm > 32768.0f) | (sm < 1024.0f));
     // m = f * 2^x, f in [0.5, 1): new e puts m * 2^e in [2^13, 2^14)
     int en = 14 - __builtin_amdgcn_frexp_expf(m);
     en = en > 100 ? 100 : (en < -100 ? -100 : en);
@@ -305,9 +306,17 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
       m0 = m_begin + ((t + 1) % nt_h) * BQ;
     }
   };
+  // Q / dO descriptors of the tile to load, walked by cursors: re-aimed at
+  // a new query head, advanced by BQ rows otherwise.
+  RowCursor cq, cg;
+  auto aim = [&](int h, int m0) {
+    cq.init(a.q.head(b, h), a.q.ss, m0, Sq, D, BQ);
+    cg.init(a.dout.head(b, h), a.dout.ss, m0, Sq, D, BQ);
+  };
+  aim(cur_h, cur_m0);
   auto load_tile = [&](int h, int m0, auto stc) {
-    stq.load(q_st(stc), a.q.head(b, h), a.q.ss, m0, Sq, w);
-    stg.load(do_st(stc), a.dout.head(b, h), a.dout.ss, m0, Sq, w);
+    stq.load(q_st(stc), cq.rsrc(), w);
+    stg.load(do_st(stc), cg.rsrc(), w);
     if (tid < BQ) {
       const int m = m0 + tid;
       const int64_t row = ((int64_t)b * a.H + h) * Sq + m;
@@ -360,7 +369,15 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
     const bool more = t + 1 < n_tiles;
     int nxt_h = cur_h, nxt_m0 = cur_m0;
     advance(t, nxt_h, nxt_m0);
-    if (more) load_tile(nxt_h, nxt_m0, std::integral_constant<int, st ^ 1>{});
+    if (more) {
+      if (nxt_h != cur_h) {
+        aim(nxt_h, nxt_m0);
+      } else {
+        cq.advance();
+        cg.advance();
+      }
+      load_tile(nxt_h, nxt_m0, std::integral_constant<int, st ^ 1>{});
+    }
 
     // 32-query sub-block sb of this wave: queries m0 + 32 * (NSUB*qh + sb)
     auto sub_m = [&](int sb) { return m0 + 32 * (NSUB * qh + sb); };
@@ -624,6 +641,17 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
     stk.load(k_st(stc), kb, a.k.ss, n0, Sk, w);
     stv.load(v_st(stc), vb, a.v.ss, n0, Sk, w);
   };
+  // the loop loads tile t + 1 during tile t: cursors from row BN, advanced
+  // by a tile per load
+  RowCursor ck, cv;
+  ck.init(kb, a.k.ss, BN, Sk, D, BN);
+  cv.init(vb, a.v.ss, BN, Sk, D, BN);
+  auto load_next = [&](auto stc) {
+    stk.load(k_st(stc), ck.rsrc(), w);
+    stv.load(v_st(stc), cv.rsrc(), w);
+    ck.advance();
+    cv.advance();
+  };
 
   // Per-lane LDS element offsets inside a stage (as in the dK/dV kernel):
   // A-operand rows l32, chunk 2cc + g; transposed reads of K rows
@@ -650,7 +678,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
     constexpr int st = decltype(stc)::value;
     const int n0 = t * BN;
     const bool more = t + 1 < n_tiles;
-    if (more) load_tile(n0 + BN, std::integral_constant<int, st ^ 1>{});
+    if (more) load_next(std::integral_constant<int, st ^ 1>{});   // tile t + 1
 
     // 32-key sub-block sb of this wave: keys n0 + 32 * (NSUB*kh + sb)
     auto sub_n = [&](int sb) { return n0 + 32 * (NSUB * kh + sb); };

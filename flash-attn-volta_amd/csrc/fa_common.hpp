@@ -144,6 +144,38 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const f16 *head, int
   return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)ext, 0x00020000);
 }
 
+// rows_rsrc for a walk through a head in steps of a fixed number of rows:
+// the base and the remaining byte count advance by a constant step, so each
+// step costs a few scalar adds instead of rows_rsrc's 64-bit multiplies.
+// rsrc() is the descriptor rows_rsrc(head, ss, r, S, D) gives at the
+// cursor's row r (extent 0 once r >= S).
+struct RowCursor {
+  const char *base;   // row r of the head
+  int64_t rem;        // bytes from row r to the end of row S-1
+  int64_t step;       // bytes per step
+  int left;           // rows S - r
+  int rows_step;      // rows per step
+
+  __device__ __forceinline__ void init(const f16 *head, int64_t ss, int r, int S, int D,
+                                       int rows) {
+    base = reinterpret_cast<const char *>(head + (int64_t)r * ss);
+    rem = (int64_t)(S - 1 - r) * ss * 2 + 2 * D;
+    step = (int64_t)rows * ss * 2;
+    left = S - r;
+    rows_step = rows;
+  }
+  __device__ __forceinline__ void advance() {
+    base += step;
+    rem -= step;
+    left -= rows_step;
+  }
+  __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc() const {
+    uint32_t ext = 0;
+    if (left > 0) ext = (rem >> 32) != 0 ? 0xffffffffu : (uint32_t)rem;
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)ext, 0x00020000);
+  }
+};
+
 __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, int byte_off) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
 }
@@ -221,7 +253,9 @@ struct DmaStager {
   }
   __device__ __forceinline__ void load(f16 *slot, const f16 *head, int64_t ss, int r0, int S,
                                        int w) const {
-    const __amdgpu_buffer_rsrc_t rs = rows_rsrc(head, ss, r0, S, D);
+    load(slot, rows_rsrc(head, ss, r0, S, D), w);
+  }
+  __device__ __forceinline__ void load(f16 *slot, __amdgpu_buffer_rsrc_t rs, int w) const {
 #pragma unroll
     for (int j = 0; j < PER_WAVE; ++j) lds_dma16(rs, slot + (w * PER_WAVE + j) * 512, off[j]);
   }

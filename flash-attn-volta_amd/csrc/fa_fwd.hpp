@@ -157,6 +157,19 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   stv.init(w, lane, a.v.ss);
   auto load_k = [&](int n0, auto sc) { stk.load(k_sl(sc), kb, a.k.ss, n0, Sk, w); };
   auto load_v = [&](int n0, auto sc) { stv.load(v_sl(sc), vb, a.v.ss, n0, Sk, w); };
+  // In the loop K is loaded two tiles ahead and V one: cursors at those
+  // rows, each advanced by a tile per load (no per-tile 64-bit multiplies).
+  RowCursor ck, cv;
+  ck.init(kb, a.k.ss, 2 * BN, Sk, D, BN);
+  cv.init(vb, a.v.ss, BN, Sk, D, BN);
+  auto load_k_next = [&](auto sc) {
+    stk.load(k_sl(sc), ck.rsrc(), w);
+    ck.advance();
+  };
+  auto load_v_next = [&](auto sc) {
+    stv.load(v_sl(sc), cv.rsrc(), w);
+    cv.advance();
+  };
 
   // Per-lane LDS element offsets inside a slot: K rows l32 (A operand of
   // S^T = K Q^T), chunk 2cc + g; V^T transpose reads of rows 4g + (l16 >> 2)
@@ -245,8 +258,8 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
     using CQ = std::integral_constant<int, pc ^ 1>;
     const int n0 = t * BN;
     const bool more1 = t + 1 < n_tiles, more2 = t + 2 < n_tiles;
-    if (more2) load_k(n0 + 2 * BN, CP{});
-    if (more1) load_v(n0 + BN, CQ{});
+    if (more2) load_k_next(CP{});   // K(t + 2)
+    if (more1) load_v_next(CQ{});   // V(t + 1)
     if (more1) qk(CQ{}, n0 + BN, s_nxt);
 
     if (!dead(n0, 0)) {
