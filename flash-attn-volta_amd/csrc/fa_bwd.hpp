@@ -190,30 +190,40 @@ __device__ __forceinline__ void merge_pair(float *buf, bool writer, floatx16 (&a
 // sums through LDS at the end.  The split doubles the waves in flight for
 // grids too small to fill the GPU (the launcher decides).  Query tiles of
 // BQ rows stream through double-buffered LDS as Q and dO (kperm row order)
-// plus LSE and delta.  With SPLIT = 2 and D <= 64 (EARLY_S) tiles are 128
-// queries, so each wave again has two 32-query sub-blocks, and both
-// sub-blocks' S and dP MFMAs are issued before the first sub-block's
-// softmax: the matrix cores work on the second sub-block while the wave's
-// VALU works on the first.  Otherwise (D = 128: no registers for two score
-// sets) tiles are 64 queries.
+// plus LSE and delta.  With SPLIT = 2 and D = 64 (KV_LDS) the workgroup's
+// K and V rows also sit in LDS rather than in per-lane registers, which
+// brings the kernel under 168 VGPRs: three waves per SIMD instead of two
+// (C4a-shaped causal dK/dV -11 %; kernel latency, not MFMA or LDS
+// throughput, bounds it, so more waves in flight pay).  With SPLIT = 2 and
+// D = 32 (EARLY_S) tiles are 128 queries, so each wave again has two
+// 32-query sub-blocks, and both sub-blocks' S and dP MFMAs are issued
+// before the first sub-block's softmax.  Otherwise tiles are 64 queries.
 template <int D, int SPLIT>
 struct DkdvTile {
   static_assert(SPLIT == 1 || SPLIT == 2, "split is 1 or 2");
   static constexpr int NKG = 4 / SPLIT;    // key groups of 32 per workgroup
+  // K and V of the workgroup's keys staged in LDS instead of held as
+  // per-lane fragments: D / 2 fewer VGPRs, which at D = 64 lets a third
+  // wave per SIMD in (with 64-query tiles the workgroup's LDS fits three
+  // times in a CU)
+  static constexpr bool KV_LDS = D == 64 && SPLIT == 2;
   // issue all S / dP MFMAs of a tile first (measured: helps the split
   // variant, costs ~1 % unsplit, where two waves per SIMD already overlap)
-  static constexpr bool EARLY_S = D <= 64 && SPLIT == 2;
+  static constexpr bool EARLY_S = D <= 64 && SPLIT == 2 && !KV_LDS;
   // 32-query sub-blocks per wave per tile (64-query tiles unless EARLY_S)
   static constexpr int NSUB = EARLY_S ? 2 : 2 / SPLIT;
   static constexpr int BK = 32 * NKG;
   static constexpr int BQ = 32 * NSUB * SPLIT;   // queries per tile
   static constexpr int NT = 256;
   static constexpr int LDS_TILE = BQ * D;   // swizzled, unpadded (fa_common.hpp)
+  static constexpr int LDS_KV = KV_LDS ? BK * D : 8;   // K (or V) tile, kperm rows
   static_assert(64 * (D / 2) * 4 <= LDS_TILE * 2, "a merge buffer must fit in one stage");
 };
 
 template <typename E, int D, bool CAUSAL, int SPLIT>
-__global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::KV_LDS ? 3 : 1))) void fa_bwd_dkdv_kernel(
+    BwdArgs a) {
   using T = DkdvTile<D, SPLIT>;
   constexpr int BK = T::BK, BQ = T::BQ, NSUB = T::NSUB;
   // One LDS object per stage: the compiler then sees that the DMA into one
@@ -222,6 +232,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) f16 s_do0[T::LDS_TILE], s_do1[T::LDS_TILE];
   __shared__ __attribute__((aligned(16))) float s_lse[2][BQ];
   __shared__ __attribute__((aligned(16))) float s_dl[2][BQ];
+  __shared__ __attribute__((aligned(16))) f16 s_k[T::LDS_KV], s_v[T::LDS_KV];
   auto q_st = [&](auto stc) -> f16 * { return decltype(stc)::value ? s_q1 : s_q0; };
   auto do_st = [&](auto stc) -> f16 * { return decltype(stc)::value ? s_do1 : s_do0; };
 
@@ -238,7 +249,9 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
   const int g = lane >> 5, l32 = lane & 31;
   const int k0 = kt * BK;
   const int wk0 = k0 + 32 * kg;
-  const int key = wk0 + l32;
+  // this lane's key: K / V rows staged in LDS come in kperm order (the
+  // tile loader's), so lane l32 then reads key wk0 + kperm(l32)
+  const int key = wk0 + (T::KV_LDS ? kperm(l32) : l32);
 
   // K^T and V^T fragments (B operands): K[key][16c + 8g .. +7].  For fp16,
   // K is pre-multiplied by +-ck = +-min(c, 1) and rounded to fp16 (as the
@@ -247,18 +260,49 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
   // rest of c, cr = c / ck, is 1 unless |sm_scale| > ln 2.  bf16 keeps K
   // unscaled (ck = 1: a second bf16 rounding would cost 8-bit accuracy),
   // only its sign follows sm_scale.
-  vec8<E> kf[D / 16], vf[D / 16];
-  load_row_frags<E, D>(kf, a.k.head(b, hk), a.k.ss, key, Sk, g);
-  load_row_frags<E, D>(vf, a.v.head(b, hk), a.v.ss, key, Sk, g);
+  constexpr int NKF = T::KV_LDS ? 1 : D / 16;
+  vec8<E> kf[NKF], vf[NKF];
   const float ck = std::is_same<E, f16>::value ? fminf(a.c, 1.0f) : 1.0f;
   const float cr = a.c / ck;
-  {
-    const float kmul = a.neg ? -ck : ck;
+  const float kmul = a.neg ? -ck : ck;
+  if constexpr (T::KV_LDS) {
+    // the workgroup's BK keys into LDS (zeros past Sk), then K scaled in
+    // place, each thread its 16-byte chunks; the barrier before the tile
+    // loop publishes the result
+    DmaStager<D, BK> stk, stv;
+    stk.init(w, lane, a.k.ss);
+    stv.init(w, lane, a.v.ss);
+    stk.load(s_k, a.k.head(b, hk), a.k.ss, k0, Sk, w);
+    stv.load(s_v, a.v.head(b, hk), a.v.ss, k0, Sk, w);
+    __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
+    __syncthreads();
+    if (kmul != 1.0f) {
+#pragma unroll
+      for (int ch = tid; ch < BK * D / 8; ch += T::NT) {
+        vec8<E> x = ld8<E>(s_k + 8 * ch);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = (E)((float)x[j] * kmul);
+        *reinterpret_cast<vec8<E> *>(s_k + 8 * ch) = x;
+      }
+    }
+  } else {
+    load_row_frags<E, D>(kf, a.k.head(b, hk), a.k.ss, key, Sk, g);
+    load_row_frags<E, D>(vf, a.v.head(b, hk), a.v.ss, key, Sk, g);
 #pragma unroll
     for (int c = 0; c < D / 16; ++c)
 #pragma unroll
       for (int j = 0; j < 8; ++j) kf[c][j] = (E)((float)kf[c][j] * kmul);
   }
+  // B operands of S and dP: K^T / V^T fragments K[key][16cc + 8g .. +7]
+  // (registers, or LDS rows 32kg + l32 read like the query tiles' A rows)
+  auto k_frag = [&](int cc, int aoff) -> vec8<E> {
+    if constexpr (T::KV_LDS) return ld8<E>(s_k + 32 * kg * D + aoff);
+    else return kf[cc];
+  };
+  auto v_frag = [&](int cc, int aoff) -> vec8<E> {
+    if constexpr (T::KV_LDS) return ld8<E>(s_v + 32 * kg * D + aoff);
+    else return vf[cc];
+  };
 
   floatx16 dk[D / 32], dv[D / 32];
 #pragma unroll
@@ -411,8 +455,8 @@ __global__ __launch_bounds__(256) void fa_bwd_dkdv_kernel(BwdArgs a) {
       const f16 *gr = do_st(stc) + 32 * qs * D;
 #pragma unroll
       for (int cc = 0; cc < D / 16; ++cc) {
-        sacc = mfma32(ld8<E>(qr + a_off[cc]), kf[cc], sacc);
-        dpacc = mfma32(ld8<E>(gr + a_off[cc]), vf[cc], dpacc);
+        sacc = mfma32(ld8<E>(qr + a_off[cc]), k_frag(cc, a_off[cc]), sacc);
+        dpacc = mfma32(ld8<E>(gr + a_off[cc]), v_frag(cc, a_off[cc]), dpacc);
       }
     };
     // Softmax-gradient of sub-block sb and its dV / dK MFMAs.
