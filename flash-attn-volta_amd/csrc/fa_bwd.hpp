@@ -183,46 +183,54 @@ __device__ __forceinline__ void merge_pair(float *buf, bool writer, floatx16 (&a
 }
 
 // ---------------------------------------------------------------------------
-// dK / dV: workgroup = 4 waves.  SPLIT = 1: wave w owns 32 keys (BK = 128)
-// and both 32-query sub-blocks of every 64-query tile.  SPLIT = 2: wave w
-// owns key group kg = w / 2 (BK = 64) and query half qh = w % 2 of every
-// tile; the two query halves of a key group merge their dK / dV partial
-// sums through LDS at the end.  The split doubles the waves in flight for
-// grids too small to fill the GPU (the launcher decides).  Query tiles of
-// BQ rows stream through double-buffered LDS as Q and dO (kperm row order)
-// plus LSE and delta.  With SPLIT = 2 and D = 64 (KV_LDS) the workgroup's
-// K and V rows also sit in LDS rather than in per-lane registers, which
-// brings the kernel under 168 VGPRs: three waves per SIMD instead of two
-// (C4a-shaped causal dK/dV -11 %; kernel latency, not MFMA or LDS
-// throughput, bounds it, so more waves in flight pay).  With SPLIT = 2 and
-// D = 32 (EARLY_S) tiles are 128 queries, so each wave again has two
-// 32-query sub-blocks, and both sub-blocks' S and dP MFMAs are issued
-// before the first sub-block's softmax.  Otherwise tiles are 64 queries.
+// dK / dV: a workgroup's waves own key groups of 32 keys; with NQH = 2 the
+// two waves of a group take the two query halves of every tile and merge
+// their dK / dV partial sums through LDS at the end (doubling the waves in
+// flight for grids too small to fill the GPU; the launcher decides the
+// split).  Query tiles of BQ rows stream through double-buffered LDS as Q
+// and dO (kperm row order) plus LSE and delta.  Layouts:
+//   * SPLIT = 1, D <= 64: 4 waves, one key group each (BK = 128), both
+//     32-query sub-blocks of every 64-query tile;
+//   * SPLIT = 2, D = 64 (KV_LDS): 4 waves = 2 key groups x 2 query halves
+//     (BK = 64), and the keys' K and V rows in LDS rather than in per-lane
+//     registers, which brings the kernel under 168 VGPRs: three waves per
+//     SIMD instead of two (C4a-shaped causal dK/dV -11 %; kernel latency,
+//     not MFMA or LDS throughput, bounds it, so more waves in flight pay);
+//   * SPLIT = 2, D = 32 (EARLY_S): as above with K / V in registers and
+//     128-query tiles, two 32-query sub-blocks per wave whose S and dP
+//     MFMAs are all issued before the first sub-block's softmax;
+//   * SPLIT = 2, D = 128: 2 key groups x 2 query halves, K / V in registers
+//     (one wave per SIMD);
+//   * SPLIT = 1, D = 128 (WIDE): 8 waves = 4 key groups x 2 query halves
+//     (BK = 128) with K and V in LDS (129 KiB: one workgroup per CU), so
+//     each SIMD runs two waves under 256 VGPRs where the 4-wave layout ran
+//     one wave with the K / V fragments spilling.
 template <int D, int SPLIT>
 struct DkdvTile {
   static_assert(SPLIT == 1 || SPLIT == 2, "split is 1 or 2");
-  static constexpr int NKG = 4 / SPLIT;    // key groups of 32 per workgroup
-  // K and V of the workgroup's keys staged in LDS instead of held as
-  // per-lane fragments: D / 2 fewer VGPRs, which at D = 64 lets a third
-  // wave per SIMD in (with 64-query tiles the workgroup's LDS fits three
-  // times in a CU)
-  static constexpr bool KV_LDS = D == 64 && SPLIT == 2;
+  static constexpr bool WIDE = D == 128 && SPLIT == 1;
+  static constexpr int NW = WIDE ? 8 : 4;                       // waves per workgroup
+  static constexpr int NQH = (SPLIT == 2 || WIDE) ? 2 : 1;      // query halves
+  static constexpr int NKG = NW / NQH;                          // key groups of 32
+  static constexpr bool KV_LDS = (D == 64 && SPLIT == 2) || WIDE;
   // issue all S / dP MFMAs of a tile first (measured: helps the split
   // variant, costs ~1 % unsplit, where two waves per SIMD already overlap)
   static constexpr bool EARLY_S = D <= 64 && SPLIT == 2 && !KV_LDS;
   // 32-query sub-blocks per wave per tile (64-query tiles unless EARLY_S)
-  static constexpr int NSUB = EARLY_S ? 2 : 2 / SPLIT;
+  static constexpr int NSUB = EARLY_S ? 2 : 2 / NQH;
   static constexpr int BK = 32 * NKG;
-  static constexpr int BQ = 32 * NSUB * SPLIT;   // queries per tile
-  static constexpr int NT = 256;
+  static constexpr int BQ = 32 * NSUB * NQH;   // queries per tile
+  static constexpr int NT = 64 * NW;
+  // waves per SIMD the register allocation is held to
+  static constexpr int WAVES_PER_EU = (D == 64 && KV_LDS) ? 3 : (WIDE ? 2 : 1);
   static constexpr int LDS_TILE = BQ * D;   // swizzled, unpadded (fa_common.hpp)
   static constexpr int LDS_KV = KV_LDS ? BK * D : 8;   // K (or V) tile, kperm rows
   static_assert(64 * (D / 2) * 4 <= LDS_TILE * 2, "a merge buffer must fit in one stage");
 };
 
 template <typename E, int D, bool CAUSAL, int SPLIT>
-__global__ __launch_bounds__(256)
-__attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::KV_LDS ? 3 : 1))) void fa_bwd_dkdv_kernel(
+__global__ __launch_bounds__((DkdvTile<D, SPLIT>::NT))
+__attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_bwd_dkdv_kernel(
     BwdArgs a) {
   using T = DkdvTile<D, SPLIT>;
   constexpr int BK = T::BK, BQ = T::BQ, NSUB = T::NSUB;
@@ -244,8 +252,8 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::KV_LDS ? 3 : 1))) void fa
   const int kt = CAUSAL ? zigzag_rank(bid / BHk, a.n_blocks) : bid / BHk;
   const int b = bhk / a.Hk, hk = bhk % a.Hk;
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
-  const int kg = SPLIT == 2 ? (w >> 1) : w;
-  const int qh = SPLIT == 2 ? (w & 1) : 0;
+  const int kg = w / T::NQH;
+  const int qh = w % T::NQH;
   const int g = lane >> 5, l32 = lane & 31;
   const int k0 = kt * BK;
   const int wk0 = k0 + 32 * kg;
@@ -269,7 +277,7 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::KV_LDS ? 3 : 1))) void fa
     // the workgroup's BK keys into LDS (zeros past Sk), then K scaled in
     // place, each thread its 16-byte chunks; the barrier before the tile
     // loop publishes the result
-    DmaStager<D, BK> stk, stv;
+    DmaStager<D, BK, T::NW> stk, stv;
     stk.init(w, lane, a.k.ss);
     stv.init(w, lane, a.v.ss);
     stk.load(s_k, a.k.head(b, hk), a.k.ss, k0, Sk, w);
@@ -325,29 +333,22 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::KV_LDS ? 3 : 1))) void fa
   // seeds: s_lse = -LSE * log2(e) / cr (-inf past S, so P = 0 there) and
   // s_dl = -delta.  Seeding the S and dP MFMAs with them yields
   // ck * s - LSE' and dP - delta with no per-score VALU work.
-  DmaStager<D, BQ> stq, stg;
+  DmaStager<D, BQ, T::NW> stq, stg;
   stq.init(w, lane, a.q.ss);
   stg.init(w, lane, a.dout.ss);
   const float lse_mul = -kLog2e / cr;
   float lse_r = 0.0f, dl_r = 0.0f;   // raw LSE / delta of row m0 + tid
   // Q and dO go straight to LDS stage `st`; LSE / delta through VGPRs.
-  // (cur_h, cur_m0) is tile t's query head and first row; advance(t)
-  // steps to tile t + 1, incrementally (no per-tile scalar division by
-  // nt_h: dK/dV -1 to -5 %), except in the D = 128 unsplit variant, which
-  // sits at the register limit and measured 2-3 % faster with the division.
-  constexpr bool kIncremental = !(D >= 128 && SPLIT == 1);
+  // (cur_h, cur_m0) is tile t's query head and first row; advance()
+  // steps to tile t + 1 incrementally (no per-tile scalar division by nt_h:
+  // dK/dV -1 to -5 %).
   const int m_end = m_begin + nt_h * BQ;
   int cur_h = hk * a.grp, cur_m0 = m_begin;
-  auto advance = [&](int t, int &h, int &m0) {
-    if constexpr (kIncremental) {
-      m0 += BQ;
-      if (m0 >= m_end) {
-        m0 = m_begin;
-        ++h;
-      }
-    } else {
-      h = hk * a.grp + (t + 1) / nt_h;
-      m0 = m_begin + ((t + 1) % nt_h) * BQ;
+  auto advance = [&](int &h, int &m0) {
+    m0 += BQ;
+    if (m0 >= m_end) {
+      m0 = m_begin;
+      ++h;
     }
   };
   // Q / dO descriptors of the tile to load, walked by cursors: re-aimed at
@@ -412,7 +413,7 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::KV_LDS ? 3 : 1))) void fa
     const int m0 = cur_m0;
     const bool more = t + 1 < n_tiles;
     int nxt_h = cur_h, nxt_m0 = cur_m0;
-    advance(t, nxt_h, nxt_m0);
+    advance(nxt_h, nxt_m0);
     if (more) {
       if (nxt_h != cur_h) {
         aim(nxt_h, nxt_m0);
@@ -545,13 +546,20 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::KV_LDS ? 3 : 1))) void fa
   }
 
   float dk_mul = a.sm_scale / sc.mul;
-  if (SPLIT == 2) {
+  if (T::NQH == 2) {
     // the loop's last barrier ordered every tile read before these writes
     const DsScale unit;
-    merge_pair<D>(reinterpret_cast<float *>(kg ? s_q1 : s_q0), qh == 1, dk, sc,
-                  lane);
-    merge_pair<D>(reinterpret_cast<float *>(kg ? s_do1 : s_do0), qh == 1, dv,
-                  unit, lane);
+    if constexpr (T::NKG == 2) {
+      merge_pair<D>(reinterpret_cast<float *>(kg ? s_q1 : s_q0), qh == 1, dk, sc, lane);
+      merge_pair<D>(reinterpret_cast<float *>(kg ? s_do1 : s_do0), qh == 1, dv, unit, lane);
+    } else {
+      // four key groups: one stage buffer each, dK then (once every reader
+      // is done) dV
+      f16 *buf = kg == 0 ? s_q0 : (kg == 1 ? s_q1 : (kg == 2 ? s_do0 : s_do1));
+      merge_pair<D>(reinterpret_cast<float *>(buf), qh == 1, dk, sc, lane);
+      __syncthreads();
+      merge_pair<D>(reinterpret_cast<float *>(buf), qh == 1, dv, unit, lane);
+    }
     if (qh == 1) return;
     dk_mul = a.sm_scale;
   }

@@ -235,11 +235,11 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, const void 
 
 // Loads one ROWS-row tile (rows r0 .. r0+ROWS-1 of a (b, h) head, zeros
 // past S) into a swizzled LDS slot: ROWS*D*2 bytes = ROWS*D/512 wave
-// instructions of 1 KiB, ROWS*D/2048 per wave of a 4-wave workgroup.  No
-// VGPRs hold tile data.
-template <int D, int ROWS = 64>
+// instructions of 1 KiB, ROWS*D/(512*NW) per wave of an NW-wave workgroup.
+// No VGPRs hold tile data.
+template <int D, int ROWS = 64, int NW = 4>
 struct DmaStager {
-  static constexpr int PER_WAVE = ROWS * D / 2048;
+  static constexpr int PER_WAVE = ROWS * D / (512 * NW);
   static_assert(PER_WAVE >= 1, "tile smaller than one DMA instruction per wave");
   int off[PER_WAVE];   // global byte offset of this lane's chunk, relative to row r0
 

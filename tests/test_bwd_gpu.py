@@ -197,7 +197,7 @@ def test_backward_tiny_upstream_gradient(D):
 # Large enough grids to run the unsplit backward kernels (the launcher splits
 # rows across waves only for grids under 2 / 4 (causal) workgroups per CU).
 @pytest.mark.parametrize("shape,causal", [((4, 1000, 32, 64), False), ((8, 600, 32, 32), True),
-                                          ((2, 1100, 64, 128), False)])
+                                          ((2, 1100, 64, 128), False), ((2, 1100, 32, 128), True)])
 def test_backward_large_grid_variant(shape, causal):
     B, S, H, D = shape
     print(f"[case] bwd large-grid {shape} causal={causal}", flush=True)

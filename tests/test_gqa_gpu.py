@@ -87,9 +87,11 @@ def test_gqa_parity(case):
         assert e < TOL, f"{case} {key} max-abs {e:.3e} >= {TOL}"
 
 
-# Grids large enough for the unsplit (one wave per 32 rows) kernels.
+# Grids large enough for the unsplit kernels (the last two run the eight-wave
+# D = 128 dK/dV layout, grouped query heads sharing its K / V in LDS).
 @pytest.mark.parametrize("case", [(4, 1000, 1000, 32, 8, 64, True), (4, 520, 777, 32, 4, 128, False),
-                                  (8, 300, 700, 32, 16, 32, True)])
+                                  (8, 300, 700, 32, 16, 32, True), (4, 600, 1100, 32, 8, 128, False),
+                                  (4, 300, 1100, 32, 16, 128, True)])
 def test_gqa_large_grid_variant(case):
     B, Sq, Sk, H, Hk, D, causal = case
     print(f"[case] gqa large-grid {case}", flush=True)
