@@ -273,33 +273,18 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   const float ck = std::is_same<E, f16>::value ? fminf(a.c, 1.0f) : 1.0f;
   const float cr = a.c / ck;
   const float kmul = a.neg ? -ck : ck;
+  // K and V loads are issued here and scaled once they land, after the
+  // first query tile's loads are issued too (one memory latency for both)
   if constexpr (T::KV_LDS) {
-    // the workgroup's BK keys into LDS (zeros past Sk), then K scaled in
-    // place, each thread its 16-byte chunks; the barrier before the tile
-    // loop publishes the result
+    // the workgroup's BK keys into LDS (zeros past Sk)
     DmaStager<D, BK, T::NW> stk, stv;
     stk.init(w, lane, a.k.ss);
     stv.init(w, lane, a.v.ss);
     stk.load(s_k, a.k.head(b, hk), a.k.ss, k0, Sk, w);
     stv.load(s_v, a.v.head(b, hk), a.v.ss, k0, Sk, w);
-    __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
-    __syncthreads();
-    if (kmul != 1.0f) {
-#pragma unroll
-      for (int ch = tid; ch < BK * D / 8; ch += T::NT) {
-        vec8<E> x = ld8<E>(s_k + 8 * ch);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] = (E)((float)x[j] * kmul);
-        *reinterpret_cast<vec8<E> *>(s_k + 8 * ch) = x;
-      }
-    }
   } else {
     load_row_frags<E, D>(kf, a.k.head(b, hk), a.k.ss, key, Sk, g);
     load_row_frags<E, D>(vf, a.v.head(b, hk), a.v.ss, key, Sk, g);
-#pragma unroll
-    for (int c = 0; c < D / 16; ++c)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) kf[c][j] = (E)((float)kf[c][j] * kmul);
   }
   // B operands of S and dP: K^T / V^T fragments K[key][16cc + 8g .. +7]
   // (registers, or LDS rows 32kg + l32 read like the query tiles' A rows)
@@ -399,11 +384,28 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
                  4 * (l16 & 1);
   }
 
-  __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): K/V fragments resident
-  if (n_tiles > 0) {
-    load_tile(cur_h, cur_m0, std::integral_constant<int, 0>{});
-    store_tile(std::integral_constant<int, 0>{});
+  if (n_tiles > 0) load_tile(cur_h, cur_m0, std::integral_constant<int, 0>{});
+  __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): K, V and the first tile resident
+  if constexpr (T::KV_LDS) {
+    // K scaled in place once every wave's part of it has landed, each
+    // thread its 16-byte chunks; the barrier below publishes the result
+    __syncthreads();
+    if (kmul != 1.0f) {
+#pragma unroll
+      for (int ch = tid; ch < BK * D / 8; ch += T::NT) {
+        vec8<E> x = ld8<E>(s_k + 8 * ch);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = (E)((float)x[j] * kmul);
+        *reinterpret_cast<vec8<E> *>(s_k + 8 * ch) = x;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) kf[c][j] = (E)((float)kf[c][j] * kmul);
   }
+  if (n_tiles > 0) store_tile(std::integral_constant<int, 0>{});
   __syncthreads();
 
   // One query tile; the LDS stage is a compile-time constant (the loop below
@@ -622,6 +624,36 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
   vec8<E> qf[D / 16], gf[D / 16];
   load_row_frags<E, D>(qf, a.q.head(b, h), a.q.ss, qrow, Sq, g);
   load_row_frags<E, D>(gf, a.dout.head(b, h), a.dout.ss, qrow, Sq, g);
+
+  int kv_end = Sk;
+  if (CAUSAL) kv_end = min(Sk, q0 + BM + off);
+  // 0 when every query of the block precedes every key (causal, Sq > Sk)
+  const int n_tiles = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
+  const float c = a.c;
+
+  // K and V tiles go straight to LDS (fa_common.hpp DmaStager).
+  DmaStager<D, BN> stk, stv;
+  stk.init(w, lane, a.k.ss);
+  stv.init(w, lane, a.v.ss);
+  auto load_tile = [&](int n0, auto stc) {
+    stk.load(k_st(stc), kb, a.k.ss, n0, Sk, w);
+    stv.load(v_st(stc), vb, a.v.ss, n0, Sk, w);
+  };
+  // the loop loads tile t + 1 during tile t: cursors from row BN, advanced
+  // by a tile per load
+  RowCursor ck, cv;
+  ck.init(kb, a.k.ss, BN, Sk, D, BN);
+  cv.init(vb, a.v.ss, BN, Sk, D, BN);
+  auto load_next = [&](auto stc) {
+    stk.load(k_st(stc), ck.rsrc(), w);
+    stv.load(v_st(stc), cv.rsrc(), w);
+    ck.advance();
+    cv.advance();
+  };
+
+  // the first key tile's DMA overlaps the row loads and the work below
+  if (n_tiles > 0) load_tile(0, std::integral_constant<int, 0>{});
+
   if (a.neg) {
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) qf[c] = neg8(qf[c]);
@@ -679,32 +711,6 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
 #pragma unroll
   for (int i = 0; i < 16; ++i) dl_seed[i] = -dl * gmul;
 
-  int kv_end = Sk;
-  if (CAUSAL) kv_end = min(Sk, q0 + BM + off);
-  // 0 when every query of the block precedes every key (causal, Sq > Sk)
-  const int n_tiles = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
-  const float c = a.c;
-
-  // K and V tiles go straight to LDS (fa_common.hpp DmaStager).
-  DmaStager<D, BN> stk, stv;
-  stk.init(w, lane, a.k.ss);
-  stv.init(w, lane, a.v.ss);
-  auto load_tile = [&](int n0, auto stc) {
-    stk.load(k_st(stc), kb, a.k.ss, n0, Sk, w);
-    stv.load(v_st(stc), vb, a.v.ss, n0, Sk, w);
-  };
-  // the loop loads tile t + 1 during tile t: cursors from row BN, advanced
-  // by a tile per load
-  RowCursor ck, cv;
-  ck.init(kb, a.k.ss, BN, Sk, D, BN);
-  cv.init(vb, a.v.ss, BN, Sk, D, BN);
-  auto load_next = [&](auto stc) {
-    stk.load(k_st(stc), ck.rsrc(), w);
-    stv.load(v_st(stc), cv.rsrc(), w);
-    ck.advance();
-    cv.advance();
-  };
-
   // Per-lane LDS element offsets inside a stage (as in the dK/dV kernel):
   // A-operand rows l32, chunk 2cc + g; transposed reads of K rows
   // 4g + (l16 >> 2).
@@ -721,9 +727,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
                  4 * (l16 & 1);
   }
 
-  __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): Q/dO fragments, LSE, delta resident
-  if (n_tiles > 0) load_tile(0, std::integral_constant<int, 0>{});
-  __builtin_amdgcn_s_waitcnt(0x0f70);
+  __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): rows, LSE, delta and the first tile resident
   __syncthreads();
 
   auto tile_step = [&](auto stc, int t) {
