@@ -24,12 +24,17 @@ Beyond the reference (its wrapper requires q, k, v of one shape):
         the attention prologue fused into one pass: optional per-head
         RMSNorm (Qwen3's q_norm / k_norm) and rotary position embedding
         of q and k.
+    flash_attn_op
+        flash_attn_gqa as torch.library custom ops (flash_attn_volta::fwd,
+        flash_attn_volta::bwd) with fake-tensor and autograd registrations,
+        so torch.compile keeps the call as one graph node.
 """
 
 from .forward import flash_attn_forward, flash_attn_forward_gqa, flash_attn_volta
 from .backward import flash_attn_backward, flash_attn_backward_gqa
 from .autograd import flash_attn, flash_attn_gqa
 from .rope import apply_rotary_qk, rope_qk_backward, rope_qk_forward
+from .ops import flash_attn_op
 
 __all__ = [
     "flash_attn_forward",
@@ -42,5 +47,6 @@ __all__ = [
     "apply_rotary_qk",
     "rope_qk_forward",
     "rope_qk_backward",
+    "flash_attn_op",
 ]
 __version__ = "0.4.0"

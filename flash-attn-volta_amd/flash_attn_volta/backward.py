@@ -74,7 +74,10 @@ def _run_bwd(do, q, k, v, o, lse, causal, sm_scale, gqa):
     do, q, k, v, o = (_kernel_ready(t) for t in (do, q, k, v, o))
     lse = lse.contiguous()
     dq = torch.empty((B, N, H, D), dtype=q.dtype, device=q.device)
-    dk, dv = torch.empty((2, B, Sk, Hk, D), dtype=q.dtype, device=q.device).unbind(0)
+    # separate allocations: outputs of the registered custom op (ops.py)
+    # must not share storage
+    dk = torch.empty((B, Sk, Hk, D), dtype=q.dtype, device=q.device)
+    dv = torch.empty_like(dk)
     if dq.numel() == 0 or dk.numel() == 0:
         # nothing attends to anything: every gradient is zero
         for t in (dq, dk, dv):
