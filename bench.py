@@ -529,7 +529,8 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}); "
-              "this build has no multi-GPU path, see DESIGN.md for how it would shard.",
+              "this build has no multi-GPU path (attention would shard by heads, one GPU per "
+              "process, with the kernels unchanged on each GPU's (B, S, H/g, D) share).",
               file=sys.stderr)
         sys.exit(2)
 
