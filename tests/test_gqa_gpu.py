@@ -167,6 +167,7 @@ BF16_CASES = [
     (2, 77, 191, 6, 3, 32, True),
     (1, 200, 333, 4, 2, 16, False),
     (1, 4096, 4096, 16, 16, 64, True),        # the C4a shape
+    (1, 600, 600, 64, 64, 128, False),        # grid for the eight-wave D = 128 dK/dV
 ]
 
 
