@@ -149,7 +149,8 @@ int launch_dkdv_split(const fa::BwdArgs &args, hipStream_t stream) {
   using T = fa::DkdvTile<D, SPLIT>;
   fa::BwdArgs a = args;
   a.n_blocks = (a.Sk + T::BK - 1) / T::BK;
-  const int64_t grid = (int64_t)a.n_blocks * a.B * a.Hk;
+  // a split key block takes two workgroups
+  const int64_t grid = ((int64_t)a.n_blocks + a.split_kt) * a.B * a.Hk;
   if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
   hipLaunchKernelGGL((fa::fa_bwd_dkdv_kernel<E, D, CAUSAL, SPLIT>), dim3((unsigned)grid), dim3(T::NT),
                      0, stream, a);
@@ -170,6 +171,10 @@ int launch_dq_split(const fa::BwdArgs &args, hipStream_t stream) {
 
 template <typename E, int D, bool CAUSAL>
 int launch_dkdv(const fa::BwdArgs &a, hipStream_t stream) {
+  // the key-block split exists in the eight-wave D = 128 kernel only
+  if constexpr (D == 128 && CAUSAL) {
+    if (a.split_kt > 0) return launch_dkdv_split<E, D, CAUSAL, 1>(a, stream);
+  }
   return row_split(a.Sk, (int64_t)a.B * a.Hk, CAUSAL, D >= 128 ? 1 : 2)
              ? launch_dkdv_split<E, D, CAUSAL, 2>(a, stream)
              : launch_dkdv_split<E, D, CAUSAL, 1>(a, stream);
@@ -411,12 +416,16 @@ int bwd_common(const void *dout, const void *q, const void *k, const void *v, co
 int run_dkdv(const void *dout, const void *q, const void *k, const void *v, const float *lse,
              const float *delta, void *dk, void *dv, const Shape &s, const int64_t *do_st,
              const int64_t *q_st, const int64_t *k_st, const int64_t *v_st, const int64_t *dk_st,
-             const int64_t *dv_st, float sm_scale, int causal, void *stream) {
+             const int64_t *dv_st, float sm_scale, int causal, void *stream, int split_kt = 0,
+             unsigned *cnt = nullptr, float *part = nullptr) {
   fa::BwdArgs a;
   int rc = bwd_common(dout, q, k, v, lse, delta, s, do_st, q_st, k_st, v_st, sm_scale, &a);
   if (rc) return rc;
   if ((rc = check_kv_like(dk, dk_st, s))) return rc;
   if ((rc = check_kv_like(dv, dv_st, s))) return rc;
+  a.split_kt = split_kt;
+  a.cnt = cnt;
+  a.part = part;
   a.dk = static_cast<f16 *>(dk);
   a.dv = static_cast<f16 *>(dv);
   a.dk_sb = dk_st[0];
@@ -434,7 +443,8 @@ int run_dkdv(const void *dout, const void *q, const void *k, const void *v, cons
 int run_dq(const void *dout, const void *q, const void *k, const void *v, const float *lse,
            const float *delta, void *dq, const Shape &s, const int64_t *do_st, const int64_t *q_st,
            const int64_t *k_st, const int64_t *v_st, const int64_t *dq_st, float sm_scale,
-           int causal, void *stream, const void *o = nullptr, const int64_t *o_st = nullptr) {
+           int causal, void *stream, const void *o = nullptr, const int64_t *o_st = nullptr,
+           unsigned *cnt_zero = nullptr, int n_cnt_zero = 0) {
   fa::BwdArgs a;
   int rc = bwd_common(dout, q, k, v, lse, delta, s, do_st, q_st, k_st, v_st, sm_scale, &a);
   if (rc) return rc;
@@ -444,6 +454,8 @@ int run_dq(const void *dout, const void *q, const void *k, const void *v, const 
     a.o = desc(o, o_st);
     a.delta_out = const_cast<float *>(delta);
   }
+  a.cnt_zero = cnt_zero;
+  a.n_cnt_zero = n_cnt_zero;
   a.dq = static_cast<f16 *>(dq);
   a.dq_sb = dq_st[0];
   a.dq_ss = dq_st[1];
@@ -455,6 +467,60 @@ int run_dq(const void *dout, const void *q, const void *k, const void *v, const 
 size_t delta_bytes(int B, int Sq, int H) {
   const size_t n = (size_t)B * (size_t)H * (size_t)Sq * sizeof(float);
   return (n + 255) & ~(size_t)255;
+}
+
+// Causal key-block split of the eight-wave D = 128 dK/dV kernel
+// (fa::BwdArgs::split_kt).  When the grid of key blocks fits one round of
+// workgroups (one per CU), the causal sweep lengths set the time: block 0
+// sees every query tile, the last block one or two, and no other workgroup
+// can take over.  The leading blocks with more than a few tiles are then
+// swept by two workgroups each.  Larger grids keep one workgroup per block:
+// later rounds already fill in behind the long sweeps.
+struct DkdvSplit {
+  int split_kt = 0;    // leading key blocks split, per (b, key/value head)
+  int64_t slots = 0;   // split_kt * B * Hk
+};
+
+DkdvSplit dkdv_split_plan(const Shape &s, int causal) {
+  using T = fa::DkdvTile<128, 1>;
+  DkdvSplit p;
+  if (!causal || s.D != 128) return p;
+  const int64_t nb = (s.Sk + T::BK - 1) / T::BK;
+  const int64_t bhk = (int64_t)s.B * s.Hk;
+  if (nb * bhk > device_cus()) return p;
+  const int64_t grp = s.H / s.Hk, off = (int64_t)s.Sk - s.Sq;
+  // query tiles key block kt sweeps (the kernel's m_begin / nt_h)
+  auto tiles = [&](int64_t kt) -> int64_t {
+    const int64_t m_first = kt * T::BK - off > 0 ? kt * T::BK - off : 0;
+    const int64_t m_begin = m_first / T::BQ * T::BQ;
+    return s.Sq > m_begin ? (s.Sq - m_begin + T::BQ - 1) / T::BQ * grp : 0;
+  };
+  // Block 0's sweep must be long enough to pay for the partials' traffic
+  // (at 16 tiles the split costs ~1 %); then every block above the
+  // threshold splits (measured: thresholds of 1/2, 1/3, 1/4, 1/8 and 1/16
+  // of block 0's tiles gave -7, -13, -14, -18 and -19 % at (1,4096,8,128)).
+  const int64_t t0 = tiles(0);
+  if (t0 < 32) return p;
+  const int64_t thr = t0 / 16 > 4 ? t0 / 16 : 4;
+  int64_t kt = 0;
+  while (kt < nb && tiles(kt) > thr) ++kt;
+  p.split_kt = (int)kt;
+  p.slots = kt * bhk;
+  return p;
+}
+
+size_t split_cnt_bytes(const DkdvSplit &p) {
+  return ((size_t)p.slots * sizeof(unsigned) + 255) & ~(size_t)255;
+}
+
+// two segments x (dK, dV) x BK keys x D fp32 per split block
+size_t split_part_bytes(const DkdvSplit &p) {
+  using T = fa::DkdvTile<128, 1>;
+  return (size_t)p.slots * 2 * 2 * T::BK * 128 * sizeof(float);
+}
+
+size_t split_bytes(const DkdvSplit &p) {
+  return p.split_kt > 0 ? split_cnt_bytes(p) + split_part_bytes(p) : 0;
 }
 
 int run_bwd(const void *dout, const void *q, const void *k, const void *v, const void *o,
@@ -477,13 +543,26 @@ int run_bwd(const void *dout, const void *q, const void *k, const void *v, const
   float *delta = static_cast<float *>(workspace);
   if ((rc = bwd_common(dout, q, k, v, lse, delta, s, do_st, q_st, k_st, v_st, sm_scale, &probe)))
     return rc;
+  // The key-block split runs when the workspace has room for it (see
+  // fa_bwd_gqa_workspace_bytes): counters, then the fp32 partials.
+  DkdvSplit plan = dkdv_split_plan(s, causal);
+  const size_t dbytes = delta_bytes(s.B, s.Sq, s.H);
+  if (plan.split_kt > 0 && workspace_bytes < dbytes + split_bytes(plan)) plan = DkdvSplit{};
+  unsigned *cnt = nullptr;
+  float *part = nullptr;
+  if (plan.split_kt > 0) {
+    cnt = reinterpret_cast<unsigned *>(static_cast<char *>(workspace) + dbytes);
+    part = reinterpret_cast<float *>(static_cast<char *>(workspace) + dbytes +
+                                     split_cnt_bytes(plan));
+  }
   // dQ first: it computes delta (the pre-pass, folded in) for the dK/dV
-  // kernel, which runs after it on the same stream.
+  // kernel, which runs after it on the same stream, and zeroes the split
+  // counters.
   if ((rc = run_dq(dout, q, k, v, lse, delta, dq, s, do_st, q_st, k_st, v_st, dq_st, sm_scale,
-                   causal, stream, o, o_st)))
+                   causal, stream, o, o_st, cnt, (int)plan.slots)))
     return rc;
   return run_dkdv(dout, q, k, v, lse, delta, dk, dv, s, do_st, q_st, k_st, v_st, dk_st, dv_st,
-                  sm_scale, causal, stream);
+                  sm_scale, causal, stream, plan.split_kt, cnt, part);
 }
 
 Shape square(int B, int S, int H, int D) { return Shape{B, S, S, H, H, D, FA_DTYPE_F16}; }
@@ -765,6 +844,12 @@ int fa_bwd_preprocess(const void *o, const void *dout, float *delta,
 size_t fa_bwd_workspace_bytes(int B, int S, int H, int D) {
   if (check_shape(square(B, S, H, D)) != FA_OK) return 0;
   return delta_bytes(B, S, H);
+}
+
+size_t fa_bwd_gqa_workspace_bytes(int B, int Sq, int Sk, int H, int Hk, int D, int causal) {
+  const Shape s{B, Sq, Sk, H, Hk, D, FA_DTYPE_F16};
+  if (check_shape(s) != FA_OK) return 0;
+  return delta_bytes(B, Sq, H) + split_bytes(dkdv_split_plan(s, causal));
 }
 
 int fa_bwd(const void *dout, const void *q, const void *k, const void *v,

@@ -11,9 +11,12 @@
 //                                 tiles; dQ = scale * dS K
 //                                 (reference: _fa_bwd_dq_kernel_*, :73-307)
 // with P = exp(scale * Q K^T - LSE) recomputed from the forward LSE and
-// dS = P * (dO V^T - delta).  No atomics and no S x S buffer: every output
-// element is written once by one lane, so results are bit-reproducible and a
-// causal query row's dQ never reads a key block it cannot see.
+// dS = P * (dO V^T - delta).  No floating-point atomics and no S x S
+// buffer: every output element is written once by one lane, so results are
+// bit-reproducible and a causal query row's dQ never reads a key block it
+// cannot see.  (The one integer atomic, in the causal key-block split of
+// the eight-wave D = 128 dK/dV kernel, only decides which of two
+// workgroups adds their two fp32 partials; the sum is the same either way.)
 //
 // Fragment layouts follow fa_common.hpp.  The dK/dV kernel computes S = Q K^T
 // with queries as the (kperm-ordered) A rows, so a lane owns one key and its
@@ -64,6 +67,19 @@ struct BwdArgs {
   float c;              // |sm_scale| * log2(e), clamped away from 0
   float sm_scale;       // signed scale applied to dQ and dK
   int neg;              // 1 when sm_scale < 0 (K or Q negated in S recompute)
+  // Causal key-block split (eight-wave D = 128 dK/dV only): key blocks
+  // [0, split_kt) of every (b, key/value head) are each swept by two
+  // workgroups, one per half of their query tiles.  Each writes its fp32
+  // dK / dV partial to part[slot][segment] and counts itself in cnt[slot]
+  // (slot = bhk * split_kt + kt); the second to finish adds the two and
+  // writes dK / dV.  split_kt = 0: no split.
+  int split_kt;
+  unsigned *cnt;
+  float *part;
+  // dQ kernel: when non-NULL, workgroup 0 zeroes cnt_zero[0 .. n_cnt_zero)
+  // (the split counters of the dK/dV launch that follows on the stream)
+  unsigned *cnt_zero;
+  int n_cnt_zero;
 };
 
 struct PreArgs {
@@ -182,6 +198,76 @@ __device__ __forceinline__ void merge_pair(float *buf, bool writer, floatx16 (&a
   }
 }
 
+// Agent-scope (device-wide) relaxed accesses for the split partials
+// (global_store / global_load with sc1 on gfx950): they go to the point
+// where all XCDs are coherent instead of a per-XCD L2 copy, so no L2
+// write-back or invalidation is needed to exchange them.
+__device__ __forceinline__ void store_agent(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(float *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// x * m + y with the product rounded before the sum (never one FMA): the
+// two segments' partials are formed as x * m, so whichever of them adds
+// the other's gets the same bits (fp32 addition commutes).
+__device__ __forceinline__ float mul_then_add(float x, float m, float y) {
+#pragma clang fp contract(off)
+  const float p = x * m;
+  return p + y;
+}
+
+// End of one segment of a split key block (see BwdArgs::split_kt): the
+// merged dK (unscaled, times sm_scale here) and dV of the `holder` waves go
+// to part[slot][seg] as fp32; thread 0 counts the segment in cnt[slot]
+// once every wave's partial stores have completed, and the workgroup that
+// counts second adds the other segment's partial to its own and stores
+// dK / dV as E.  The first workgroup leaves: no workgroup ever waits for
+// another.  Ordering: all partial accesses are agent-scope atomics, so the
+// release / acquire that a device-scope fence would add reduce to waiting
+// for the stores to complete (vmcnt(0)) before the barrier that precedes
+// the counter update; the loads follow the counter's returned value.  A
+// __threadfence() here would also write back and invalidate the XCD's
+// whole L2 in every such workgroup, which costs more than the split gains.
+// `pl` = the lane's index among the holders (key group * 64 + lane).
+template <typename E, int D, int NKG>
+__device__ __forceinline__ void split_finish(const BwdArgs &a, floatx16 (&dk)[D / 32],
+                                             floatx16 (&dv)[D / 32], int slot, int seg,
+                                             bool holder, int pl, bool in_range, f16 *dk_row,
+                                             f16 *dv_row, int g) {
+  constexpr int HALF = (D / 32) * 16;   // floats per lane and tensor
+  constexpr int LANES = 64 * NKG;
+  __shared__ unsigned s_order;
+  if (holder) {
+    float *mine = a.part + ((size_t)slot * 2 + seg) * (2 * HALF * LANES) + pl;
+#pragma unroll
+    for (int d = 0; d < D / 32; ++d)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        store_agent(mine + (16 * d + i) * LANES, dk[d][i] * a.sm_scale);
+        store_agent(mine + (HALF + 16 * d + i) * LANES, dv[d][i]);
+      }
+  }
+  __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's partial stored
+  __syncthreads();
+  if (threadIdx.x == 0) s_order = atomicAdd(a.cnt + slot, 1u);
+  __syncthreads();
+  if (s_order == 0) return;   // the other segment finishes this block
+  if (holder && in_range) {
+    float *other = a.part + ((size_t)slot * 2 + (seg ^ 1)) * (2 * HALF * LANES) + pl;
+#pragma unroll
+    for (int d = 0; d < D / 32; ++d)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        dk[d][i] = mul_then_add(dk[d][i], a.sm_scale, load_agent(other + (16 * d + i) * LANES));
+        dv[d][i] = mul_then_add(dv[d][i], 1.0f, load_agent(other + (HALF + 16 * d + i) * LANES));
+      }
+    store_row<E, D>(dk_row, dk, 1.0f, g);
+    store_row<E, D>(dv_row, dv, 1.0f, g);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // dK / dV: a workgroup's waves own key groups of 32 keys; with NQH = 2 the
 // two waves of a group take the two query halves of every tile and merge
@@ -248,8 +334,17 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   const int BHk = a.B * a.Hk;
   const int bid = blockIdx.x;
   const int bhk = bid % BHk;
-  // Causal: low key blocks see the most queries; zigzag heavy/light.
-  const int kt = CAUSAL ? zigzag_rank(bid / BHk, a.n_blocks) : bid / BHk;
+  const int rank = bid / BHk;
+  // Causal: low key blocks see the most queries.  Unsplit grids zigzag
+  // heavy / light blocks.  With the key-block split, ranks 2kt and 2kt + 1
+  // are the two halves of block kt < split_kt, then the unsplit blocks
+  // follow in order of decreasing work (heaviest first overall).
+  const int nsplit = (T::WIDE && CAUSAL) ? a.split_kt : 0;
+  const bool split = rank < 2 * nsplit;
+  const int seg = split ? (rank & 1) : 0;
+  const int kt = split ? (rank >> 1)
+                       : (nsplit > 0 ? rank - nsplit
+                                     : (CAUSAL ? zigzag_rank(rank, a.n_blocks) : rank));
   const int b = bhk / a.Hk, hk = bhk % a.Hk;
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int kg = w / T::NQH;
@@ -312,7 +407,11 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   const int m_first = CAUSAL ? max(0, k0 - off) : 0;
   const int m_begin = (m_first / BQ) * BQ;
   const int nt_h = (Sq > m_begin) ? (Sq - m_begin + BQ - 1) / BQ : 0;
-  const int n_tiles = nt_h * a.grp;
+  // A split block's segment 0 takes the first half of these tiles,
+  // segment 1 the rest.
+  const int n_all = nt_h * a.grp;
+  const int t_begin = seg ? n_all / 2 : 0;
+  const int n_tiles = split ? (seg ? n_all - n_all / 2 : n_all / 2) : n_all;
 
   // Per-query rows staged beside each tile, laid out as MFMA accumulator
   // seeds: s_lse = -LSE * log2(e) / cr (-inf past S, so P = 0 there) and
@@ -328,7 +427,8 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   // steps to tile t + 1 incrementally (no per-tile scalar division by nt_h:
   // dK/dV -1 to -5 %).
   const int m_end = m_begin + nt_h * BQ;
-  int cur_h = hk * a.grp, cur_m0 = m_begin;
+  int cur_h = hk * a.grp + (t_begin > 0 ? t_begin / nt_h : 0);
+  int cur_m0 = m_begin + (t_begin > 0 ? (t_begin % nt_h) * BQ : 0);
   auto advance = [&](int &h, int &m0) {
     m0 += BQ;
     if (m0 >= m_end) {
@@ -562,6 +662,15 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
       __syncthreads();
       merge_pair<D>(reinterpret_cast<float *>(buf), qh == 1, dv, unit, lane);
     }
+    if constexpr (T::WIDE && CAUSAL) {
+      if (split) {
+        split_finish<E, D, T::NKG>(a, dk, dv, bhk * nsplit + kt, seg, qh == 0, kg * 64 + lane,
+                                  key < Sk,
+                                  a.dk + b * a.dk_sb + hk * a.dk_sh + (int64_t)key * a.dk_ss,
+                                  a.dv + b * a.dv_sb + hk * a.dv_sh + (int64_t)key * a.dv_ss, g);
+        return;
+      }
+    }
     if (qh == 1) return;
     dk_mul = a.sm_scale;
   }
@@ -605,6 +714,10 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
   const int Sq = a.Sq, Sk = a.Sk, off = a.off;
   const int BH = a.B * a.H;
   const int bid = blockIdx.x;
+  // zero the split counters of the dK/dV launch that follows on the stream
+  if (a.cnt_zero != nullptr && bid == 0) {
+    for (int i = threadIdx.x; i < a.n_cnt_zero; i += 256) a.cnt_zero[i] = 0u;
+  }
   const int bh = bid % BH;
   // Causal: late query blocks see the most keys; zigzag heavy/light.
   const int qt = CAUSAL ? a.n_blocks - 1 - zigzag_rank(bid / BH, a.n_blocks) : bid / BH;

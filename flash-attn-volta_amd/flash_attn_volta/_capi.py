@@ -14,7 +14,7 @@ import threading
 LIB_NAME = "libfa_mi355x.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # status codes (enum fa_status)
 FA_OK = 0
@@ -44,6 +44,7 @@ EXPORTED_SYMBOLS = (
     "fa_fwd_splitkv_workspace_bytes",
     "fa_bwd_preprocess",
     "fa_bwd_workspace_bytes",
+    "fa_bwd_gqa_workspace_bytes",
     "fa_bwd",
     "fa_bwd_gqa",
     "fa_bwd_dkdv",
@@ -97,6 +98,8 @@ def _declare(lib):
     lib.fa_bwd_preprocess.argtypes = [_vp, _vp, _vp, _ci, _ci, _ci, _ci, _i64x4, _i64x4, _vp]
     lib.fa_bwd_workspace_bytes.restype = ctypes.c_size_t
     lib.fa_bwd_workspace_bytes.argtypes = [_ci, _ci, _ci, _ci]
+    lib.fa_bwd_gqa_workspace_bytes.restype = ctypes.c_size_t
+    lib.fa_bwd_gqa_workspace_bytes.argtypes = [_ci, _ci, _ci, _ci, _ci, _ci, _ci]
     lib.fa_bwd.restype = _ci
     lib.fa_bwd.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp,
                            _vp, _vp, _vp,

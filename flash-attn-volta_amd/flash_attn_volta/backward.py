@@ -83,15 +83,18 @@ def _run_bwd(do, q, k, v, o, lse, causal, sm_scale, gqa):
         for t in (dq, dk, dv):
             t.zero_()
         return dq, dk, dv
-    key = (B, N, H, D)
-    ws_bytes = _WS_BYTES.get(key)
-    if ws_bytes is None:
-        ws_bytes = _WS_BYTES[key] = lib.fa_bwd_workspace_bytes(B, N, H, D)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
     sq_, sk_ = kernel_strides(dq), kernel_strides(dk)
     st = (kernel_strides(do), kernel_strides(q), kernel_strides(k), kernel_strides(v),
           kernel_strides(o), sq_, sk_, sk_)
     with _on_device(q.device):
+        # the size that lets small causal D = 128 grids split their longest
+        # key blocks (fa_bwd_gqa_workspace_bytes); delta alone otherwise
+        key = (B, N, Sk, H, Hk, D, bool(causal))
+        ws_bytes = _WS_BYTES.get(key)
+        if ws_bytes is None:
+            ws_bytes = _WS_BYTES[key] = lib.fa_bwd_gqa_workspace_bytes(B, N, Sk, H, Hk, D,
+                                                                       int(bool(causal)))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
         if gqa:
             rc = lib.fa_bwd_gqa(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
                                 o.data_ptr(), lse.data_ptr(), dq.data_ptr(), dk.data_ptr(),

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 5
+#define FA_ABI_VERSION 6
 
 enum fa_status {
   FA_OK = 0,
@@ -143,12 +143,29 @@ int fa_bwd_preprocess(const void *o, const void *dout, float *delta,
 size_t fa_bwd_workspace_bytes(int B, int S, int H, int D);
 
 /*
+ * Bytes of device workspace with which fa_bwd / fa_bwd_gqa run their
+ * fastest schedule for these sizes (0 on bad sizes): the
+ * fa_bwd_workspace_bytes minimum plus, for causal D = 128 problems whose
+ * key blocks fit one round of workgroups, room for the key-block split
+ * (the longest causal key blocks swept by two workgroups each, fp32
+ * partials added by whichever finishes second; at most 64 MiB + 1 KiB).
+ * Any workspace of at least the minimum is valid: with less than this
+ * size the backward runs unsplit.  Split and unsplit results differ in
+ * rounding only; each is bit-reproducible.
+ *
+ * No counterpart in the reference (its backward has no workspace,
+ * flash_attn_volta/triton_fa_bwd.py:636-700).
+ */
+size_t fa_bwd_gqa_workspace_bytes(int B, int Sq, int Sk, int H, int Hk, int D, int causal);
+
+/*
  * Backward attention: (dq, dk, dv) of L = <o, dout> with o = fa_fwd(q,k,v),
  * given the forward's `lse`. Two launches: the dQ kernel (one workgroup
  * per query block), which also computes delta = rowsum(o * dout) -- what
  * fa_bwd_preprocess computes -- into the workspace, then the dK/dV kernel
- * (one workgroup per key block), which reads it. No atomics: results are
- * bit-reproducible.
+ * (one workgroup per key block, or two for the longest causal blocks when
+ * the workspace has room: fa_bwd_gqa_workspace_bytes). No floating-point
+ * atomics: results are bit-reproducible.
  *
  * Replaces flash_attn_volta/triton_fa_bwd.py:587-700 (flash_attn_backward
  * and _run_bwd_kernels, launching _fa_bwd_dq_kernel_* and

@@ -246,3 +246,65 @@ def test_backward_upstream_rows_of_very_different_magnitude():
           flush=True)
     assert np.all(np.isfinite(gq)) and worst <= 1.0
     assert ek <= 1e-2 and ev <= 1e-2
+
+
+def _bwd_capi(do, q, k, v, o, lse, causal, ws_bytes, fill):
+    """fa_bwd_gqa through the C ABI with a workspace of `ws_bytes` bytes, every
+    byte set to `fill` first (stale split counters and partials)."""
+    from flash_attn_volta import _capi
+    from flash_attn_volta.forward import kernel_strides
+    lib = _capi.load()
+    B, Sq, H, D = q.shape
+    Sk, Hk = k.shape[1], k.shape[2]
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ws = torch.full((ws_bytes,), fill, dtype=torch.uint8, device="cuda")
+    st = tuple(kernel_strides(t) for t in (do, q, k, v, o, dq, dk, dv))
+    dtype = _capi.FA_DTYPE_F16 if q.dtype == torch.float16 else _capi.FA_DTYPE_BF16
+    rc = lib.fa_bwd_gqa(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                        lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                        ws.data_ptr(), ws_bytes, B, Sq, Sk, H, Hk, D, *st,
+                        1.0 / math.sqrt(D), int(causal), dtype,
+                        torch.cuda.current_stream().cuda_stream)
+    _capi.check(rc, "fa_bwd_gqa")
+    torch.cuda.synchronize()
+    return dq, dk, dv
+
+
+# Causal D = 128 problems whose key blocks fit one round of workgroups: with
+# the workspace fa_bwd_gqa_workspace_bytes sizes, the longest key blocks are
+# swept by two workgroups whose fp32 partials the second to finish adds.
+@pytest.mark.parametrize("B,Sq,Sk,H,Hk,dtype", [
+    (1, 2048, 2048, 4, 4, torch.float16),
+    (1, 700, 1000, 8, 2, torch.float16),     # grouped heads, offset 300, ragged split block
+    (1, 2100, 2100, 2, 2, torch.bfloat16),   # ragged last key block (unsplit)
+])
+def test_backward_causal_key_block_split(B, Sq, Sk, H, Hk, dtype):
+    from flash_attn_volta import _capi, flash_attn_forward_gqa
+    D = 128
+    print(f"[case] bwd key-block split B={B} Sq={Sq} Sk={Sk} H={H} Hk={Hk} {dtype}", flush=True)
+    lib = _capi.load()
+    full = lib.fa_bwd_gqa_workspace_bytes(B, Sq, Sk, H, Hk, D, 1)
+    minimum = lib.fa_bwd_workspace_bytes(B, Sq, H, D)
+    assert full > minimum, "the split must apply to this shape"
+    q, k, v, do = orc.make_inputs_gqa(B, Sq, Sk, H, Hk, D, seed=13, dtype=dtype)
+    sc = default_scale(D, None)
+    o_ref, _ = orc.attention_fwd_gqa(q, k, v, True, sc)
+    dq_ref, dk_ref, dv_ref, _ = orc.attention_bwd_gqa(do, q, k, v, True, sc, o=o_ref)
+    qd, kd, vd, dod = (t.cuda() for t in (q, k, v, do))
+    o, lse = flash_attn_forward_gqa(qd, kd, vd, causal=True, return_softmax_lse=True)
+    unsplit = _bwd_capi(dod, qd, kd, vd, o, lse, True, minimum, 0)
+    split = _bwd_capi(dod, qd, kd, vd, o, lse, True, full, 0xFF)
+    again = _bwd_capi(dod, qd, kd, vd, o, lse, True, full, 0x00)
+    tol = TOL if dtype == torch.float16 else 4e-2
+    errs = dict(dq=max_abs(split[0], dq_ref), dk=max_abs(split[1], dk_ref),
+                dv=max_abs(split[2], dv_ref))
+    report(f"bwd split {B},{Sq},{Sk},{H},{Hk}", **errs)
+    for key, e in errs.items():
+        assert e < tol, f"{key} max-abs {e:.3e} >= {tol}"
+    # the dQ kernel is the same either way; dK / dV differ by rounding only
+    assert torch.equal(split[0], unsplit[0])
+    for a, b in zip(split[1:], unsplit[1:]):
+        assert max_abs(a, b.float()) < tol / 4
+    # bit-reproducible whatever the workspace held before
+    for a, b in zip(split, again):
+        assert torch.equal(a, b)

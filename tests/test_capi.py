@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.fa_abi_version() == _capi.ABI_VERSION == 5
+    assert lib.fa_abi_version() == _capi.ABI_VERSION == 6
 
 
 def test_strerror_covers_every_code(lib):
@@ -94,6 +94,32 @@ def test_workspace_bytes(lib):
     assert lib.fa_bwd_workspace_bytes(1, 3, 1, 64) == 256          # rounded to 256 B
     assert lib.fa_bwd_workspace_bytes(1, 3, 1, 48) == 0            # bad D
     assert lib.fa_bwd_workspace_bytes(0, 3, 1, 64) == 0            # bad B
+
+
+def test_split_workspace_bytes(lib):
+    """fa_bwd_gqa_workspace_bytes: the delta minimum, plus room for the
+    causal key-block split only for D = 128 causal grids of at most one
+    workgroup per CU (256 here: without a GPU the CU count defaults to
+    MI355X's) whose longest sweep has at least 32 query tiles."""
+    mini = lib.fa_bwd_workspace_bytes(1, 4096, 8, 128)
+    # (1,4096,8,128) causal: 32 key blocks x 8 heads; blocks with > 4 of
+    # their 64-query tiles (kt < 30) split: 240 slots, 2 x 2 x 128 x 128
+    # fp32 each, plus 240 counters rounded up to 1 KiB
+    slots = 30 * 8
+    assert lib.fa_bwd_gqa_workspace_bytes(1, 4096, 4096, 8, 8, 128, 1) == \
+        mini + 1024 + slots * 2 * 2 * 128 * 128 * 4
+    assert lib.fa_bwd_gqa_workspace_bytes(1, 4096, 4096, 8, 8, 128, 0) == mini   # non-causal
+    assert lib.fa_bwd_gqa_workspace_bytes(1, 4096, 4096, 16, 16, 64, 1) == \
+        lib.fa_bwd_workspace_bytes(1, 4096, 16, 64)                                # D = 64
+    assert lib.fa_bwd_gqa_workspace_bytes(1, 4096, 4096, 16, 16, 128, 1) == \
+        lib.fa_bwd_workspace_bytes(1, 4096, 16, 128)                               # 512 blocks
+    assert lib.fa_bwd_gqa_workspace_bytes(1, 1024, 1024, 16, 16, 128, 1) == \
+        lib.fa_bwd_workspace_bytes(1, 1024, 16, 128)                               # 16 tiles
+    # grouped heads: tiles count over the 4 query heads of each key head
+    assert lib.fa_bwd_gqa_workspace_bytes(1, 700, 1000, 8, 2, 128, 1) > \
+        lib.fa_bwd_workspace_bytes(1, 700, 8, 128)
+    assert lib.fa_bwd_gqa_workspace_bytes(1, 700, 1000, 8, 3, 128, 1) == 0       # H % Hk
+    assert lib.fa_bwd_gqa_workspace_bytes(1, 700, 1000, 8, 2, 96, 1) == 0        # bad D
 
 
 def test_bwd_validation(lib):
