@@ -57,6 +57,7 @@ struct FwdArgs {
   int n_qtiles;
   float c;             // |sm_scale| * log2(e), clamped away from 0
   int neg;             // 1 when sm_scale < 0: Q is negated on load
+  int zigzag;          // causal tile order: 1 zigzag heavy / light, 0 heaviest first
   // split-KV mode only (fa_fwd_kernel<..., SPLITKV = true>):
   int kv_split;        // keys per split, a multiple of the 64-key tile
   float *part_o;       // (n_splits, B, H, Sq, D) fp32: each split's normalised O
@@ -112,11 +113,15 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   const int BH = SPLITKV ? a.B * (a.H / grp) : a.B * a.H;
   const int bid = blockIdx.x;
   const int bh = bid % BH;
-  // Causal: zigzag heavy/light query tiles (heavy = late tiles); workgroups
-  // of one (b, h) are BH apart, so with BH % 8 == 0 they land on one XCD and
-  // share its L2.
-  const int qt = (CAUSAL && !SPLITKV) ? a.n_qtiles - 1 - zigzag_rank(bid / BH, a.n_qtiles)
-                                      : bid / BH;
+  // Causal: late query tiles are the heavy ones.  The launcher picks the
+  // order: heaviest first when the grid takes several rounds of resident
+  // workgroups (each freed slot then takes the heaviest tile left), zigzag
+  // heavy / light when it fits one round (co-resident workgroups then share
+  // a CU's time evenly).  Workgroups of one (b, h) are BH apart, so with
+  // BH % 8 == 0 they land on one XCD and share its L2.
+  const int qt = (CAUSAL && !SPLITKV)
+                     ? a.n_qtiles - 1 - (a.zigzag ? zigzag_rank(bid / BH, a.n_qtiles) : bid / BH)
+                     : bid / BH;
   const int hx = SPLITKV ? a.H / grp : a.H;
   const int b = bh / hx;
   const int h = SPLITKV ? 0 : bh % hx;               // SPLITKV: the head is per lane
