@@ -207,9 +207,13 @@ int launch_dq_split(const fa::BwdArgs &args, hipStream_t stream) {
 
 template <typename E, int D, bool CAUSAL>
 int launch_dkdv(const fa::BwdArgs &a, hipStream_t stream) {
-  // the key-block split exists in the eight-wave D = 128 kernel only
+  // the key-block split runs in the eight-wave D = 128 kernel and in the
+  // D = 64 query-split kernel (dkdv_split_plan)
   if constexpr (D == 128 && CAUSAL) {
     if (a.split_kt > 0) return launch_dkdv_split<E, D, CAUSAL, 1>(a, stream);
+  }
+  if constexpr (D == 64 && CAUSAL) {
+    if (a.split_kt > 0) return launch_dkdv_split<E, D, CAUSAL, 2>(a, stream);
   }
   return row_split(a.Sk, (int64_t)a.B * a.Hk, CAUSAL, D >= 128 ? 1 : 2)
              ? launch_dkdv_split<E, D, CAUSAL, 2>(a, stream)
@@ -505,44 +509,68 @@ size_t delta_bytes(int B, int Sq, int H) {
   return (n + 255) & ~(size_t)255;
 }
 
-// Causal key-block split of the eight-wave D = 128 dK/dV kernel
-// (fa::BwdArgs::split_kt).  When the grid of key blocks fits one round of
-// workgroups (one per CU), the causal sweep lengths set the time: block 0
-// sees every query tile, the last block one or two, and no other workgroup
-// can take over.  The leading blocks with more than a few tiles are then
-// swept by two workgroups each.  Larger grids keep one workgroup per block:
-// later rounds already fill in behind the long sweeps.
+// Causal key-block split of the dK/dV kernel (fa::BwdArgs::split_kt;
+// the eight-wave D = 128 and the D = 64 query-split layouts).  When the
+// grid of key blocks fits one round of resident workgroups, the causal
+// sweep lengths set the time: block 0 sees every query tile, the last
+// block one or two, and no other workgroup can take over.  The leading
+// blocks with the longest sweeps are then swept by two workgroups each.
+// Larger grids keep one workgroup per block: later rounds already fill in
+// behind the long sweeps (heaviest blocks first).
 struct DkdvSplit {
   int split_kt = 0;    // leading key blocks split, per (b, key/value head)
   int64_t slots = 0;   // split_kt * B * Hk
+  int bk = 0, d = 0;   // the kernel's key block and head dimension
 };
 
-DkdvSplit dkdv_split_plan(const Shape &s, int causal) {
-  using T = fa::DkdvTile<128, 1>;
-  DkdvSplit p;
-  if (!causal || s.D != 128) return p;
-  const int64_t nb = (s.Sk + T::BK - 1) / T::BK;
-  const int64_t bhk = (int64_t)s.B * s.Hk;
-  if (nb * bhk > device_cus()) return p;
+// Query tiles key block kt of a causal (B, Sq, Sk, H, Hk) problem sweeps
+// with BK-key blocks and BQ-query tiles (the dK/dV kernel's m_begin / nt_h),
+// counted over the H / Hk query heads of the group.
+int64_t causal_tiles(const Shape &s, int64_t kt, int BK, int BQ) {
   const int64_t grp = s.H / s.Hk, off = (int64_t)s.Sk - s.Sq;
-  // query tiles key block kt sweeps (the kernel's m_begin / nt_h)
-  auto tiles = [&](int64_t kt) -> int64_t {
-    const int64_t m_first = kt * T::BK - off > 0 ? kt * T::BK - off : 0;
-    const int64_t m_begin = m_first / T::BQ * T::BQ;
-    return s.Sq > m_begin ? (s.Sq - m_begin + T::BQ - 1) / T::BQ * grp : 0;
-  };
-  // Block 0's sweep must be long enough to pay for the partials' traffic
-  // (at 16 tiles the split costs ~1 %); then every block above the
-  // threshold splits (measured: thresholds of 1/2, 1/3, 1/4, 1/8 and 1/16
-  // of block 0's tiles gave -7, -13, -14, -18 and -19 % at (1,4096,8,128)).
-  const int64_t t0 = tiles(0);
+  const int64_t m_first = kt * BK - off > 0 ? kt * BK - off : 0;
+  const int64_t m_begin = m_first / BQ * BQ;
+  return s.Sq > m_begin ? (s.Sq - m_begin + BQ - 1) / BQ * grp : 0;
+}
+
+// Plan for one dK/dV layout T (BK keys per block, BQ-query tiles): split
+// only grids that fit one round of resident workgroups (T::WAVES_PER_EU
+// waves per SIMD, four SIMDs per CU) and whose block 0 sweeps at least 32
+// tiles; then every leading block with more than `thr(t0)` tiles splits.
+template <typename T, typename Thr>
+DkdvSplit split_plan_for(const Shape &s, Thr thr_of) {
+  DkdvSplit p;
+  const int64_t bhk = (int64_t)s.B * s.Hk;
+  const int64_t nb = (s.Sk + T::BK - 1) / T::BK;
+  const int64_t per_cu = 4 * T::WAVES_PER_EU / T::NW;
+  if (nb * bhk > per_cu * device_cus()) return p;
+  const int64_t t0 = causal_tiles(s, 0, T::BK, T::BQ);
   if (t0 < 32) return p;
-  const int64_t thr = t0 / 16 > 4 ? t0 / 16 : 4;
+  const int64_t thr = thr_of(t0);
   int64_t kt = 0;
-  while (kt < nb && tiles(kt) > thr) ++kt;
+  while (kt < nb && causal_tiles(s, kt, T::BK, T::BQ) > thr) ++kt;
   p.split_kt = (int)kt;
   p.slots = kt * bhk;
+  p.bk = T::BK;
+  p.d = s.D;
   return p;
+}
+
+// Measured (fa_bwd time, same box): D = 128 (eight-wave kernel, one
+// workgroup per CU) at (1,4096,8,128): thresholds of 1/2, 1/3, 1/4, 1/8 and
+// 1/16 of block 0's tiles gave -7, -13, -14, -18 and -19 %; (1,1024,16,128)
+// (16 tiles) lost ~1 % and stays unsplit.  D = 64 (query-split kernel,
+// three per CU): 1/3 gave -18 % at (1,4096,8,64), -10 % at (1,2048,16,64),
+// -34 % at (1,4096,16 heads / 4 kv heads,64); grids of more than one round
+// lost 2-8 % ((1,4096,16,64), (1,2048,32,64)) and stay unsplit.
+DkdvSplit dkdv_split_plan(const Shape &s, int causal) {
+  if (!causal) return DkdvSplit{};
+  if (s.D == 128)
+    return split_plan_for<fa::DkdvTile<128, 1>>(
+        s, [](int64_t t0) { return t0 / 16 > 4 ? t0 / 16 : (int64_t)4; });
+  if (s.D == 64 && row_split(s.Sk, (int64_t)s.B * s.Hk, true, 2))
+    return split_plan_for<fa::DkdvTile<64, 2>>(s, [](int64_t t0) { return t0 / 3; });
+  return DkdvSplit{};
 }
 
 size_t split_cnt_bytes(const DkdvSplit &p) {
@@ -551,8 +579,7 @@ size_t split_cnt_bytes(const DkdvSplit &p) {
 
 // two segments x (dK, dV) x BK keys x D fp32 per split block
 size_t split_part_bytes(const DkdvSplit &p) {
-  using T = fa::DkdvTile<128, 1>;
-  return (size_t)p.slots * 2 * 2 * T::BK * 128 * sizeof(float);
+  return (size_t)p.slots * 2 * 2 * (size_t)p.bk * (size_t)p.d * sizeof(float);
 }
 
 size_t split_bytes(const DkdvSplit &p) {

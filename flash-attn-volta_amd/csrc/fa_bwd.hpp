@@ -68,7 +68,7 @@ struct BwdArgs {
   float sm_scale;       // signed scale applied to dQ and dK
   int neg;              // 1 when sm_scale < 0 (K or Q negated in S recompute)
   int zigzag;           // dQ causal block order: 1 zigzag heavy / light, 0 heaviest first
-  // Causal key-block split (eight-wave D = 128 dK/dV only): key blocks
+  // Causal key-block split (dK/dV layouts with KEY_SPLIT): key blocks
   // [0, split_kt) of every (b, key/value head) are each swept by two
   // workgroups, one per half of their query tiles.  Each writes its fp32
   // dK / dV partial to part[slot][segment] and counts itself in cnt[slot]
@@ -312,6 +312,8 @@ struct DkdvTile {
   static constexpr int WAVES_PER_EU = (D == 64 && KV_LDS) ? 3 : (WIDE ? 2 : 1);
   static constexpr int LDS_TILE = BQ * D;   // swizzled, unpadded (fa_common.hpp)
   static constexpr int LDS_KV = KV_LDS ? BK * D : 8;   // K (or V) tile, kperm rows
+  // layouts that implement the causal key-block split (BwdArgs::split_kt)
+  static constexpr bool KEY_SPLIT = WIDE || (D == 64 && SPLIT == 2);
   static_assert(64 * (D / 2) * 4 <= LDS_TILE * 2, "a merge buffer must fit in one stage");
 };
 
@@ -342,7 +344,7 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   // grids of every size, +-0 at (1,4096,16,64)).  With the key-block
   // split, ranks 2kt and 2kt + 1 are the two halves of block kt < split_kt,
   // then the unsplit blocks follow.
-  const int nsplit = (T::WIDE && CAUSAL) ? a.split_kt : 0;
+  const int nsplit = (T::KEY_SPLIT && CAUSAL) ? a.split_kt : 0;
   const bool split = rank < 2 * nsplit;
   const int seg = split ? (rank & 1) : 0;
   const int kt = split ? (rank >> 1) : rank - nsplit;
@@ -663,7 +665,7 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
       __syncthreads();
       merge_pair<D>(reinterpret_cast<float *>(buf), qh == 1, dv, unit, lane);
     }
-    if constexpr (T::WIDE && CAUSAL) {
+    if constexpr (T::KEY_SPLIT && CAUSAL) {
       if (split) {
         split_finish<E, D, T::NKG>(a, dk, dv, bhk * nsplit + kt, seg, qh == 0, kg * 64 + lane,
                                   key < Sk,

@@ -145,10 +145,11 @@ size_t fa_bwd_workspace_bytes(int B, int S, int H, int D);
 /*
  * Bytes of device workspace with which fa_bwd / fa_bwd_gqa run their
  * fastest schedule for these sizes (0 on bad sizes): the
- * fa_bwd_workspace_bytes minimum plus, for causal D = 128 problems whose
- * key blocks fit one round of workgroups, room for the key-block split
- * (the longest causal key blocks swept by two workgroups each, fp32
- * partials added by whichever finishes second; at most 64 MiB + 1 KiB).
+ * fa_bwd_workspace_bytes minimum plus, for causal D = 64 / 128 problems
+ * whose key blocks fit one round of resident workgroups, room for the
+ * key-block split (the longest causal key blocks swept by two workgroups
+ * each, fp32 partials added by whichever finishes second; at most
+ * 64 MiB + 4 KiB).
  * Any workspace of at least the minimum is valid: with less than this
  * size the backward runs unsplit.  Split and unsplit results differ in
  * rounding only; each is bit-reproducible.

@@ -270,18 +270,20 @@ def _bwd_capi(do, q, k, v, o, lse, causal, ws_bytes, fill):
     return dq, dk, dv
 
 
-# Causal D = 128 problems whose key blocks fit one round of workgroups: with
-# the workspace fa_bwd_gqa_workspace_bytes sizes, the longest key blocks are
-# swept by two workgroups whose fp32 partials the second to finish adds.
-@pytest.mark.parametrize("B,Sq,Sk,H,Hk,dtype", [
-    (1, 2048, 2048, 4, 4, torch.float16),
-    (1, 700, 1000, 8, 2, torch.float16),     # grouped heads, offset 300, ragged split block
-    (1, 2100, 2100, 2, 2, torch.bfloat16),   # ragged last key block (unsplit)
+# Causal D = 64 / 128 problems whose key blocks fit one round of resident
+# workgroups: with the workspace fa_bwd_gqa_workspace_bytes sizes, the
+# longest key blocks are swept by two workgroups whose fp32 partials the
+# second to finish adds.
+@pytest.mark.parametrize("B,Sq,Sk,H,Hk,D,dtype", [
+    (1, 2048, 2048, 4, 4, 128, torch.float16),
+    (1, 700, 1000, 8, 2, 128, torch.float16),     # grouped heads, offset 300, ragged split block
+    (1, 2100, 2100, 2, 2, 128, torch.bfloat16),   # ragged last key block (unsplit)
+    (1, 2048, 2048, 16, 16, 64, torch.float16),
+    (1, 1500, 2048, 16, 4, 64, torch.bfloat16),   # grouped heads, offset 548
 ])
-def test_backward_causal_key_block_split(B, Sq, Sk, H, Hk, dtype):
+def test_backward_causal_key_block_split(B, Sq, Sk, H, Hk, D, dtype):
     from flash_attn_volta import _capi, flash_attn_forward_gqa
-    D = 128
-    print(f"[case] bwd key-block split B={B} Sq={Sq} Sk={Sk} H={H} Hk={Hk} {dtype}", flush=True)
+    print(f"[case] bwd key-block split B={B} Sq={Sq} Sk={Sk} H={H} Hk={Hk} D={D} {dtype}", flush=True)
     lib = _capi.load()
     full = lib.fa_bwd_gqa_workspace_bytes(B, Sq, Sk, H, Hk, D, 1)
     minimum = lib.fa_bwd_workspace_bytes(B, Sq, H, D)

@@ -98,9 +98,10 @@ def test_workspace_bytes(lib):
 
 def test_split_workspace_bytes(lib):
     """fa_bwd_gqa_workspace_bytes: the delta minimum, plus room for the
-    causal key-block split only for D = 128 causal grids of at most one
-    workgroup per CU (256 here: without a GPU the CU count defaults to
-    MI355X's) whose longest sweep has at least 32 query tiles."""
+    causal key-block split only for D = 64 / 128 causal grids of at most one
+    round of resident workgroups (one per CU at D = 128, three at D = 64;
+    256 CUs here: without a GPU the count defaults to MI355X's) whose
+    longest sweep has at least 32 query tiles."""
     mini = lib.fa_bwd_workspace_bytes(1, 4096, 8, 128)
     # (1,4096,8,128) causal: 32 key blocks x 8 heads; blocks with > 4 of
     # their 64-query tiles (kt < 30) split: 240 slots, 2 x 2 x 128 x 128
@@ -110,7 +111,14 @@ def test_split_workspace_bytes(lib):
         mini + 1024 + slots * 2 * 2 * 128 * 128 * 4
     assert lib.fa_bwd_gqa_workspace_bytes(1, 4096, 4096, 8, 8, 128, 0) == mini   # non-causal
     assert lib.fa_bwd_gqa_workspace_bytes(1, 4096, 4096, 16, 16, 64, 1) == \
-        lib.fa_bwd_workspace_bytes(1, 4096, 16, 64)                                # D = 64
+        lib.fa_bwd_workspace_bytes(1, 4096, 16, 64)          # D = 64: 1024 blocks > 3 per CU
+    # (1,4096,8,64) causal: 64-key blocks x 8 heads = 512, one round at three
+    # per CU; blocks with more than 64 / 3 = 21 tiles (kt < 43) split
+    slots64 = 43 * 8
+    assert lib.fa_bwd_gqa_workspace_bytes(1, 4096, 4096, 8, 8, 64, 1) == \
+        lib.fa_bwd_workspace_bytes(1, 4096, 8, 64) + 1536 + slots64 * 2 * 2 * 64 * 64 * 4
+    assert lib.fa_bwd_gqa_workspace_bytes(1, 4096, 4096, 8, 8, 32, 1) == \
+        lib.fa_bwd_workspace_bytes(1, 4096, 8, 32)                                 # D = 32
     assert lib.fa_bwd_gqa_workspace_bytes(1, 4096, 4096, 16, 16, 128, 1) == \
         lib.fa_bwd_workspace_bytes(1, 4096, 16, 128)                               # 512 blocks
     assert lib.fa_bwd_gqa_workspace_bytes(1, 1024, 1024, 16, 16, 128, 1) == \
