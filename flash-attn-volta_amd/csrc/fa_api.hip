@@ -126,11 +126,12 @@ int resident_per_cu(int threads) {
   int n = cache.load(std::memory_order_relaxed);
   if (n < 0) {
     int blocks = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, Kernel, threads, 0) != hipSuccess ||
-        blocks < 0)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, Kernel, threads, 0) != hipSuccess) {
       blocks = 0;
-    (void)hipGetLastError();   // an occupancy query error must not look like a launch error
-    n = blocks;
+      // the failed query's error must not look like a launch error
+      (void)hipGetLastError();
+    }
+    n = blocks > 0 ? blocks : 0;
     cache.store(n, std::memory_order_relaxed);
   }
   return n;
