@@ -198,7 +198,8 @@ int launch_dq_split(const fa::BwdArgs &args, hipStream_t stream) {
   using T = fa::DqTile<D, SPLIT>;
   fa::BwdArgs a = args;
   a.n_blocks = (a.Sq + T::BM - 1) / T::BM;
-  const int64_t grid = (int64_t)a.n_blocks * a.B * a.H;
+  // a split query block takes two workgroups
+  const int64_t grid = ((int64_t)a.n_blocks + a.dq_split) * a.B * a.H;
   if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
   constexpr auto kernel = fa::fa_bwd_dq_kernel<E, D, CAUSAL, SPLIT>;
   a.zigzag = CAUSAL ? zigzag_order(grid, a.n_blocks, resident_per_cu<kernel>(T::NT)) : 0;
@@ -454,62 +455,6 @@ int bwd_common(const void *dout, const void *q, const void *k, const void *v, co
   return FA_OK;
 }
 
-int run_dkdv(const void *dout, const void *q, const void *k, const void *v, const float *lse,
-             const float *delta, void *dk, void *dv, const Shape &s, const int64_t *do_st,
-             const int64_t *q_st, const int64_t *k_st, const int64_t *v_st, const int64_t *dk_st,
-             const int64_t *dv_st, float sm_scale, int causal, void *stream, int split_kt = 0,
-             unsigned *cnt = nullptr, float *part = nullptr) {
-  fa::BwdArgs a;
-  int rc = bwd_common(dout, q, k, v, lse, delta, s, do_st, q_st, k_st, v_st, sm_scale, &a);
-  if (rc) return rc;
-  if ((rc = check_kv_like(dk, dk_st, s))) return rc;
-  if ((rc = check_kv_like(dv, dv_st, s))) return rc;
-  a.split_kt = split_kt;
-  a.cnt = cnt;
-  a.part = part;
-  a.dk = static_cast<f16 *>(dk);
-  a.dv = static_cast<f16 *>(dv);
-  a.dk_sb = dk_st[0];
-  a.dk_ss = dk_st[1];
-  a.dk_sh = dk_st[2];
-  a.dv_sb = dv_st[0];
-  a.dv_ss = dv_st[1];
-  a.dv_sh = dv_st[2];
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  FA_DISPATCH(launch_dkdv, s, causal, a, st);
-}
-
-// dQ; with `o` given (the full backward), the kernel also computes delta
-// from O and dO and writes it to `delta` instead of reading it.
-int run_dq(const void *dout, const void *q, const void *k, const void *v, const float *lse,
-           const float *delta, void *dq, const Shape &s, const int64_t *do_st, const int64_t *q_st,
-           const int64_t *k_st, const int64_t *v_st, const int64_t *dq_st, float sm_scale,
-           int causal, void *stream, const void *o = nullptr, const int64_t *o_st = nullptr,
-           unsigned *cnt_zero = nullptr, int n_cnt_zero = 0) {
-  fa::BwdArgs a;
-  int rc = bwd_common(dout, q, k, v, lse, delta, s, do_st, q_st, k_st, v_st, sm_scale, &a);
-  if (rc) return rc;
-  if ((rc = check_q_like(dq, dq_st, s))) return rc;
-  if (o != nullptr) {
-    if ((rc = check_q_like(o, o_st, s))) return rc;
-    a.o = desc(o, o_st);
-    a.delta_out = const_cast<float *>(delta);
-  }
-  a.cnt_zero = cnt_zero;
-  a.n_cnt_zero = n_cnt_zero;
-  a.dq = static_cast<f16 *>(dq);
-  a.dq_sb = dq_st[0];
-  a.dq_ss = dq_st[1];
-  a.dq_sh = dq_st[2];
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  FA_DISPATCH(launch_dq, s, causal, a, st);
-}
-
-size_t delta_bytes(int B, int Sq, int H) {
-  const size_t n = (size_t)B * (size_t)H * (size_t)Sq * sizeof(float);
-  return (n + 255) & ~(size_t)255;
-}
-
 // Causal key-block split of the dK/dV kernel (fa::BwdArgs::split_kt;
 // the eight-wave D = 128 and the D = 64 query-split layouts).  When the
 // grid of key blocks fits one round of resident workgroups, the causal
@@ -566,12 +511,71 @@ DkdvSplit split_plan_for(const Shape &s, Thr thr_of) {
 // lost 2-8 % ((1,4096,16,64), (1,2048,32,64)) and stay unsplit.
 DkdvSplit dkdv_split_plan(const Shape &s, int causal) {
   if (!causal) return DkdvSplit{};
-  if (s.D == 128)
-    return split_plan_for<fa::DkdvTile<128, 1>>(
-        s, [](int64_t t0) { return t0 / 16 > 4 ? t0 / 16 : (int64_t)4; });
+  if (s.D == 128) {
+    // a full round whose block 0 sweeps under 64 tiles gains nothing since
+    // the blocks go heaviest first ((1,2048,16,128): +3 %)
+    using T = fa::DkdvTile<128, 1>;
+    const int64_t blocks = (s.Sk + T::BK - 1) / T::BK * ((int64_t)s.B * s.Hk);
+    if (causal_tiles(s, 0, T::BK, T::BQ) < 64 && 2 * blocks > device_cus()) return DkdvSplit{};
+    return split_plan_for<T>(s, [](int64_t t0) { return t0 / 16 > 4 ? t0 / 16 : (int64_t)4; });
+  }
   if (s.D == 64 && row_split(s.Sk, (int64_t)s.B * s.Hk, true, 2))
     return split_plan_for<fa::DkdvTile<64, 2>>(s, [](int64_t t0) { return t0 / 3; });
   return DkdvSplit{};
+}
+
+// Causal query-block split of the dQ kernel (fa::BwdArgs::dq_split): the
+// mirror image of the key-block split, for dQ grids of at most half a
+// round whose last query blocks sweep the most key tiles (measured with
+// the dK/dV split: (1,4096,4,128) backward -20 % instead of -11 %,
+// (1,2048,8,128) -11 % instead of -7 %).  The two halves' fp32 rows are
+// added by the dK/dV kernel that follows (no counters: the dQ kernel runs
+// first and nothing could zero them in time).
+struct DqSplit {
+  int split = 0;       // last query blocks split, per (b, h)
+  int bm = 0;          // rows per block of the dQ layout in use
+  int nblocks = 0;     // query blocks per (b, h)
+  int64_t slots = 0;   // split * B * H
+  int d = 0;
+};
+
+DqSplit dq_split_plan(const Shape &s, int causal) {
+  DqSplit p;
+  if (!causal || (s.D != 64 && s.D != 128)) return p;
+  const int64_t bh = (int64_t)s.B * s.H;
+  const bool sp = row_split(s.Sq, bh, true);
+  const int BM = s.D == 64 ? (sp ? fa::DqTile<64, 2>::BM : fa::DqTile<64, 1>::BM)
+                           : (sp ? fa::DqTile<128, 2>::BM : fa::DqTile<128, 1>::BM);
+  constexpr int BN = fa::DqTile<64, 1>::BN;
+  // resident dQ workgroups per CU on gfx950 (VGPR-bound: 150-152 registers
+  // at D = 64, 238-240 at D = 128)
+  const int64_t per_cu = s.D == 64 ? 3 : 2;
+  // at most half a round: on a full round the extra workgroups cost more
+  // than the balance gains ((1,4096,8,128) +3.5 %, (1,2048,16,64) +6.5 %)
+  const int64_t nq = (s.Sq + BM - 1) / BM;
+  if (2 * nq * bh > per_cu * device_cus()) return p;
+  const int64_t off = (int64_t)s.Sk - s.Sq;
+  auto tiles = [&](int64_t qt) -> int64_t {
+    int64_t end = (qt + 1) * BM + off;
+    end = end < s.Sk ? end : s.Sk;
+    return end > 0 ? (end + BN - 1) / BN : 0;
+  };
+  const int64_t tmax = tiles(nq - 1);
+  if (tmax < 32) return p;
+  const int64_t thr = tmax / 3;
+  int64_t n = 0;
+  while (n < nq && tiles(nq - 1 - n) > thr) ++n;
+  p.split = (int)n;
+  p.bm = BM;
+  p.nblocks = (int)nq;
+  p.slots = n * bh;
+  p.d = s.D;
+  return p;
+}
+
+// two segments x BM rows x D fp32 per split query block
+size_t dq_split_bytes(const DqSplit &p) {
+  return p.split > 0 ? (size_t)p.slots * 2 * (size_t)p.bm * (size_t)p.d * sizeof(float) : 0;
 }
 
 size_t split_cnt_bytes(const DkdvSplit &p) {
@@ -586,6 +590,77 @@ size_t split_part_bytes(const DkdvSplit &p) {
 size_t split_bytes(const DkdvSplit &p) {
   return p.split_kt > 0 ? split_cnt_bytes(p) + split_part_bytes(p) : 0;
 }
+
+int run_dkdv(const void *dout, const void *q, const void *k, const void *v, const float *lse,
+             const float *delta, void *dk, void *dv, const Shape &s, const int64_t *do_st,
+             const int64_t *q_st, const int64_t *k_st, const int64_t *v_st, const int64_t *dk_st,
+             const int64_t *dv_st, float sm_scale, int causal, void *stream, int split_kt = 0,
+             unsigned *cnt = nullptr, float *part = nullptr, const DqSplit *dqs = nullptr,
+             float *dq_part = nullptr, void *dq = nullptr, const int64_t *dq_st = nullptr) {
+  fa::BwdArgs a;
+  int rc = bwd_common(dout, q, k, v, lse, delta, s, do_st, q_st, k_st, v_st, sm_scale, &a);
+  if (rc) return rc;
+  if ((rc = check_kv_like(dk, dk_st, s))) return rc;
+  if ((rc = check_kv_like(dv, dv_st, s))) return rc;
+  a.split_kt = split_kt;
+  a.cnt = cnt;
+  a.part = part;
+  if (dqs != nullptr && dqs->split > 0) {
+    a.dq_split = dqs->split;
+    a.dq_bm = dqs->bm;
+    a.dq_nblocks = dqs->nblocks;
+    a.dq_part = dq_part;
+    a.dq = static_cast<f16 *>(dq);
+    a.dq_sb = dq_st[0];
+    a.dq_ss = dq_st[1];
+    a.dq_sh = dq_st[2];
+  }
+  a.dk = static_cast<f16 *>(dk);
+  a.dv = static_cast<f16 *>(dv);
+  a.dk_sb = dk_st[0];
+  a.dk_ss = dk_st[1];
+  a.dk_sh = dk_st[2];
+  a.dv_sb = dv_st[0];
+  a.dv_ss = dv_st[1];
+  a.dv_sh = dv_st[2];
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  FA_DISPATCH(launch_dkdv, s, causal, a, st);
+}
+
+// dQ; with `o` given (the full backward), the kernel also computes delta
+// from O and dO and writes it to `delta` instead of reading it.
+int run_dq(const void *dout, const void *q, const void *k, const void *v, const float *lse,
+           const float *delta, void *dq, const Shape &s, const int64_t *do_st, const int64_t *q_st,
+           const int64_t *k_st, const int64_t *v_st, const int64_t *dq_st, float sm_scale,
+           int causal, void *stream, const void *o = nullptr, const int64_t *o_st = nullptr,
+           unsigned *cnt_zero = nullptr, int n_cnt_zero = 0, int dq_split = 0,
+           float *dq_part = nullptr) {
+  fa::BwdArgs a;
+  int rc = bwd_common(dout, q, k, v, lse, delta, s, do_st, q_st, k_st, v_st, sm_scale, &a);
+  if (rc) return rc;
+  if ((rc = check_q_like(dq, dq_st, s))) return rc;
+  if (o != nullptr) {
+    if ((rc = check_q_like(o, o_st, s))) return rc;
+    a.o = desc(o, o_st);
+    a.delta_out = const_cast<float *>(delta);
+  }
+  a.cnt_zero = cnt_zero;
+  a.n_cnt_zero = n_cnt_zero;
+  a.dq_split = dq_split;
+  a.dq_part = dq_part;
+  a.dq = static_cast<f16 *>(dq);
+  a.dq_sb = dq_st[0];
+  a.dq_ss = dq_st[1];
+  a.dq_sh = dq_st[2];
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  FA_DISPATCH(launch_dq, s, causal, a, st);
+}
+
+size_t delta_bytes(int B, int Sq, int H) {
+  const size_t n = (size_t)B * (size_t)H * (size_t)Sq * sizeof(float);
+  return (n + 255) & ~(size_t)255;
+}
+
 
 int run_bwd(const void *dout, const void *q, const void *k, const void *v, const void *o,
             const float *lse, void *dq, void *dk, void *dv, void *workspace,
@@ -609,24 +684,33 @@ int run_bwd(const void *dout, const void *q, const void *k, const void *v, const
     return rc;
   // The key-block split runs when the workspace has room for it (see
   // fa_bwd_gqa_workspace_bytes): counters, then the fp32 partials.
+  // Layout: delta, then the dK/dV split's counters and partials, then the
+  // dQ split's partials -- both splits or neither, by workspace size.
   DkdvSplit plan = dkdv_split_plan(s, causal);
+  DqSplit qplan = dq_split_plan(s, causal);
   const size_t dbytes = delta_bytes(s.B, s.Sq, s.H);
-  if (plan.split_kt > 0 && workspace_bytes < dbytes + split_bytes(plan)) plan = DkdvSplit{};
+  if (workspace_bytes < dbytes + split_bytes(plan) + dq_split_bytes(qplan)) {
+    plan = DkdvSplit{};
+    qplan = DqSplit{};
+  }
+  char *ws = static_cast<char *>(workspace);
   unsigned *cnt = nullptr;
   float *part = nullptr;
   if (plan.split_kt > 0) {
-    cnt = reinterpret_cast<unsigned *>(static_cast<char *>(workspace) + dbytes);
-    part = reinterpret_cast<float *>(static_cast<char *>(workspace) + dbytes +
-                                     split_cnt_bytes(plan));
+    cnt = reinterpret_cast<unsigned *>(ws + dbytes);
+    part = reinterpret_cast<float *>(ws + dbytes + split_cnt_bytes(plan));
   }
+  float *dq_part =
+      qplan.split > 0 ? reinterpret_cast<float *>(ws + dbytes + split_bytes(plan)) : nullptr;
   // dQ first: it computes delta (the pre-pass, folded in) for the dK/dV
-  // kernel, which runs after it on the same stream, and zeroes the split
-  // counters.
+  // kernel, which runs after it on the same stream, zeroes the key-block
+  // split's counters and leaves its split query blocks' halves for the
+  // dK/dV kernel to add.
   if ((rc = run_dq(dout, q, k, v, lse, delta, dq, s, do_st, q_st, k_st, v_st, dq_st, sm_scale,
-                   causal, stream, o, o_st, cnt, (int)plan.slots)))
+                   causal, stream, o, o_st, cnt, (int)plan.slots, qplan.split, dq_part)))
     return rc;
   return run_dkdv(dout, q, k, v, lse, delta, dk, dv, s, do_st, q_st, k_st, v_st, dk_st, dv_st,
-                  sm_scale, causal, stream, plan.split_kt, cnt, part);
+                  sm_scale, causal, stream, plan.split_kt, cnt, part, &qplan, dq_part, dq, dq_st);
 }
 
 Shape square(int B, int S, int H, int D) { return Shape{B, S, S, H, H, D, FA_DTYPE_F16}; }
@@ -913,7 +997,8 @@ size_t fa_bwd_workspace_bytes(int B, int S, int H, int D) {
 size_t fa_bwd_gqa_workspace_bytes(int B, int Sq, int Sk, int H, int Hk, int D, int causal) {
   const Shape s{B, Sq, Sk, H, Hk, D, FA_DTYPE_F16};
   if (check_shape(s) != FA_OK) return 0;
-  return delta_bytes(B, Sq, H) + split_bytes(dkdv_split_plan(s, causal));
+  return delta_bytes(B, Sq, H) + split_bytes(dkdv_split_plan(s, causal)) +
+         dq_split_bytes(dq_split_plan(s, causal));
 }
 
 int fa_bwd(const void *dout, const void *q, const void *k, const void *v,

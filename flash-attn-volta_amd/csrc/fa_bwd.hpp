@@ -81,6 +81,15 @@ struct BwdArgs {
   // (the split counters of the dK/dV launch that follows on the stream)
   unsigned *cnt_zero;
   int n_cnt_zero;
+  // Causal query-block split of the dQ kernel: the last dq_split query
+  // blocks (dq_bm rows each, dq_nblocks per (b, h)) are each swept by two
+  // workgroups, one per half of the block's key tiles, which write their
+  // fp32 dQ rows (already scaled) to dq_part[slot][segment] (row-major
+  // dq_bm x D; slot = bh * dq_split + block - (dq_nblocks - dq_split)).
+  // The dK/dV kernel that follows on the stream adds the two halves and
+  // writes dq (the kernel boundary orders the accesses).  0: no split.
+  int dq_split, dq_bm, dq_nblocks;
+  float *dq_part;
 };
 
 struct PreArgs {
@@ -162,6 +171,51 @@ __device__ __forceinline__ void store_row(f16 *dst, const floatx16 (&acc)[D / 32
       for (int j = 0; j < 4; ++j) v4[j] = (E)(acc[d][4 * r + j] * mul);
       *(vec4<E> *)(dst + 32 * d + c_row(4 * r, g)) = v4;
     }
+  }
+}
+
+// The same rows as store_row, as fp32 (split partials).
+template <int D>
+__device__ __forceinline__ void store_row_f32(float *dst, const floatx16 (&acc)[D / 32], float mul,
+                                              int g) {
+#pragma unroll
+  for (int d = 0; d < D / 32; ++d) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      floatx4 v4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v4[j] = acc[d][4 * r + j] * mul;
+      *(floatx4 *)(dst + 32 * d + c_row(4 * r, g)) = v4;
+    }
+  }
+}
+
+// dQ rows of split query blocks (BwdArgs::dq_split): dq = part[.][0] +
+// part[.][1] (fp32 addition commutes, so the sum does not depend on which
+// half is which), converted to E.  Every workgroup of the calling grid
+// takes an equal share of the 4-element groups, `nt` threads each.
+template <typename E, int D>
+__device__ __forceinline__ void dq_split_combine(const BwdArgs &a, int nt) {
+  const int64_t per_slot = (int64_t)a.dq_bm * (D / 4);
+  const int64_t total = (int64_t)a.B * a.H * a.dq_split * per_slot;
+  const int64_t grid = gridDim.x;
+  const int64_t lo = total * blockIdx.x / grid, hi = total * (blockIdx.x + 1) / grid;
+  for (int64_t gi = lo + threadIdx.x; gi < hi; gi += nt) {
+    const int64_t slot = gi / per_slot;
+    const int rem = (int)(gi - slot * per_slot);
+    const int r = rem / (D / 4), c4 = rem % (D / 4);
+    const int bh = (int)(slot / a.dq_split);
+    const int qt = a.dq_nblocks - a.dq_split + (int)(slot - (int64_t)bh * a.dq_split);
+    const int q = qt * a.dq_bm + r;
+    if (q >= a.Sq) continue;
+    const float *p0 = a.dq_part + (slot * 2 * a.dq_bm + r) * D + 4 * c4;
+    const floatx4 x = *(const floatx4 *)p0;
+    const floatx4 y = *(const floatx4 *)(p0 + (int64_t)a.dq_bm * D);
+    vec4<E> v;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = (E)(x[j] + y[j]);
+    const int b = bh / a.H, h = bh % a.H;
+    *(vec4<E> *)(a.dq + b * a.dq_sb + h * a.dq_sh + (int64_t)q * a.dq_ss + 4 * c4) = v;
   }
 }
 
@@ -332,6 +386,9 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   __shared__ __attribute__((aligned(16))) f16 s_k[T::LDS_KV], s_v[T::LDS_KV];
   auto q_st = [&](auto stc) -> f16 * { return decltype(stc)::value ? s_q1 : s_q0; };
   auto do_st = [&](auto stc) -> f16 * { return decltype(stc)::value ? s_do1 : s_do0; };
+
+  // first the dQ rows of the preceding dQ launch's split query blocks
+  if (CAUSAL && a.dq_split > 0) dq_split_combine<E, D>(a, T::NT);
 
   const int Sq = a.Sq, Sk = a.Sk, off = a.off;
   const int BHk = a.B * a.Hk;
@@ -722,11 +779,19 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
     for (int i = threadIdx.x; i < a.n_cnt_zero; i += 256) a.cnt_zero[i] = 0u;
   }
   const int bh = bid % BH;
-  // Causal: late query blocks see the most keys; zigzag heavy/light.
+  const int rank = bid / BH;
   // Causal: late query blocks are the heavy ones; order chosen by the
-  // launcher as in the forward kernel.
-  const int qt = CAUSAL ? a.n_blocks - 1 - (a.zigzag ? zigzag_rank(bid / BH, a.n_blocks) : bid / BH)
-                        : bid / BH;
+  // launcher as in the forward kernel.  With the query-block split, ranks
+  // 2j and 2j + 1 are the two halves of the j-th heaviest block, then the
+  // unsplit blocks follow, heaviest first.
+  const int nsplit = CAUSAL ? a.dq_split : 0;
+  const bool split = rank < 2 * nsplit;
+  const int seg = split ? (rank & 1) : 0;
+  const int qt = !CAUSAL ? rank
+                 : a.n_blocks - 1 -
+                       (split ? (rank >> 1)
+                              : (nsplit > 0 ? rank - nsplit
+                                            : (a.zigzag ? zigzag_rank(rank, a.n_blocks) : rank)));
   const int b = bh / a.H, h = bh % a.H;
   const int hk = h / a.grp;
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
@@ -748,6 +813,10 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
   if (CAUSAL) kv_end = min(Sk, q0 + BM + off);
   // 0 when every query of the block precedes every key (causal, Sq > Sk)
   const int n_tiles = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
+  // key tiles [t_lo, t_hi) of this workgroup: a split block's segment 0
+  // takes the first half, segment 1 the rest
+  const int t_lo = seg ? n_tiles / 2 : 0;
+  const int t_hi = (split && seg == 0) ? n_tiles / 2 : n_tiles;
   const float c = a.c;
 
   // K and V tiles go straight to LDS (fa_common.hpp DmaStager).
@@ -758,11 +827,11 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
     stk.load(k_st(stc), kb, a.k.ss, n0, Sk, w);
     stv.load(v_st(stc), vb, a.v.ss, n0, Sk, w);
   };
-  // the loop loads tile t + 1 during tile t: cursors from row BN, advanced
-  // by a tile per load
+  // the loop loads tile t + 1 during tile t: cursors from tile t_lo + 1,
+  // advanced by a tile per load
   RowCursor ck, cv;
-  ck.init(kb, a.k.ss, BN, Sk, D, BN);
-  cv.init(vb, a.v.ss, BN, Sk, D, BN);
+  ck.init(kb, a.k.ss, (t_lo + 1) * BN, Sk, D, BN);
+  cv.init(vb, a.v.ss, (t_lo + 1) * BN, Sk, D, BN);
   auto load_next = [&](auto stc) {
     stk.load(k_st(stc), ck.rsrc(), w);
     stv.load(v_st(stc), cv.rsrc(), w);
@@ -771,7 +840,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
   };
 
   // the first key tile's DMA overlaps the row loads and the work below
-  if (n_tiles > 0) load_tile(0, std::integral_constant<int, 0>{});
+  if (t_hi > t_lo) load_tile(t_lo * BN, std::integral_constant<int, 0>{});
 
   if (a.neg) {
 #pragma unroll
@@ -792,7 +861,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
       for (int j = 0; j < 8; ++j) acc = __builtin_fmaf((float)of[c][j], (float)gf[c][j], acc);
     acc += xor32(acc);
     dl = qrow < Sq ? acc : 0.0f;
-    if (qrow < Sq && g == 0 && kh == 0) a.delta_out[(int64_t)bh * Sq + qrow] = dl;
+    if (qrow < Sq && g == 0 && kh == 0 && seg == 0) a.delta_out[(int64_t)bh * Sq + qrow] = dl;
   } else {
     dl = qrow < Sq ? a.delta[(int64_t)bh * Sq + qc] : 0.0f;
   }
@@ -852,7 +921,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
   auto tile_step = [&](auto stc, int t) {
     constexpr int st = decltype(stc)::value;
     const int n0 = t * BN;
-    const bool more = t + 1 < n_tiles;
+    const bool more = t + 1 < t_hi;
     if (more) load_next(std::integral_constant<int, st ^ 1>{});   // tile t + 1
 
     // 32-key sub-block sb of this wave: keys n0 + 32 * (NSUB*kh + sb)
@@ -918,9 +987,9 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
     __syncthreads();
   };
 
-  for (int t = 0; t < n_tiles; t += 2) {
+  for (int t = t_lo; t < t_hi; t += 2) {
     tile_step(std::integral_constant<int, 0>{}, t);
-    if (t + 1 < n_tiles) tile_step(std::integral_constant<int, 1>{}, t + 1);
+    if (t + 1 < t_hi) tile_step(std::integral_constant<int, 1>{}, t + 1);
   }
 
   const float dq_mul = a.sm_scale / gmul;
@@ -929,6 +998,12 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
     // both key halves of a query carry the same scale
     merge_pair<D>(reinterpret_cast<float *>(qg ? s_k1 : s_k0), kh == 1, dq, DsScale{}, lane);
     if (kh == 1) return;
+  }
+  if (split) {
+    // this segment's scaled fp32 rows; the dK/dV kernel adds the halves
+    const int slot = bh * nsplit + qt - (a.n_blocks - nsplit);
+    store_row_f32<D>(a.dq_part + ((int64_t)(slot * 2 + seg) * BM + (qrow - q0)) * D, dq, dq_mul, g);
+    return;
   }
   if (qrow < Sq)
     store_row<E, D>(a.dq + b * a.dq_sb + h * a.dq_sh + (int64_t)qrow * a.dq_ss, dq, dq_mul, g);

@@ -148,8 +148,10 @@ size_t fa_bwd_workspace_bytes(int B, int S, int H, int D);
  * fa_bwd_workspace_bytes minimum plus, for causal D = 64 / 128 problems
  * whose key blocks fit one round of resident workgroups, room for the
  * key-block split (the longest causal key blocks swept by two workgroups
- * each, fp32 partials added by whichever finishes second; at most
- * 64 MiB + 4 KiB).
+ * each, fp32 partials added by whichever finishes second) and, when the
+ * dQ grid is at most half a round, for the query-block split of the dQ
+ * kernel (its longest query blocks swept by two workgroups, fp32 halves
+ * added by the dK/dV kernel); at most 80 MiB + 4 KiB in all.
  * Any workspace of at least the minimum is valid: with less than this
  * size the backward runs unsplit.  Split and unsplit results differ in
  * rounding only; each is bit-reproducible.

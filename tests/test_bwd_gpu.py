@@ -273,7 +273,9 @@ def _bwd_capi(do, q, k, v, o, lse, causal, ws_bytes, fill):
 # Causal D = 64 / 128 problems whose key blocks fit one round of resident
 # workgroups: with the workspace fa_bwd_gqa_workspace_bytes sizes, the
 # longest key blocks are swept by two workgroups whose fp32 partials the
-# second to finish adds.
+# second to finish adds; likewise the dQ kernel's longest query blocks,
+# whose halves the dK/dV kernel adds (all cases but the second split dQ,
+# and the third and fifth have a ragged last query block among them).
 @pytest.mark.parametrize("B,Sq,Sk,H,Hk,D,dtype", [
     (1, 2048, 2048, 4, 4, 128, torch.float16),
     (1, 700, 1000, 8, 2, 128, torch.float16),     # grouped heads, offset 300, ragged split block
@@ -303,9 +305,8 @@ def test_backward_causal_key_block_split(B, Sq, Sk, H, Hk, D, dtype):
     report(f"bwd split {B},{Sq},{Sk},{H},{Hk}", **errs)
     for key, e in errs.items():
         assert e < tol, f"{key} max-abs {e:.3e} >= {tol}"
-    # the dQ kernel is the same either way; dK / dV differ by rounding only
-    assert torch.equal(split[0], unsplit[0])
-    for a, b in zip(split[1:], unsplit[1:]):
+    # split and unsplit differ by rounding only
+    for a, b in zip(split, unsplit):
         assert max_abs(a, b.float()) < tol / 4
     # bit-reproducible whatever the workspace held before
     for a, b in zip(split, again):

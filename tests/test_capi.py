@@ -98,7 +98,8 @@ def test_workspace_bytes(lib):
 
 def test_split_workspace_bytes(lib):
     """fa_bwd_gqa_workspace_bytes: the delta minimum, plus room for the
-    causal key-block split only for D = 64 / 128 causal grids of at most one
+    causal key-block (dK/dV) and query-block (dQ) splits only for D = 64 /
+    128 causal grids of at most one
     round of resident workgroups (one per CU at D = 128, three at D = 64;
     256 CUs here: without a GPU the count defaults to MI355X's) whose
     longest sweep has at least 32 query tiles."""
@@ -109,6 +110,16 @@ def test_split_workspace_bytes(lib):
     slots = 30 * 8
     assert lib.fa_bwd_gqa_workspace_bytes(1, 4096, 4096, 8, 8, 128, 1) == \
         mini + 1024 + slots * 2 * 2 * 128 * 128 * 4
+    # (1,4096,4,128): the same key-block split over 4 heads (120 slots, 480 B
+    # of counters rounded to 512), and the dQ grid (64-row blocks x 4 heads,
+    # half a round at two per CU) splits its last blocks with more than
+    # 64 / 3 = 21 key tiles (43 of 64): 2 x 64 x 128 fp32 each
+    assert lib.fa_bwd_gqa_workspace_bytes(1, 4096, 4096, 4, 4, 128, 1) == \
+        lib.fa_bwd_workspace_bytes(1, 4096, 4, 128) + 512 + 30 * 4 * 2 * 2 * 128 * 128 * 4 + \
+        43 * 4 * 2 * 64 * 128 * 4
+    # a full round whose block 0 sweeps only 32 tiles: unsplit
+    assert lib.fa_bwd_gqa_workspace_bytes(1, 2048, 2048, 16, 16, 128, 1) == \
+        lib.fa_bwd_workspace_bytes(1, 2048, 16, 128)
     assert lib.fa_bwd_gqa_workspace_bytes(1, 4096, 4096, 8, 8, 128, 0) == mini   # non-causal
     assert lib.fa_bwd_gqa_workspace_bytes(1, 4096, 4096, 16, 16, 64, 1) == \
         lib.fa_bwd_workspace_bytes(1, 4096, 16, 64)          # D = 64: 1024 blocks > 3 per CU
