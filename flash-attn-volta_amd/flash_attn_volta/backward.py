@@ -44,10 +44,10 @@ def flash_attn_backward(
     _require(q.dtype == torch.float16 == k.dtype == v.dtype == o.dtype == do.dtype, "fp16 only")
     _require(lse.dtype == torch.float32, "lse must be fp32")
     _require(q.shape == k.shape == v.shape == o.shape == do.shape, "shape mismatch")
-    _require(q.dim() == 4, f"expected (B, N, H, D) tensors, got {tuple(q.shape)}")
+    _require(q.dim() == 4, lambda: f"expected (B, N, H, D) tensors, got {tuple(q.shape)}")
     B, N, H, D = q.shape
-    _require(D in SUPPORTED_HEAD_DIMS, f"unsupported head_dim {D}")
-    _require(tuple(lse.shape) == (B, H, N), f"lse shape {tuple(lse.shape)} expected ({B},{H},{N})")
+    _require(D in SUPPORTED_HEAD_DIMS, lambda: f"unsupported head_dim {D}")
+    _require(tuple(lse.shape) == (B, H, N), lambda: f"lse shape {tuple(lse.shape)} expected ({B},{H},{N})")
     _require(lse.is_cuda and lse.device == q.device, "lse must be on the same device")
 
     if sm_scale is None:
@@ -133,8 +133,8 @@ def flash_attn_backward_gqa(
     _check_gqa(q, k, v)
     _require(q.shape == o.shape == do.shape, "q, o and do shapes differ")
     B, N, H, D = q.shape
-    _require(D in SUPPORTED_HEAD_DIMS, f"unsupported head_dim {D}")
-    _require(tuple(lse.shape) == (B, H, N), f"lse shape {tuple(lse.shape)} expected ({B},{H},{N})")
+    _require(D in SUPPORTED_HEAD_DIMS, lambda: f"unsupported head_dim {D}")
+    _require(tuple(lse.shape) == (B, H, N), lambda: f"lse shape {tuple(lse.shape)} expected ({B},{H},{N})")
     _require(lse.is_cuda and lse.device == q.device, "lse must be on the same device")
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(D)
@@ -148,7 +148,7 @@ def bwd_preprocess(o: torch.Tensor, do: torch.Tensor) -> torch.Tensor:
     _require(o.shape == do.shape and o.dim() == 4, "shape mismatch")
     _require(o.dtype == torch.float16 == do.dtype, "fp16 only")
     B, N, H, D = o.shape
-    _require(D in NATIVE_HEAD_DIMS, f"unsupported head_dim {D}")
+    _require(D in NATIVE_HEAD_DIMS, lambda: f"unsupported head_dim {D}")
     o, do = _kernel_ready(o), _kernel_ready(do)
     delta = torch.empty((B, H, N), dtype=torch.float32, device=o.device)
     with _on_device(o.device):

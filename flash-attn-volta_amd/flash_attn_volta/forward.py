@@ -29,9 +29,13 @@ class FlashAttnArgumentError(AssertionError, ValueError):
     ValueError."""
 
 
-def _require(cond: bool, msg: str) -> None:
+def _require(cond: bool, msg) -> None:
+    """Raise FlashAttnArgumentError(msg) unless `cond`.  `msg` is a string,
+    or a callable returning one: messages that format tensor shapes are
+    passed as lambdas so that a passing check costs no string formatting
+    (a few microseconds per call on the launch path)."""
     if not cond:
-        raise FlashAttnArgumentError(msg)
+        raise FlashAttnArgumentError(msg() if callable(msg) else msg)
 
 
 def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
@@ -123,11 +127,11 @@ def flash_attn_forward(
     """
     _require(q.is_cuda and k.is_cuda and v.is_cuda, "tensors must be on CUDA")
     _require(q.dtype == torch.float16 == k.dtype == v.dtype, "fp16 only")
-    _require(q.shape == k.shape == v.shape, f"qkv shape mismatch {q.shape} {k.shape} {v.shape}")
-    _require(q.dim() == 4, f"expected (B, N, H, D) tensors, got {tuple(q.shape)}")
+    _require(q.shape == k.shape == v.shape, lambda: f"qkv shape mismatch {q.shape} {k.shape} {v.shape}")
+    _require(q.dim() == 4, lambda: f"expected (B, N, H, D) tensors, got {tuple(q.shape)}")
     _require(q.device == k.device == v.device, "q, k, v must be on one device")
     B, N, H, D = q.shape
-    _require(D in SUPPORTED_HEAD_DIMS, f"unsupported head_dim {D} (allowed: 16,32,64,128)")
+    _require(D in SUPPORTED_HEAD_DIMS, lambda: f"unsupported head_dim {D} (allowed: 16,32,64,128)")
 
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(D)
@@ -212,9 +216,9 @@ def _check_gqa(q, k, v):
     k and v (B, Sk, Hk, D) with H a multiple of Hk."""
     _require(q.dim() == 4 and k.dim() == 4 and v.dim() == 4,
              f"expected 4-D (B, N, H, D) tensors, got {tuple(q.shape)} {tuple(k.shape)} {tuple(v.shape)}")
-    _require(k.shape == v.shape, f"k and v shapes differ: {tuple(k.shape)} {tuple(v.shape)}")
-    _require(q.shape[0] == k.shape[0], f"batch mismatch {q.shape[0]} vs {k.shape[0]}")
-    _require(q.shape[3] == k.shape[3], f"head_dim mismatch {q.shape[3]} vs {k.shape[3]}")
+    _require(k.shape == v.shape, lambda: f"k and v shapes differ: {tuple(k.shape)} {tuple(v.shape)}")
+    _require(q.shape[0] == k.shape[0], lambda: f"batch mismatch {q.shape[0]} vs {k.shape[0]}")
+    _require(q.shape[3] == k.shape[3], lambda: f"head_dim mismatch {q.shape[3]} vs {k.shape[3]}")
     H, Hk = q.shape[2], k.shape[2]
     _require(Hk > 0 and H % Hk == 0,
              f"query heads ({H}) must be a multiple of key/value heads ({Hk})")
@@ -249,7 +253,7 @@ def flash_attn_forward_gqa(
     _require(q.device == k.device == v.device, "q, k, v must be on one device")
     _check_gqa(q, k, v)
     D = q.shape[3]
-    _require(D in SUPPORTED_HEAD_DIMS, f"unsupported head_dim {D} (allowed: 16,32,64,128)")
+    _require(D in SUPPORTED_HEAD_DIMS, lambda: f"unsupported head_dim {D} (allowed: 16,32,64,128)")
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(D)
     return _forward(q, k, v, causal, sm_scale, return_softmax_lse, gqa=True)

@@ -39,12 +39,12 @@ __all__ = ["apply_rotary_qk", "rope_qk_forward", "rope_qk_backward", "ROPE_HEAD_
 def _table(t: torch.Tensor, name: str, B: int, S: int, D: int, dtype, device) -> torch.Tensor:
     """cos / sin as a (1 or B, S, D) tensor the kernel can read: unit D
     stride, 16-byte aligned, other strides multiples of 8 elements."""
-    _require(isinstance(t, torch.Tensor), f"{name} must be a tensor")
+    _require(isinstance(t, torch.Tensor), lambda: f"{name} must be a tensor")
     if t.dim() == 2:
         t = t.unsqueeze(0)
     _require(t.dim() == 3 and t.shape[1:] == (S, D) and t.shape[0] in (1, B),
              f"{name} must be (B or 1, S, D) = (.., {S}, {D}), got {tuple(t.shape)}")
-    _require(t.device == device, f"{name} must be on {device}")
+    _require(t.device == device, lambda: f"{name} must be on {device}")
     if t.dtype != dtype:
         t = t.to(dtype)
     ok = t.stride(2) == 1 and t.data_ptr() % 16 == 0 and \
@@ -62,7 +62,7 @@ def _weight(w, name: str, D: int, dtype, device):
         return None
     _require(isinstance(w, torch.Tensor) and w.shape == (D,),
              f"{name} must be a ({D},) tensor, got {getattr(w, 'shape', type(w))}")
-    _require(w.device == device, f"{name} must be on {device}")
+    _require(w.device == device, lambda: f"{name} must be on {device}")
     w = w.detach()
     if w.dtype != dtype:
         w = w.to(dtype)
@@ -101,7 +101,7 @@ def rope_qk_forward(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: to
     k_out = torch.empty((B, S, Hk, D), dtype=q.dtype, device=q.device)
     if q_out.numel() == 0 and k_out.numel() == 0:
         return q_out, k_out
-    _require(H > 0 and Hk > 0, f"head counts must be positive, got {H}, {Hk}")
+    _require(H > 0 and Hk > 0, lambda: f"head counts must be positive, got {H}, {Hk}")
     q, k = _kernel_ready(q), _kernel_ready(k)
     lib = _capi.load()
     with _on_device(q.device):
