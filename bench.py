@@ -243,8 +243,10 @@ def cpu_time(fn, max_seconds):
 
 def run_configs(steps, warmup, with_cpu):
     """Every BASELINE config: GPU forward and fwd+bwd (autograd) on the HIP
-    kernels, and the CPU baseline (fp32 eager path, all host threads) for the
-    same inputs.  One JSON line per config, then a markdown table."""
+    kernels, the same fwd+bwd step replayed from a HIP graph (no host work
+    per step: what small, host-bound configs reach on the GPU), and the CPU
+    baseline (fp32 eager path, all host threads) for the same inputs.  One
+    JSON line per config, then a markdown table."""
     import torch
     from flash_attn_volta import flash_attn, flash_attn_forward
     from oracle.attention import attention_ref_fp32
@@ -266,13 +268,31 @@ def run_configs(steps, warmup, with_cpu):
             qg.grad = kg.grad = vg.grad = None
             flash_attn(qg, kg, vg, causal=causal, sm_scale=sc).backward(do)
         t_fb = time_loop(gpu_fb, steps, warmup)[1] if with_bwd else None
+        # the same step captured once into a HIP graph and replayed: no
+        # Python / autograd work on the host per step
+        t_fbg = None
+        if with_bwd:
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                gpu_fb()
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            qg.grad = kg.grad = vg.grad = None
+            with torch.cuda.graph(graph):
+                flash_attn(qg, kg, vg, causal=causal, sm_scale=sc).backward(do)
+            t_fbg = time_loop(graph.replay, steps, warmup)[1]
+            del graph
         row = {"config": name, "shape": [b, s, h, d], "causal": causal,
                "gpu_fwd_us": round(t_f * 1e6, 2), "gpu_fwd_tflops": round(flops / t_f / 1e12, 2),
                "gpu_fwd_pct_peak": round(100 * flops / t_f / 1e12 / PEAK_FP16_TFLOPS, 2)}
         if with_bwd:
             row.update({"gpu_fwd_bwd_us": round(t_fb * 1e6, 2),
                         "gpu_fwd_bwd_tflops": round(5 * flops / t_fb / 1e12, 2),
-                        "gpu_fwd_bwd_pct_peak": round(100 * 5 * flops / t_fb / 1e12 / PEAK_FP16_TFLOPS, 2)})
+                        "gpu_fwd_bwd_pct_peak": round(100 * 5 * flops / t_fb / 1e12 / PEAK_FP16_TFLOPS, 2),
+                        "gpu_fwd_bwd_graph_us": round(t_fbg * 1e6, 2),
+                        "gpu_fwd_bwd_graph_tflops": round(5 * flops / t_fbg / 1e12, 2)})
         if with_cpu:
             with torch.no_grad():
                 t_cf, n_f = cpu_time(lambda: attention_ref_fp32(qc, kc, vc, causal=causal, sm_scale=sc), 10.0)
@@ -288,12 +308,14 @@ def run_configs(steps, warmup, with_cpu):
         rows.append(row)
         print(json.dumps(row), flush=True)
     hdr = ("| config | shape | GPU fwd us | GPU fwd TFLOP/s (% peak) | GPU fwd+bwd us | "
-           "GPU fwd+bwd TFLOP/s (% peak) | CPU fwd TFLOP/s | CPU fwd+bwd TFLOP/s |")
+           "GPU fwd+bwd TFLOP/s (% peak) | fwd+bwd graph replay us (TFLOP/s) | CPU fwd TFLOP/s | "
+           "CPU fwd+bwd TFLOP/s |")
     print(hdr)
-    print("|---|---|---:|---:|---:|---:|---:|---:|")
+    print("|---|---|---:|---:|---:|---:|---:|---:|---:|")
     for r in rows:
-        fb = (f"{r['gpu_fwd_bwd_us']} | {r['gpu_fwd_bwd_tflops']} ({r['gpu_fwd_bwd_pct_peak']} %)"
-              if "gpu_fwd_bwd_us" in r else "n/a | n/a")
+        fb = (f"{r['gpu_fwd_bwd_us']} | {r['gpu_fwd_bwd_tflops']} ({r['gpu_fwd_bwd_pct_peak']} %) | "
+              f"{r['gpu_fwd_bwd_graph_us']} ({r['gpu_fwd_bwd_graph_tflops']})"
+              if "gpu_fwd_bwd_us" in r else "n/a | n/a | n/a")
         print(f"| {r['config']} | {tuple(r['shape'])}{' causal' if r['causal'] else ''} | "
               f"{r['gpu_fwd_us']} | {r['gpu_fwd_tflops']} ({r['gpu_fwd_pct_peak']} %) | {fb} | "
               f"{r.get('cpu_fwd_tflops', '-')} | {r.get('cpu_fwd_bwd_tflops', '-')} |")
