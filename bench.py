@@ -597,6 +597,21 @@ def main():
     log(f"[bench] fwd+bwd {ev_fb * 1e3:.3f} ms/step (events), {wall_fb * 1e3:.3f} ms (wall)")
     wall_f, ev_f = time_loop(fwd, args.steps, args.warmup)
     log(f"[bench] fwd {ev_f * 1e3:.3f} ms/step (events), {wall_f * 1e3:.3f} ms (wall)")
+    # the same step captured once into a HIP graph and replayed (reported
+    # beside `value`, which stays the eager autograd step)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fwd_bwd()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    qg.grad = kg.grad = vg.grad = None
+    with torch.cuda.graph(graph):
+        flash_attn(qg, kg, vg, causal=CAUSAL).backward(do)
+    wall_g, ev_g = time_loop(graph.replay, args.steps, args.warmup)
+    del graph
+    log(f"[bench] fwd+bwd graph replay {ev_g * 1e3:.3f} ms/step (events), {wall_g * 1e3:.3f} ms (wall)")
     kt = kernel_times(q, k, v, do, args.steps, args.warmup)
     for name, r in kt.items():
         log(f"[bench] kernel {name:15s} {r['avg_us']:9.2f} us  {r['tflops']:8.1f} TFLOP/s  {r['gbs']:8.1f} GB/s")
@@ -653,6 +668,9 @@ def main():
                 "causal_useful_tflops": round(causal_useful_fwd_flops(B, S, H, D) / t_fwd / 1e12, 3)},
         "baseline": {"fwd_bwd": REF_FWD_BWD_TFLOPS, "fwd": REF_FWD_TFLOPS,
                      "hardware": "V100-SXM2-32GB (reference's published numbers)"},
+        "fwd_bwd_graph_replay": {"value": round(5.0 * flops_f / max(wall_g, ev_g) / 1e12, 3),
+                                 "unit": "TFLOP/s", "ms": round(max(wall_g, ev_g) * 1e3, 4),
+                                 "note": "same step captured once into a HIP graph and replayed"},
         "roofline": roofline,
         "kernels": all_kernels,
         "step_launches": ["fa_fwd_kernel", "fa_bwd_dq_kernel (also computes delta)",
