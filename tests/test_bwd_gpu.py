@@ -282,6 +282,8 @@ def _bwd_capi(do, q, k, v, o, lse, causal, ws_bytes, fill):
     (1, 2100, 2100, 2, 2, 128, torch.bfloat16),   # ragged last key block (unsplit)
     (1, 2048, 2048, 16, 16, 64, torch.float16),
     (1, 1500, 2048, 16, 4, 64, torch.bfloat16),   # grouped heads, offset 548
+    (2, 2048, 2048, 2, 2, 128, torch.float16),     # batch 2: slots and dQ rows per (b, h)
+    (2, 2048, 2048, 4, 2, 64, torch.float16),      # batch 2, grouped heads
 ])
 def test_backward_causal_key_block_split(B, Sq, Sk, H, Hk, D, dtype):
     from flash_attn_volta import _capi, flash_attn_forward_gqa
