@@ -67,7 +67,7 @@ struct BwdArgs {
   float c;              // |sm_scale| * log2(e), clamped away from 0
   float sm_scale;       // signed scale applied to dQ and dK
   int neg;              // 1 when sm_scale < 0 (K or Q negated in S recompute)
-  int zigzag;           // dQ causal block order: 1 zigzag heavy / light, 0 heaviest first
+  int zigzag;           // causal block order: 1 zigzag heavy / light, 0 heaviest first
   // Causal key-block split (dK/dV layouts with KEY_SPLIT): key blocks
   // [0, split_kt) of every (b, key/value head) are each swept by two
   // workgroups, one per half of their query tiles.  Each writes its fp32
@@ -395,16 +395,19 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   const int bid = blockIdx.x;
   const int bhk = bid % BHk;
   const int rank = bid / BHk;
-  // Causal: low key blocks see the most queries, and blocks go heaviest
-  // first: each slot that frees up takes the heaviest block left
-  // (measured against a zigzag heavy / light order: -5 to -19 % on causal
-  // grids of every size, +-0 at (1,4096,16,64)).  With the key-block
+  // Causal: low key blocks see the most queries.  Blocks go heaviest
+  // first (each slot that frees up takes the heaviest block left), or
+  // zigzag heavy / light where the launcher measured that better (long
+  // sweeps on grids of at most 1.5 rounds: a.zigzag).  With the key-block
   // split, ranks 2kt and 2kt + 1 are the two halves of block kt < split_kt,
-  // then the unsplit blocks follow.
+  // then the unsplit blocks follow, heaviest first.
   const int nsplit = (T::KEY_SPLIT && CAUSAL) ? a.split_kt : 0;
   const bool split = rank < 2 * nsplit;
   const int seg = split ? (rank & 1) : 0;
-  const int kt = split ? (rank >> 1) : rank - nsplit;
+  const int kt = split ? (rank >> 1)
+                       : (nsplit > 0 ? rank - nsplit
+                                     : ((CAUSAL && a.zigzag) ? zigzag_rank(rank, a.n_blocks)
+                                                             : rank));
   const int b = bhk / a.Hk, hk = bhk % a.Hk;
   const int tid = threadIdx.x, lane = tid & 63, w = wave_id();
   const int kg = w / T::NQH;
