@@ -241,6 +241,49 @@ def cpu_time(fn, max_seconds):
     return statistics.median(ts), n
 
 
+def run_llama(steps, warmup):
+    """one training step (causal LM loss, fwd + bwd, no
+    optimizer) of a 16-layer Llama (hidden 2048, 16 heads x 128, SwiGLU
+    5632, vocab 32000, random N(0, 0.02) init, fp16) at B=1, S=4096 on
+    random token ids, with the attention routed to the HIP kernels by
+    patch_hf (with and without the fused QK-norm / rotary prologue) and,
+    for comparison, on PyTorch's own SDPA.  One JSON line per variant."""
+    import torch
+    from transformers import LlamaConfig, LlamaForCausalLM
+    from flash_attn_volta import patch_hf
+    cfg = LlamaConfig(vocab_size=32000, hidden_size=2048, intermediate_size=5632,
+                      num_hidden_layers=16, num_attention_heads=16, num_key_value_heads=16,
+                      rms_norm_eps=1e-6, rope_theta=10000.0, initializer_range=0.02,
+                      max_position_embeddings=4096, tie_word_embeddings=False)
+    torch.manual_seed(0)
+    with torch.device("cuda"):
+        model = LlamaForCausalLM(cfg).half().train()
+    gen = torch.Generator(device="cpu").manual_seed(5)
+    ids = torch.randint(0, 32000, (1, 4096), generator=gen).cuda()
+    n_params = sum(p.numel() for p in model.parameters())
+    # dense training FLOPs: 6 * params * tokens for the matmuls, plus the
+    # attention's 4*B*H*S^2*D per layer forward, x3 with the backward
+    # (dense-counted as everywhere here)
+    flops = 6.0 * n_params * 4096 + 3.0 * 16 * fwd_flops(1, 4096, 16, 128)
+
+    def step():
+        model.zero_grad(set_to_none=True)
+        model(input_ids=ids, labels=ids).loss.backward()
+
+    variants = [("patch_hf (fused rope)", lambda: patch_hf.patch_llama(model)),
+                ("patch_hf", lambda: patch_hf.patch_llama(model, fuse_rope=False)),
+                ("torch sdpa", lambda: 0)]
+    for name, apply in variants:
+        n = apply()
+        _, t = time_loop(step, steps, warmup)
+        row = {"config": "C5 Llama training step", "attention": name, "patched_layers": n,
+               "ms_per_step": round(t * 1e3, 2), "tokens_per_s": round(4096 / t, 1),
+               "model_tflops": round(flops / t / 1e12, 1), "params": n_params}
+        print(json.dumps(row), flush=True)
+        if n:
+            patch_hf.unpatch_llama(model)
+
+
 def run_configs(steps, warmup, with_cpu):
     """Every BASELINE config: GPU forward and fwd+bwd (autograd) on the HIP
     kernels, the same fwd+bwd step replayed from a HIP graph (no host work
@@ -542,6 +585,9 @@ def main():
     ap.add_argument("--decode", action="store_true",
                     help="instead of the benchmark line, time decode-step attention "
                          "(split-KV against the unsplit kernel) and print a table")
+    ap.add_argument("--llama", action="store_true",
+                    help="config 5: one 16-layer Llama training step (fwd+bwd of the LM loss), "
+                         "attention routed by patch_hf vs PyTorch's SDPA")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="instead of the benchmark, run 10 plain device copies of MIB MiB "
                          "(a kernel of known HBM traffic, to scale rocprofv3 FETCH_SIZE / "
@@ -573,6 +619,10 @@ def main():
     if args.decode:
         torch.cuda.set_device(0)
         run_decode(args.steps, args.warmup)
+        return
+    if args.llama:
+        torch.cuda.set_device(0)
+        run_llama(min(args.steps, 5), min(args.warmup, 2))
         return
     if args.rope:
         torch.cuda.set_device(0)
