@@ -119,20 +119,21 @@ bool row_split(int rows, int64_t heads, bool causal, int per_cu = 2) {
 // per CU, from the runtime's occupancy calculator; cached per kernel
 // instantiation (the template argument is the kernel itself: kernels of
 // one argument type share a function-pointer type) -- every device here is
-// the same gfx950 part.  0 when the runtime cannot tell.
+// the same gfx950 part.  0 when the runtime cannot tell (not cached: a
+// later call asks again).
 template <auto Kernel>
 int resident_per_cu(int threads) {
-  static std::atomic<int> cache{-1};
+  static std::atomic<int> cache{0};
   int n = cache.load(std::memory_order_relaxed);
-  if (n < 0) {
+  if (n <= 0) {
     int blocks = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, Kernel, threads, 0) != hipSuccess) {
-      blocks = 0;
       // the failed query's error must not look like a launch error
       (void)hipGetLastError();
+      return 0;
     }
     n = blocks > 0 ? blocks : 0;
-    cache.store(n, std::memory_order_relaxed);
+    if (n > 0) cache.store(n, std::memory_order_relaxed);
   }
   return n;
 }
