@@ -137,6 +137,32 @@ def kernel_times(q, k, v, do, steps, warmup):
         _, ev = time_loop(fn, steps, warmup)
         res[name] = {"kernel": sym, "avg_us": ev * 1e6, "flops": flops, "bytes": nbytes,
                      "tflops": flops / ev / 1e12, "gbs": nbytes / ev / 1e9}
+
+    # The same kernels in the training step's order (forward, dQ, dK/dV)
+    # with an event between consecutive launches, so each kernel is timed
+    # in the step's context (clock and cache state) rather than in a loop
+    # of its own.  The step's dQ launch also computes delta; here delta
+    # comes from the pre-pass above, otherwise the launches are the step's.
+    def fwd_lse():
+        _capi.check(lib.fa_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                               lse.data_ptr(), B, S, H, D, st["q"], st["k"], st["v"], st["o"],
+                               scale, int(CAUSAL), stream), "fa_fwd")
+    seq = (("fwd", fwd_lse), ("bwd_dq", dqk), ("bwd_dkdv", dkdv))
+    for _ in range(warmup):
+        for _, fn in seq:
+            fn()
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(seq) + 1)] for _ in range(steps)]
+    for i in range(steps):
+        ev[i][0].record()
+        for j, (_, fn) in enumerate(seq):
+            fn()
+            ev[i][j + 1].record()
+    torch.cuda.synchronize()
+    for j, (name, _) in enumerate(seq):
+        us = [ev[i][j].elapsed_time(ev[i][j + 1]) * 1e3 for i in range(steps)]
+        res[name]["avg_us_in_step"] = statistics.mean(us)
+        res[name]["median_us_in_step"] = statistics.median(us)
     return res
 
 
@@ -159,6 +185,32 @@ def profiled_traffic(kernel_sym):
             if sym == kernel_sym or (kernel_sym.endswith(" ") and sym.startswith(kernel_sym)):
                 return float(nbytes), os.path.relpath(path, ROOT), sym
     return None, None, kernel_sym
+
+
+def useful_fraction(s, causal):
+    """Share of the dense-counted FLOPs that a causal kernel actually has to
+    do: the score matrix's lower triangle with its diagonal, S(S+1)/2 of S^2
+    entries, for every GEMM of the forward and the backward alike."""
+    return (s + 1) / (2.0 * s) if causal else 1.0
+
+
+def profiled_counters(kernel_sym):
+    """Counter-derived figures for the kernel whose symbol starts with
+    `kernel_sym`, from the committed rocprofv3 PMC summaries
+    (profiles/*_counters.md, JSON block written by `bench.py --pmc-summary`).
+    Returns (dict, source) or (None, None)."""
+    import glob
+    import re
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*_counters.md"))):
+        text = open(path).read()
+        m = re.search(r"```json\s*(\{.*?\})\s*```", text, re.S)
+        if not m:
+            continue
+        table = json.loads(m.group(1)).get("kernels", {})
+        for sym, row in table.items():
+            if sym == kernel_sym or (kernel_sym.endswith(" ") and sym.startswith(kernel_sym)):
+                return row, os.path.relpath(path, ROOT)
+    return None, None
 
 
 def cpu_baseline(max_seconds=30.0):
@@ -284,6 +336,22 @@ def run_llama(steps, warmup):
             patch_hf.unpatch_llama(model)
 
 
+def peak_extra_bytes(step, grads):
+    """Peak allocator bytes above what is allocated before one fwd+bwd step
+    (inputs and dO), after a warm-up step -- the reference's measurement
+    (bench/backward.py:69-85): outputs, LSE, gradients and workspace."""
+    import torch
+    step()
+    for t in grads:
+        t.grad = None
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    step()
+    torch.cuda.synchronize()
+    return torch.cuda.max_memory_allocated() - base
+
+
 def run_configs(steps, warmup, with_cpu):
     """Every BASELINE config: GPU forward and fwd+bwd (autograd) on the HIP
     kernels, the same fwd+bwd step replayed from a HIP graph (no host work
@@ -327,6 +395,13 @@ def run_configs(steps, warmup, with_cpu):
                 flash_attn(qg, kg, vg, causal=causal, sm_scale=sc).backward(do)
             t_fbg = time_loop(graph.replay, steps, warmup)[1]
             del graph
+        mem = {}
+        if with_bwd:
+            from flash_attn_volta import backward as fa_backward
+            for split in (True, False):
+                fa_backward.split_workspace = split
+                mem[split] = peak_extra_bytes(gpu_fb, (qg, kg, vg))
+            fa_backward.split_workspace = True
         row = {"config": name, "shape": [b, s, h, d], "causal": causal,
                "gpu_fwd_us": round(t_f * 1e6, 2), "gpu_fwd_tflops": round(flops / t_f / 1e12, 2),
                "gpu_fwd_pct_peak": round(100 * flops / t_f / 1e12 / PEAK_FP16_TFLOPS, 2)}
@@ -335,7 +410,9 @@ def run_configs(steps, warmup, with_cpu):
                         "gpu_fwd_bwd_tflops": round(5 * flops / t_fb / 1e12, 2),
                         "gpu_fwd_bwd_pct_peak": round(100 * 5 * flops / t_fb / 1e12 / PEAK_FP16_TFLOPS, 2),
                         "gpu_fwd_bwd_graph_us": round(t_fbg * 1e6, 2),
-                        "gpu_fwd_bwd_graph_tflops": round(5 * flops / t_fbg / 1e12, 2)})
+                        "gpu_fwd_bwd_graph_tflops": round(5 * flops / t_fbg / 1e12, 2),
+                        "peak_extra_mb": round(mem[True] / 1e6, 2),
+                        "peak_extra_mb_no_split": round(mem[False] / 1e6, 2)})
         if with_cpu:
             with torch.no_grad():
                 t_cf, n_f = cpu_time(lambda: attention_ref_fp32(qc, kc, vc, causal=causal, sm_scale=sc), 10.0)
@@ -351,14 +428,15 @@ def run_configs(steps, warmup, with_cpu):
         rows.append(row)
         print(json.dumps(row), flush=True)
     hdr = ("| config | shape | GPU fwd us | GPU fwd TFLOP/s (% peak) | GPU fwd+bwd us | "
-           "GPU fwd+bwd TFLOP/s (% peak) | fwd+bwd graph replay us (TFLOP/s) | CPU fwd TFLOP/s | "
-           "CPU fwd+bwd TFLOP/s |")
+           "GPU fwd+bwd TFLOP/s (% peak) | fwd+bwd graph replay us (TFLOP/s) | peak extra MB "
+           "(no split) | CPU fwd TFLOP/s | CPU fwd+bwd TFLOP/s |")
     print(hdr)
-    print("|---|---|---:|---:|---:|---:|---:|---:|---:|")
+    print("|---|---|---:|---:|---:|---:|---:|---:|---:|---:|")
     for r in rows:
         fb = (f"{r['gpu_fwd_bwd_us']} | {r['gpu_fwd_bwd_tflops']} ({r['gpu_fwd_bwd_pct_peak']} %) | "
-              f"{r['gpu_fwd_bwd_graph_us']} ({r['gpu_fwd_bwd_graph_tflops']})"
-              if "gpu_fwd_bwd_us" in r else "n/a | n/a | n/a")
+              f"{r['gpu_fwd_bwd_graph_us']} ({r['gpu_fwd_bwd_graph_tflops']}) | "
+              f"{r['peak_extra_mb']} ({r['peak_extra_mb_no_split']})"
+              if "gpu_fwd_bwd_us" in r else "n/a | n/a | n/a | n/a")
         print(f"| {r['config']} | {tuple(r['shape'])}{' causal' if r['causal'] else ''} | "
               f"{r['gpu_fwd_us']} | {r['gpu_fwd_tflops']} ({r['gpu_fwd_pct_peak']} %) | {fb} | "
               f"{r.get('cpu_fwd_tflops', '-')} | {r.get('cpu_fwd_bwd_tflops', '-')} |")
@@ -569,6 +647,148 @@ def run_decode(steps, warmup):
               f"({100 * r['splitkv_frac_hbm']:.1f} %) | {r['speedup']}x |")
 
 
+def run_profile_config(name, steps, warmup):
+    """The training step's kernels for one BASELINE config, as the program
+    that rocprofv3 counter passes run: `warmup` + `steps` rounds of
+    flash_attn_forward (with LSE) and flash_attn_backward on the same
+    inputs as --configs, nothing else on the GPU in between."""
+    import torch
+    from flash_attn_volta import flash_attn_backward, flash_attn_forward
+    rows = [r for r in CONFIG_TABLE if r[0] == name]
+    if not rows:
+        raise SystemExit(f"unknown config {name!r}; one of {[r[0] for r in CONFIG_TABLE]}")
+    _, b, s, h, d, causal, sc, in_scale, _ = rows[0]
+    g = torch.Generator(device="cpu").manual_seed(0)
+    q, k, v = (((torch.randn((b, s, h, d), generator=g)).half() * in_scale).cuda() for _ in range(3))
+    do = torch.randn((b, s, h, d), generator=torch.Generator(device="cpu").manual_seed(1)).half().cuda()
+    for _ in range(warmup + steps):
+        o, lse = flash_attn_forward(q, k, v, causal=causal, sm_scale=sc, return_softmax_lse=True)
+        flash_attn_backward(do, q, k, v, o, lse, causal=causal, sm_scale=sc)
+    torch.cuda.synchronize()
+    log(f"[bench] profiled {name} ({b},{s},{h},{d}) causal={causal}: {warmup + steps} steps")
+
+
+def demangle_fa(name):
+    """`fa_fwd_kernel<_Float16, 64, true, 2, false>` for this library's
+    kernel symbols, mangled (`_ZN2fa13fa_fwd_kernelIDF16_Li64ELb1E...`, as
+    some rocprofv3 outputs give them; binutils' c++filt does not know the
+    _Float16 mangling) or demangled (`void fa::fa_fwd_kernel<...>(...)`)."""
+    import re
+    if not name.startswith("_ZN2fa"):
+        return name.replace("void ", "").replace("fa::", "").split("(")[0].strip()
+    m = re.match(r"_ZN2fa(\d+)", name)
+    n = int(m.group(1))
+    pos = m.end()
+    kname = name[pos:pos + n]
+    pos += n
+    args = []
+    if name[pos:pos + 1] == "I":
+        pos += 1
+        tokens = [(r"DF16_", "_Float16"), (r"DF16b", "__bf16"), (r"Li(-?\d+)E", None),
+                  (r"Lb([01])E", None)]
+        while pos < len(name) and name[pos] != "E":
+            for pat, text in tokens:
+                t = re.match(pat, name[pos:])
+                if t:
+                    if text is not None:
+                        args.append(text)
+                    elif pat.startswith("Lb"):
+                        args.append("true" if t.group(1) == "1" else "false")
+                    else:
+                        args.append(t.group(1))
+                    pos += t.end()
+                    break
+            else:
+                return name          # not one of ours: leave it
+    return f"{kname}<{', '.join(args)}>" if args else kname
+
+
+# rocprofv3 --pmc passes summarised by --pmc-summary (each within the
+# per-pass limits: at most 8 SQ and 2 GRBM counters)
+PMC_PASSES = {
+    "A": "SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA SQ_INSTS_VALU SQ_INSTS_SALU SQ_INSTS_LDS "
+         "SQ_LDS_BANK_CONFLICT SQ_LDS_IDX_ACTIVE SQ_INSTS_VALU_TRANS_F32 GRBM_GUI_ACTIVE",
+    "B": "SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY SQ_ACTIVE_INST_ANY "
+         "SQ_ACTIVE_INST_VALU SQ_VALU_MFMA_COEXEC_CYCLES SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE",
+}
+XCDS = 8            # MI355X: GRBM_GUI_ACTIVE comes back summed over the 8 XCDs
+SIMDS = 4 * 256     # 256 CUs x 4 SIMDs
+
+
+def pmc_summary(dirs):
+    """Per-kernel averages of rocprofv3 --pmc counter_collection.csv files
+    (one directory per pass) for the fa:: kernels, with the derived figures:
+
+      mfma_busy   = SQ_VALU_MFMA_BUSY_CYCLES / (cycles * SIMDS), cycles =
+                    GRBM_GUI_ACTIVE / XCDS (rocprofiler's MfmaUtil);
+      *_per_mfma  = instruction counts per MFMA instruction (VALU excludes
+                    the MFMAs, which SQ_INSTS_VALU counts among its own);
+      lds_bank_conflict = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE;
+      waves_per_simd = SQ_WAVE_CYCLES * 4 / (cycles * SIMDS) (wave-cycles
+                    come in quad-cycles): mean resident waves per SIMD;
+      wait_any, wait_issue, active = SQ_WAIT_ANY, SQ_WAIT_INST_ANY,
+                    SQ_ACTIVE_INST_ANY as shares of SQ_WAVE_CYCLES;
+      mfma_coexec = SQ_VALU_MFMA_COEXEC_CYCLES / SQ_VALU_MFMA_BUSY_CYCLES
+                    (share of MFMA-busy cycles in which a VALU op issued).
+
+    Prints a markdown table and the JSON block that bench.py reads back
+    (profiles/*_counters.md)."""
+    import collections
+    import csv
+    import glob
+    vals = collections.defaultdict(lambda: collections.defaultdict(list))
+    meta = {}
+    for dr in dirs:
+        for path in glob.glob(os.path.join(dr, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(path)):
+                name = r["Kernel_Name"]
+                if "fa_" not in name:
+                    continue
+                vals[name][r["Counter_Name"]].append(float(r["Counter_Value"]))
+                meta[name] = {"grid": int(r["Grid_Size"]), "workgroup": int(r["Workgroup_Size"]),
+                              "lds_bytes": int(r["LDS_Block_Size"])}
+    out = {}
+    for raw in sorted(vals):
+        key = demangle_fa(raw)
+        av = {c: statistics.mean(v) for c, v in vals[raw].items()}
+        cyc = av.get("GRBM_GUI_ACTIVE", 0.0) / XCDS
+        row = dict(meta[raw])
+        row["cycles"] = round(cyc)
+        mf = av.get("SQ_INSTS_MFMA")
+        if cyc and "SQ_VALU_MFMA_BUSY_CYCLES" in av:
+            row["mfma_busy"] = round(av["SQ_VALU_MFMA_BUSY_CYCLES"] / (cyc * SIMDS), 4)
+        if mf:
+            row["mfma_insts"] = round(mf)
+            if "SQ_INSTS_VALU" in av:
+                row["valu_per_mfma"] = round((av["SQ_INSTS_VALU"] - mf) / mf, 3)
+            for c, k in (("SQ_INSTS_SALU", "salu_per_mfma"), ("SQ_INSTS_LDS", "lds_per_mfma"),
+                         ("SQ_INSTS_VALU_TRANS_F32", "trans_per_mfma")):
+                if c in av:
+                    row[k] = round(av[c] / mf, 3)
+        if av.get("SQ_LDS_IDX_ACTIVE"):
+            row["lds_bank_conflict"] = round(av["SQ_LDS_BANK_CONFLICT"] / av["SQ_LDS_IDX_ACTIVE"], 4)
+        wc = av.get("SQ_WAVE_CYCLES")
+        if wc and cyc:
+            row["waves_per_simd"] = round(wc * 4 / (cyc * SIMDS), 3)
+            for c, k in (("SQ_WAIT_ANY", "wait_any"), ("SQ_WAIT_INST_ANY", "wait_issue"),
+                         ("SQ_ACTIVE_INST_ANY", "active")):
+                if c in av:
+                    row[k] = round(av[c] / wc, 4)
+        if av.get("SQ_VALU_MFMA_BUSY_CYCLES") and "SQ_VALU_MFMA_COEXEC_CYCLES" in av:
+            row["mfma_coexec"] = round(av["SQ_VALU_MFMA_COEXEC_CYCLES"] / av["SQ_VALU_MFMA_BUSY_CYCLES"], 4)
+        out[key] = row
+    cols = ["cycles", "mfma_busy", "valu_per_mfma", "salu_per_mfma", "lds_per_mfma", "trans_per_mfma",
+            "lds_bank_conflict", "waves_per_simd", "wait_any", "wait_issue", "active", "mfma_coexec",
+            "lds_bytes", "grid", "workgroup"]
+    print("| kernel | " + " | ".join(cols) + " |")
+    print("|---|" + "---:|" * len(cols))
+    for key, row in out.items():
+        print(f"| `{key}` | " + " | ".join(str(row.get(c, "")) for c in cols) + " |")
+    print("\n```json")
+    print(json.dumps({"kernels": out, "xcds": XCDS, "simds": SIMDS}, indent=1))
+    print("```")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -592,7 +812,17 @@ def main():
                     help="instead of the benchmark, run 10 plain device copies of MIB MiB "
                          "(a kernel of known HBM traffic, to scale rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE readings) and exit")
+    ap.add_argument("--profile-config", metavar="NAME",
+                    help="instead of the benchmark, run the training step's kernels for one "
+                         "BASELINE config (C1 ... C5-layer) --warmup + --steps times, e.g. under "
+                         "rocprofv3 --pmc")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
+                    help="summarise rocprofv3 --pmc output directories (one per counter pass) "
+                         "into per-kernel counter figures and exit (no GPU needed)")
     args = ap.parse_args()
+    if args.pmc_summary:
+        pmc_summary(args.pmc_summary)
+        return
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -611,6 +841,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         log(f"[bench] copy calibration: 10 x {n} bytes read + {n} bytes written")
+        return
+    if args.profile_config:
+        torch.cuda.set_device(0)
+        run_profile_config(args.profile_config, args.steps, args.warmup)
         return
     if args.configs:
         torch.cuda.set_device(0)
@@ -675,19 +909,40 @@ def main():
     # the training step launches fwd, then fa_bwd = dQ (which also computes
     # delta) and dK/dV; the pre-pass kernel is timed only as a standalone
     step_kernels = ("bwd_dkdv", "bwd_dq", "fwd")
-    dom = max(step_kernels, key=lambda n: kt[n]["avg_us"])
+    dom = max(step_kernels, key=lambda n: kt[n]["avg_us_in_step"])
     d = kt[dom]
     traffic, traffic_src, sym = profiled_traffic(d["kernel"])
-    roofline = {"bound": "mfma", "achieved": round(d["tflops"], 2), "peak": PEAK_FP16_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(d["tflops"] / PEAK_FP16_TFLOPS, 4),
+    useful = useful_fraction(S, CAUSAL)
+    t_in = d["avg_us_in_step"] * 1e-6
+    achieved = d["flops"] / t_in / 1e12
+    counters, counters_src = profiled_counters(sym)
+    roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
+                "frac_useful": round(useful * achieved / PEAK_FP16_TFLOPS, 4),
                 "traffic": traffic, "traffic_source": traffic_src,
                 "algorithmic_bytes": d["bytes"],
-                "kernel": sym, "avg_us": round(d["avg_us"], 3),
-                "flops_per_launch": d["flops"]}
-    all_kernels = {n: {"kernel": profiled_traffic(r["kernel"])[2], "avg_us": round(r["avg_us"], 3),
-                       "tflops": round(r["tflops"], 2), "frac_mfma": round(r["tflops"] / PEAK_FP16_TFLOPS, 4),
-                       "gbs": round(r["gbs"], 1), "frac_hbm": round(r["gbs"] / PEAK_HBM_GBS, 4)}
-                   for n, r in kt.items()}
+                "kernel": sym, "avg_us": round(d["avg_us_in_step"], 3),
+                "avg_us_in_step": round(d["avg_us_in_step"], 3),
+                "avg_us_standalone": round(d["avg_us"], 3),
+                "frac_standalone": round(d["tflops"] / PEAK_FP16_TFLOPS, 4),
+                "flops_per_launch": d["flops"],
+                "mfma_busy_counter": counters.get("mfma_busy") if counters else None,
+                "counters_source": counters_src}
+    all_kernels = {}
+    for n, r in kt.items():
+        sym_n = profiled_traffic(r["kernel"])[2]
+        row = {"kernel": sym_n, "avg_us": round(r["avg_us"], 3),
+               "tflops": round(r["tflops"], 2), "frac_mfma": round(r["tflops"] / PEAK_FP16_TFLOPS, 4),
+               "gbs": round(r["gbs"], 1), "frac_hbm": round(r["gbs"] / PEAK_HBM_GBS, 4)}
+        if "avg_us_in_step" in r:
+            tf = r["flops"] / (r["avg_us_in_step"] * 1e-6) / 1e12
+            row.update({"avg_us_in_step": round(r["avg_us_in_step"], 3),
+                        "frac_mfma_in_step": round(tf / PEAK_FP16_TFLOPS, 4),
+                        "frac_useful_in_step": round(useful * tf / PEAK_FP16_TFLOPS, 4)})
+            c, _ = profiled_counters(sym_n)
+            if c:
+                row["mfma_busy_counter"] = c.get("mfma_busy")
+        all_kernels[n] = row
 
     cpu = None
     if not args.no_cpu:

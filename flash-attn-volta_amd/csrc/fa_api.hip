@@ -11,7 +11,7 @@
 
 #include <atomic>
 
-#include "../../include/fa_mi355x.h"
+#include "fa_mi355x.h"
 #include "fa_bwd.hpp"
 #include "fa_fwd.hpp"
 #include "fa_rope.hpp"
@@ -42,8 +42,43 @@ int check_shape(const Shape &s) {
   return FA_OK;
 }
 
-// A (B, S, H, D) tensor with the given element strides.
-int check_tensor(const void *p, const int64_t *st, int B, int S, int H, int D) {
+// Rows of one head that the attention kernels stage per tile, at most (the
+// dK/dV layouts' 128-key / 128-query tiles): inside a tile a lane addresses
+// its row with a 32-bit buffer offset, row * seq_stride * 2 bytes
+// (fa_common.hpp DmaStager), so (kMaxTileRows - 1) rows must span < 2^31.
+constexpr int64_t kMaxTileRows = 128;
+
+// True when the (b, s, h) rows of D elements never share an element: with
+// the dimensions of size > 1 taken in increasing stride order, each stride
+// is at least the extent of the rows nested inside it.  Every layout the
+// wrappers produce (contiguous tensors, permuted and sliced views) passes;
+// a written tensor that fails would have workgroups store the same bytes.
+bool rows_disjoint(const int64_t *st, int B, int S, int H, int D) {
+  int64_t stride[3] = {st[0], st[1], st[2]};
+  int64_t size[3] = {B, S, H};
+  for (int i = 1; i < 3; ++i)   // insertion sort of three dims by stride
+    for (int j = i; j > 0 && stride[j] < stride[j - 1]; --j) {
+      const int64_t ts = stride[j], tn = size[j];
+      stride[j] = stride[j - 1];
+      size[j] = size[j - 1];
+      stride[j - 1] = ts;
+      size[j - 1] = tn;
+    }
+  int64_t extent = D;
+  for (int i = 0; i < 3; ++i) {
+    if (size[i] == 1) continue;
+    if (stride[i] < extent) return false;
+    extent += stride[i] * (size[i] - 1);
+  }
+  return true;
+}
+
+// A (B, S, H, D) tensor with the given element strides.  `tile_rows` > 0
+// bounds the sequence stride for kernels that address that many rows of a
+// head with 32-bit offsets (0: every offset is 64-bit).  `output`: the
+// tensor is written, so its rows must not overlap.
+int check_tensor(const void *p, const int64_t *st, int B, int S, int H, int D, bool output,
+                 int64_t tile_rows) {
   if (p == nullptr || st == nullptr) return FA_ERR_NULL_POINTER;
   if (!aligned16(p)) return FA_ERR_ALIGNMENT;
   if (st[3] != 1) return FA_ERR_STRIDE;
@@ -54,19 +89,26 @@ int check_tensor(const void *p, const int64_t *st, int B, int S, int H, int D) {
   const double span = (double)(B - 1) * st[0] + (double)(S - 1) * st[1] +
                       (double)(H - 1) * st[2] + D;
   if (span > 4.0e18) return FA_ERR_TOO_LARGE;
+  if (tile_rows > 0 && S > 1 && (tile_rows - 1) * st[1] * 2 + 2 * (int64_t)D > INT32_MAX)
+    return FA_ERR_TOO_LARGE;
+  if (output && !rows_disjoint(st, B, S, H, D)) return FA_ERR_STRIDE;
   return FA_OK;
 }
 
-int check_q_like(const void *p, const int64_t *st, const Shape &s) {
-  return check_tensor(p, st, s.B, s.Sq, s.H, s.D);
+int check_q_like(const void *p, const int64_t *st, const Shape &s, bool output = false) {
+  return check_tensor(p, st, s.B, s.Sq, s.H, s.D, output, kMaxTileRows);
 }
 
-int check_kv_like(const void *p, const int64_t *st, const Shape &s) {
-  return check_tensor(p, st, s.B, s.Sk, s.Hk, s.D);
+int check_kv_like(const void *p, const int64_t *st, const Shape &s, bool output = false) {
+  return check_tensor(p, st, s.B, s.Sk, s.Hk, s.D, output, kMaxTileRows);
 }
 
-fa::TensorDesc desc(const void *p, const int64_t *st) {
-  return fa::TensorDesc{static_cast<const f16 *>(p), st[0], st[1], st[2]};
+// Kernel view of a tensor with S rows per head; a single row's sequence
+// stride is never used to address anything, so it is passed as 0 (a large
+// one would otherwise wrap the 32-bit offsets of the rows a tile reads past
+// the end).
+fa::TensorDesc desc(const void *p, const int64_t *st, int S) {
+  return fa::TensorDesc{static_cast<const f16 *>(p), st[0], S > 1 ? st[1] : 0, st[2]};
 }
 
 // Kernel-side score scale: |sm_scale| * log2(e), never exactly zero so that
@@ -338,7 +380,7 @@ int check_fwd(const void *q, const void *k, const void *v, void *o, float *lse, 
   if ((rc = check_q_like(q, q_st, s))) return rc;
   if ((rc = check_kv_like(k, k_st, s))) return rc;
   if ((rc = check_kv_like(v, v_st, s))) return rc;
-  if ((rc = check_q_like(o, o_st, s))) return rc;
+  if ((rc = check_q_like(o, o_st, s, true))) return rc;
   if (lse != nullptr && !aligned16(lse)) return FA_ERR_ALIGNMENT;
   if (!isfinite(sm_scale)) return FA_ERR_SCALE;
   return FA_OK;
@@ -348,9 +390,9 @@ fa::FwdArgs fwd_args(const void *q, const void *k, const void *v, void *o, float
                      const Shape &s, const int64_t *q_st, const int64_t *k_st,
                      const int64_t *v_st, const int64_t *o_st, float sm_scale) {
   fa::FwdArgs a{};
-  a.q = desc(q, q_st);
-  a.k = desc(k, k_st);
-  a.v = desc(v, v_st);
+  a.q = desc(q, q_st, s.Sq);
+  a.k = desc(k, k_st, s.Sk);
+  a.v = desc(v, v_st, s.Sk);
   a.o = static_cast<f16 *>(o);
   a.o_sb = o_st[0];
   a.o_ss = o_st[1];
@@ -418,8 +460,8 @@ int run_pre(const void *o, const void *dout, float *delta, const Shape &s, const
   if (delta == nullptr) return FA_ERR_NULL_POINTER;
   if (!aligned16(delta)) return FA_ERR_ALIGNMENT;
   fa::PreArgs a{};
-  a.o = desc(o, o_st);
-  a.dout = desc(dout, do_st);
+  a.o = desc(o, o_st, s.Sq);
+  a.dout = desc(dout, do_st, s.Sq);
   a.delta = delta;
   a.B = s.B;
   a.S = s.Sq;
@@ -448,10 +490,10 @@ int bwd_common(const void *dout, const void *q, const void *k, const void *v, co
   if (!aligned16(lse) || !aligned16(delta)) return FA_ERR_ALIGNMENT;
   if (!isfinite(sm_scale)) return FA_ERR_SCALE;
   fa::BwdArgs a{};
-  a.q = desc(q, q_st);
-  a.k = desc(k, k_st);
-  a.v = desc(v, v_st);
-  a.dout = desc(dout, do_st);
+  a.q = desc(q, q_st, s.Sq);
+  a.k = desc(k, k_st, s.Sk);
+  a.v = desc(v, v_st, s.Sk);
+  a.dout = desc(dout, do_st, s.Sq);
   a.lse = lse;
   a.delta = delta;
   a.B = s.B;
@@ -613,8 +655,8 @@ int run_dkdv(const void *dout, const void *q, const void *k, const void *v, cons
   fa::BwdArgs a;
   int rc = bwd_common(dout, q, k, v, lse, delta, s, do_st, q_st, k_st, v_st, sm_scale, &a);
   if (rc) return rc;
-  if ((rc = check_kv_like(dk, dk_st, s))) return rc;
-  if ((rc = check_kv_like(dv, dv_st, s))) return rc;
+  if ((rc = check_kv_like(dk, dk_st, s, true))) return rc;
+  if ((rc = check_kv_like(dv, dv_st, s, true))) return rc;
   a.split_kt = split_kt;
   a.cnt = cnt;
   a.part = part;
@@ -651,10 +693,10 @@ int run_dq(const void *dout, const void *q, const void *k, const void *v, const 
   fa::BwdArgs a;
   int rc = bwd_common(dout, q, k, v, lse, delta, s, do_st, q_st, k_st, v_st, sm_scale, &a);
   if (rc) return rc;
-  if ((rc = check_q_like(dq, dq_st, s))) return rc;
+  if ((rc = check_q_like(dq, dq_st, s, true))) return rc;
   if (o != nullptr) {
     if ((rc = check_q_like(o, o_st, s))) return rc;
-    a.o = desc(o, o_st);
+    a.o = desc(o, o_st, s.Sq);
     a.delta_out = const_cast<float *>(delta);
   }
   a.cnt_zero = cnt_zero;
@@ -675,26 +717,41 @@ size_t delta_bytes(int B, int Sq, int H) {
 }
 
 
+// Every check of the full backward but the workspace's: a call that passes
+// launches nothing invalid.
+int check_bwd(const void *dout, const void *q, const void *k, const void *v, const void *o,
+              const float *lse, void *dq, void *dk, void *dv, const Shape &s,
+              const int64_t *do_st, const int64_t *q_st, const int64_t *k_st,
+              const int64_t *v_st, const int64_t *o_st, const int64_t *dq_st,
+              const int64_t *dk_st, const int64_t *dv_st, float sm_scale) {
+  int rc = check_shape(s);
+  if (rc) return rc;
+  if ((rc = check_q_like(o, o_st, s))) return rc;
+  if ((rc = check_q_like(dq, dq_st, s, true))) return rc;
+  if ((rc = check_kv_like(dk, dk_st, s, true))) return rc;
+  if ((rc = check_kv_like(dv, dv_st, s, true))) return rc;
+  if ((rc = check_q_like(dout, do_st, s))) return rc;
+  if ((rc = check_q_like(q, q_st, s))) return rc;
+  if ((rc = check_kv_like(k, k_st, s))) return rc;
+  if ((rc = check_kv_like(v, v_st, s))) return rc;
+  if (lse == nullptr) return FA_ERR_NULL_POINTER;
+  if (!aligned16(lse)) return FA_ERR_ALIGNMENT;
+  if (!isfinite(sm_scale)) return FA_ERR_SCALE;
+  return FA_OK;
+}
+
 int run_bwd(const void *dout, const void *q, const void *k, const void *v, const void *o,
             const float *lse, void *dq, void *dk, void *dv, void *workspace,
             size_t workspace_bytes, const Shape &s, const int64_t *do_st, const int64_t *q_st,
             const int64_t *k_st, const int64_t *v_st, const int64_t *o_st, const int64_t *dq_st,
             const int64_t *dk_st, const int64_t *dv_st, float sm_scale, int causal, void *stream) {
-  int rc = check_shape(s);
+  int rc = check_bwd(dout, q, k, v, o, lse, dq, dk, dv, s, do_st, q_st, k_st, v_st, o_st, dq_st,
+                     dk_st, dv_st, sm_scale);
   if (rc) return rc;
-  if ((rc = check_q_like(o, o_st, s))) return rc;
-  if ((rc = check_q_like(dq, dq_st, s))) return rc;
-  if ((rc = check_kv_like(dk, dk_st, s))) return rc;
-  if ((rc = check_kv_like(dv, dv_st, s))) return rc;
   if (workspace == nullptr || workspace_bytes < delta_bytes(s.B, s.Sq, s.H))
     return FA_ERR_WORKSPACE;
   if (!aligned16(workspace)) return FA_ERR_ALIGNMENT;
-  // Validate the inputs shared by the two main kernels before the first
-  // launch, so a bad call launches nothing.
-  fa::BwdArgs probe;
   float *delta = static_cast<float *>(workspace);
-  if ((rc = bwd_common(dout, q, k, v, lse, delta, s, do_st, q_st, k_st, v_st, sm_scale, &probe)))
-    return rc;
   // The key-block split runs when the workspace has room for it (see
   // fa_bwd_gqa_workspace_bytes): counters, then the fp32 partials.
   // Layout: delta, then the dK/dV split's counters and partials, then the
@@ -834,10 +891,10 @@ int run_rope_fwd(const void *q, const void *k, void *q_out, void *k_out, const v
                  const int64_t *ko_st, const int64_t *cs_st, void *stream) {
   int rc = check_rope_shape(s);
   if (rc) return rc;
-  if ((rc = check_tensor(q, q_st, s.B, s.S, s.H, s.D))) return rc;
-  if ((rc = check_tensor(k, k_st, s.B, s.S, s.Hk, s.D))) return rc;
-  if ((rc = check_tensor(q_out, qo_st, s.B, s.S, s.H, s.D))) return rc;
-  if ((rc = check_tensor(k_out, ko_st, s.B, s.S, s.Hk, s.D))) return rc;
+  if ((rc = check_tensor(q, q_st, s.B, s.S, s.H, s.D, false, 0))) return rc;
+  if ((rc = check_tensor(k, k_st, s.B, s.S, s.Hk, s.D, false, 0))) return rc;
+  if ((rc = check_tensor(q_out, qo_st, s.B, s.S, s.H, s.D, true, 0))) return rc;
+  if ((rc = check_tensor(k_out, ko_st, s.B, s.S, s.Hk, s.D, true, 0))) return rc;
   if ((rc = check_rope_table(cos, sin, cs_st))) return rc;
   if ((rc = check_rope_eps(wq, wk, eps))) return rc;
 
@@ -876,21 +933,21 @@ int run_rope_bwd(const void *dq_out, const void *dk_out, const void *q, const vo
                  const int64_t *dq_st, const int64_t *dk_st, const int64_t *cs_st, void *stream) {
   int rc = check_rope_shape(s);
   if (rc) return rc;
-  if ((rc = check_tensor(dq_out, dqo_st, s.B, s.S, s.H, s.D))) return rc;
-  if ((rc = check_tensor(dk_out, dko_st, s.B, s.S, s.Hk, s.D))) return rc;
-  if ((rc = check_tensor(dq, dq_st, s.B, s.S, s.H, s.D))) return rc;
-  if ((rc = check_tensor(dk, dk_st, s.B, s.S, s.Hk, s.D))) return rc;
+  if ((rc = check_tensor(dq_out, dqo_st, s.B, s.S, s.H, s.D, false, 0))) return rc;
+  if ((rc = check_tensor(dk_out, dko_st, s.B, s.S, s.Hk, s.D, false, 0))) return rc;
+  if ((rc = check_tensor(dq, dq_st, s.B, s.S, s.H, s.D, true, 0))) return rc;
+  if ((rc = check_tensor(dk, dk_st, s.B, s.S, s.Hk, s.D, true, 0))) return rc;
   if ((rc = check_rope_table(cos, sin, cs_st))) return rc;
   if ((rc = check_rope_eps(wq, wk, eps))) return rc;
   const bool norm = wq != nullptr || wk != nullptr;
   // The forward's inputs and the dw outputs matter only for a normed side.
   if (wq != nullptr) {
-    if ((rc = check_tensor(q, q_st, s.B, s.S, s.H, s.D))) return rc;
+    if ((rc = check_tensor(q, q_st, s.B, s.S, s.H, s.D, false, 0))) return rc;
     if (dwq == nullptr) return FA_ERR_NULL_POINTER;
     if (!aligned16(dwq)) return FA_ERR_ALIGNMENT;
   }
   if (wk != nullptr) {
-    if ((rc = check_tensor(k, k_st, s.B, s.S, s.Hk, s.D))) return rc;
+    if ((rc = check_tensor(k, k_st, s.B, s.S, s.Hk, s.D, false, 0))) return rc;
     if (dwk == nullptr) return FA_ERR_NULL_POINTER;
     if (!aligned16(dwk)) return FA_ERR_ALIGNMENT;
   }
@@ -947,12 +1004,14 @@ const char *fa_strerror(int status) {
       return "B, sequence lengths and head counts must be positive, and the query head "
              "count a multiple of the key/value head count";
     case FA_ERR_STRIDE:
-      return "bad stride: the head_dim stride must be 1 and the other strides "
-             "non-negative multiples of 8 elements";
+      return "bad stride: the head_dim stride must be 1, the other strides non-negative "
+             "multiples of 8 elements, and an output's rows must not overlap";
     case FA_ERR_ALIGNMENT: return "tensor data pointer is not 16-byte aligned";
     case FA_ERR_SCALE: return "sm_scale is not finite";
     case FA_ERR_WORKSPACE: return "workspace is NULL or smaller than fa_bwd_workspace_bytes()";
-    case FA_ERR_TOO_LARGE: return "sizes exceed the kernel's index or grid limits";
+    case FA_ERR_TOO_LARGE:
+      return "sizes or strides exceed the kernel's index or grid limits (a sequence stride "
+             "must keep 127 rows under 2^31 bytes)";
     case FA_ERR_LAUNCH: return "the HIP runtime rejected a kernel launch";
     case FA_ERR_DTYPE: return "unsupported dtype (supported: FA_DTYPE_F16, FA_DTYPE_BF16)";
     case FA_ERR_EPS: return "norm eps is negative or not finite";

@@ -285,7 +285,20 @@ __device__ __forceinline__ float mul_then_add(float x, float m, float y) {
 // the counter update; the loads follow the counter's returned value.  A
 // __threadfence() here would also write back and invalidate the XCD's
 // whole L2 in every such workgroup, which costs more than the split gains.
+//
+// This is a hardware assumption, outside the HIP memory model's formal
+// guarantees (which would need a release on the counter update and an
+// acquire on its result): on gfx950, agent-scope relaxed stores and loads
+// are issued with sc1 and bypass the non-coherent per-XCD L2, a store has
+// reached the coherent level once vmcnt counts it complete, and the
+// counter's atomicAdd is performed at that same level after the barrier.
+// The library is built for gfx950 only (the #error below); another target
+// must re-establish the ordering, e.g. with __hip_atomic_fetch_add(...,
+// __ATOMIC_RELEASE / __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT).
 // `pl` = the lane's index among the holders (key group * 64 + lane).
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "the split dK/dV exchange's ordering argument holds for gfx950 only"
+#endif
 template <typename E, int D, int NKG>
 __device__ __forceinline__ void split_finish(const BwdArgs &a, floatx16 (&dk)[D / 32],
                                              floatx16 (&dv)[D / 32], int slot, int seg,

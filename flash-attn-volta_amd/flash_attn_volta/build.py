@@ -16,6 +16,10 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG_DIR)                  # flash-attn-volta_amd/
 CSRC = os.path.join(ROOT, "csrc")
 SOURCES = [os.path.join(CSRC, "fa_api.hip")]
+# The C-ABI header (fa_mi355x.h): the repository's include/ directory, or the
+# directory named by FA_MI355X_INCLUDE when the package is built elsewhere.
+INCLUDE_DIR = os.environ.get("FA_MI355X_INCLUDE",
+                             os.path.join(os.path.dirname(ROOT), "include"))
 HEADERS = [os.path.join(CSRC, f) for f in ("fa_common.hpp", "fa_fwd.hpp", "fa_bwd.hpp", "fa_rope.hpp")]
 OUT = os.path.join(PKG_DIR, "libfa_mi355x.so")
 
@@ -41,7 +45,11 @@ def hipcc() -> str:
 def build_library(verbose: bool = True) -> str:
     """Compile libfa_mi355x.so in place (always recompiles) and return its path."""
     tmp = OUT + ".tmp"
-    cmd = [hipcc()] + HIPCC_FLAGS + SOURCES + ["-o", tmp]
+    header = os.path.join(INCLUDE_DIR, "fa_mi355x.h")
+    if not os.path.exists(header):
+        raise RuntimeError(f"{header} not found: set FA_MI355X_INCLUDE to the directory "
+                           "holding the C-ABI header")
+    cmd = [hipcc()] + HIPCC_FLAGS + ["-I", INCLUDE_DIR] + SOURCES + ["-o", tmp]
     if verbose:
         print("[build]", " ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -37,13 +37,17 @@ enum fa_status {
   FA_ERR_HEAD_DIM = -2,       /* D not in {32, 64, 128}                     */
   FA_ERR_SHAPE = -3,          /* B, a sequence length or a head count <= 0,
                                  or H not a multiple of Hk                  */
-  FA_ERR_STRIDE = -4,         /* D stride != 1, or a stride not a multiple
-                                 of 8 elements (16-byte vector access)      */
+  FA_ERR_STRIDE = -4,         /* D stride != 1, a stride not a multiple of
+                                 8 elements (16-byte vector access), or an
+                                 output whose (b, s, h) rows overlap        */
   FA_ERR_ALIGNMENT = -5,      /* a base pointer not 16-byte aligned         */
   FA_ERR_SCALE = -6,          /* sm_scale not finite                        */
   FA_ERR_WORKSPACE = -7,      /* workspace NULL or smaller than required    */
-  FA_ERR_TOO_LARGE = -8,      /* sizes whose element offsets overflow int64
-                                 or whose grid exceeds the launch limits    */
+  FA_ERR_TOO_LARGE = -8,      /* sizes whose element offsets overflow int64,
+                                 a sequence stride over ~8.45e6 elements
+                                 (127 rows of a 128-row tile must span
+                                 < 2^31 bytes: 32-bit offsets), or
+                                 a grid beyond the launch limits            */
   FA_ERR_LAUNCH = -9,         /* the HIP runtime rejected a kernel launch   */
   FA_ERR_DTYPE = -10,         /* dtype not one of enum fa_dtype             */
   FA_ERR_EPS = -11            /* norm eps negative or not finite            */
@@ -210,8 +214,9 @@ int fa_bwd_gqa(const void *dout, const void *q, const void *k, const void *v,
                float sm_scale, int causal, int dtype, void *stream);
 
 /*
- * The two main backward kernels as separate steps (fa_bwd runs
- * fa_bwd_preprocess, then fa_bwd_dkdv, then fa_bwd_dq).  `delta` is the
+ * The two main backward kernels as separate steps (fa_bwd runs the dQ
+ * kernel, computing delta on the way, then the dK/dV kernel; called
+ * separately they take delta from fa_bwd_preprocess).  `delta` is the
  * fa_bwd_preprocess output, (B, H, S) fp32 contiguous.
  *
  * fa_bwd_dkdv replaces the launch of _fa_bwd_dkdv_kernel_{d64,d128}

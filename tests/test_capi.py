@@ -49,6 +49,7 @@ def test_abi_version(lib):
     assert lib.fa_abi_version() == _capi.ABI_VERSION == 6
 
 
+
 def test_strerror_covers_every_code(lib):
     codes = [0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10, -11]
     msgs = [lib.fa_strerror(c).decode() for c in codes]
@@ -281,3 +282,91 @@ def test_splitkv_plan_and_validation(lib):
     assert call(w=BAD) == _capi.FA_ERR_ALIGNMENT
     assert lib.fa_fwd_splitkv(P, P, P, P, None, P, n, 1, 1, 4096, 32, 8, 96, sq, sk, sk, sq,
                               0.1, 1, 0, None) == _capi.FA_ERR_HEAD_DIM
+
+
+def test_sequence_stride_bound_for_32bit_tile_offsets(lib):
+    """Inside a tile the kernels address up to 128 rows of a head with 32-bit
+    byte offsets (row * seq_stride * 2): a sequence stride that would carry
+    127 rows past 2^31 bytes is FA_ERR_TOO_LARGE, not a silent wrap.  The
+    bound is checked on every attention tensor, input or output, and is
+    moot for a single row (its stride addresses nothing).  Calls meant to
+    pass the stride checks carry a NaN scale, which is checked after every
+    tensor, so they return FA_ERR_SCALE and launch nothing (the pointers
+    are fake)."""
+    B, S, H, D = 1, 256, 1, 64
+    nan = float("nan")
+    ok = (2**31 - 1 - 2 * D) // 254 // 8 * 8          # largest multiple of 8 that fits
+    big = ok + 8
+
+    def st(seq):
+        return (ctypes.c_int64 * 4)(seq * S, seq, D, 1)
+    good, bad, base = st(ok), st(big), _st(B, S, H, D)
+    f = lib.fa_fwd
+    assert f(P, P, P, P, None, B, S, H, D, good, good, good, good, nan, 0, None) == \
+        _capi.FA_ERR_SCALE
+    for args in ((bad, base, base, base), (base, bad, base, base), (base, base, bad, base),
+                 (base, base, base, bad)):
+        assert f(P, P, P, P, None, B, S, H, D, *args, 0.1, 0, None) == _capi.FA_ERR_TOO_LARGE
+    # one query row: its stride is never used
+    one = (ctypes.c_int64 * 4)(big, big, D, 1)
+    assert lib.fa_fwd_gqa(P, P, P, P, None, B, 1, S, H, H, D, one, base, base, _st(B, 1, H, D),
+                          nan, 0, _capi.FA_DTYPE_F16, None) == _capi.FA_ERR_SCALE
+    # the backward checks its tensors the same way
+    sq = _st(B, S, H, D)
+    ws = lib.fa_bwd_workspace_bytes(B, S, H, D)
+    assert lib.fa_bwd(P, P, P, P, P, P, P, P, P, P, ws, B, S, H, D, sq, sq, bad, sq, sq, sq, sq,
+                      sq, 0.1, 1, None) == _capi.FA_ERR_TOO_LARGE
+
+
+def test_sequence_stride_bound_is_exact():
+    """The bound is the exact one the kernels need: 127 rows of the largest
+    accepted stride plus one D-row end below 2^31 bytes; eight more
+    elements do not."""
+    D = 64
+    ok = (2**31 - 1 - 2 * D) // 254 // 8 * 8
+    assert 127 * ok * 2 + 2 * D <= 2**31 - 1 < 127 * (ok + 8) * 2 + 2 * D
+
+
+def test_output_rows_must_not_overlap(lib):
+    """Written tensors (o, dq, dk, dv, rope outputs) whose (b, s, h) rows
+    share elements -- a zero stride on a dimension of size > 1, or a stride
+    below the extent of the rows nested inside it -- are FA_ERR_STRIDE:
+    workgroups would store the same bytes in a schedule-dependent order.
+    Inputs may overlap (broadcast reads are fine), size-1 dimensions may
+    have any stride, and sliced views pass.  Calls meant to pass carry a NaN
+    scale (checked after every tensor): FA_ERR_SCALE, nothing launched."""
+    B, S, H, D = 2, 64, 4, 64
+    nan = float("nan")
+    base = _st(B, S, H, D)
+    f = lib.fa_fwd
+    for o_st in ((0, H * D, D, 1),              # two batches on one output
+                 (S * H * D, 0, D, 1),          # every position on one row
+                 (S * H * D, H * D, 0, 1),      # heads collapse
+                 (S * H * D, 64, D, 1)):        # seq stride inside a position's heads
+        o = (ctypes.c_int64 * 4)(*o_st)
+        assert f(P, P, P, P, None, B, S, H, D, base, base, base, o, 0.1, 0, None) == \
+            _capi.FA_ERR_STRIDE, o_st
+    # broadcast input (zero batch stride on k and v): not an output
+    kb = (ctypes.c_int64 * 4)(0, H * D, D, 1)
+    assert f(P, P, P, P, None, B, S, H, D, base, kb, kb, base, nan, 0, None) == _capi.FA_ERR_SCALE
+    # a (B,S,H,D) output that is a slice of a (B,S,2H,D) buffer, and the
+    # (B,H,S,D).transpose(1,2) layout, are disjoint
+    for o_st in ((S * 2 * H * D, 2 * H * D, D, 1), (H * S * D, D, S * D, 1)):
+        o = (ctypes.c_int64 * 4)(*o_st)
+        assert f(P, P, P, P, None, B, S, H, D, base, base, base, o, nan, 0, None) == \
+            _capi.FA_ERR_SCALE
+    # size-1 dims may carry any stride, zero included
+    o1 = (ctypes.c_int64 * 4)(0, 0, D, 1)
+    b1 = _st(1, 1, H, D)
+    assert f(P, P, P, P, None, 1, 1, H, D, b1, b1, b1, o1, nan, 0, None) == _capi.FA_ERR_SCALE
+    # backward outputs and the rope outputs are checked the same way
+    ws = lib.fa_bwd_workspace_bytes(B, S, H, D)
+    z = (ctypes.c_int64 * 4)(0, H * D, D, 1)
+    assert lib.fa_bwd(P, P, P, P, P, P, P, P, P, P, ws, B, S, H, D, base, base, base, base, base,
+                      base, base, z, 0.1, 1, None) == _capi.FA_ERR_STRIDE
+    assert lib.fa_bwd(P, P, P, P, P, P, P, P, P, P, ws, B, S, H, D, base, base, base, base, base,
+                      z, base, base, 0.1, 1, None) == _capi.FA_ERR_STRIDE
+    cs = (ctypes.c_int64 * 2)(0, D)
+    assert lib.fa_rope_qk_fwd(P, P, P, P, P, P, None, None, 0.0, B, S, H, H, D, base, base, z,
+                              base, cs, _capi.FA_DTYPE_F16, None) == _capi.FA_ERR_STRIDE
+
