@@ -991,6 +991,45 @@ int run_rope_bwd(const void *dq_out, const void *dk_out, const void *q, const vo
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// Allocation-free backward (fa_bwd_gqa_noalloc).  Its workspace -- delta,
+// and the split schedule's counters and fp32 partials when they fit -- is
+// this file-scope device array: each GPU the library runs on holds its own
+// copy, FA_NOALLOC_SCRATCH_BYTES, until the process ends.  In host code the
+// name is only a stand-in, never an address: the device copy's address is
+// looked up once per device (with that device current) and that pointer is
+// what the kernels get.  Nothing in the array needs clearing between calls:
+// the dQ kernel writes delta and zeroes the split counters before the dK/dV
+// kernel reads them, and every partial is written before it is read.
+static __device__ __align__(256) unsigned char scratch[FA_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+// Device address of `scratch` per device index (0: not looked up yet).  The
+// lookup stores the same value from any thread, so the cache is race-free.
+constexpr int kScratchDevices = 64;
+std::atomic<uintptr_t> g_scratch_addr[kScratchDevices];
+
+int scratch_on_current_device(void **out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return FA_ERR_LAUNCH;
+  const bool cached = dev >= 0 && dev < kScratchDevices;
+  uintptr_t p = cached ? g_scratch_addr[dev].load(std::memory_order_relaxed) : 0;
+  if (p == 0) {
+    void *addr = nullptr;
+    if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || addr == nullptr) {
+      (void)hipGetLastError();   // not a launch error of the next call
+      return FA_ERR_LAUNCH;
+    }
+    p = reinterpret_cast<uintptr_t>(addr);
+    if (cached) g_scratch_addr[dev].store(p, std::memory_order_relaxed);
+  }
+  *out = reinterpret_cast<void *>(p);
+  return FA_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 int fa_abi_version(void) { return FA_ABI_VERSION; }
@@ -1012,7 +1051,12 @@ const char *fa_strerror(int status) {
     case FA_ERR_TOO_LARGE:
       return "sizes or strides exceed the kernel's index or grid limits (a sequence stride "
              "must keep 127 rows under 2^31 bytes)";
-    case FA_ERR_LAUNCH: return "the HIP runtime rejected a kernel launch";
+    case FA_ERR_LAUNCH:
+      return "the HIP runtime reported an error (a kernel launch, or the device address of "
+             "the no-alloc scratch buffer)";
+    case FA_ERR_SCRATCH:
+      return "fa_bwd_gqa_noalloc: delta (4 * B * H * Sq bytes) exceeds the static scratch "
+             "buffer (FA_NOALLOC_SCRATCH_BYTES)";
     case FA_ERR_DTYPE: return "unsupported dtype (supported: FA_DTYPE_F16, FA_DTYPE_BF16)";
     case FA_ERR_EPS: return "norm eps is negative or not finite";
     default: return "unknown status code";
@@ -1101,6 +1145,27 @@ int fa_bwd_gqa(const void *dout, const void *q, const void *k, const void *v,
   return run_bwd(dout, q, k, v, o, lse, dq, dk, dv, workspace, workspace_bytes,
                  Shape{B, Sq, Sk, H, Hk, D, dtype}, do_strides, q_strides, k_strides, v_strides,
                  o_strides, dq_strides, dk_strides, dv_strides, sm_scale, causal, stream);
+}
+
+int fa_bwd_gqa_noalloc(const void *dout, const void *q, const void *k, const void *v,
+                       const void *o, const float *lse,
+                       void *dq, void *dk, void *dv,
+                       int B, int Sq, int Sk, int H, int Hk, int D,
+                       const int64_t do_strides[4], const int64_t q_strides[4],
+                       const int64_t k_strides[4], const int64_t v_strides[4],
+                       const int64_t o_strides[4], const int64_t dq_strides[4],
+                       const int64_t dk_strides[4], const int64_t dv_strides[4],
+                       float sm_scale, int causal, int dtype, void *stream) {
+  const Shape s{B, Sq, Sk, H, Hk, D, dtype};
+  int rc = check_bwd(dout, q, k, v, o, lse, dq, dk, dv, s, do_strides, q_strides, k_strides,
+                     v_strides, o_strides, dq_strides, dk_strides, dv_strides, sm_scale);
+  if (rc) return rc;
+  if (delta_bytes(B, Sq, H) > (size_t)FA_NOALLOC_SCRATCH_BYTES) return FA_ERR_SCRATCH;
+  void *ws = nullptr;
+  if ((rc = scratch_on_current_device(&ws))) return rc;
+  return run_bwd(dout, q, k, v, o, lse, dq, dk, dv, ws, FA_NOALLOC_SCRATCH_BYTES, s, do_strides,
+                 q_strides, k_strides, v_strides, o_strides, dq_strides, dk_strides, dv_strides,
+                 sm_scale, causal, stream);
 }
 
 int fa_bwd_dkdv(const void *dout, const void *q, const void *k, const void *v,

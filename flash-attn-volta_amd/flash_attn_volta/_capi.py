@@ -14,7 +14,7 @@ import threading
 LIB_NAME = "libfa_mi355x.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # status codes (enum fa_status)
 FA_OK = 0
@@ -29,6 +29,10 @@ FA_ERR_TOO_LARGE = -8
 FA_ERR_LAUNCH = -9
 FA_ERR_DTYPE = -10
 FA_ERR_EPS = -11
+FA_ERR_SCRATCH = -12
+
+# bytes of the static device buffer fa_bwd_gqa_noalloc uses as its workspace
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 # element types (enum fa_dtype)
 FA_DTYPE_F16 = 0
@@ -47,6 +51,7 @@ EXPORTED_SYMBOLS = (
     "fa_bwd_gqa_workspace_bytes",
     "fa_bwd",
     "fa_bwd_gqa",
+    "fa_bwd_gqa_noalloc",
     "fa_bwd_dkdv",
     "fa_bwd_dq",
     "fa_rope_qk_fwd",
@@ -116,6 +121,13 @@ def _declare(lib):
                                _i64x4, _i64x4, _i64x4, _i64x4,
                                _i64x4, _i64x4, _i64x4, _i64x4,
                                ctypes.c_float, _ci, _ci, _vp]
+    lib.fa_bwd_gqa_noalloc.restype = _ci
+    lib.fa_bwd_gqa_noalloc.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp,
+                                       _vp, _vp, _vp,
+                                       _ci, _ci, _ci, _ci, _ci, _ci,
+                                       _i64x4, _i64x4, _i64x4, _i64x4,
+                                       _i64x4, _i64x4, _i64x4, _i64x4,
+                                       ctypes.c_float, _ci, _ci, _vp]
     lib.fa_bwd_dkdv.restype = _ci
     lib.fa_bwd_dkdv.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                 _ci, _ci, _ci, _ci,

@@ -29,7 +29,11 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 6
+#define FA_ABI_VERSION 7
+
+/* Size of the static device scratch buffer that fa_bwd_gqa_noalloc uses as
+ * its workspace (one per GPU, held for the life of the process). */
+#define FA_NOALLOC_SCRATCH_BYTES (64u << 20)
 
 enum fa_status {
   FA_OK = 0,
@@ -48,9 +52,12 @@ enum fa_status {
                                  (127 rows of a 128-row tile must span
                                  < 2^31 bytes: 32-bit offsets), or
                                  a grid beyond the launch limits            */
-  FA_ERR_LAUNCH = -9,         /* the HIP runtime rejected a kernel launch   */
+  FA_ERR_LAUNCH = -9,         /* the HIP runtime rejected a kernel launch
+                                 (or a device query it needed)              */
   FA_ERR_DTYPE = -10,         /* dtype not one of enum fa_dtype             */
-  FA_ERR_EPS = -11            /* norm eps negative or not finite            */
+  FA_ERR_EPS = -11,           /* norm eps negative or not finite            */
+  FA_ERR_SCRATCH = -12        /* fa_bwd_gqa_noalloc: the problem's delta does
+                                 not fit FA_NOALLOC_SCRATCH_BYTES           */
 };
 
 /* Element type of the 16-bit tensors (fa_fwd_gqa / fa_bwd_gqa; the other
@@ -212,6 +219,34 @@ int fa_bwd_gqa(const void *dout, const void *q, const void *k, const void *v,
                const int64_t o_strides[4], const int64_t dq_strides[4],
                const int64_t dk_strides[4], const int64_t dv_strides[4],
                float sm_scale, int causal, int dtype, void *stream);
+
+/*
+ * fa_bwd_gqa for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): the same arguments minus the workspace, which is a static
+ * device buffer of FA_NOALLOC_SCRATCH_BYTES that the library holds per GPU
+ * for the life of the process.  delta (4 * B * H * Sq bytes) must fit it,
+ * else FA_ERR_SCRATCH (checked before any HIP call); the split schedule of
+ * fa_bwd_gqa_workspace_bytes runs when it fits too, and results are then
+ * bit-identical to fa_bwd_gqa given a workspace of the same size.  Calls
+ * and allocates nothing else: no hipMalloc, no memset.
+ *
+ * Every call on a GPU shares that GPU's buffer, so calls that overlap on
+ * one GPU (concurrent streams, or host threads without ordering) race and
+ * must be serialised by the caller.
+ *
+ * No counterpart in the reference (its backward allocates through torch,
+ * flash_attn_volta/triton_fa_bwd.py:650-654).
+ */
+int fa_bwd_gqa_noalloc(const void *dout, const void *q, const void *k, const void *v,
+                       const void *o, const float *lse,
+                       void *dq, void *dk, void *dv,
+                       int B, int Sq, int Sk, int H, int Hk, int D,
+                       const int64_t do_strides[4], const int64_t q_strides[4],
+                       const int64_t k_strides[4], const int64_t v_strides[4],
+                       const int64_t o_strides[4], const int64_t dq_strides[4],
+                       const int64_t dk_strides[4], const int64_t dv_strides[4],
+                       float sm_scale, int causal, int dtype, void *stream);
 
 /*
  * The two main backward kernels as separate steps (fa_bwd runs the dQ

@@ -46,12 +46,16 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.fa_abi_version() == _capi.ABI_VERSION == 6
+    assert lib.fa_abi_version() == _capi.ABI_VERSION == 7
 
+
+def test_noalloc_scratch_size_matches_header():
+    m = re.search(r"#define FA_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", open(HEADER).read())
+    assert m and int(m.group(1)) << int(m.group(2)) == _capi.NOALLOC_SCRATCH_BYTES
 
 
 def test_strerror_covers_every_code(lib):
-    codes = [0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10, -11]
+    codes = [0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10, -11, -12]
     msgs = [lib.fa_strerror(c).decode() for c in codes]
     assert len(set(msgs)) == len(codes)
     assert "unknown" in lib.fa_strerror(-1234).decode()
@@ -370,3 +374,30 @@ def test_output_rows_must_not_overlap(lib):
     assert lib.fa_rope_qk_fwd(P, P, P, P, P, P, None, None, 0.0, B, S, H, H, D, base, base, z,
                               base, cs, _capi.FA_DTYPE_F16, None) == _capi.FA_ERR_STRIDE
 
+
+def _bwd_noalloc(lib, B=1, Sq=128, Sk=128, H=2, Hk=2, D=64, lse=P, dq=P, dk_st=None,
+                 scale=0.125, dtype=_capi.FA_DTYPE_F16):
+    sq, sk = _st(B, Sq, H, D), _st(B, Sk, Hk, D)
+    return lib.fa_bwd_gqa_noalloc(P, P, P, P, P, lse, dq, P, P, B, Sq, Sk, H, Hk, D,
+                                  sq, sq, sk, sk, sq, sq, dk_st or sk, sk, scale, 1, dtype, None)
+
+
+def test_noalloc_validation_before_any_hip_call(lib):
+    """fa_bwd_gqa_noalloc validates everything fa_bwd_gqa does (but the
+    workspace, which it does not take) and rejects a problem whose delta
+    (4 * B * H * Sq bytes) exceeds the static scratch buffer with
+    FA_ERR_SCRATCH -- all before any HIP call, so on a GPU-less machine the
+    codes come back exactly (and on a GPU box nothing launches: every call
+    here is invalid)."""
+    assert _bwd_noalloc(lib, D=96) == _capi.FA_ERR_HEAD_DIM
+    assert _bwd_noalloc(lib, Hk=3) == _capi.FA_ERR_SHAPE
+    assert _bwd_noalloc(lib, lse=None) == _capi.FA_ERR_NULL_POINTER
+    assert _bwd_noalloc(lib, lse=BAD) == _capi.FA_ERR_ALIGNMENT
+    assert _bwd_noalloc(lib, dq=BAD) == _capi.FA_ERR_ALIGNMENT
+    assert _bwd_noalloc(lib, scale=float("inf")) == _capi.FA_ERR_SCALE
+    assert _bwd_noalloc(lib, dtype=3) == _capi.FA_ERR_DTYPE
+    assert _bwd_noalloc(lib, dk_st=(ctypes.c_int64 * 4)(0, 0, 64, 1)) == _capi.FA_ERR_STRIDE
+    # one query row more than the scratch holds: 64 heads x Sq rows x 4 bytes
+    rows = _capi.NOALLOC_SCRATCH_BYTES // 4
+    assert _bwd_noalloc(lib, B=1, Sq=rows // 64 + 1, Sk=128, H=64, Hk=64) == _capi.FA_ERR_SCRATCH
+    assert lib.fa_strerror(_capi.FA_ERR_SCRATCH).decode().startswith("fa_bwd_gqa_noalloc")
