@@ -64,6 +64,18 @@ struct FwdArgs {
   float *part_lse;     // (n_splits, B, H, Sq) fp32: each split's LSE in log2 units
 };
 
+// f(integral_constant<int, 0>), ..., f(integral_constant<int, N - 1>): a loop
+// whose index is a compile-time constant in the body (register arrays
+// indexed by it stay in registers, and scheduling builtins take it).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F &f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 template <int D, int KSPLIT>
 struct FwdTile {
   static_assert(KSPLIT == 1 || KSPLIT == 2, "key split is 1 or 2");
@@ -161,12 +173,11 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   stk.init(w, lane, a.k.ss);
   stv.init(w, lane, a.v.ss);
   auto load_k = [&](int n0, auto sc) { stk.load(k_sl(sc), kb, a.k.ss, n0, Sk, w); };
-  auto load_v = [&](int n0, auto sc) { stv.load(v_sl(sc), vb, a.v.ss, n0, Sk, w); };
-  // In the loop K is loaded two tiles ahead and V one: cursors at those
-  // rows, each advanced by a tile per load (no per-tile 64-bit multiplies).
+  // Iteration t loads K(t + 2) and V(t): cursors at those rows, each
+  // advanced by a tile per load (no per-tile 64-bit multiplies).
   RowCursor ck, cv;
   ck.init(kb, a.k.ss, 2 * BN, Sk, D, BN);
-  cv.init(vb, a.v.ss, BN, Sk, D, BN);
+  cv.init(vb, a.v.ss, 0, Sk, D, BN);
   auto load_k_next = [&](auto sc) {
     stk.load(k_sl(sc), ck.rsrc(), w);
     ck.advance();
@@ -198,13 +209,29 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   auto sub_key = [&](int n0, int sb) { return n0 + 32 * (NSUB * kh + sb); };
   auto dead = [&](int n0, int sb) { return CAUSAL && sub_key(n0, sb) > wpos_hi + off; };
 
-  // ---- S^T = K Q^T for this wave's sub-blocks of a tile
+  // Tiles that need no mask for this wave: every key of its part of the
+  // tile (offsets up to kmax inside the tile) exists and, causal, is
+  // visible to the wave's first query.  Such tiles form a prefix
+  // [0, t_mask) of the sweep (masks only start at the diagonal or the
+  // ragged end); the loop runs them through a branch-free body.
+  int t_mask;
+  {
+    const int kmax = 32 * (NSUB * kh + NSUB) - 1;
+    const int x = Sk - kmax;   // first tile t with t * BN + kmax >= Sk
+    t_mask = x <= 0 ? 0 : (x + BN - 1) / BN;
+    if (CAUSAL) {
+      const int y = wpos_lo + off - kmax;   // first t with t * BN + kmax > wpos_lo + off
+      t_mask = min(t_mask, y < 0 ? 0 : y / BN + 1);
+    }
+  }
+
+  // ---- S^T = K Q^T for this wave's sub-blocks of a tile (dead sub-blocks
+  // skipped when CHECK: the diagonal mask overwrites them)
   vec8<E> qf[D / 16];
-  auto qk = [&](auto sc, int n0, floatx16 (&s)[NSUB]) {
+  auto qk = [&](auto sc, auto checkc, int n0, floatx16 (&s)[NSUB]) {
 #pragma unroll
     for (int sb = 0; sb < NSUB; ++sb) {
-      // dead sub-blocks are skipped; the diagonal mask overwrites them
-      if (dead(n0, sb)) continue;
+      if (decltype(checkc)::value && dead(n0, sb)) continue;
       const f16 *kr = k_sl(sc) + 32 * (NSUB * kh + sb) * D;
       floatx16 acc = mfma32(ld8<E>(kr + a_off[0]), qf[0], floatx16{});
 #pragma unroll
@@ -213,13 +240,32 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
     }
   };
 
+  // ---- O^T += V^T P^T for the tile at n0, from V slot sc
+  floatx16 oacc[D / 32];
+#pragma unroll
+  for (int d = 0; d < D / 32; ++d) oacc[d] = floatx16{};
+  auto pv = [&](auto sc, auto checkc, int n0, vec8<E> (&pf)[NSUB][2]) {
+#pragma unroll
+    for (int sb = 0; sb < NSUB; ++sb) {
+      if (decltype(checkc)::value && dead(n0, sb)) continue;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        // kperm rows 32 * (sub-block) + 16hh + 4g (+8): keys 16hh + 8g + 0..7
+        const int rb = (32 * (NSUB * kh + sb) + 16 * hh) * D;
+#pragma unroll
+        for (int d = 0; d < D / 32; ++d)
+          oacc[d] = mfma32(load_tr_pair<E>(v_sl(sc) + rb + t_off[d], 8 * D), pf[sb][hh], oacc[d]);
+      }
+    }
+  };
+
   using C0 = std::integral_constant<int, 0>;
   using C1 = std::integral_constant<int, 1>;
-  // ---- prologue: K(0), V(0) -> slot 0, K(1) -> K slot 1
-  if (n_tiles > 0) {
-    load_k(0, C0{});
-    load_v(0, C0{});
-  }
+  using Fast = std::false_type;    // no dead-sub-block checks
+  using Check = std::true_type;
+  // ---- prologue: K(0) -> K slot 0, K(1) -> K slot 1, Q to registers,
+  // then the scores of tile 0
+  if (n_tiles > 0) load_k(0, C0{});
   if (n_tiles > 1) load_k(BN, C1{});
   {
     const int qr = min(qrow, nrows - 1);
@@ -238,35 +284,99 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
   __syncthreads();
 
-  // Scores ping-pong between two register sets (no copy at the end of a
-  // tile, which would wait for the next tile's S MFMAs right after issuing
-  // them): tile t's scores live in s_a when t is even, s_b when odd.
+  // Scores and probabilities ping-pong between two register sets (tile t's
+  // in the `a` sets when t is even, `b` when odd), so no copy waits for the
+  // MFMAs that produce the next tile's scores.
   floatx16 s_a[NSUB], s_b[NSUB];
-  if (n_tiles > 0) qk(C0{}, 0, s_a);
+  vec8<E> p_a[NSUB][2], p_b[NSUB][2];
+  if (n_tiles > 0) qk(C0{}, Check{}, 0, s_a);
   // K slot 0 is refilled with K(2) at the start of the first iteration
   __syncthreads();
 
-  floatx16 oacc[D / 32];
-#pragma unroll
-  for (int d = 0; d < D / 32; ++d) oacc[d] = floatx16{};
   float m_run = kNegInf;   // running max of c*s (log2 units), stale by <= log2 kFastSum
   float l_run = 0.0f;      // this lane's share of the running sum
   const float c = a.c;
 
-  // One key tile; `pc` = t & 1 as a compile-time constant (the loop is
-  // unrolled by two): S^T of tile t+1 reads K slot pc^1, P V reads V slot
-  // pc, and the DMAs of K(t+2) / V(t+1) refill K slot pc / V slot pc^1,
-  // whose last readers finished before the previous barrier.
-  auto tile_step = [&](auto pcc, int t, floatx16 (&s_cur)[NSUB], floatx16 (&s_nxt)[NSUB]) {
+  // P = exp2(c*s - m) rounded to E, against the running max m, and the
+  // lane's sum of the rounded values (two partial sums: shorter chains).
+  auto probs = [&](auto checkc, int n0, floatx16 (&s)[NSUB], vec8<E> (&pf)[NSUB][2],
+                   float neg_m) -> float {
+    float l0 = 0.0f, l1 = 0.0f;
+#pragma unroll
+    for (int sb = 0; sb < NSUB; ++sb) {
+      if (decltype(checkc)::value && dead(n0, sb)) continue;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+          vec2<E> pr = __builtin_convertvector(
+              (floatx2){fast_exp2(__builtin_fmaf(s[sb][8 * hh + j], c, neg_m)),
+                        fast_exp2(__builtin_fmaf(s[sb][8 * hh + j + 1], c, neg_m))},
+              vec2<E>);
+          if (hh == 0) l0 = dot2_acc(pr, l0);
+          else l1 = dot2_acc(pr, l1);
+          pf[sb][hh][j] = pr[0];
+          pf[sb][hh][j + 1] = pr[1];
+        }
+      }
+    }
+    return l0 + l1;
+  };
+
+  // The softmax step of tile t (scores s, probabilities into pf): p >= 0,
+  // so the lane's sum of its rounded p bounds each of them: a sum <=
+  // kFastSum proves every p inside E's range and the tile needs no row
+  // max.  Otherwise (the first tile with a visible key, or a score grown
+  // past m by more than log2 kFastSum) the wave takes the row max,
+  // rescales what has been accumulated (O includes tile t - 1's P V, issued
+  // earlier in the same iteration) and recomputes.
+  auto finish_softmax = [&](auto checkc, int n0, floatx16 (&s)[NSUB], vec8<E> (&pf)[NSUB][2],
+                            float l_tile) {
+    const bool slow = m_run == kNegInf || !(l_tile <= kFastSum);
+    if (__any(slow)) {
+      float mx = kNegInf;
+#pragma unroll
+      for (int sb = 0; sb < NSUB; ++sb) {
+        if (decltype(checkc)::value && dead(n0, sb)) continue;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[sb][i]);
+      }
+      mx = max_xor32(mx);
+      const float m_new = fmaxf(m_run, mx * c);
+      const bool grow = m_new > m_run;
+      const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f;   // 0 from -inf
+      m_run = grow ? m_new : m_run;
+      l_run *= alpha;
+#pragma unroll
+      for (int d = 0; d < D / 32; ++d)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) oacc[d][i] *= alpha;
+      l_tile = probs(checkc, n0, s, pf, m_run == kNegInf ? 0.0f : -m_run);
+    }
+    l_run += l_tile;
+  };
+
+  // One key tile.  Iteration t issues the MFMAs of two other tiles -- S^T
+  // of tile t + 1 (K slot pc ^ 1) and P V of tile t - 1 (V slot pc ^ 1) --
+  // alongside the softmax of tile t, whose scores came from the previous
+  // iteration: none of the three depends on another, so the wave keeps the
+  // matrix pipe busy while its VALU work runs.  The DMAs of K(t + 2) / V(t)
+  // refill K slot pc / V slot pc, whose last readers (S^T of tile t, P V of
+  // tile t - 2) finished before the previous barrier.  `pc` = t & 1 as a
+  // compile-time constant (the loops are unrolled by two).
+  //
+  // General step: any tile (first, last, diagonal, ragged), with the
+  // neighbours' existence, dead sub-blocks and the mask checked.
+  auto step_general = [&](auto pcc, int t, floatx16 (&s_cur)[NSUB], floatx16 (&s_nxt)[NSUB],
+                          vec8<E> (&p_prev)[NSUB][2], vec8<E> (&p_cur)[NSUB][2]) {
     constexpr int pc = decltype(pcc)::value;
     using CP = std::integral_constant<int, pc>;
     using CQ = std::integral_constant<int, pc ^ 1>;
     const int n0 = t * BN;
-    const bool more1 = t + 1 < n_tiles, more2 = t + 2 < n_tiles;
-    if (more2) load_k_next(CP{});   // K(t + 2)
-    if (more1) load_v_next(CQ{});   // V(t + 1)
-    if (more1) qk(CQ{}, n0 + BN, s_nxt);
-
+    if (t + 2 < n_tiles) load_k_next(CP{});   // K(t + 2)
+    load_v_next(CP{});                        // V(t)
+    if (t + 1 < n_tiles) qk(CQ{}, Check{}, n0 + BN, s_nxt);
+    if (t >= 1) pv(CQ{}, Check{}, n0 - BN, p_prev);
     if (!dead(n0, 0)) {
       // ---- masking (diagonal / ragged sub-blocks only)
 #pragma unroll
@@ -281,80 +391,111 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
           }
         }
       }
-
-      // ---- P = exp2(c*s - m) rounded to E, against the running max m.
-      // p >= 0, so the lane's sum of its rounded p bounds each of them: a
-      // sum <= kFastSum proves every p inside E's range, and the tile needs
-      // no row max.  Otherwise (the first tile with a visible key, or a
-      // score grown past m by more than log2 kFastSum) the wave takes the
-      // row max, rescales and recomputes.
-      vec8<E> pf[NSUB][2];
-      float l_tile = 0.0f;
-      auto probs = [&](float neg_m) {
-        l_tile = 0.0f;
-#pragma unroll
-        for (int sb = 0; sb < NSUB; ++sb) {
-          if (dead(n0, sb)) continue;
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
-#pragma unroll
-            for (int j = 0; j < 8; j += 2) {
-              vec2<E> pr = __builtin_convertvector(
-                  (floatx2){fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + j], c, neg_m)),
-                            fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + j + 1], c, neg_m))},
-                  vec2<E>);
-              l_tile = dot2_acc(pr, l_tile);
-              pf[sb][hh][j] = pr[0];
-              pf[sb][hh][j + 1] = pr[1];
-            }
-          }
-        }
-      };
-      probs(-m_run);
-      const bool slow = m_run == kNegInf || !(l_tile <= kFastSum);
-      if (__any(slow)) {
-        float mx = s_cur[0][0];
-#pragma unroll
-        for (int sb = 0; sb < NSUB; ++sb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s_cur[sb][i]);
-        mx = max_xor32(mx);
-        const float m_new = fmaxf(m_run, mx * c);
-        const bool grow = m_new > m_run;
-        const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f;   // 0 from -inf
-        m_run = grow ? m_new : m_run;
-        l_run *= alpha;
-#pragma unroll
-        for (int d = 0; d < D / 32; ++d)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) oacc[d][i] *= alpha;
-        probs(m_run == kNegInf ? 0.0f : -m_run);
-      }
-      l_run += l_tile;
-
-      // ---- O^T += V^T P^T
-#pragma unroll
-      for (int sb = 0; sb < NSUB; ++sb) {
-        if (dead(n0, sb)) continue;
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          // kperm rows 32 * (sub-block) + 16hh + 4g (+8): keys 16hh + 8g + 0..7
-          const int rb = (32 * (NSUB * kh + sb) + 16 * hh) * D;
-#pragma unroll
-          for (int d = 0; d < D / 32; ++d)
-            oacc[d] = mfma32(load_tr_pair<E>(v_sl(CP{}) + rb + t_off[d], 8 * D), pf[sb][hh],
-                             oacc[d]);
-        }
-      }
+      const float l_tile = probs(Check{}, n0, s_cur, p_cur, -m_run);
+      finish_softmax(Check{}, n0, s_cur, p_cur, l_tile);
     }
-
-    if (more1) __builtin_amdgcn_s_waitcnt(0x0f70);   // this wave's DMAs into the next slots
+    __builtin_amdgcn_s_waitcnt(0x0f70);   // this wave's DMAs into the next slots
     __syncthreads();
   };
 
-  for (int t = 0; t < n_tiles; t += 2) {
-    tile_step(C0{}, t, s_a, s_b);
-    if (t + 1 < n_tiles) tile_step(C1{}, t + 1, s_b, s_a);
+  // Interior step: 1 <= t, t + 1 < n_tiles and t < t_mask, so both
+  // neighbours exist and every sub-block of tiles t - 1 and t is visible
+  // with nothing to mask -- one straight-line block for the scheduler.
+  // K(t + 2) past the last tile is a DMA of zeros (the cursor's extent is
+  // 0 there) into a slot nobody reads again.
+  auto step_interior = [&](auto pcc, int t, floatx16 (&s_cur)[NSUB], floatx16 (&s_nxt)[NSUB],
+                           vec8<E> (&p_prev)[NSUB][2], vec8<E> (&p_cur)[NSUB][2]) {
+    constexpr int pc = decltype(pcc)::value;
+    using CP = std::integral_constant<int, pc>;
+    using CQ = std::integral_constant<int, pc ^ 1>;
+    load_k_next(CP{});   // K(t + 2)
+    load_v_next(CP{});   // V(t)
+    // The block in issue order: MQ S^T MFMAs (K slot pc ^ 1) and MP P V
+    // MFMAs (V slot pc ^ 1), alternating while both remain, each followed
+    // by its share of tile t's softmax (NPAIR pairs of scores: two FMAs, two
+    // exp2, one conversion, one dot2).  A MFMA runs ~32 cycles in the
+    // matrix pipe while the wave issues the VALU slice after it; its A
+    // operand was read from LDS two MFMAs earlier.  sched_barrier(0) keeps
+    // the compiler from regrouping the slices.
+    constexpr int MQ = NSUB * (D / 16), MP = NSUB * 2 * (D / 32), M = MQ + MP;
+    constexpr int NPAIR = NSUB * 8;
+    const f16 *ks = k_sl(CQ{});
+    const f16 *vs = v_sl(CQ{});
+    // MFMA i of the block: S^T (sb, cc) or P V (sb, hh, d), ordered
+    // Q0 P0 Q1 P1 ... while both kinds remain.
+    auto kind_index = [](int i, bool &is_q, int &j) {
+      const int lo = MQ < MP ? MQ : MP;
+      if (i < 2 * lo) { is_q = (i & 1) == 0; j = i >> 1; }
+      else { is_q = MQ > MP; j = i - lo; }
+    };
+    auto operand = [&](auto ic) -> vec8<E> {
+      constexpr int i = decltype(ic)::value;
+      bool is_q = false; int j = 0;
+      kind_index(i, is_q, j);
+      if (is_q) {
+        const int sb = j / (D / 16), cc = j % (D / 16);
+        return ld8<E>(ks + 32 * (NSUB * kh + sb) * D + a_off[cc]);
+      }
+      const int sb = j / (2 * (D / 32)), hh = (j / (D / 32)) % 2, d = j % (D / 32);
+      return load_tr_pair<E>(vs + (32 * (NSUB * kh + sb) + 16 * hh) * D + t_off[d], 8 * D);
+    };
+    const float c_ = c, neg_m = -m_run;
+    float l0 = 0.0f, l1 = 0.0f;
+    vec8<E> op[3];
+    op[0] = operand(std::integral_constant<int, 0>{});
+    if constexpr (M > 1) op[1] = operand(std::integral_constant<int, 1>{});
+    static_for<M>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      if constexpr (i + 2 < M) op[(i + 2) % 3] = operand(std::integral_constant<int, i + 2>{});
+      bool is_q = false; int j = 0;
+      kind_index(i, is_q, j);
+      if (is_q) {
+        const int sb = j / (D / 16), cc = j % (D / 16);
+        s_nxt[sb] = mfma32(op[i % 3], qf[cc], cc == 0 ? floatx16{} : s_nxt[sb]);
+      } else {
+        const int sb = j / (2 * (D / 32)), hh = (j / (D / 32)) % 2, d = j % (D / 32);
+        oacc[d] = mfma32(op[i % 3], p_prev[sb][hh], oacc[d]);
+      }
+      // softmax pairs [i * NPAIR / M, (i + 1) * NPAIR / M) of tile t
+      static_for<(i + 1) * NPAIR / M - i * NPAIR / M>([&](auto kc) {
+        constexpr int q = i * NPAIR / M + decltype(kc)::value;   // pair index
+        constexpr int sb = q / 8, hh = (q / 4) % 2, jj = 2 * (q % 4);
+        vec2<E> pr = __builtin_convertvector(
+            (floatx2){fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + jj], c_, neg_m)),
+                      fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + jj + 1], c_, neg_m))},
+            vec2<E>);
+        if (q & 1) l1 = dot2_acc(pr, l1);
+        else l0 = dot2_acc(pr, l0);
+        p_cur[sb][hh][jj] = pr[0];
+        p_cur[sb][hh][jj + 1] = pr[1];
+      });
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    finish_softmax(Fast{}, t * BN, s_cur, p_cur, l0 + l1);
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    __syncthreads();
+  };
+
+  // Tile 0, then the interior tiles two at a time, then the rest two at a
+  // time.  Every loop starts at an odd tile, so tile t's register sets are
+  // fixed by its parity in all three (tile t's scores in s_a when t is
+  // even, s_b when odd; likewise its probabilities in p_a / p_b).
+  if (n_tiles > 0) step_general(C0{}, 0, s_a, s_b, p_b, p_a);
+  const int t_fast_end = min(t_mask, n_tiles - 1);
+  int t = 1;
+  for (; t + 1 < t_fast_end; t += 2) {
+    step_interior(C1{}, t, s_b, s_a, p_a, p_b);
+    step_interior(C0{}, t + 1, s_a, s_b, p_b, p_a);
+  }
+  for (; t < n_tiles; t += 2) {
+    step_general(C1{}, t, s_b, s_a, p_a, p_b);
+    if (t + 1 < n_tiles) step_general(C0{}, t + 1, s_a, s_b, p_b, p_a);
+  }
+  // P V of the last tile (V slot and probabilities of its parity)
+  if (n_tiles > 0) {
+    const int nl = (n_tiles - 1) * BN;
+    if ((n_tiles - 1) & 1) pv(C1{}, Check{}, nl, p_b);
+    else pv(C0{}, Check{}, nl, p_a);
   }
 
   // ---- merge the two key halves of each query group (K slots reused; the
