@@ -10,6 +10,7 @@
 #include <stdint.h>
 
 #include <atomic>
+#include <type_traits>
 
 #include "fa_mi355x.h"
 #include "fa_bwd.hpp"
@@ -193,23 +194,41 @@ int zigzag_order(int64_t grid, int n_blocks, int per_cu) {
   return grid <= (int64_t)per_cu * device_cus() ? 1 : 0;
 }
 
-template <typename E, int D, bool CAUSAL, int KSPLIT>
+// The forward kernel's pre-scaled mode (Q scaled by c in fp16, the score
+// MFMAs seeded with -max): fp16 with c <= 1, where the scaled Q cannot
+// overflow; bf16 and larger scales apply c in the softmax instead.
+template <typename E>
+bool fwd_prescaled(const fa::FwdArgs &a) {
+  return std::is_same<E, fa::f16>::value && a.c <= 1.0f;
+}
+
+template <typename E, int D, bool CAUSAL, int KSPLIT, bool PRE>
 int launch_fwd_split(const fa::FwdArgs &args, hipStream_t stream) {
   using T = fa::FwdTile<D, KSPLIT>;
   fa::FwdArgs a = args;
   a.n_qtiles = (a.Sq + T::BM - 1) / T::BM;
   const int64_t grid = (int64_t)a.n_qtiles * a.B * a.H;
   if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
-  constexpr auto kernel = fa::fa_fwd_kernel<E, D, CAUSAL, KSPLIT>;
+  constexpr auto kernel = fa::fa_fwd_kernel<E, D, CAUSAL, KSPLIT, false, PRE>;
   a.zigzag = CAUSAL ? zigzag_order(grid, a.n_qtiles, resident_per_cu<kernel>(T::NT)) : 0;
   hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(T::NT), 0, stream, a);
   return launch_status();
 }
 
+template <typename E, int D, bool CAUSAL, int KSPLIT>
+int launch_fwd_mode(const fa::FwdArgs &a, hipStream_t stream) {
+  // (not the unsplit D = 128 layout: the -max seed's 16 registers would
+  // push it past 256 VGPRs, measured +3-4 % on the grids that use it)
+  if constexpr (std::is_same<E, fa::f16>::value && !(D == 128 && KSPLIT == 1)) {
+    if (fwd_prescaled<E>(a)) return launch_fwd_split<E, D, CAUSAL, KSPLIT, true>(a, stream);
+  }
+  return launch_fwd_split<E, D, CAUSAL, KSPLIT, false>(a, stream);
+}
+
 template <typename E, int D, bool CAUSAL>
 int launch_fwd(const fa::FwdArgs &a, hipStream_t stream) {
-  return row_split(a.Sq, (int64_t)a.B * a.H, CAUSAL) ? launch_fwd_split<E, D, CAUSAL, 2>(a, stream)
-                                                     : launch_fwd_split<E, D, CAUSAL, 1>(a, stream);
+  return row_split(a.Sq, (int64_t)a.B * a.H, CAUSAL) ? launch_fwd_mode<E, D, CAUSAL, 2>(a, stream)
+                                                     : launch_fwd_mode<E, D, CAUSAL, 1>(a, stream);
 }
 
 template <typename E, int D>
@@ -355,8 +374,17 @@ int launch_fwd_splitkv(const SplitLaunch &L, hipStream_t stream) {
   a.n_qtiles = (a.grp * a.Sq + T::BM - 1) / T::BM;
   const int64_t gx = (int64_t)a.n_qtiles * a.B * (a.H / a.grp);
   if (gx > 0x7fffffff) return FA_ERR_TOO_LARGE;
-  hipLaunchKernelGGL((fa::fa_fwd_kernel<E, D, CAUSAL, 2, true>), dim3((unsigned)gx, L.n_splits),
-                     dim3(T::NT), 0, stream, a);
+  if constexpr (std::is_same<E, fa::f16>::value) {
+    if (fwd_prescaled<E>(a))
+      hipLaunchKernelGGL((fa::fa_fwd_kernel<E, D, CAUSAL, 2, true, true>),
+                         dim3((unsigned)gx, L.n_splits), dim3(T::NT), 0, stream, a);
+    else
+      hipLaunchKernelGGL((fa::fa_fwd_kernel<E, D, CAUSAL, 2, true, false>),
+                         dim3((unsigned)gx, L.n_splits), dim3(T::NT), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((fa::fa_fwd_kernel<E, D, CAUSAL, 2, true, false>),
+                       dim3((unsigned)gx, L.n_splits), dim3(T::NT), 0, stream, a);
+  }
   int rc = launch_status();
   if (rc) return rc;
   const int64_t rows = (int64_t)a.B * a.H * a.Sq;

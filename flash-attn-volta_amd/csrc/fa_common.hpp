@@ -219,6 +219,22 @@ __device__ __forceinline__ constexpr int swz(int r) {
   return D >= 64 ? (((r & 3) << 1) | ((r >> 2) & 1)) : ((((r >> 1) & 1) << 1) | ((r >> 2) & 1));
 }
 
+// Chunk swizzle for tiles read only as A operands, one ds_read_b128 of a
+// whole row chunk per lane (lane l32 reads LDS row l32): the 16-byte chunks
+// that any 8 consecutive lanes read fall in 8 distinct 16-byte bank groups
+// of a 128-byte window, and those of any 16 consecutive lanes in 16
+// distinct groups of a 256-byte window -- conflict-free whether the LDS
+// serves 8 or 16 lanes of a 128-bit read per cycle.  (swz above has the
+// first property only; a search over XOR-linear maps of the row bits found
+// these.)  Not usable for the transposed reads, which need swz's 4-row
+// pair property.
+template <int D>
+__device__ __forceinline__ constexpr int swz_a(int r) {
+  return D >= 128 ? (r & 15)
+       : D == 64  ? (((r >> 1) & 3) | (((r ^ (r >> 3)) & 1) << 2))
+                  : (((r >> 2) & 1) | ((((r >> 1) ^ (r >> 3)) & 1) << 1));
+}
+
 // Element offset of (row, col) in a swizzled tile.
 template <int D>
 __device__ __forceinline__ constexpr int sw_off(int row, int col) {
@@ -238,7 +254,7 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, const void 
 // past S) into a swizzled LDS slot: ROWS*D*2 bytes = ROWS*D/512 wave
 // instructions of 1 KiB, ROWS*D/(512*NW) per wave of an NW-wave workgroup.
 // No VGPRs hold tile data.
-template <int D, int ROWS = 64, int NW = 4>
+template <int D, int ROWS = 64, int NW = 4, bool A_ONLY = false>
 struct DmaStager {
   static constexpr int PER_WAVE = ROWS * D / (512 * NW);
   static_assert(PER_WAVE >= 1, "tile smaller than one DMA instruction per wave");
@@ -249,7 +265,8 @@ struct DmaStager {
     for (int j = 0; j < PER_WAVE; ++j) {
       const int byte = (w * PER_WAVE + j) * 1024 + 16 * lane;
       const int p = byte / (2 * D), pc = (byte % (2 * D)) / 16;
-      off[j] = kperm_row(p) * (int)ss * 2 + 16 * (pc ^ swz<D>(p));
+      const int sw = A_ONLY ? swz_a<D>(p) : swz<D>(p);
+      off[j] = kperm_row(p) * (int)ss * 2 + 16 * (pc ^ sw);
     }
   }
   __device__ __forceinline__ void load(f16 *slot, const f16 *head, int64_t ss, int r0, int S,

@@ -42,6 +42,10 @@
 
 namespace fa {
 
+#ifndef FA_FWD_W4
+#define FA_FWD_W4 0
+#endif
+
 // Bound on a lane's per-tile sum of probabilities taken against a stale
 // running max (so every probability is <= 2^15, inside fp16's range).
 constexpr float kFastSum = 32768.0f;
@@ -85,6 +89,8 @@ struct FwdTile {
   static constexpr int BN = 64;            // keys per tile
   static constexpr int NT = 256;           // 4 waves
   static constexpr int LDS_TILE = BN * D;  // swizzled, unpadded (fa_common.hpp)
+  // waves per SIMD the register allocation is held to
+  static constexpr int WAVES_PER_EU = FA_FWD_W4 && D == 64 && KSPLIT == 2 ? 4 : 1;
   // O^T partial sums of a key-half wave handed over for the final merge
   static_assert(64 * (D / 2) * 4 <= LDS_TILE * 2, "a merge buffer must fit in one K slot");
 };
@@ -106,8 +112,10 @@ struct FwdTile {
 // tile; blockIdx.y selects a range of kv_split keys, and the workgroup
 // writes its rows' normalised O and log2-domain LSE over that range to
 // part_o / part_lse, which fa_fwd_combine_kernel merges.
-template <typename E, int D, bool CAUSAL, int KSPLIT, bool SPLITKV = false>
-__global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
+template <typename E, int D, bool CAUSAL, int KSPLIT, bool SPLITKV = false, bool PRE = false>
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(FwdTile<D, KSPLIT>::WAVES_PER_EU))) void fa_fwd_kernel(FwdArgs a) {
+  static_assert(!PRE || std::is_same<E, f16>::value, "the pre-scaled mode is fp16 only");
   using T = FwdTile<D, KSPLIT>;
   constexpr int NSUB = T::NSUB;
   constexpr int BM = T::BM, BN = T::BN;
@@ -169,7 +177,8 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
 
   // ---- K and V tiles go straight to LDS (fa_common.hpp DmaStager): both
   // in kperm row order, chunks swizzled; rows past Sk read as zeros.
-  DmaStager<D> stk, stv;
+  DmaStager<D, 64, 4, true> stk;   // K: read only as A operands
+  DmaStager<D> stv;                 // V: read transposed
   stk.init(w, lane, a.k.ss);
   stv.init(w, lane, a.v.ss);
   auto load_k = [&](int n0, auto sc) { stk.load(k_sl(sc), kb, a.k.ss, n0, Sk, w); };
@@ -192,7 +201,7 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   // (and + 8), i.e. natural V rows 8g + (l16 >> 2) (and + 4).
   int a_off[D / 16], t_off[D / 32];
   {
-    const int sa = swz<D>(l32);
+    const int sa = swz_a<D>(l32);
 #pragma unroll
     for (int cc = 0; cc < D / 16; ++cc) a_off[cc] = l32 * D + (((2 * cc + g) ^ sa) << 3);
     const int l16 = lane & 15, tr = 4 * g + (l16 >> 2);
@@ -228,12 +237,23 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   // ---- S^T = K Q^T for this wave's sub-blocks of a tile (dead sub-blocks
   // skipped when CHECK: the diagonal mask overwrites them)
   vec8<E> qf[D / 16];
+  // PRE (fp16 with c <= 1, chosen by the launcher): Q is pre-scaled by c
+  // once, rounded to fp16 as the reference's kernel pre-scales Q
+  // (triton_fa.py:108; c <= 1 cannot overflow), and every S^T MFMA chain
+  // starts from negm = -m instead of 0, so the MFMAs produce c*s - m
+  // directly and the softmax is one v_exp_f32 per score.  Invariant: the
+  // scores of a tile are relative to the running max m (or to 0 while m is
+  // -inf).  Otherwise (bf16, whose 8-bit mantissa would make the extra
+  // rounding visible, or c > 1) negm stays 0 and the softmax applies c in
+  // an FMA.
+  constexpr bool pre = PRE;
+  floatx16 negm = {};
   auto qk = [&](auto sc, auto checkc, int n0, floatx16 (&s)[NSUB]) {
 #pragma unroll
     for (int sb = 0; sb < NSUB; ++sb) {
       if (decltype(checkc)::value && dead(n0, sb)) continue;
       const f16 *kr = k_sl(sc) + 32 * (NSUB * kh + sb) * D;
-      floatx16 acc = mfma32(ld8<E>(kr + a_off[0]), qf[0], floatx16{});
+      floatx16 acc = mfma32(ld8<E>(kr + a_off[0]), qf[0], negm);
 #pragma unroll
       for (int cc = 1; cc < D / 16; ++cc) acc = mfma32(ld8<E>(kr + a_off[cc]), qf[cc], acc);
       s[sb] = acc;
@@ -273,6 +293,12 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
                              : a.q.head(b, h) + (int64_t)qr * a.q.ss) + 8 * g;
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) qf[c] = ld8<E>(qp + 16 * c);
+    if (pre) {
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) qf[c][j] = (E)((float)qf[c][j] * a.c);
+    }
     if (a.neg) {
 #pragma unroll
       for (int c = 0; c < D / 16; ++c) qf[c] = neg8(qf[c]);
@@ -297,8 +323,10 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   float l_run = 0.0f;      // this lane's share of the running sum
   const float c = a.c;
 
-  // P = exp2(c*s - m) rounded to E, against the running max m, and the
-  // lane's sum of the rounded values (two partial sums: shorter chains).
+  // P = exp2(beta * s + neg_mu) rounded to E -- exp2(c*s - m) for the
+  // stored scores s of either mode -- and the lane's sum of the rounded
+  // values (two partial sums: shorter chains).
+  const float beta = pre ? 1.0f : c;
   auto probs = [&](auto checkc, int n0, floatx16 (&s)[NSUB], vec8<E> (&pf)[NSUB][2],
                    float neg_m) -> float {
     float l0 = 0.0f, l1 = 0.0f;
@@ -310,8 +338,8 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
 #pragma unroll
         for (int j = 0; j < 8; j += 2) {
           vec2<E> pr = __builtin_convertvector(
-              (floatx2){fast_exp2(__builtin_fmaf(s[sb][8 * hh + j], c, neg_m)),
-                        fast_exp2(__builtin_fmaf(s[sb][8 * hh + j + 1], c, neg_m))},
+              (floatx2){fast_exp2(__builtin_fmaf(s[sb][8 * hh + j], beta, neg_m)),
+                        fast_exp2(__builtin_fmaf(s[sb][8 * hh + j + 1], beta, neg_m))},
               vec2<E>);
           if (hh == 0) l0 = dot2_acc(pr, l0);
           else l1 = dot2_acc(pr, l1);
@@ -329,9 +357,11 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   // max.  Otherwise (the first tile with a visible key, or a score grown
   // past m by more than log2 kFastSum) the wave takes the row max,
   // rescales what has been accumulated (O includes tile t - 1's P V, issued
-  // earlier in the same iteration) and recomputes.
+  // earlier in the same iteration) and recomputes.  In the pre mode the
+  // next tile's scores s_nxt, already issued against the old m, move to the
+  // new one (when `has_next`), and so does negm for the MFMAs to come.
   auto finish_softmax = [&](auto checkc, int n0, floatx16 (&s)[NSUB], vec8<E> (&pf)[NSUB][2],
-                            float l_tile) {
+                            float l_tile, floatx16 (&s_nxt)[NSUB], bool has_next) {
     const bool slow = m_run == kNegInf || !(l_tile <= kFastSum);
     if (__any(slow)) {
       float mx = kNegInf;
@@ -342,7 +372,9 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[sb][i]);
       }
       mx = max_xor32(mx);
-      const float m_new = fmaxf(m_run, mx * c);
+      // reference of the stored scores: m (pre, finite m) or 0
+      const float ref = pre && m_run != kNegInf ? m_run : 0.0f;
+      const float m_new = fmaxf(m_run, pre ? mx + ref : mx * c);
       const bool grow = m_new > m_run;
       const float alpha = grow ? fast_exp2(m_run - m_new) : 1.0f;   // 0 from -inf
       m_run = grow ? m_new : m_run;
@@ -351,7 +383,20 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
       for (int d = 0; d < D / 32; ++d)
 #pragma unroll
         for (int i = 0; i < 16; ++i) oacc[d][i] *= alpha;
-      l_tile = probs(checkc, n0, s, pf, m_run == kNegInf ? 0.0f : -m_run);
+      // shift of the stored scores' reference: m - ref (0 while m is -inf)
+      const float shift = m_run == kNegInf ? 0.0f : m_run - ref;
+      l_tile = probs(checkc, n0, s, pf, pre ? -shift : (m_run == kNegInf ? 0.0f : -m_run));
+      if (pre) {
+        if (has_next) {
+#pragma unroll
+          for (int sb = 0; sb < NSUB; ++sb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s_nxt[sb][i] -= shift;
+        }
+        const float nm = m_run == kNegInf ? 0.0f : -m_run;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) negm[i] = nm;
+      }
     }
     l_run += l_tile;
   };
@@ -391,8 +436,8 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
           }
         }
       }
-      const float l_tile = probs(Check{}, n0, s_cur, p_cur, -m_run);
-      finish_softmax(Check{}, n0, s_cur, p_cur, l_tile);
+      const float l_tile = probs(Check{}, n0, s_cur, p_cur, pre ? 0.0f : -m_run);
+      finish_softmax(Check{}, n0, s_cur, p_cur, l_tile, s_nxt, t + 1 < n_tiles);
     }
     __builtin_amdgcn_s_waitcnt(0x0f70);   // this wave's DMAs into the next slots
     __syncthreads();
@@ -451,7 +496,7 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
       kind_index(i, is_q, j);
       if (is_q) {
         const int sb = j / (D / 16), cc = j % (D / 16);
-        s_nxt[sb] = mfma32(op[i % 3], qf[cc], cc == 0 ? floatx16{} : s_nxt[sb]);
+        s_nxt[sb] = mfma32(op[i % 3], qf[cc], cc == 0 ? negm : s_nxt[sb]);
       } else {
         const int sb = j / (2 * (D / 32)), hh = (j / (D / 32)) % 2, d = j % (D / 32);
         oacc[d] = mfma32(op[i % 3], p_prev[sb][hh], oacc[d]);
@@ -460,10 +505,14 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
       static_for<(i + 1) * NPAIR / M - i * NPAIR / M>([&](auto kc) {
         constexpr int q = i * NPAIR / M + decltype(kc)::value;   // pair index
         constexpr int sb = q / 8, hh = (q / 4) % 2, jj = 2 * (q % 4);
-        vec2<E> pr = __builtin_convertvector(
-            (floatx2){fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + jj], c_, neg_m)),
-                      fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + jj + 1], c_, neg_m))},
-            vec2<E>);
+        floatx2 e;
+        if constexpr (PRE) {
+          e = (floatx2){fast_exp2(s_cur[sb][8 * hh + jj]), fast_exp2(s_cur[sb][8 * hh + jj + 1])};
+        } else {
+          e = (floatx2){fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + jj], c_, neg_m)),
+                        fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + jj + 1], c_, neg_m))};
+        }
+        vec2<E> pr = __builtin_convertvector(e, vec2<E>);
         if (q & 1) l1 = dot2_acc(pr, l1);
         else l0 = dot2_acc(pr, l0);
         p_cur[sb][hh][jj] = pr[0];
@@ -471,7 +520,7 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
       });
       __builtin_amdgcn_sched_barrier(0);
     });
-    finish_softmax(Fast{}, t * BN, s_cur, p_cur, l0 + l1);
+    finish_softmax(Fast{}, t * BN, s_cur, p_cur, l0 + l1, s_nxt, true);
     __builtin_amdgcn_s_waitcnt(0x0f70);
     __syncthreads();
   };
