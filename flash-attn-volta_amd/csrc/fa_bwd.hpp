@@ -48,6 +48,11 @@
 
 namespace fa {
 
+#ifndef FA_DKDV_SW
+#define FA_DKDV_SW SW_P8
+#endif
+constexpr int kDkdvSwizzle = FA_DKDV_SW;
+
 struct BwdArgs {
   TensorDesc q, k, v, dout;   // q, dout: (B, Sq, H, D); k, v: (B, Sk, Hk, D)
   const float *lse;     // (B, H, Sq) natural log
@@ -448,7 +453,7 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   // first query tile's loads are issued too (one memory latency for both)
   if constexpr (T::KV_LDS) {
     // the workgroup's BK keys into LDS (zeros past Sk)
-    DmaStager<D, BK, T::NW> stk, stv;
+    DmaStager<D, kDkdvSwizzle, BK, T::NW> stk, stv;
     stk.init(w, lane, a.k.ss);
     stv.init(w, lane, a.v.ss);
     stk.load(s_k, a.k.head(b, hk), a.k.ss, k0, Sk, w);
@@ -493,7 +498,7 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   // seeds: s_lse = -LSE * log2(e) / cr (-inf past S, so P = 0 there) and
   // s_dl = -delta.  Seeding the S and dP MFMAs with them yields
   // ck * s - LSE' and dP - delta with no per-score VALU work.
-  DmaStager<D, BQ, T::NW> stq, stg;
+  DmaStager<D, kDkdvSwizzle, BQ, T::NW> stq, stg;
   stq.init(w, lane, a.q.ss);
   stg.init(w, lane, a.dout.ss);
   const float lse_mul = -kLog2e / cr;
@@ -547,17 +552,13 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   // A-operand rows (Q, dO of this wave's 32-query sub-block): row l32, chunk
   // 2cc + g; transposed reads: rows 4g + (l16 >> 2), column chunk
   // 4d + 2((lane >> 4) & 1) + ((l16 >> 1) & 1), half 4 * (l16 & 1).
-  int a_off[D / 16], t_off[D / 32];
+  int a_off[D / 16];
+  TrOffsets<D, kDkdvSwizzle> t_off;
   {
-    const int sa = swz<D>(l32);
+    const int sa = swz<D, kDkdvSwizzle>(l32);
 #pragma unroll
     for (int cc = 0; cc < D / 16; ++cc) a_off[cc] = l32 * D + (((2 * cc + g) ^ sa) << 3);
-    const int l16 = lane & 15, tr = 4 * g + (l16 >> 2);
-    const int st_ = swz<D>(tr);
-#pragma unroll
-    for (int d = 0; d < D / 32; ++d)
-      t_off[d] = tr * D + (((4 * d + 2 * ((lane >> 4) & 1) + ((l16 >> 1) & 1)) ^ st_) << 3) +
-                 4 * (l16 & 1);
+    t_off.init(lane);
   }
 
   if (n_tiles > 0) load_tile(cur_h, cur_m0, std::integral_constant<int, 0>{});
@@ -688,8 +689,8 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
         const int rb = (32 * qs + 16 * hh) * D;
 #pragma unroll
         for (int d = 0; d < D / 32; ++d) {
-          dv[d] = mfma32(load_tr_pair<E>(do_st(stc) + rb + t_off[d], 8 * D), pf[hh], dv[d]);
-          dk[d] = mfma32(load_tr_pair<E>(q_st(stc) + rb + t_off[d], 8 * D), dsf[hh], dk[d]);
+          dv[d] = mfma32(load_tr_pair<E>(do_st(stc) + rb, t_off.lo(d), t_off.hi(d)), pf[hh], dv[d]);
+          dk[d] = mfma32(load_tr_pair<E>(q_st(stc) + rb, t_off.lo(d), t_off.hi(d)), dsf[hh], dk[d]);
         }
       }
     };
@@ -836,7 +837,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
   const float c = a.c;
 
   // K and V tiles go straight to LDS (fa_common.hpp DmaStager).
-  DmaStager<D, BN> stk, stv;
+  DmaStager<D, SW_AT, BN> stk, stv;
   stk.init(w, lane, a.k.ss);
   stv.init(w, lane, a.v.ss);
   auto load_tile = [&](int n0, auto stc) {
@@ -918,17 +919,13 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
   // Per-lane LDS element offsets inside a stage (as in the dK/dV kernel):
   // A-operand rows l32, chunk 2cc + g; transposed reads of K rows
   // 4g + (l16 >> 2).
-  int a_off[D / 16], t_off[D / 32];
+  int a_off[D / 16];
+  TrOffsets<D, SW_AT> t_off;
   {
-    const int sa = swz<D>(l32);
+    const int sa = swz<D, SW_AT>(l32);
 #pragma unroll
     for (int cc = 0; cc < D / 16; ++cc) a_off[cc] = l32 * D + (((2 * cc + g) ^ sa) << 3);
-    const int l16 = lane & 15, tr = 4 * g + (l16 >> 2);
-    const int st_ = swz<D>(tr);
-#pragma unroll
-    for (int d = 0; d < D / 32; ++d)
-      t_off[d] = tr * D + (((4 * d + 2 * ((lane >> 4) & 1) + ((l16 >> 1) & 1)) ^ st_) << 3) +
-                 4 * (l16 & 1);
+    t_off.init(lane);
   }
 
   __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): rows, LSE, delta and the first tile resident
@@ -987,7 +984,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
         const int rb = (32 * ks + 16 * hh) * D;
 #pragma unroll
         for (int d = 0; d < D / 32; ++d)
-          dq[d] = mfma32(load_tr_pair<E>(k_st(stc) + rb + t_off[d], 8 * D), dsf[hh], dq[d]);
+          dq[d] = mfma32(load_tr_pair<E>(k_st(stc) + rb, t_off.lo(d), t_off.hi(d)), dsf[hh], dq[d]);
       }
     };
 

@@ -203,42 +203,50 @@ __device__ __forceinline__ int wave_id() {
 }
 
 // ---------------------------------------------------------------------------
-// Swizzled 64-row tiles staged straight from global memory into LDS.
+// Swizzled tiles staged straight from global memory into LDS.
 //
-// A tile is 64 rows x D fp16, unpadded (row stride 2*D bytes), with 32-row
-// blocks in kperm row order.  Each row's 16-byte chunks are XOR-permuted by
-// swz<D>(row): physical chunk = logical chunk ^ swz(row).  swz takes 8
-// distinct values over any 8 consecutive rows (so eight lanes reading the
-// same logical chunk of consecutive rows with ds_read_b128 hit eight
-// different 16-byte bank groups), and over any aligned group of 4 rows it
-// maps the chunk pair {2j, 2j+1} to 4 disjoint pairs (the 4-row x 32-byte
-// footprint of ds_read_b64_tr_b16).  For D = 32 (4 chunks per row, two rows
-// per 128 bytes) the same holds for rows of equal parity.
-template <int D>
+// A tile is ROWS rows x D fp16, unpadded (row stride 2*D bytes), with 32-row
+// blocks in kperm row order.  Each row's 16-byte chunks are XOR-permuted:
+// physical chunk = logical chunk ^ swz(row).  The LDS serves a wave's read
+// in groups of lanes (gfx950: 64 banks of 4 bytes; 16 lanes of a 128-bit
+// read, 32 lanes of a 64-bit transposed read per cycle), so a read is
+// conflict-free when each group's bytes fall in distinct banks.  The two
+// ways the kernels read tiles ask different things of the swizzle:
+//   * A operands, ds_read_b128 of one logical chunk by lanes reading
+//     consecutive rows (lane l32 reads row l32): any 16 consecutive rows
+//     must land in 16 distinct 16-byte bank groups of a 256-byte window;
+//   * transposed operands, ds_read_b64_tr_b16: an aligned group of 4 rows x
+//     4 consecutive chunks {4q..4q+3} must cover 16 distinct groups of 256
+//     bytes.
+// Each map's output bits are parities of subsets of the row's low 4 bits,
+// found by a search over all such maps (a map meeting only the 8-lane form
+// of the first property measured 25-49 % bank-conflicted LDS cycles).
+//   SW_A  (tiles read only as A operands): the first property.
+//   SW_T  (tiles read only transposed): the second, with period 8 in the
+//         row, so a transposed fragment's second read (8 rows further) is
+//         the first's address plus an immediate.
+//   SW_AT (tiles read both ways): both properties; period 16, so the second
+//         transposed read takes its own offset (TrOffsets).
+//   SW_P8 (tiles read both ways where the registers of those extra offsets
+//         would cost occupancy): period 8, the 8-lane form of the first
+//         property and the second at D <= 64.
+enum { SW_A = 0, SW_T = 1, SW_AT = 2, SW_P8 = 3 };
+template <int D, int SW>
 __device__ __forceinline__ constexpr int swz(int r) {
-  return D >= 64 ? (((r & 3) << 1) | ((r >> 2) & 1)) : ((((r >> 1) & 1) << 1) | ((r >> 2) & 1));
-}
-
-// Chunk swizzle for tiles read only as A operands, one ds_read_b128 of a
-// whole row chunk per lane (lane l32 reads LDS row l32): the 16-byte chunks
-// that any 8 consecutive lanes read fall in 8 distinct 16-byte bank groups
-// of a 128-byte window, and those of any 16 consecutive lanes in 16
-// distinct groups of a 256-byte window -- conflict-free whether the LDS
-// serves 8 or 16 lanes of a 128-bit read per cycle.  (swz above has the
-// first property only; a search over XOR-linear maps of the row bits found
-// these.)  Not usable for the transposed reads, which need swz's 4-row
-// pair property.
-template <int D>
-__device__ __forceinline__ constexpr int swz_a(int r) {
-  return D >= 128 ? (r & 15)
-       : D == 64  ? (((r >> 1) & 3) | (((r ^ (r >> 3)) & 1) << 2))
+  if (SW == SW_A)
+    return D >= 128 ? (r & 15)
+         : D == 64  ? (((r >> 1) & 3) | (((r ^ (r >> 3)) & 1) << 2))
+                    : (((r >> 2) & 1) | ((((r >> 1) ^ (r >> 3)) & 1) << 1));
+  if (SW == SW_P8)
+    return D >= 64 ? (((r & 3) << 1) | ((r >> 2) & 1)) : ((((r >> 1) & 1) << 1) | ((r >> 2) & 1));
+  if (SW == SW_T)
+    return D >= 128 ? ((r & 3) << 2)
+         : D == 64  ? (((r & 3) << 1) | ((r >> 2) & 1))
+                    : ((((r >> 1) & 1) << 1) | ((r >> 2) & 1));
+  return D >= 128 ? ((r & 3) | (((r ^ (r >> 2)) & 3) << 2))
+       : D == 64  ? (((r >> 1) & 1) | (((r ^ (r >> 2)) & 1) << 1) |
+                     (((r ^ (r >> 1) ^ (r >> 3)) & 1) << 2))
                   : (((r >> 2) & 1) | ((((r >> 1) ^ (r >> 3)) & 1) << 1));
-}
-
-// Element offset of (row, col) in a swizzled tile.
-template <int D>
-__device__ __forceinline__ constexpr int sw_off(int row, int col) {
-  return row * D + ((((col >> 3) ^ swz<D>(row))) << 3) + (col & 7);
 }
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -254,7 +262,7 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, const void 
 // past S) into a swizzled LDS slot: ROWS*D*2 bytes = ROWS*D/512 wave
 // instructions of 1 KiB, ROWS*D/(512*NW) per wave of an NW-wave workgroup.
 // No VGPRs hold tile data.
-template <int D, int ROWS = 64, int NW = 4, bool A_ONLY = false>
+template <int D, int SW, int ROWS = 64, int NW = 4>
 struct DmaStager {
   static constexpr int PER_WAVE = ROWS * D / (512 * NW);
   static_assert(PER_WAVE >= 1, "tile smaller than one DMA instruction per wave");
@@ -265,8 +273,7 @@ struct DmaStager {
     for (int j = 0; j < PER_WAVE; ++j) {
       const int byte = (w * PER_WAVE + j) * 1024 + 16 * lane;
       const int p = byte / (2 * D), pc = (byte % (2 * D)) / 16;
-      const int sw = A_ONLY ? swz_a<D>(p) : swz<D>(p);
-      off[j] = kperm_row(p) * (int)ss * 2 + 16 * (pc ^ sw);
+      off[j] = kperm_row(p) * (int)ss * 2 + 16 * (pc ^ swz<D, SW>(p));
     }
   }
   __device__ __forceinline__ void load(f16 *slot, const f16 *head, int64_t ss, int r0, int S,
@@ -280,24 +287,53 @@ struct DmaStager {
 };
 
 // A-operand (32 x 16) fragment of X^T from a row-major LDS tile X with two
-// ds_read_b64_tr_b16 transpose loads, at `p` and `p + hi` (elements).
-// Transpose-load lane layout (measured on gfx950): in each 16-lane group,
-// source lane L addresses row L/4, columns 4*(L%4) .. +3 of a 4 x 16 block,
-// and lane i receives column i of the four rows.  So with p = the lane's
-// address of (row_lo + L/4, col0 + 16*((lane/16)%2) + 4*(L%4)) the lane
-// receives X[row_lo + j][col0 + lane % 32] in slots j = 0..3, and from the
-// block `hi` elements further the slots 4..7 (callers precompute p).
-// The transpose read moves 16-bit values without interpreting them, so one
-// fp16-typed read serves both element types (the result is bit-cast).
+// ds_read_b64_tr_b16 transpose loads, at `base + lo` and `base + hi`
+// (elements).  Transpose-load lane layout (measured on gfx950): in each
+// 16-lane group, source lane L addresses row L/4, columns 4*(L%4) .. +3 of a
+// 4 x 16 block, and lane i receives column i of the four rows.  So with the
+// lane's address of (row_lo + L/4, col0 + 16*((lane/16)%2) + 4*(L%4)) the
+// lane receives X[row_lo + j][col0 + lane % 32] in slots j = 0..3, and from
+// the same block 8 rows further the slots 4..7 (TrOffsets).  The transpose
+// read moves 16-bit values without interpreting them, so one fp16-typed
+// read serves both element types (the result is bit-cast).
 template <typename E>
-__device__ __forceinline__ vec8<E> load_tr_pair(const f16 *p, int hi) {
+__device__ __forceinline__ vec8<E> load_tr_pair(const f16 *base, int lo, int hi) {
   typedef __fp16 h4 __attribute__((vector_size(8)));
-  h4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) h4 *)p);
-  h4 up = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) h4 *)(p + hi));
-  const u32x2 a = __builtin_bit_cast(u32x2, lo), b = __builtin_bit_cast(u32x2, up);
-  const u32x4 r = {a[0], a[1], b[0], b[1]};
+  h4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) h4 *)(base + lo));
+  h4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) h4 *)(base + hi));
+  const u32x2 x = __builtin_bit_cast(u32x2, a0), y = __builtin_bit_cast(u32x2, a1);
+  const u32x4 r = {x[0], x[1], y[0], y[1]};
   return __builtin_bit_cast(vec8<E>, r);
 }
+
+// Per-lane element offsets of the transposed reads of a swizzled tile: for
+// column block d (32 columns), rows 4g + (l16 >> 2) (`lo`) and 8 rows
+// further (`hi`), column chunk 4d + 2((lane >> 4) & 1) + ((l16 >> 1) & 1),
+// half 4 * (l16 & 1).  Row offsets that are multiples of 16 (sub-blocks of
+// 32 rows, the 16-row halves) keep the swizzle.  With SW_T the swizzle
+// repeats every 8 rows and hi(d) is lo(d) + 8 D, an immediate; with SW_AT
+// the two reads take different chunk permutations and hi is a register.
+template <int D, int SW>
+struct TrOffsets {
+  static constexpr bool SPLIT = SW == SW_A || SW == SW_AT;
+  int lo_[D / 32];
+  int hi_[SPLIT ? D / 32 : 1];
+  __device__ __forceinline__ void init(int lane) {
+    const int l16 = lane & 15, tr = 4 * (lane >> 5) + (l16 >> 2);
+    const int half = 4 * (l16 & 1);
+#pragma unroll
+    for (int d = 0; d < D / 32; ++d) {
+      const int c = 4 * d + 2 * ((lane >> 4) & 1) + ((l16 >> 1) & 1);
+      lo_[d] = tr * D + ((c ^ swz<D, SW>(tr)) << 3) + half;
+      if constexpr (SPLIT) hi_[d] = (tr + 8) * D + ((c ^ swz<D, SW>(tr + 8)) << 3) + half;
+    }
+  }
+  __device__ __forceinline__ int lo(int d) const { return lo_[d]; }
+  __device__ __forceinline__ int hi(int d) const {
+    if constexpr (SPLIT) return hi_[d];
+    else return lo_[d] + 8 * D;
+  }
+};
 
 // 8 consecutive 16-bit values at p (16-byte aligned), as an E vector.
 template <typename E>

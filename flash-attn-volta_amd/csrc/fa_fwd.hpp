@@ -42,8 +42,8 @@
 
 namespace fa {
 
-#ifndef FA_FWD_W4
-#define FA_FWD_W4 0
+#ifndef FA_FWD_PFD
+#define FA_FWD_PFD 2
 #endif
 
 // Bound on a lane's per-tile sum of probabilities taken against a stale
@@ -89,8 +89,6 @@ struct FwdTile {
   static constexpr int BN = 64;            // keys per tile
   static constexpr int NT = 256;           // 4 waves
   static constexpr int LDS_TILE = BN * D;  // swizzled, unpadded (fa_common.hpp)
-  // waves per SIMD the register allocation is held to
-  static constexpr int WAVES_PER_EU = FA_FWD_W4 && D == 64 && KSPLIT == 2 ? 4 : 1;
   // O^T partial sums of a key-half wave handed over for the final merge
   static_assert(64 * (D / 2) * 4 <= LDS_TILE * 2, "a merge buffer must fit in one K slot");
 };
@@ -113,8 +111,7 @@ struct FwdTile {
 // writes its rows' normalised O and log2-domain LSE over that range to
 // part_o / part_lse, which fa_fwd_combine_kernel merges.
 template <typename E, int D, bool CAUSAL, int KSPLIT, bool SPLITKV = false, bool PRE = false>
-__global__ __launch_bounds__(256)
-__attribute__((amdgpu_waves_per_eu(FwdTile<D, KSPLIT>::WAVES_PER_EU))) void fa_fwd_kernel(FwdArgs a) {
+__global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   static_assert(!PRE || std::is_same<E, f16>::value, "the pre-scaled mode is fp16 only");
   using T = FwdTile<D, KSPLIT>;
   constexpr int NSUB = T::NSUB;
@@ -177,8 +174,8 @@ __attribute__((amdgpu_waves_per_eu(FwdTile<D, KSPLIT>::WAVES_PER_EU))) void fa_f
 
   // ---- K and V tiles go straight to LDS (fa_common.hpp DmaStager): both
   // in kperm row order, chunks swizzled; rows past Sk read as zeros.
-  DmaStager<D, 64, 4, true> stk;   // K: read only as A operands
-  DmaStager<D> stv;                 // V: read transposed
+  DmaStager<D, SW_A> stk;   // K: read only as A operands
+  DmaStager<D, SW_T> stv;   // V: read only transposed
   stk.init(w, lane, a.k.ss);
   stv.init(w, lane, a.v.ss);
   auto load_k = [&](int n0, auto sc) { stk.load(k_sl(sc), kb, a.k.ss, n0, Sk, w); };
@@ -199,17 +196,13 @@ __attribute__((amdgpu_waves_per_eu(FwdTile<D, KSPLIT>::WAVES_PER_EU))) void fa_f
   // Per-lane LDS element offsets inside a slot: K rows l32 (A operand of
   // S^T = K Q^T), chunk 2cc + g; V^T transpose reads of rows 4g + (l16 >> 2)
   // (and + 8), i.e. natural V rows 8g + (l16 >> 2) (and + 4).
-  int a_off[D / 16], t_off[D / 32];
+  int a_off[D / 16];
+  TrOffsets<D, SW_T> t_off;
   {
-    const int sa = swz_a<D>(l32);
+    const int sa = swz<D, SW_A>(l32);
 #pragma unroll
     for (int cc = 0; cc < D / 16; ++cc) a_off[cc] = l32 * D + (((2 * cc + g) ^ sa) << 3);
-    const int l16 = lane & 15, tr = 4 * g + (l16 >> 2);
-    const int st_ = swz<D>(tr);
-#pragma unroll
-    for (int d = 0; d < D / 32; ++d)
-      t_off[d] = tr * D + (((4 * d + 2 * ((lane >> 4) & 1) + ((l16 >> 1) & 1)) ^ st_) << 3) +
-                 4 * (l16 & 1);
+    t_off.init(lane);
   }
 
   // Sub-block sb (32 keys) of this wave in the tile at n0 starts at key
@@ -274,7 +267,8 @@ __attribute__((amdgpu_waves_per_eu(FwdTile<D, KSPLIT>::WAVES_PER_EU))) void fa_f
         const int rb = (32 * (NSUB * kh + sb) + 16 * hh) * D;
 #pragma unroll
         for (int d = 0; d < D / 32; ++d)
-          oacc[d] = mfma32(load_tr_pair<E>(v_sl(sc) + rb + t_off[d], 8 * D), pf[sb][hh], oacc[d]);
+          oacc[d] = mfma32(load_tr_pair<E>(v_sl(sc) + rb, t_off.lo(d), t_off.hi(d)), pf[sb][hh],
+                           oacc[d]);
       }
     }
   };
@@ -482,24 +476,26 @@ __attribute__((amdgpu_waves_per_eu(FwdTile<D, KSPLIT>::WAVES_PER_EU))) void fa_f
         return ld8<E>(ks + 32 * (NSUB * kh + sb) * D + a_off[cc]);
       }
       const int sb = j / (2 * (D / 32)), hh = (j / (D / 32)) % 2, d = j % (D / 32);
-      return load_tr_pair<E>(vs + (32 * (NSUB * kh + sb) + 16 * hh) * D + t_off[d], 8 * D);
+      return load_tr_pair<E>(vs + (32 * (NSUB * kh + sb) + 16 * hh) * D, t_off.lo(d), t_off.hi(d));
     };
     const float c_ = c, neg_m = -m_run;
     float l0 = 0.0f, l1 = 0.0f;
-    vec8<E> op[3];
-    op[0] = operand(std::integral_constant<int, 0>{});
-    if constexpr (M > 1) op[1] = operand(std::integral_constant<int, 1>{});
+    constexpr int PF = FA_FWD_PFD;   // operands read this many MFMAs ahead
+    vec8<E> op[PF + 1];
+    static_for<PF>([&](auto ic) {
+      if constexpr (decltype(ic)::value < M) op[decltype(ic)::value] = operand(ic);
+    });
     static_for<M>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
-      if constexpr (i + 2 < M) op[(i + 2) % 3] = operand(std::integral_constant<int, i + 2>{});
+      if constexpr (i + PF < M) op[(i + PF) % (PF + 1)] = operand(std::integral_constant<int, i + PF>{});
       bool is_q = false; int j = 0;
       kind_index(i, is_q, j);
       if (is_q) {
         const int sb = j / (D / 16), cc = j % (D / 16);
-        s_nxt[sb] = mfma32(op[i % 3], qf[cc], cc == 0 ? negm : s_nxt[sb]);
+        s_nxt[sb] = mfma32(op[i % (PF + 1)], qf[cc], cc == 0 ? negm : s_nxt[sb]);
       } else {
         const int sb = j / (2 * (D / 32)), hh = (j / (D / 32)) % 2, d = j % (D / 32);
-        oacc[d] = mfma32(op[i % 3], p_prev[sb][hh], oacc[d]);
+        oacc[d] = mfma32(op[i % (PF + 1)], p_prev[sb][hh], oacc[d]);
       }
       // softmax pairs [i * NPAIR / M, (i + 1) * NPAIR / M) of tile t
       static_for<(i + 1) * NPAIR / M - i * NPAIR / M>([&](auto kc) {
