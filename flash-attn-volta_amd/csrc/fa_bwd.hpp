@@ -48,10 +48,9 @@
 
 namespace fa {
 
-#ifndef FA_DKDV_SW
-#define FA_DKDV_SW SW_P8
-#endif
-constexpr int kDkdvSwizzle = FA_DKDV_SW;
+// Swizzle of the dK/dV kernel's tiles: SW_P8 (fa_common.hpp), not SW_AT,
+// whose second-read offsets would spill its registers.
+constexpr int kDkdvSwizzle = SW_P8;
 
 struct BwdArgs {
   TensorDesc q, k, v, dout;   // q, dout: (B, Sq, H, D); k, v: (B, Sk, Hk, D)

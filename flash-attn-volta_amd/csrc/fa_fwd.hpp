@@ -42,10 +42,6 @@
 
 namespace fa {
 
-#ifndef FA_FWD_PFD
-#define FA_FWD_PFD 2
-#endif
-
 // Bound on a lane's per-tile sum of probabilities taken against a stale
 // running max (so every probability is <= 2^15, inside fp16's range).
 constexpr float kFastSum = 32768.0f;
@@ -480,7 +476,7 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
     };
     const float c_ = c, neg_m = -m_run;
     float l0 = 0.0f, l1 = 0.0f;
-    constexpr int PF = FA_FWD_PFD;   // operands read this many MFMAs ahead
+    constexpr int PF = 2;   // operands read this many MFMAs ahead
     vec8<E> op[PF + 1];
     static_for<PF>([&](auto ic) {
       if constexpr (decltype(ic)::value < M) op[decltype(ic)::value] = operand(ic);
