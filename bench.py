@@ -339,17 +339,95 @@ def run_llama(steps, warmup):
 def peak_extra_bytes(step, grads):
     """Peak allocator bytes above what is allocated before one fwd+bwd step
     (inputs and dO), after a warm-up step -- the reference's measurement
-    (bench/backward.py:69-85): outputs, LSE, gradients and workspace."""
+    (bench/backward.py:69-85): outputs, LSE, gradients and workspace.  The
+    wrappers cache the workspace per stream; it is released before the
+    measured step, so the step allocates (and counts) it again."""
     import torch
+    from flash_attn_volta import release_workspaces
     step()
     for t in grads:
         t.grad = None
     torch.cuda.synchronize()
+    release_workspaces()
     torch.cuda.reset_peak_memory_stats()
     base = torch.cuda.memory_allocated()
     step()
     torch.cuda.synchronize()
     return torch.cuda.max_memory_allocated() - base
+
+
+def host_costs(q, k, v, do, causal, n=400):
+    """Host time per call (issue time: n calls back to back, no
+    synchronisation inside the timed loop) of the raw C-ABI calls with
+    prepared arguments, the Python wrappers, the autograd fwd+bwd step and
+    PyTorch SDPA's autograd step on the same inputs.  For a small config
+    (C2) the GPU keeps up with the host, so these are host costs; the
+    wrappers' overhead is wrapper minus raw call."""
+    import torch
+    from flash_attn_volta import _capi, flash_attn, flash_attn_backward, flash_attn_forward
+    from flash_attn_volta.forward import kernel_strides
+    lib = _capi.load()
+    b, s, h, d = q.shape
+    sc = 1.0 / math.sqrt(d)
+    out, lse = flash_attn_forward(q, k, v, causal=causal, return_softmax_lse=True)
+    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+    stv = kernel_strides(q)
+    stream = torch.cuda.current_stream().cuda_stream
+    ws_bytes = lib.fa_bwd_gqa_workspace_bytes(b, s, s, h, h, d, int(causal))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
+    qt, kt, vt = (t.detach().transpose(1, 2).clone().requires_grad_() for t in (q, k, v))
+    dot = do.transpose(1, 2).contiguous()
+
+    def c_fwd():
+        lib.fa_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                   b, s, h, d, stv, stv, stv, stv, sc, int(causal), stream)
+
+    def c_bwd():
+        lib.fa_bwd(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                   lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(),
+                   ws_bytes, b, s, h, d, stv, stv, stv, stv, stv, stv, stv, stv, sc, int(causal),
+                   stream)
+
+    def step():
+        qg.grad = kg.grad = vg.grad = None
+        flash_attn(qg, kg, vg, causal=causal).backward(do)
+
+    def sdpa_step():
+        qt.grad = kt.grad = vt.grad = None
+        torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, is_causal=causal).backward(dot)
+
+    items = (("c_fwd_us", c_fwd), ("wrapper_fwd_us", lambda: flash_attn_forward(q, k, v, causal=causal)),
+             ("c_bwd_us", c_bwd),
+             ("wrapper_bwd_us", lambda: flash_attn_backward(do, q, k, v, out, lse, causal=causal)),
+             ("autograd_step_us", step), ("sdpa_autograd_step_us", sdpa_step))
+    res = {}
+    for name, fn in items:
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        res[name] = round((time.perf_counter() - t0) / n * 1e6, 2)
+        torch.cuda.synchronize()
+    res["wrapper_fwd_overhead_us"] = round(res["wrapper_fwd_us"] - res["c_fwd_us"], 2)
+    res["wrapper_bwd_overhead_us"] = round(res["wrapper_bwd_us"] - res["c_bwd_us"], 2)
+    return res
+
+
+def steps_for(fn, steps, min_seconds=0.05):
+    """`steps`, raised so the timed loop lasts about min_seconds: a short
+    step (a small config's host-bound eager step) timed over 20 launches
+    is mostly noise."""
+    import torch
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    per = (time.perf_counter() - t0) / 3
+    return max(steps, min(2000, int(min_seconds / max(per, 1e-7))))
 
 
 def run_configs(steps, warmup, with_cpu):
@@ -373,12 +451,15 @@ def run_configs(steps, warmup, with_cpu):
         q, k, v, do = (t.cuda() for t in (qc, kc, vc, doc))
         qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
         flops = fwd_flops(b, s, h, d)
-        _, t_f = time_loop(lambda: flash_attn_forward(q, k, v, causal=causal, sm_scale=sc), steps, warmup)
+
+        def gpu_f():
+            flash_attn_forward(q, k, v, causal=causal, sm_scale=sc)
+        _, t_f = time_loop(gpu_f, steps_for(gpu_f, steps), warmup)
 
         def gpu_fb():
             qg.grad = kg.grad = vg.grad = None
             flash_attn(qg, kg, vg, causal=causal, sm_scale=sc).backward(do)
-        t_fb = time_loop(gpu_fb, steps, warmup)[1] if with_bwd else None
+        t_fb = time_loop(gpu_fb, steps_for(gpu_fb, steps), warmup)[1] if with_bwd else None
         # the same step captured once into a HIP graph and replayed: no
         # Python / autograd work on the host per step
         t_fbg = None
@@ -393,7 +474,7 @@ def run_configs(steps, warmup, with_cpu):
             qg.grad = kg.grad = vg.grad = None
             with torch.cuda.graph(graph):
                 flash_attn(qg, kg, vg, causal=causal, sm_scale=sc).backward(do)
-            t_fbg = time_loop(graph.replay, steps, warmup)[1]
+            t_fbg = time_loop(graph.replay, steps_for(graph.replay, steps), warmup)[1]
             del graph
         mem = {}
         if with_bwd:
@@ -402,6 +483,7 @@ def run_configs(steps, warmup, with_cpu):
                 fa_backward.split_workspace = split
                 mem[split] = peak_extra_bytes(gpu_fb, (qg, kg, vg))
             fa_backward.split_workspace = True
+        host = host_costs(q, k, v, do, causal) if name == "C2" else None
         row = {"config": name, "shape": [b, s, h, d], "causal": causal,
                "gpu_fwd_us": round(t_f * 1e6, 2), "gpu_fwd_tflops": round(flops / t_f / 1e12, 2),
                "gpu_fwd_pct_peak": round(100 * flops / t_f / 1e12 / PEAK_FP16_TFLOPS, 2)}
@@ -413,6 +495,8 @@ def run_configs(steps, warmup, with_cpu):
                         "gpu_fwd_bwd_graph_tflops": round(5 * flops / t_fbg / 1e12, 2),
                         "peak_extra_mb": round(mem[True] / 1e6, 2),
                         "peak_extra_mb_no_split": round(mem[False] / 1e6, 2)})
+        if host is not None:
+            row["host"] = host
         if with_cpu:
             with torch.no_grad():
                 t_cf, n_f = cpu_time(lambda: attention_ref_fp32(qc, kc, vc, causal=causal, sm_scale=sc), 10.0)

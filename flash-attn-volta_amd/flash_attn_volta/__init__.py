@@ -28,6 +28,9 @@ Beyond the reference (its wrapper requires q, k, v of one shape):
         flash_attn_gqa as torch.library custom ops (flash_attn_volta::fwd,
         flash_attn_volta::bwd) with fake-tensor and autograd registrations,
         so torch.compile keeps the call as one graph node.
+    release_workspaces
+        free the backward / split-KV workspaces, which are cached per stream
+        and reused by later calls.
 """
 
 from .forward import flash_attn_forward, flash_attn_forward_gqa, flash_attn_volta
@@ -35,6 +38,7 @@ from .backward import flash_attn_backward, flash_attn_backward_gqa
 from .autograd import flash_attn, flash_attn_gqa
 from .rope import apply_rotary_qk, rope_qk_backward, rope_qk_forward
 from .ops import flash_attn_op
+from ._runtime import release_workspaces
 
 __all__ = [
     "flash_attn_forward",
@@ -48,5 +52,6 @@ __all__ = [
     "rope_qk_forward",
     "rope_qk_backward",
     "flash_attn_op",
+    "release_workspaces",
 ]
 __version__ = "0.4.0"

@@ -401,3 +401,20 @@ def test_noalloc_validation_before_any_hip_call(lib):
     rows = _capi.NOALLOC_SCRATCH_BYTES // 4
     assert _bwd_noalloc(lib, B=1, Sq=rows // 64 + 1, Sk=128, H=64, Hk=64) == _capi.FA_ERR_SCRATCH
     assert lib.fa_strerror(_capi.FA_ERR_SCRATCH).decode().startswith("fa_bwd_gqa_noalloc")
+
+
+def test_torch_node_module_loads():
+    """The C++ autograd node (_fa_torch.so, built on the C ABI) imports on a
+    machine without a GPU and rejects a malformed plan."""
+    import pytest
+    try:
+        from flash_attn_volta import _fa_torch
+    except ImportError as e:
+        pytest.fail(f"_fa_torch is not built or does not load: {e}")
+    assert _fa_torch.PLAN_INTS == 36
+    with pytest.raises(RuntimeError, match="expected 36 integers"):
+        _fa_torch.make_plan([1, 2, 3], 0.125)
+    with pytest.raises(RuntimeError, match="unknown plan handle"):
+        import torch
+        t = torch.zeros(8)
+        _fa_torch.attn(12345, t, t, t, True)
