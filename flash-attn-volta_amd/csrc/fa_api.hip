@@ -479,6 +479,137 @@ int run_fwd_splitkv(const void *q, const void *k, const void *v, void *o, float 
   FA_DISPATCH(launch_fwd_splitkv, s, causal, L, st);
 }
 
+// ---------------------------------------------------------------------------
+// Balanced causal forward (fa_fwd_bal_item in fa_fwd.hpp): causal tiles
+// paired light with heavy, each pair cut in three work items dispatched
+// largest first, the split heavy tiles' halves merged by
+// fa_fwd_combine_kernel (pair mode).  For square causal grids (Sq == Sk)
+// with at least kBalMinTiles 64-row tiles per head whose plain grid is at
+// most one workgroup per CU.  There the plain schedule ends on single
+// workgroups sweeping every key tile alone (a lone workgroup's sweep runs
+// at about 90 % of a CU's two-workgroup throughput, so splitting it is what
+// shortens the kernel).  Measured on MI355X against the plain schedule
+// (merge included): (1, 4096, 4, 128) -17 %, (1, 4096, 2, 128) -26 %,
+// (1, 8192, 2, 128) -30 %, (1, 4096, 4, 64) -15 %; with fewer tiles per
+// head or two workgroups per CU it loses (+3 to +50 %: every work item
+// pays a workgroup's start-up of several microseconds, and the merge
+// launch costs about 4 us): (1, 2048, 8, 128) +3 %, (1, 4096, 8, 128)
+// +6 to +11 %, (4, 512, 4, 32) +50 %.
+
+constexpr int kBalMinTiles = 64;
+
+struct BalPlan {
+  int nb;   // 64-row query tiles per (b, h); 0: the balanced schedule does not apply
+};
+
+BalPlan bal_plan(const Shape &s, int causal) {
+  if (!causal || s.Sq != s.Sk) return BalPlan{0};
+  if (!row_split(s.Sq, (int64_t)s.B * s.H, true)) return BalPlan{0};
+  const int nb = (s.Sq + 63) / 64;
+  const int64_t grid = (int64_t)nb * s.B * s.H;
+  if (nb < kBalMinTiles || grid > (int64_t)device_cus()) return BalPlan{0};
+  return BalPlan{nb};
+}
+
+// Workspace: part_o (2, B, H, nb / 2, 64, D) fp32, then part_lse (2, B, H, nb / 2, 64) fp32.
+size_t bal_rows(const Shape &s, const BalPlan &p) {
+  return (size_t)s.B * (size_t)s.H * (size_t)(p.nb / 2) * 64;
+}
+
+size_t bal_bytes(const Shape &s, const BalPlan &p) {
+  if (p.nb == 0) return 0;
+  const size_t n = 2 * bal_rows(s, p) * (size_t)(s.D + 1) * sizeof(float);
+  return (n + 255) & ~(size_t)255;
+}
+
+struct BalLaunch {
+  fa::FwdArgs f;
+  fa::CombineArgs c;
+};
+
+template <typename E, int D, bool PRE>
+int launch_fwd_bal_mode(const BalLaunch &L, hipStream_t stream) {
+  using T = fa::FwdTile<D, 2>;
+  fa::FwdArgs a = L.f;
+  a.n_qtiles = (a.Sq + T::BM - 1) / T::BM;
+  a.zigzag = 0;
+  const int64_t grid = (int64_t)fa::bal_items(a.n_qtiles) * a.B * a.H;
+  if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
+  hipLaunchKernelGGL((fa::fa_fwd_kernel<E, D, true, 2, false, PRE, true>), dim3((unsigned)grid),
+                     dim3(T::NT), 0, stream, a);
+  int rc = launch_status();
+  if (rc) return rc;
+  fa::CombineArgs c = L.c;
+  c.pair_bm = T::BM;
+  c.nb = a.n_qtiles;
+  c.bn = T::BN;
+  c.Sk = a.Sk;
+  c.off = a.off;
+  c.n_splits = 2;
+  c.zgroups = 1;
+  constexpr int SLOTS = 256 / (D / 8);
+  const int64_t rows = (int64_t)a.B * a.H * (a.n_qtiles / 2) * T::BM;
+  const int64_t rpb = SLOTS / c.zgroups;
+  const int64_t gc = (rows + rpb - 1) / rpb;
+  if (gc > 0x7fffffff) return FA_ERR_TOO_LARGE;
+  hipLaunchKernelGGL((fa::fa_fwd_combine_kernel<E, D>), dim3((unsigned)gc), dim3(256), 0, stream,
+                     c);
+  return launch_status();
+}
+
+template <typename E, int D, bool CAUSAL>
+int launch_fwd_bal(const BalLaunch &L, hipStream_t stream) {
+  if constexpr (!CAUSAL) {
+    return FA_ERR_SHAPE;   // bal_plan applies to causal grids only
+  } else {
+    if constexpr (std::is_same<E, fa::f16>::value) {
+      if (fwd_prescaled<E>(L.f)) return launch_fwd_bal_mode<E, D, true>(L, stream);
+    }
+    return launch_fwd_bal_mode<E, D, false>(L, stream);
+  }
+}
+
+size_t fwd_ws_bytes(const Shape &s, int causal) {
+  const SplitPlan kv = splitkv_plan(s);
+  if (kv.n_splits) return splitkv_bytes(s, kv);
+  return bal_bytes(s, bal_plan(s, causal));
+}
+
+int run_fwd_ws(const void *q, const void *k, const void *v, void *o, float *lse, void *workspace,
+               size_t workspace_bytes, const Shape &s, const int64_t *q_st, const int64_t *k_st,
+               const int64_t *v_st, const int64_t *o_st, float sm_scale, int causal,
+               void *stream) {
+  int rc = check_fwd(q, k, v, o, lse, s, q_st, k_st, v_st, o_st, sm_scale);
+  if (rc) return rc;
+  // less than the schedule's workspace (none included): the plain forward
+  const size_t need = fwd_ws_bytes(s, causal);
+  if (need == 0 || workspace == nullptr || workspace_bytes < need)
+    return run_fwd(q, k, v, o, lse, s, q_st, k_st, v_st, o_st, sm_scale, causal, stream);
+  if (!aligned16(workspace)) return FA_ERR_ALIGNMENT;
+  if (splitkv_plan(s).n_splits)
+    return run_fwd_splitkv(q, k, v, o, lse, workspace, workspace_bytes, s, q_st, k_st, v_st, o_st,
+                           sm_scale, causal, stream);
+  const BalPlan plan = bal_plan(s, causal);
+  if (plan.nb == 0)
+    return run_fwd(q, k, v, o, lse, s, q_st, k_st, v_st, o_st, sm_scale, causal, stream);
+  BalLaunch L{};
+  L.f = fwd_args(q, k, v, o, lse, s, q_st, k_st, v_st, o_st, sm_scale);
+  L.f.part_o = static_cast<float *>(workspace);
+  L.f.part_lse = L.f.part_o + 2 * bal_rows(s, plan) * (size_t)s.D;
+  L.c.part_o = L.f.part_o;
+  L.c.part_lse = L.f.part_lse;
+  L.c.o = static_cast<f16 *>(o);
+  L.c.o_sb = o_st[0];
+  L.c.o_ss = o_st[1];
+  L.c.o_sh = o_st[2];
+  L.c.lse = lse;
+  L.c.B = s.B;
+  L.c.Sq = s.Sq;
+  L.c.H = s.H;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  FA_DISPATCH(launch_fwd_bal, s, causal, L, st);
+}
+
 int run_pre(const void *o, const void *dout, float *delta, const Shape &s, const int64_t *o_st,
             const int64_t *do_st, void *stream) {
   int rc = check_shape(s);
@@ -1124,6 +1255,22 @@ int fa_fwd_splitkv(const void *q, const void *k, const void *v, void *o, float *
   return run_fwd_splitkv(q, k, v, o, lse, workspace, workspace_bytes,
                          Shape{B, Sq, Sk, H, Hk, D, dtype}, q_strides, k_strides, v_strides,
                          o_strides, sm_scale, causal, stream);
+}
+
+size_t fa_fwd_workspace_bytes(int B, int Sq, int Sk, int H, int Hk, int D, int causal) {
+  const Shape s{B, Sq, Sk, H, Hk, D, FA_DTYPE_F16};
+  if (check_shape(s) != FA_OK) return 0;
+  return fwd_ws_bytes(s, causal);
+}
+
+int fa_fwd_ws(const void *q, const void *k, const void *v, void *o, float *lse,
+              void *workspace, size_t workspace_bytes,
+              int B, int Sq, int Sk, int H, int Hk, int D,
+              const int64_t q_strides[4], const int64_t k_strides[4],
+              const int64_t v_strides[4], const int64_t o_strides[4],
+              float sm_scale, int causal, int dtype, void *stream) {
+  return run_fwd_ws(q, k, v, o, lse, workspace, workspace_bytes, Shape{B, Sq, Sk, H, Hk, D, dtype},
+                    q_strides, k_strides, v_strides, o_strides, sm_scale, causal, stream);
 }
 
 int fa_bwd_preprocess(const void *o, const void *dout, float *delta,

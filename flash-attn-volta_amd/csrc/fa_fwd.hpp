@@ -62,7 +62,86 @@ struct FwdArgs {
   int kv_split;        // keys per split, a multiple of the 64-key tile
   float *part_o;       // (n_splits, B, H, Sq, D) fp32: each split's normalised O
   float *part_lse;     // (n_splits, B, H, Sq) fp32: each split's LSE in log2 units
+  // The balanced causal mode (BAL = true) writes its split tiles' halves to
+  // part_o / part_lse as (2, B, H, n_qtiles / 2, BM, D) and (2, B, H,
+  // n_qtiles / 2, BM): half, (b, h), pair, row in the tile.
 };
+
+// Key tiles (BN keys each) that query tile qt of BM rows sees under the
+// causal mask: keys up to the tile's last row + off, at most Sk.
+__device__ __forceinline__ int causal_tiles_of(int Sk, int off, int qt, int BM, int BN) {
+  const int e = min(Sk, qt * BM + BM + off);
+  return e > 0 ? (e + BN - 1) / BN : 0;
+}
+
+// Balanced causal schedule (fa_fwd_kernel<..., BAL = true>), for square
+// causal grids (Sq == Sk, 64-row tiles: query tile i sees n(i) = i + 1 key
+// tiles).  Tiles pair up light with heavy -- i = p and j = nb - 1 - p for
+// pair p -- and each pair's n(i) + n(j) = nb + 1 key tiles are cut in
+// three work items of one segment each:
+//   X: heavy tile j, key tiles [0, hx), hx = ceil((nb + 1) / 2);
+//   Y: heavy tile j, key tiles [hx, n(j)) (empty, and X whole, when
+//      n(j) <= hx);
+//   Z: light tile i, all its key tiles.
+// X and Y write tile j's two halves as partial results (slot (b, h, p),
+// half 0 and 1) that fa_fwd_combine_kernel merges.  With nb odd, the middle
+// tile (n = (nb + 1) / 2 key tiles) is one more item.  Items are ordered by
+// size, largest first -- every X (hx), the middle tile, then Y and Z
+// alternating as their sizes fall (Z of pair np - 1 - k, then Y of pair k)
+// -- and the grid is rank-major (workgroup = rank * B * H + (b, h)), so
+// each freed workgroup slot takes the largest item left: every slot ends
+// within about one item of the average instead of on the heaviest tile.
+struct BalItem {
+  int qt, t0, t1, part;   // tile qt, key tiles [t0, t1), partial slot * 2 + half or -1
+};
+
+__device__ __forceinline__ bool bal_split(int ni, int nj, int &hx) {
+  hx = min((ni + nj + 1) >> 1, nj);
+  return hx > 0 && hx < nj;
+}
+
+__device__ __forceinline__ BalItem fa_fwd_bal_item(const FwdArgs &a, int u, int bh, int BM,
+                                                   int BN) {
+  const int nb = a.n_qtiles, np = nb >> 1, odd = nb & 1;
+  BalItem it{0, 0, 0, -1};
+  int p, kind;   // kind 0: X, 1: Y, 2: Z
+  if (u < np) {
+    p = u;
+    kind = 0;
+  } else if (odd && u == np) {
+    it.qt = np;   // the middle tile, whole
+    it.t1 = causal_tiles_of(a.Sk, a.off, np, BM, BN);
+    return it;
+  } else {
+    const int r = u - np - odd, k = r >> 1;
+    p = (r & 1) ? k : np - 1 - k;
+    kind = (r & 1) ? 1 : 2;
+  }
+  const int i = p, j = nb - 1 - p;
+  const int ni = causal_tiles_of(a.Sk, a.off, i, BM, BN);
+  const int nj = causal_tiles_of(a.Sk, a.off, j, BM, BN);
+  int hx;
+  const bool split = bal_split(ni, nj, hx);
+  const int slot = bh * np + p;
+  if (kind == 0) {
+    it.qt = j;
+    it.t1 = split ? hx : nj;
+    it.part = split ? 2 * slot : -1;
+  } else if (kind == 1) {
+    it.qt = split ? j : -1;   // -1: nothing to do
+    it.t0 = hx;
+    it.t1 = nj;
+    it.part = 2 * slot + 1;
+  } else {
+    it.qt = i;
+    it.t1 = ni;
+  }
+  return it;
+}
+
+// Work items per (b, h) of the balanced schedule: three per pair, one more
+// for an odd middle tile.
+__host__ __device__ constexpr int bal_items(int nb) { return 3 * (nb >> 1) + (nb & 1); }
 
 // f(integral_constant<int, 0>), ..., f(integral_constant<int, N - 1>): a loop
 // whose index is a compile-time constant in the body (register arrays
@@ -106,9 +185,11 @@ struct FwdTile {
 // tile; blockIdx.y selects a range of kv_split keys, and the workgroup
 // writes its rows' normalised O and log2-domain LSE over that range to
 // part_o / part_lse, which fa_fwd_combine_kernel merges.
-template <typename E, int D, bool CAUSAL, int KSPLIT, bool SPLITKV = false, bool PRE = false>
+template <typename E, int D, bool CAUSAL, int KSPLIT, bool SPLITKV = false, bool PRE = false,
+          bool BAL = false>
 __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   static_assert(!PRE || std::is_same<E, f16>::value, "the pre-scaled mode is fp16 only");
+  static_assert(!BAL || (CAUSAL && !SPLITKV), "the balanced schedule is for causal grids");
   using T = FwdTile<D, KSPLIT>;
   constexpr int NSUB = T::NSUB;
   constexpr int BM = T::BM, BN = T::BN;
@@ -132,9 +213,22 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   // heavy / light when it fits one round (co-resident workgroups then share
   // a CU's time evenly).  Workgroups of one (b, h) are BH apart, so with
   // BH % 8 == 0 they land on one XCD and share its L2.
-  const int qt = (CAUSAL && !SPLITKV)
-                     ? a.n_qtiles - 1 - (a.zigzag ? zigzag_rank(bid / BH, a.n_qtiles) : bid / BH)
-                     : bid / BH;
+  //
+  // BAL: the work item of rank bid / BH (fa_fwd_bal_item): query tile qt
+  // against key tiles [t0, t1), into O or, part >= 0, into a partial.
+  int qt, t0 = 0, t1 = 0, part = -1;
+  if constexpr (BAL) {
+    const BalItem it = fa_fwd_bal_item(a, bid / BH, bh, BM, BN);
+    if (it.qt < 0) return;   // an empty half of a tile that runs whole
+    qt = it.qt;
+    t0 = it.t0;
+    t1 = it.t1;
+    part = it.part;
+  } else {
+    qt = (CAUSAL && !SPLITKV)
+             ? a.n_qtiles - 1 - (a.zigzag ? zigzag_rank(bid / BH, a.n_qtiles) : bid / BH)
+             : bid / BH;
+  }
   const int hx = SPLITKV ? a.H / grp : a.H;
   const int b = bh / hx;
   const int h = SPLITKV ? 0 : bh % hx;               // SPLITKV: the head is per lane
@@ -155,9 +249,10 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   const int wpos_hi = SPLITKV ? (wq0 + 31) / grp : wq0 + 31;
   const int bpos_hi = SPLITKV ? min((q0 + BM - 1) / grp, Sq - 1) : q0 + BM - 1;
 
-  // Key range of this workgroup: all keys, or split blockIdx.y's
-  const int kbase = SPLITKV ? (int)blockIdx.y * a.kv_split : 0;
-  const int Sk = SPLITKV ? min(a.kv_split, a.Sk - kbase) : a.Sk;
+  // Key range of this workgroup: all keys, split blockIdx.y's, or (BAL)
+  // key tiles [t0, t1)
+  const int kbase = SPLITKV ? (int)blockIdx.y * a.kv_split : (BAL ? t0 * BN : 0);
+  const int Sk = SPLITKV ? min(a.kv_split, a.Sk - kbase) : (BAL ? min(a.Sk, t1 * BN) - kbase : a.Sk);
   const int off = a.off - kbase;   // key j (relative) is visible to position i iff j <= i + off
 
   const f16 *kb = a.k.head(b, hk) + (int64_t)kbase * a.k.ss;
@@ -570,11 +665,18 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   // ---- epilogue: O = acc / l, LSE = (m + log2 l) * ln2
   const float l_tot = l_run + xor32(l_run);
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  if (SPLITKV) {
+  if (SPLITKV || (BAL && part >= 0)) {
     // this split's normalised O and log2-domain LSE (-inf: no visible key)
     if (qrow < nrows) {
-      const int hq = hk * grp + qrow % grp;
-      const int64_t prow = (((int64_t)blockIdx.y * a.B + b) * a.H + hq) * Sq + qrow / grp;
+      int64_t prow;
+      if (SPLITKV) {
+        const int hq = hk * grp + qrow % grp;
+        prow = (((int64_t)blockIdx.y * a.B + b) * a.H + hq) * Sq + qrow / grp;
+      } else {
+        // (half, slot (b, h, pair), row in the tile)
+        const int64_t rows = (int64_t)BH * (a.n_qtiles >> 1) * BM;
+        prow = (part & 1) * rows + (int64_t)(part >> 1) * BM + (qrow - q0);
+      }
       float *po = a.part_o + prow * D;
 #pragma unroll
       for (int d = 0; d < D / 32; ++d) {
@@ -616,13 +718,20 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
 // `zgroups` lane groups (split z to group z % zgroups), each merging its
 // splits online with a running maximum; the groups then merge through LDS
 // in group order.  Every sum has a fixed order (reproducible results).
+//
+// Pair mode (pair_bm > 0): the partials of the balanced causal schedule
+// (fa_fwd_bal_item), two per row of a split heavy tile; rows of tiles that
+// ran whole are skipped (the forward kernel wrote them).
 struct CombineArgs {
-  const float *part_o, *part_lse;   // as written by fa_fwd_kernel<..., SPLITKV>
+  const float *part_o, *part_lse;   // as written by fa_fwd_kernel<..., SPLITKV or BAL>
   f16 *o;
   int64_t o_sb, o_ss, o_sh;
   float *lse;                       // (B, H, Sq) or nullptr
   int B, Sq, H, n_splits;
   int zgroups;                      // power of two, at most 256 / (D / 8)
+  // pair mode: the forward's tile rows (0: split-KV layout), query tiles
+  // per (b, h), key tile and causal offset
+  int pair_bm, nb, bn, Sk, off;
 };
 
 template <typename E, int D>
@@ -635,9 +744,28 @@ __global__ __launch_bounds__(256) void fa_fwd_combine_kernel(CombineArgs a) {
   const int rpb = SLOTS / zn;
   const int slot = threadIdx.x / LPR, j = threadIdx.x % LPR;
   const int rloc = slot / zn, zg = slot % zn;
-  const int64_t rows = (int64_t)a.B * a.H * a.Sq;
   const int64_t row = (int64_t)blockIdx.x * rpb + rloc;
-  const bool valid = row < rows;
+  // the partials' row count, and this row's (b, h) and position
+  int64_t rows, bh;
+  int s;
+  bool valid;
+  if (a.pair_bm > 0) {
+    const int np = a.nb >> 1;
+    rows = (int64_t)a.B * a.H * np * a.pair_bm;
+    const int64_t ps = row / a.pair_bm;   // slot (b, h, pair)
+    const int p = (int)(ps % np), jt = a.nb - 1 - p;
+    bh = ps / np;
+    s = jt * a.pair_bm + (int)(row % a.pair_bm);
+    int hx;
+    valid = row < rows && s < a.Sq &&
+            bal_split(causal_tiles_of(a.Sk, a.off, p, a.pair_bm, a.bn),
+                      causal_tiles_of(a.Sk, a.off, jt, a.pair_bm, a.bn), hx);
+  } else {
+    rows = (int64_t)a.B * a.H * a.Sq;
+    bh = row / a.Sq;
+    s = (int)(row % a.Sq);
+    valid = row < rows;
+  }
 
   float m = kNegInf, sum = 0.0f;
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -687,14 +815,13 @@ __global__ __launch_bounds__(256) void fa_fwd_combine_kernel(CombineArgs a) {
     }
   }
   const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
-  const int s = (int)(row % a.Sq);
-  const int64_t bh = row / a.Sq;
   const int hh = (int)(bh % a.H), b = (int)(bh / a.H);
   vec8<E> out;
 #pragma unroll
   for (int i = 0; i < 8; ++i) out[i] = (E)(o8[i] * inv);
   *(vec8<E> *)(a.o + b * a.o_sb + s * a.o_ss + hh * a.o_sh + 8 * j) = out;
-  if (a.lse != nullptr && j == 0) a.lse[row] = tot > 0.0f ? (mt + fast_log2(tot)) * kLn2 : kPosInf;
+  if (a.lse != nullptr && j == 0)
+    a.lse[bh * a.Sq + s] = tot > 0.0f ? (mt + fast_log2(tot)) * kLn2 : kPosInf;
 }
 
 }  // namespace fa

@@ -40,7 +40,7 @@ struct Plan {
   float scale;
   int64_t q_st[4], k_st[4], v_st[4], o_st[4];   // kernel strides, 0 for size-1 dims
   int64_t dq_st[4], dk_st[4];                   // contiguous gradients
-  size_t fwd_ws;                                // fa_fwd_splitkv workspace, 0: no split
+  size_t fwd_ws;                                // fa_fwd_ws workspace, 0: plain forward
   size_t ws_split, ws_plain;                    // backward workspace, split schedule or not
 };
 
@@ -103,11 +103,10 @@ struct FlashAttnFn : public torch::autograd::Function<FlashAttnFn> {
     void *stream = stream_of(q);
     if (p.fwd_ws) {
       Tensor ws = at::empty({(int64_t)p.fwd_ws}, q.options().dtype(at::kByte));
-      check(fa_fwd_splitkv(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-                           lse.data_ptr<float>(), ws.data_ptr(), p.fwd_ws, p.B, p.Sq, p.Sk, p.H,
-                           p.Hk, p.D, p.q_st, p.k_st, p.v_st, p.o_st, p.scale, p.causal, p.dtype,
-                           stream),
-            "fa_fwd_splitkv");
+      check(fa_fwd_ws(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                      lse.data_ptr<float>(), ws.data_ptr(), p.fwd_ws, p.B, p.Sq, p.Sk, p.H, p.Hk,
+                      p.D, p.q_st, p.k_st, p.v_st, p.o_st, p.scale, p.causal, p.dtype, stream),
+            "fa_fwd_ws");
     } else if (p.gqa) {
       check(fa_fwd_gqa(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                        lse.data_ptr<float>(), p.B, p.Sq, p.Sk, p.H, p.Hk, p.D, p.q_st, p.k_st,

@@ -14,7 +14,7 @@ import threading
 LIB_NAME = "libfa_mi355x.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # status codes (enum fa_status)
 FA_OK = 0
@@ -46,6 +46,8 @@ EXPORTED_SYMBOLS = (
     "fa_fwd_gqa",
     "fa_fwd_splitkv",
     "fa_fwd_splitkv_workspace_bytes",
+    "fa_fwd_ws",
+    "fa_fwd_workspace_bytes",
     "fa_bwd_preprocess",
     "fa_bwd_workspace_bytes",
     "fa_bwd_gqa_workspace_bytes",
@@ -99,6 +101,13 @@ def _declare(lib):
                                    ctypes.c_float, _ci, _ci, _vp]
     lib.fa_fwd_splitkv_workspace_bytes.restype = ctypes.c_size_t
     lib.fa_fwd_splitkv_workspace_bytes.argtypes = [_ci, _ci, _ci, _ci, _ci, _ci]
+    lib.fa_fwd_ws.restype = _ci
+    lib.fa_fwd_ws.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t,
+                              _ci, _ci, _ci, _ci, _ci, _ci,
+                              _i64x4, _i64x4, _i64x4, _i64x4,
+                              ctypes.c_float, _ci, _ci, _vp]
+    lib.fa_fwd_workspace_bytes.restype = ctypes.c_size_t
+    lib.fa_fwd_workspace_bytes.argtypes = [_ci, _ci, _ci, _ci, _ci, _ci, _ci]
     lib.fa_bwd_preprocess.restype = _ci
     lib.fa_bwd_preprocess.argtypes = [_vp, _vp, _vp, _ci, _ci, _ci, _ci, _i64x4, _i64x4, _vp]
     lib.fa_bwd_workspace_bytes.restype = ctypes.c_size_t

@@ -219,21 +219,20 @@ class _FwdPlan:
         p.like = q.stride() == o_st          # empty_like(q) is then contiguous
         st = (kernel_strides(q), kernel_strides(k), kernel_strides(v), _strides_c(p.out_shape, o_st))
         p.sizes, p.st, p.q_stride, p.k_stride = (B, Sq, Sk, H, Hk, D), st, q.stride(), k.stride()
-        p.ws_bytes = 0
         p.bwd = None
         p.cpp = 0
-        if gqa:
-            dt = _DTYPES[q.dtype]
-            if (H // Hk) * Sq <= 64:
-                p.ws_bytes = int(_capi.load().fa_fwd_splitkv_workspace_bytes(B, Sq, Sk, H, Hk, D))
-            if p.ws_bytes:
-                p.name = "fa_fwd_splitkv"
-                p.args = _runtime.convert(p.name, 6, (p.ws_bytes, B, Sq, Sk, H, Hk, D, *st,
-                                                      p.sm_scale, int(p.causal), dt))
-            else:
-                p.name = "fa_fwd_gqa"
-                p.args = _runtime.convert(p.name, 5, (B, Sq, Sk, H, Hk, D, *st, p.sm_scale,
-                                                      int(p.causal), dt))
+        dt = _DTYPES[q.dtype]
+        # the schedule with a workspace (split-KV for decode shapes, the
+        # balanced causal one for square one-round causal grids), if any
+        p.ws_bytes = int(_capi.load().fa_fwd_workspace_bytes(B, Sq, Sk, H, Hk, D, int(p.causal)))
+        if p.ws_bytes:
+            p.name = "fa_fwd_ws"
+            p.args = _runtime.convert(p.name, 6, (p.ws_bytes, B, Sq, Sk, H, Hk, D, *st,
+                                                  p.sm_scale, int(p.causal), dt))
+        elif gqa:
+            p.name = "fa_fwd_gqa"
+            p.args = _runtime.convert(p.name, 5, (B, Sq, Sk, H, Hk, D, *st, p.sm_scale,
+                                                  int(p.causal), dt))
         else:
             p.name = "fa_fwd"
             p.args = _runtime.convert(p.name, 5, (B, Sq, H, D, *st, p.sm_scale, int(p.causal)))
@@ -326,14 +325,14 @@ def _run_fwd(q, k, v, causal, sm_scale, write_lse, gqa):
     lse_ptr = lse.data_ptr() if lse is not None else None
     with _on_device(q.device):
         stream = _stream_ptr(q.device)
-        nbytes = _splitkv_bytes(lib, B, N, Sk, H, Hk, D) if gqa else 0
+        nbytes = _fwd_ws_bytes(lib, B, N, Sk, H, Hk, D, causal)
         if nbytes:
-            # short query block against long keys (decode): split the keys
+            # a schedule with a workspace: split-KV (decode) or balanced causal
             ws = _runtime.workspace(nbytes, q.device, stream)
-            rc = lib.fa_fwd_splitkv(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-                                    lse_ptr, ws.data_ptr(), nbytes, B, N, Sk, H, Hk, D, *st,
-                                    float(sm_scale), int(bool(causal)), _DTYPES[q.dtype], stream)
-            _capi.check(rc, "fa_fwd_splitkv")
+            rc = lib.fa_fwd_ws(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                               lse_ptr, ws.data_ptr(), nbytes, B, N, Sk, H, Hk, D, *st,
+                               float(sm_scale), int(bool(causal)), _DTYPES[q.dtype], stream)
+            _capi.check(rc, "fa_fwd_ws")
             return out, lse
         if gqa:
             rc = lib.fa_fwd_gqa(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse_ptr,
@@ -346,19 +345,17 @@ def _run_fwd(q, k, v, causal, sm_scale, write_lse, gqa):
     return out, lse
 
 
-_SPLITKV_BYTES = {}
+_FWD_WS_BYTES = {}
 
 
-def _splitkv_bytes(lib, B, Sq, Sk, H, Hk, D) -> int:
-    """Workspace bytes of fa_fwd_splitkv when the library would split the
-    keys for these sizes on this device (decode-like shapes), else 0.  Only
-    short query blocks can qualify, so longer ones skip the query."""
-    if (H // Hk) * Sq > 64:
-        return 0
-    key = (B, Sq, Sk, H, Hk, D, _runtime.current_device())
-    nbytes = _SPLITKV_BYTES.get(key)
+def _fwd_ws_bytes(lib, B, Sq, Sk, H, Hk, D, causal) -> int:
+    """fa_fwd_workspace_bytes for these sizes on the current device (0: the
+    plain forward), cached."""
+    key = (B, Sq, Sk, H, Hk, D, bool(causal), _runtime.current_device())
+    nbytes = _FWD_WS_BYTES.get(key)
     if nbytes is None:
-        nbytes = _SPLITKV_BYTES[key] = int(lib.fa_fwd_splitkv_workspace_bytes(B, Sq, Sk, H, Hk, D))
+        nbytes = _FWD_WS_BYTES[key] = int(lib.fa_fwd_workspace_bytes(B, Sq, Sk, H, Hk, D,
+                                                                     int(bool(causal))))
     return nbytes
 
 

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 7
+#define FA_ABI_VERSION 8
 
 /* Size of the static device scratch buffer that fa_bwd_gqa_noalloc uses as
  * its workspace (one per GPU, held for the life of the process). */
@@ -140,6 +140,38 @@ int fa_fwd_splitkv(const void *q, const void *k, const void *v, void *o, float *
  * device (its compute-unit count sets the split), 0 when it would not split
  * (or for invalid sizes). */
 size_t fa_fwd_splitkv_workspace_bytes(int B, int Sq, int Sk, int H, int Hk, int D);
+
+/*
+ * Forward with a workspace: the schedule that is fastest for these sizes.
+ * Same arguments and results as fa_fwd_gqa (to fp32 rounding of a merge),
+ * plus `workspace`, `workspace_bytes`.
+ *   - Short query blocks against long keys: fa_fwd_splitkv's key split.
+ *   - Causal, Sq == Sk, at least 64 query tiles of 64 rows per head and at
+ *     most one tile per compute unit in the plain grid: query tiles paired
+ *     light with heavy (tile p with tile nb - 1 - p), each pair cut in
+ *     three work items of about a third of the pair each (the heavy tile's
+ *     two key halves, the light tile); the heavy tile's halves go to the
+ *     workspace in fp32 and a second kernel merges them through their
+ *     log-sum-exps.  The plain schedule ends on the heaviest query tiles,
+ *     each sweeping every key tile alone on its compute unit.
+ *   - Otherwise: fa_fwd_gqa, the workspace untouched.
+ * A workspace smaller than fa_fwd_workspace_bytes (NULL / 0 included)
+ * selects the plain forward; a used workspace must be 16-byte aligned.
+ *
+ * No counterpart in the reference, whose causal kernel sweeps each query
+ * block's keys in one program (flash_attn_volta/triton_fa.py:110-117).
+ */
+int fa_fwd_ws(const void *q, const void *k, const void *v, void *o, float *lse,
+              void *workspace, size_t workspace_bytes,
+              int B, int Sq, int Sk, int H, int Hk, int D,
+              const int64_t q_strides[4], const int64_t k_strides[4],
+              const int64_t v_strides[4], const int64_t o_strides[4],
+              float sm_scale, int causal, int dtype, void *stream);
+
+/* Workspace bytes with which fa_fwd_ws runs its fastest schedule for these
+ * sizes on the current device (its compute-unit count decides), 0 when the
+ * plain forward is that schedule (or for invalid sizes). */
+size_t fa_fwd_workspace_bytes(int B, int Sq, int Sk, int H, int Hk, int D, int causal);
 
 /*
  * Backward pre-pass: delta[b,h,s] = sum_d o[b,s,h,d] * do[b,s,h,d] in fp32.

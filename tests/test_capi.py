@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.fa_abi_version() == _capi.ABI_VERSION == 7
+    assert lib.fa_abi_version() == _capi.ABI_VERSION == 8
 
 
 def test_noalloc_scratch_size_matches_header():
@@ -259,6 +259,33 @@ def test_rope_bwd_validation(lib):
     assert call(dq=None) == _capi.FA_ERR_NULL_POINTER
     assert call(dq=BAD) == _capi.FA_ERR_ALIGNMENT
     assert call(eps=-1.0) == _capi.FA_ERR_EPS
+
+
+def test_fwd_workspace_plan_and_validation(lib):
+    """fa_fwd_ws: the workspace query (256 compute units assumed on the CPU)
+    is the split-KV size for decode shapes, the balanced causal size for
+    square causal grids of at least 64 tiles per head and one tile per CU,
+    0 otherwise; a call that would use a workspace rejects a misaligned one
+    before any HIP call."""
+    ws = lib.fa_fwd_workspace_bytes
+    kv = lib.fa_fwd_splitkv_workspace_bytes
+    assert ws(1, 1, 4096, 32, 8, 128, 1) == kv(1, 1, 4096, 32, 8, 128) > 0   # decode
+    n = ws(1, 4096, 4096, 4, 4, 128, 1)          # 64 tiles x 4 heads: one per CU
+    rows = 1 * 4 * (4096 // 64 // 2) * 64        # (b, h, pair, row) of the split tiles
+    assert n % 256 == 0 and n >= 2 * rows * (128 + 1) * 4
+    assert ws(1, 4096, 4096, 4, 2, 128, 1) == n  # grouped heads: same grid
+    assert ws(1, 4096, 4096, 4, 4, 128, 0) == 0  # not causal
+    assert ws(1, 4096, 4096, 8, 8, 128, 1) == 0  # two tiles per CU (config C4b)
+    assert ws(1, 2048, 2048, 4, 4, 128, 1) == 0  # 32 tiles per head: too few
+    assert ws(1, 4000, 4096, 4, 4, 128, 1) == 0  # Sq != Sk
+    assert ws(1, 4096, 4096, 4, 3, 128, 1) == 0  # invalid (H % Hk)
+    st = _st(1, 4096, 4, 128)
+    assert lib.fa_fwd_ws(P, P, P, P, None, BAD, n, 1, 4096, 4096, 4, 4, 128, st, st, st, st,
+                         0.1, 1, _capi.FA_DTYPE_F16, None) == _capi.FA_ERR_ALIGNMENT
+    assert lib.fa_fwd_ws(None, P, P, P, None, P, n, 1, 4096, 4096, 4, 4, 128, st, st, st, st,
+                         0.1, 1, _capi.FA_DTYPE_F16, None) == _capi.FA_ERR_NULL_POINTER
+    assert lib.fa_fwd_ws(P, P, P, P, None, P, n, 1, 4096, 4096, 4, 4, 96, st, st, st, st,
+                         0.1, 1, _capi.FA_DTYPE_F16, None) == _capi.FA_ERR_HEAD_DIM
 
 
 def test_splitkv_plan_and_validation(lib):
