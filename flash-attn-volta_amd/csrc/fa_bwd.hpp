@@ -694,6 +694,121 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
       }
     };
 
+    // One sub-block's S, dP, softmax gradient and dV / dK MFMAs as one block
+    // in program order, so the VALU work issues under MFMAs it does not
+    // depend on --
+    //   S MFMAs;  dP MFMAs, with exp2 of S (P, rounded to E) between them;
+    //   dV MFMAs (they need only P), with dS = P (dP - delta) and its max
+    //   between them;  dK MFMAs, with dS's scaled conversion between.
+    // A MFMA runs ~32 cycles in the matrix pipe while the wave issues the
+    // VALU slice after it; sched_barrier(0) keeps the compiler from
+    // regrouping the slices.  Invisible scores (diagonal and ragged
+    // sub-blocks only) get a -inf seed, so S is -inf and P = 0 there, as in
+    // grad(); |sm_scale| > ln 2 scales S by cr before the exp2, as grad()
+    // does.  Same operations on the same values as s_dp() + grad().
+    auto sdp_grad = [&](int sb) {
+      constexpr int NC = D / 16;          // S / dP MFMAs (K-dim chunks of 16)
+      constexpr int NO = 2 * (D / 32);    // dV / dK MFMAs (2 query halves x D / 32)
+      const int qs = NSUB * qh + sb;
+      floatx16 sacc, dpacc;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int r = 32 * qs + 16 * hh + 8 * g;
+        const floatx4 l_lo = *(const floatx4 *)&s_lse[st][r];
+        const floatx4 l_hi = *(const floatx4 *)&s_lse[st][r + 4];
+        const floatx4 d_lo = *(const floatx4 *)&s_dl[st][r];
+        const floatx4 d_hi = *(const floatx4 *)&s_dl[st][r + 4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          sacc[8 * hh + j] = l_lo[j];
+          sacc[8 * hh + 4 + j] = l_hi[j];
+          dpacc[8 * hh + j] = d_lo[j];
+          dpacc[8 * hh + 4 + j] = d_hi[j];
+        }
+      }
+      const int ms = sub_m(sb);
+      if ((CAUSAL && ms + off < wk0 + 31) || (ms + 31 >= Sq) || (wk0 + 31 >= Sk)) {
+        // query ms + slot_row(i, g) sees this lane's key iff
+        // lo <= slot_row(i, 0) < hi (nothing when the key is past Sk)
+        const int base = ms + 8 * g;
+        const int hi = key < Sk ? Sq - base : -(1 << 30);
+        const int lo = CAUSAL ? key - off - base : -(1 << 30);
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          sacc[i] = (slot_row(i, 0) >= lo && slot_row(i, 0) < hi) ? sacc[i] : kNegInf;
+      }
+      const f16 *qr = q_st(stc) + 32 * qs * D;
+      const f16 *gr = do_st(stc) + 32 * qs * D;
+      static_for<NC>([&](auto ic) {
+        constexpr int cc = decltype(ic)::value;
+        sacc = mfma32(ld8<E>(qr + a_off[cc]), k_frag(cc, a_off[cc]), sacc);
+      });
+      if (cr != 1.0f) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sacc[i] *= cr;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // dP MFMAs; exp2 of S in NC - 1 slices after the second one onwards
+      // (S's last MFMA has finished by then)
+      floatx16 p;
+      vec8<E> pf[2];
+      static_for<NC>([&](auto ic) {
+        constexpr int cc = decltype(ic)::value;
+        dpacc = mfma32(ld8<E>(gr + a_off[cc]), v_frag(cc, a_off[cc]), dpacc);
+        if constexpr (cc >= 1) {
+          constexpr int i0 = (cc - 1) * 16 / (NC - 1), i1 = cc * 16 / (NC - 1);
+          static_for<i1 - i0>([&](auto kc) {
+            constexpr int i = i0 + decltype(kc)::value;
+            p[i] = fast_exp2(sacc[i]);
+            pf[i >> 3][i & 7] = (E)p[i];
+          });
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      // dV^T += dO^T P, with dS = P dP (into p: P is needed as E only from
+      // here on) and its max in NO - 1 slices
+      floatx16 &ds = p;
+      float mk = 0.0f;
+      const int rb0 = (32 * qs) * D;
+      static_for<NO>([&](auto io) {
+        constexpr int o = decltype(io)::value;
+        constexpr int hh = o / (D / 32), d = o % (D / 32);
+        dv[d] = mfma32(load_tr_pair<E>(do_st(stc) + rb0 + 16 * hh * D, t_off.lo(d), t_off.hi(d)),
+                       pf[hh], dv[d]);
+        if constexpr (o >= 1) {
+          constexpr int i0 = (o - 1) * 16 / (NO - 1), i1 = o * 16 / (NO - 1);
+          static_for<i1 - i0>([&](auto kc) {
+            constexpr int i = i0 + decltype(kc)::value;
+            ds[i] *= dpacc[i];
+            mk = fmaxf(mk, fabsf(ds[i]));
+          });
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      });
+      // adaptive power-of-two scale of this key's dS column (as grad())
+      {
+        const float f = sc.update(max_xor32(mk));
+        if (__any(f != 1.0f)) {
+#pragma unroll
+          for (int d = 0; d < D / 32; ++d)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) dk[d][i] *= f;
+        }
+      }
+      // dK^T += Q^T dS: each query half's 8 conversions before its MFMAs
+      vec8<E> dsf[2];
+      static_for<2>([&](auto ih) {
+        constexpr int hh = decltype(ih)::value;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dsf[hh][j] = (E)(ds[8 * hh + j] * sc.mul);
+        static_for<D / 32>([&](auto id) {
+          constexpr int d = decltype(id)::value;
+          dk[d] = mfma32(load_tr_pair<E>(q_st(stc) + rb0 + 16 * hh * D, t_off.lo(d), t_off.hi(d)),
+                         dsf[hh], dk[d]);
+        });
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    };
     if constexpr (T::EARLY_S) {
       floatx16 sacc[NSUB], dpacc[NSUB];
 #pragma unroll
@@ -705,10 +820,7 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
     } else {
 #pragma unroll
       for (int sb = 0; sb < NSUB; ++sb) {
-        if (!live(sb)) continue;
-        floatx16 sacc, dpacc;
-        s_dp(sb, sacc, dpacc);
-        grad(sb, sacc, dpacc);
+        if (live(sb)) sdp_grad(sb);
       }
     }
 

@@ -197,6 +197,18 @@ __device__ __forceinline__ int zigzag_rank(int r, int n) {
   return r < half ? r : n - 1 - (r - half);
 }
 
+// f(integral_constant<int, 0>), ..., f(integral_constant<int, N - 1>): a loop
+// whose index is a compile-time constant in the body (register arrays
+// indexed by it stay in registers, and scheduling builtins take it).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F &f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 // Index of this thread's wave, as a wave-uniform (scalar) value.
 __device__ __forceinline__ int wave_id() {
   return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);

@@ -143,18 +143,6 @@ __device__ __forceinline__ BalItem fa_fwd_bal_item(const FwdArgs &a, int u, int 
 // for an odd middle tile.
 __host__ __device__ constexpr int bal_items(int nb) { return 3 * (nb >> 1) + (nb & 1); }
 
-// f(integral_constant<int, 0>), ..., f(integral_constant<int, N - 1>): a loop
-// whose index is a compile-time constant in the body (register arrays
-// indexed by it stay in registers, and scheduling builtins take it).
-template <typename F, int... I>
-__device__ __forceinline__ void static_for_impl(F &f, std::integer_sequence<int, I...>) {
-  (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F &&f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
 template <int D, int KSPLIT>
 struct FwdTile {
   static_assert(KSPLIT == 1 || KSPLIT == 2, "key split is 1 or 2");
