@@ -393,33 +393,26 @@ def _is_llama_attention(mod) -> bool:
     return type(mod).__name__ in _LLAMA_NAMES
 
 
-# Linear-attention / state-space families the kernel must refuse
-# (reference patch_hf.py:358-387).
-_LINEAR_ATTN_CLASS_NAMES = {
-    "MambaMixer", "MambaModel", "MambaForCausalLM",
-    "Mamba2Mixer", "Mamba2Model", "Mamba2ForCausalLM",
-    "RwkvSelfAttention", "RwkvLinearAttention", "RwkvModel", "RwkvForCausalLM",
-    "RecurrentGemmaRecurrentBlock", "RecurrentGemmaModel", "RecurrentGemmaForCausalLM",
-    "RetNetAttention", "RetNetModel", "RetNetForCausalLM",
-}
+# Linear-attention / state-space families the kernel must refuse (the
+# families of reference patch_hf.py:358-387): each family's marker module
+# classes, tested in this order (a model holding markers of two families
+# reports the first).
+_LINEAR_ATTN_MARKERS = (
+    ("mamba", ("MambaMixer",)),
+    ("mamba2", ("Mamba2Mixer",)),
+    ("rwkv", ("RwkvSelfAttention", "RwkvLinearAttention")),
+    ("recurrent_gemma", ("RecurrentGemmaRecurrentBlock",)),
+    ("retnet", ("RetNetAttention",)),
+)
 
 
 def _linear_attn_family(model: torch.nn.Module) -> Optional[str]:
-    """Family name (mamba / mamba2 / rwkv / recurrent_gemma / retnet) of a
-    linear-attention or state-space model, else None."""
-    seen = {type(m).__name__ for m in model.modules()}
-    seen.add(type(model).__name__)
-    if "MambaMixer" in seen:
-        return "mamba"
-    if "Mamba2Mixer" in seen:
-        return "mamba2"
-    if "RwkvSelfAttention" in seen or "RwkvLinearAttention" in seen:
-        return "rwkv"
-    if "RecurrentGemmaRecurrentBlock" in seen:
-        return "recurrent_gemma"
-    if "RetNetAttention" in seen:
-        return "retnet"
-    return None
+    """Family name of a linear-attention or state-space model (the first
+    entry of _LINEAR_ATTN_MARKERS with a marker class among the model's
+    modules), else None."""
+    classes = {type(model).__name__} | {type(m).__name__ for m in model.modules()}
+    return next((fam for fam, markers in _LINEAR_ATTN_MARKERS if classes.intersection(markers)),
+                None)
 
 
 def patch_model(model: torch.nn.Module, fuse_rope: bool = True) -> Tuple[str, int]:
