@@ -160,11 +160,12 @@ def kernel_times(q, k, v, do, steps, warmup):
             ev[i][j + 1].record()
     torch.cuda.synchronize()
     # The events between launches add their own gap to each interval (a
-    # few us each).  The same sequence timed with events around whole steps
-    # only gives the step's true length; each kernel keeps its share of the
-    # evented step, scaled to that length (avg_us_in_step).  Both figures
-    # are reported; the clean loop runs last, so a kernel trace of this run
-    # ends with exactly these launches.
+    # few us each, about the same for every launch).  The same sequence
+    # timed with events around whole steps only gives the step's true
+    # length; the difference, spread evenly over the step's launches, is
+    # taken off each kernel's evented interval (avg_us_in_step).  Both
+    # figures are reported; the clean loop runs last, so a kernel trace of
+    # this run ends with exactly these launches.
     per = {name: [ev[i][j].elapsed_time(ev[i][j + 1]) * 1e3 for i in range(steps)]
            for j, (name, _) in enumerate(seq)}
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -176,12 +177,13 @@ def kernel_times(q, k, v, do, steps, warmup):
     torch.cuda.synchronize()
     step_clean = e0.elapsed_time(e1) * 1e3 / steps
     step_evented = sum(statistics.mean(v) for v in per.values())
-    scale_clean = step_clean / step_evented
+    gap = max(0.0, (step_evented - step_clean) / len(per))
     for name, us in per.items():
         res[name]["avg_us_in_step_evented"] = statistics.mean(us)
-        res[name]["median_us_in_step"] = statistics.median(us) * scale_clean
-        res[name]["avg_us_in_step"] = statistics.mean(us) * scale_clean
+        res[name]["median_us_in_step"] = statistics.median(us) - gap
+        res[name]["avg_us_in_step"] = statistics.mean(us) - gap
         res[name]["step_us_clean"] = step_clean
+        res[name]["event_gap_us"] = gap
     return res
 
 
@@ -1028,6 +1030,7 @@ def main():
                 "avg_us_in_step": round(d["avg_us_in_step"], 3),
                 "avg_us_in_step_evented": round(d["avg_us_in_step_evented"], 3),
                 "step_us_clean": round(d["step_us_clean"], 3),
+                "event_gap_us": round(d["event_gap_us"], 3),
                 "avg_us_standalone": round(d["avg_us"], 3),
                 "frac_standalone": round(d["tflops"] / PEAK_FP16_TFLOPS, 4),
                 "flops_per_launch": d["flops"],

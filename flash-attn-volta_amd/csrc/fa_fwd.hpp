@@ -258,8 +258,10 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   stk.init(w, lane, a.k.ss);
   stv.init(w, lane, a.v.ss);
   auto load_k = [&](int n0, auto sc) { stk.load(k_sl(sc), kb, a.k.ss, n0, Sk, w); };
-  // Iteration t loads K(t + 2) and V(t): cursors at those rows, each
-  // advanced by a tile per load (no per-tile 64-bit multiplies).
+  // Iteration t loads K(t + 2) and V(t) (the prologue K(0), K(1) and, at
+  // D = 128, V(0)):
+  // cursors at those rows, each advanced by a tile per load (no per-tile
+  // 64-bit multiplies).
   RowCursor ck, cv;
   ck.init(kb, a.k.ss, 2 * BN, Sk, D, BN);
   cv.init(vb, a.v.ss, 0, Sk, D, BN);
@@ -356,10 +358,16 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
   using C1 = std::integral_constant<int, 1>;
   using Fast = std::false_type;    // no dead-sub-block checks
   using Check = std::true_type;
-  // ---- prologue: K(0) -> K slot 0, K(1) -> K slot 1, Q to registers,
-  // then the scores of tile 0
+  // ---- prologue: K(0) -> K slot 0, K(1) -> K slot 1, (D = 128) V(0) ->
+  // V slot 0, Q to registers, then the scores of tile 0
   if (n_tiles > 0) load_k(0, C0{});
   if (n_tiles > 1) load_k(BN, C1{});
+  // D = 128: V(0) as well, so that its latency overlaps Q's and K's (one
+  // memory round trip before the first tile instead of two; step 0 skips
+  // it).  Measured: the C5 layer's forward -1.5 to -2.8 %; at D = 64 the
+  // larger first burst costs more than it saves (+0.3 to +1.9 % at C4a).
+  constexpr bool v0_early = D >= 128;
+  if (v0_early && n_tiles > 0) load_v_next(C0{});
   {
     const int qr = min(qrow, nrows - 1);
     const f16 *qp = (SPLITKV ? a.q.head(b, hk * grp + qr % grp) + (int64_t)(qr / grp) * a.q.ss
@@ -492,7 +500,7 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
     using CQ = std::integral_constant<int, pc ^ 1>;
     const int n0 = t * BN;
     if (t + 2 < n_tiles) load_k_next(CP{});   // K(t + 2)
-    load_v_next(CP{});                        // V(t)
+    if (!v0_early || t > 0) load_v_next(CP{});   // V(t) (V(0) at D = 128: the prologue)
     if (t + 1 < n_tiles) qk(CQ{}, Check{}, n0 + BN, s_nxt);
     if (t >= 1) pv(CQ{}, Check{}, n0 - BN, p_prev);
     if (!dead(n0, 0)) {
