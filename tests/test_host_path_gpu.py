@@ -181,3 +181,71 @@ def test_cpp_node_gradient_forms():
         Bw.split_workspace = True
     for got, want in zip((qg.grad, kg.grad, vg.grad), ref):
         assert (got.float() - want.float()).abs().max().item() < 1e-2    # the suite's max-abs bar
+
+
+def test_plan_cache_eviction(monkeypatch):
+    """More signatures than the plan caches hold: they are cleared and
+    rebuilt, and every call still matches the general path."""
+    from flash_attn_volta import backward as Bw, forward as F
+    from flash_attn_volta import flash_attn, flash_attn_backward, flash_attn_forward
+    monkeypatch.setattr(F, "_MAX_PLANS", 4)
+    monkeypatch.setattr(Bw, "_MAX_PLANS", 4)
+    print("[case] plan cache eviction", flush=True)
+    for rep in range(2):
+        for S in (64, 96, 130, 200, 256, 300):
+            q, k, v, do = _inputs(1, S, S, 2, 2, 64, "bshd", seed=S)
+            o_g, l_g = F._forward(q, k, v, True, 0.125, True, False)
+            o, lse = flash_attn_forward(q, k, v, causal=True, sm_scale=0.125, return_softmax_lse=True)
+            assert _eq(o, o_g) and _eq(lse, l_g)
+            g = flash_attn_backward(do, q, k, v, o, lse, causal=True, sm_scale=0.125)
+            g_g = Bw._backward(do, q, k, v, o_g, l_g, True, 0.125, False)
+            assert all(_eq(x, y) for x, y in zip(g, g_g))
+            qg = q.clone().requires_grad_()
+            flash_attn(qg, k, v, causal=True, sm_scale=0.125).backward(do)
+            assert _eq(qg.grad, g_g[0])
+        assert len(F._FWD_PLANS) <= 4 and len(Bw._BWD_PLANS) <= 4
+
+
+def test_two_threads_two_streams():
+    """Two host threads, each on its own stream, run autograd steps at once:
+    the plan caches, the workspace cache and the C++ node are shared; every
+    step's gradients equal the single-threaded ones."""
+    import threading
+    from flash_attn_volta import flash_attn
+    print("[case] two threads", flush=True)
+    shapes = [(2, 512, 4, 64), (1, 1024, 8, 128)]
+    refs = []
+    inputs = []
+    for i, (B, S, H, D) in enumerate(shapes):
+        q, k, v, do = _inputs(B, S, S, H, H, D, "bshd", seed=40 + i)
+        qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
+        flash_attn(qg, kg, vg, causal=True).backward(do)
+        refs.append((qg.grad.clone(), kg.grad.clone(), vg.grad.clone()))
+        inputs.append((q, k, v, do))
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(i):
+        try:
+            q, k, v, do = inputs[i]
+            stream = torch.cuda.Stream()
+            stream.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(stream):
+                for _ in range(10):
+                    qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
+                    flash_attn(qg, kg, vg, causal=True).backward(do)
+                    got = (qg.grad, kg.grad, vg.grad)
+                    stream.synchronize()
+                    if not all(_eq(a, b) for a, b in zip(got, refs[i])):
+                        errors.append(f"thread {i}: gradients differ")
+                        return
+        except Exception as e:       # reported below, in the test's own thread
+            errors.append(f"thread {i}: {e!r}")
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(len(shapes))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=100)
+    assert not any(t.is_alive() for t in threads), "a worker thread did not finish"
+    assert not errors, errors
