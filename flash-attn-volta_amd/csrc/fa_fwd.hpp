@@ -534,15 +534,15 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
     constexpr int pc = decltype(pcc)::value;
     using CP = std::integral_constant<int, pc>;
     using CQ = std::integral_constant<int, pc ^ 1>;
-    load_k_next(CP{});   // K(t + 2)
-    load_v_next(CP{});   // V(t)
     // The block in issue order: MQ S^T MFMAs (K slot pc ^ 1) and MP P V
     // MFMAs (V slot pc ^ 1), alternating while both remain, each followed
     // by its share of tile t's softmax (NPAIR pairs of scores: two FMAs, two
     // exp2, one conversion, one dot2).  A MFMA runs ~32 cycles in the
     // matrix pipe while the wave issues the VALU slice after it; its A
-    // operand was read from LDS two MFMAs earlier.  sched_barrier(0) keeps
-    // the compiler from regrouping the slices.
+    // operand was read from LDS PF MFMAs earlier.  sched_barrier(0) keeps
+    // the compiler from regrouping the slices.  The first operand reads go
+    // out before this iteration's DMAs (K(t + 2), V(t)) and their scalar
+    // address updates, so the first MFMA waits less after the barrier.
     constexpr int MQ = NSUB * (D / 16), MP = NSUB * 2 * (D / 32), M = MQ + MP;
     constexpr int NPAIR = NSUB * 8;
     const f16 *ks = k_sl(CQ{});
@@ -567,11 +567,47 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
     };
     const float c_ = c, neg_m = -m_run;
     float l0 = 0.0f, l1 = 0.0f;
-    constexpr int PF = 2;   // operands read this many MFMAs ahead
+    // softmax pair q of tile t: scores 2 (q % 4) and + 1 of half (q / 4) % 2
+    // of sub-block q / 8
+    auto pair_exp = [&](auto qc) -> floatx2 {
+      constexpr int q = decltype(qc)::value;
+      constexpr int sb = q / 8, hh = (q / 4) % 2, jj = 2 * (q % 4);
+      if constexpr (PRE) {
+        return (floatx2){fast_exp2(s_cur[sb][8 * hh + jj]), fast_exp2(s_cur[sb][8 * hh + jj + 1])};
+      } else {
+        return (floatx2){fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + jj], c_, neg_m)),
+                         fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + jj + 1], c_, neg_m))};
+      }
+    };
+    auto pair_store = [&](auto qc, floatx2 e) -> vec2<E> {
+      constexpr int q = decltype(qc)::value;
+      constexpr int sb = q / 8, hh = (q / 4) % 2, jj = 2 * (q % 4);
+      const vec2<E> pr = __builtin_convertvector(e, vec2<E>);
+      p_cur[sb][hh][jj] = pr[0];
+      p_cur[sb][hh][jj + 1] = pr[1];
+      return pr;
+    };
+    auto pair_sum = [&](auto qc, vec2<E> pr) {
+      if constexpr (decltype(qc)::value & 1) l1 = dot2_acc(pr, l1);
+      else l0 = dot2_acc(pr, l0);
+    };
+    // Software-pipelined slices: -1 to -2.5 % on the forward configs
+    // measured, except the D = 64 key-split kernel (+1 %), which keeps the
+    // plain order.
+    constexpr bool SWP = !(D == 64 && KSPLIT == 2);
+    constexpr int MAXP = (NPAIR + M - 1) / M;   // pairs per slice, at most
+    floatx2 eh[MAXP];                           // exp2s awaiting conversion
+    // operands read this many MFMAs ahead (3 at D = 128: -1 to -2 % there;
+    // at D = 64 it gains nothing)
+    constexpr int PF = D >= 128 ? 3 : 2;
     vec8<E> op[PF + 1];
     static_for<PF>([&](auto ic) {
       if constexpr (decltype(ic)::value < M) op[decltype(ic)::value] = operand(ic);
     });
+    __builtin_amdgcn_sched_barrier(0);
+    load_k_next(CP{});   // K(t + 2)
+    load_v_next(CP{});   // V(t)
+    __builtin_amdgcn_sched_barrier(0);
     static_for<M>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
       if constexpr (i + PF < M) op[(i + PF) % (PF + 1)] = operand(std::integral_constant<int, i + PF>{});
@@ -584,25 +620,42 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
         const int sb = j / (2 * (D / 32)), hh = (j / (D / 32)) % 2, d = j % (D / 32);
         oacc[d] = mfma32(op[i % (PF + 1)], p_prev[sb][hh], oacc[d]);
       }
-      // softmax pairs [i * NPAIR / M, (i + 1) * NPAIR / M) of tile t
-      static_for<(i + 1) * NPAIR / M - i * NPAIR / M>([&](auto kc) {
-        constexpr int q = i * NPAIR / M + decltype(kc)::value;   // pair index
-        constexpr int sb = q / 8, hh = (q / 4) % 2, jj = 2 * (q % 4);
-        floatx2 e;
-        if constexpr (PRE) {
-          e = (floatx2){fast_exp2(s_cur[sb][8 * hh + jj]), fast_exp2(s_cur[sb][8 * hh + jj + 1])};
-        } else {
-          e = (floatx2){fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + jj], c_, neg_m)),
-                        fast_exp2(__builtin_fmaf(s_cur[sb][8 * hh + jj + 1], c_, neg_m))};
-        }
-        vec2<E> pr = __builtin_convertvector(e, vec2<E>);
-        if (q & 1) l1 = dot2_acc(pr, l1);
-        else l0 = dot2_acc(pr, l0);
-        p_cur[sb][hh][jj] = pr[0];
-        p_cur[sb][hh][jj + 1] = pr[1];
-      });
+      // softmax pairs [i * NPAIR / M, (i + 1) * NPAIR / M) of tile t.  SWP:
+      // their exp2s now, their conversion and sum in the next slice (the
+      // previous slice's pairs are converted first and summed last), so no
+      // instruction waits on the result of the one before it
+      constexpr int b_cur = i * NPAIR / M, n_cur = (i + 1) * NPAIR / M - b_cur;
+      if constexpr (SWP) {
+        constexpr int b_prv = i > 0 ? (i - 1) * NPAIR / M : 0, n_prv = i > 0 ? b_cur - b_prv : 0;
+        vec2<E> pr[MAXP];
+        static_for<n_prv>([&](auto kc) {
+          constexpr int k = decltype(kc)::value;
+          pr[k] = pair_store(std::integral_constant<int, b_prv + k>{}, eh[k]);
+        });
+        static_for<n_cur>([&](auto kc) {
+          constexpr int k = decltype(kc)::value;
+          eh[k] = pair_exp(std::integral_constant<int, b_cur + k>{});
+        });
+        static_for<n_prv>([&](auto kc) {
+          constexpr int k = decltype(kc)::value;
+          pair_sum(std::integral_constant<int, b_prv + k>{}, pr[k]);
+        });
+      } else {
+        static_for<n_cur>([&](auto kc) {
+          constexpr auto q = std::integral_constant<int, b_cur + decltype(kc)::value>{};
+          pair_sum(q, pair_store(q, pair_exp(q)));
+        });
+      }
       __builtin_amdgcn_sched_barrier(0);
     });
+    if constexpr (SWP) {
+      constexpr int b_last = (M - 1) * NPAIR / M;
+      static_for<NPAIR - b_last>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        pair_sum(std::integral_constant<int, b_last + k>{},
+                 pair_store(std::integral_constant<int, b_last + k>{}, eh[k]));
+      });
+    }
     finish_softmax(Fast{}, t * BN, s_cur, p_cur, l0 + l1, s_nxt, true);
     __builtin_amdgcn_s_waitcnt(0x0f70);
     __syncthreads();
