@@ -267,7 +267,7 @@ int launch_dkdv_split(const fa::BwdArgs &args, hipStream_t stream) {
   return launch_status();
 }
 
-template <typename E, int D, bool CAUSAL, int SPLIT>
+template <typename E, int D, bool CAUSAL, int SPLIT, bool PRE>
 int launch_dq_split(const fa::BwdArgs &args, hipStream_t stream) {
   using T = fa::DqTile<D, SPLIT>;
   fa::BwdArgs a = args;
@@ -275,7 +275,7 @@ int launch_dq_split(const fa::BwdArgs &args, hipStream_t stream) {
   // a split query block takes two workgroups
   const int64_t grid = ((int64_t)a.n_blocks + a.dq_split) * a.B * a.H;
   if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
-  constexpr auto kernel = fa::fa_bwd_dq_kernel<E, D, CAUSAL, SPLIT>;
+  constexpr auto kernel = fa::fa_bwd_dq_kernel<E, D, CAUSAL, SPLIT, PRE>;
   a.zigzag = CAUSAL ? zigzag_order(grid, a.n_blocks, resident_per_cu<kernel>(T::NT)) : 0;
   hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(T::NT), 0, stream, a);
   return launch_status();
@@ -298,8 +298,16 @@ int launch_dkdv(const fa::BwdArgs &a, hipStream_t stream) {
 
 template <typename E, int D, bool CAUSAL>
 int launch_dq(const fa::BwdArgs &a, hipStream_t stream) {
-  return row_split(a.Sq, (int64_t)a.B * a.H, CAUSAL) ? launch_dq_split<E, D, CAUSAL, 2>(a, stream)
-                                                     : launch_dq_split<E, D, CAUSAL, 1>(a, stream);
+  const bool split = row_split(a.Sq, (int64_t)a.B * a.H, CAUSAL);
+  // the pre-scaled mode under the forward's condition (fp16, c <= 1); not at
+  // D = 128, where its seed registers would cost the second wave per SIMD
+  if constexpr (std::is_same<E, fa::f16>::value && D <= 64) {
+    if (a.c <= 1.0f)
+      return split ? launch_dq_split<E, D, CAUSAL, 2, true>(a, stream)
+                   : launch_dq_split<E, D, CAUSAL, 1, true>(a, stream);
+  }
+  return split ? launch_dq_split<E, D, CAUSAL, 2, false>(a, stream)
+               : launch_dq_split<E, D, CAUSAL, 1, false>(a, stream);
 }
 
 // (dtype, D, causal) -> one instantiation of launcher L<E, D, CAUSAL>.

@@ -444,6 +444,17 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   // unscaled (ck = 1: a second bf16 rounding would cost 8-bit accuracy),
   // only its sign follows sm_scale.
   constexpr int NKF = T::KV_LDS ? 1 : D / 16;
+  // K and V staged in LDS are read only as B operands, row by row like an
+  // A operand: at D = 64 they take SW_A (conflict-free for those reads)
+  // and offsets of their own; the D = 128 layout, out of registers, keeps
+  // the query tiles' swizzle and offsets.
+  constexpr int kKvSwizzle = (T::KV_LDS && D == 64) ? SW_A : kDkdvSwizzle;
+  int kv_off[T::KV_LDS ? D / 16 : 1];
+  if constexpr (T::KV_LDS) {
+    const int sk = swz<D, kKvSwizzle>(l32);
+#pragma unroll
+    for (int cc = 0; cc < D / 16; ++cc) kv_off[cc] = l32 * D + (((2 * cc + g) ^ sk) << 3);
+  }
   vec8<E> kf[NKF], vf[NKF];
   const float ck = std::is_same<E, f16>::value ? fminf(a.c, 1.0f) : 1.0f;
   const float cr = a.c / ck;
@@ -452,7 +463,7 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   // first query tile's loads are issued too (one memory latency for both)
   if constexpr (T::KV_LDS) {
     // the workgroup's BK keys into LDS (zeros past Sk)
-    DmaStager<D, kDkdvSwizzle, BK, T::NW> stk, stv;
+    DmaStager<D, kKvSwizzle, BK, T::NW> stk, stv;
     stk.init(w, lane, a.k.ss);
     stv.init(w, lane, a.v.ss);
     stk.load(s_k, a.k.head(b, hk), a.k.ss, k0, Sk, w);
@@ -463,12 +474,12 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   }
   // B operands of S and dP: K^T / V^T fragments K[key][16cc + 8g .. +7]
   // (registers, or LDS rows 32kg + l32 read like the query tiles' A rows)
-  auto k_frag = [&](int cc, int aoff) -> vec8<E> {
-    if constexpr (T::KV_LDS) return ld8<E>(s_k + 32 * kg * D + aoff);
+  auto k_frag = [&](int cc) -> vec8<E> {
+    if constexpr (T::KV_LDS) return ld8<E>(s_k + 32 * kg * D + kv_off[cc]);
     else return kf[cc];
   };
-  auto v_frag = [&](int cc, int aoff) -> vec8<E> {
-    if constexpr (T::KV_LDS) return ld8<E>(s_v + 32 * kg * D + aoff);
+  auto v_frag = [&](int cc) -> vec8<E> {
+    if constexpr (T::KV_LDS) return ld8<E>(s_v + 32 * kg * D + kv_off[cc]);
     else return vf[cc];
   };
 
@@ -634,8 +645,8 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
       const f16 *gr = do_st(stc) + 32 * qs * D;
 #pragma unroll
       for (int cc = 0; cc < D / 16; ++cc) {
-        sacc = mfma32(ld8<E>(qr + a_off[cc]), k_frag(cc, a_off[cc]), sacc);
-        dpacc = mfma32(ld8<E>(gr + a_off[cc]), v_frag(cc, a_off[cc]), dpacc);
+        sacc = mfma32(ld8<E>(qr + a_off[cc]), k_frag(cc), sacc);
+        dpacc = mfma32(ld8<E>(gr + a_off[cc]), v_frag(cc), dpacc);
       }
     };
     // Softmax-gradient of sub-block sb and its dV / dK MFMAs.
@@ -741,7 +752,7 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
       const f16 *gr = do_st(stc) + 32 * qs * D;
       static_for<NC>([&](auto ic) {
         constexpr int cc = decltype(ic)::value;
-        sacc = mfma32(ld8<E>(qr + a_off[cc]), k_frag(cc, a_off[cc]), sacc);
+        sacc = mfma32(ld8<E>(qr + a_off[cc]), k_frag(cc), sacc);
       });
       if (cr != 1.0f) {
 #pragma unroll
@@ -754,7 +765,7 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
       vec8<E> pf[2];
       static_for<NC>([&](auto ic) {
         constexpr int cc = decltype(ic)::value;
-        dpacc = mfma32(ld8<E>(gr + a_off[cc]), v_frag(cc, a_off[cc]), dpacc);
+        dpacc = mfma32(ld8<E>(gr + a_off[cc]), v_frag(cc), dpacc);
         if constexpr (cc >= 1) {
           constexpr int i0 = (cc - 1) * 16 / (NC - 1), i1 = cc * 16 / (NC - 1);
           static_for<i1 - i0>([&](auto kc) {
@@ -889,8 +900,14 @@ struct DqTile {
   static_assert(64 * (D / 2) * 4 <= LDS_TILE * 2, "a merge buffer must fit in one K stage");
 };
 
-template <typename E, int D, bool CAUSAL, int SPLIT>
-__global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
+// PRE (fp16 with c <= 1, chosen by the launcher): Q is scaled by c once and
+// rounded to fp16, as in the forward's pre-scaled mode, and the S^T MFMAs
+// start from -LSE * log2(e), so they produce c s - LSE' and P is one exp2
+// per score, no FMA.
+template <typename E, int D, bool CAUSAL, int SPLIT, bool PRE = false>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3 : 1)))
+void fa_bwd_dq_kernel(BwdArgs a) {
+  static_assert(!PRE || std::is_same<E, f16>::value, "the pre-scaled mode is fp16 only");
   using T = DqTile<D, SPLIT>;
   constexpr int BM = T::BM, BN = T::BN, NSUB = T::NSUB;
   // One LDS object per stage (see the dK/dV kernel).
@@ -974,6 +991,12 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) qf[c] = neg8(qf[c]);
   }
+  if constexpr (PRE) {
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qf[c][j] = (E)((float)qf[c][j] * a.c);
+  }
   const int qc = min(qrow, Sq - 1);
   const float l2 = qrow < Sq ? a.lse[(int64_t)bh * Sq + qc] * kLog2e : kPosInf;
   float dl;
@@ -1023,9 +1046,12 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
   for (int d = 0; d < D / 32; ++d) dq[d] = floatx16{};
   const float shift = -l2;   // P = exp2(c s - LSE * log2(e))
   // dP^T MFMAs start from -delta (the lane's query), so they yield dP - delta
-  floatx16 dl_seed;
+  floatx16 dl_seed, s_seed;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) dl_seed[i] = -dl * gmul;
+  for (int i = 0; i < 16; ++i) {
+    dl_seed[i] = -dl * gmul;
+    s_seed[i] = PRE ? shift : 0.0f;
+  }
 
   // Per-lane LDS element offsets inside a stage (as in the dK/dV kernel):
   // A-operand rows l32, chunk 2cc + g; transposed reads of K rows
@@ -1054,18 +1080,24 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
       const int ns = sub_n(sb);
       return !(CAUSAL && ns > wq0 + 31 + off) && ns < Sk;
     };
-    // S^T = K Q^T and dP^T = V dO^T for sub-block sb
+    // S^T = K Q^T (PRE: c s - LSE') and dP^T = V dO^T for sub-block sb;
+    // each pair of K / V operands is read from LDS one MFMA pair ahead
     auto s_dp = [&](int sb, floatx16 &sacc, floatx16 &dpacc) {
       const int ks = NSUB * kh + sb;
       const f16 *kr = k_st(stc) + 32 * ks * D;
       const f16 *vr = v_st(stc) + 32 * ks * D;
-      sacc = mfma32(ld8<E>(kr + a_off[0]), qf[0], floatx16{});
-      dpacc = mfma32(ld8<E>(vr + a_off[0]), gf[0], dl_seed);
-#pragma unroll
-      for (int cc = 1; cc < D / 16; ++cc) {
-        sacc = mfma32(ld8<E>(kr + a_off[cc]), qf[cc], sacc);
-        dpacc = mfma32(ld8<E>(vr + a_off[cc]), gf[cc], dpacc);
-      }
+      vec8<E> ko[2], vo[2];
+      ko[0] = ld8<E>(kr + a_off[0]);
+      vo[0] = ld8<E>(vr + a_off[0]);
+      static_for<D / 16>([&](auto ic) {
+        constexpr int cc = decltype(ic)::value;
+        if constexpr (cc + 1 < D / 16) {
+          ko[(cc + 1) & 1] = ld8<E>(kr + a_off[cc + 1]);
+          vo[(cc + 1) & 1] = ld8<E>(vr + a_off[cc + 1]);
+        }
+        sacc = mfma32(ko[cc & 1], qf[cc], cc == 0 ? s_seed : sacc);
+        dpacc = mfma32(vo[cc & 1], gf[cc], cc == 0 ? dl_seed : dpacc);
+      });
     };
     auto grad = [&](int sb, floatx16 &sacc, const floatx16 &dpacc) {
       const int ks = NSUB * kh + sb;
@@ -1083,7 +1115,7 @@ __global__ __launch_bounds__(256) void fa_bwd_dq_kernel(BwdArgs a) {
       floatx16 ds;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float p = fast_exp2(__builtin_fmaf(sacc[i], c, shift));
+        const float p = PRE ? fast_exp2(sacc[i]) : fast_exp2(__builtin_fmaf(sacc[i], c, shift));
         ds[i] = p * dpacc[i];
       }
       vec8<E> dsf[2];
