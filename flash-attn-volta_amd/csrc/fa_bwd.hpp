@@ -383,6 +383,9 @@ struct DkdvTile {
   static constexpr int WAVES_PER_EU = (D == 64 && KV_LDS) ? 3 : (WIDE ? 2 : 1);
   static constexpr int LDS_TILE = BQ * D;   // swizzled, unpadded (fa_common.hpp)
   static constexpr int LDS_KV = KV_LDS ? BK * D : 8;   // K (or V) tile, kperm rows
+  // operand reads of sdp_grad's MFMAs this many MFMAs ahead (0: each just
+  // before its MFMA)
+  static constexpr int PF_OPS = (D == 64 && KV_LDS) ? 1 : 0;
   // layouts that implement the causal key-block split (BwdArgs::split_kt)
   static constexpr bool KEY_SPLIT = WIDE || (D == 64 && SPLIT == 2);
   static_assert(64 * (D / 2) * 4 <= LDS_TILE * 2, "a merge buffer must fit in one stage");
@@ -720,6 +723,8 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
     auto sdp_grad = [&](int sb) {
       constexpr int NC = D / 16;          // S / dP MFMAs (K-dim chunks of 16)
       constexpr int NO = 2 * (D / 32);    // dV / dK MFMAs (2 query halves x D / 32)
+      constexpr int NM = 2 * NC + 2 * NO;
+      constexpr int PFD = T::PF_OPS;      // operand reads this many MFMAs ahead
       const int qs = NSUB * qh + sb;
       floatx16 sacc, dpacc;
 #pragma unroll
@@ -750,9 +755,37 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
       }
       const f16 *qr = q_st(stc) + 32 * qs * D;
       const f16 *gr = do_st(stc) + 32 * qs * D;
+      const int rb0 = (32 * qs) * D;
+      // LDS operands of MFMA i of the block (S: Q and K^T; dP: dO and V^T;
+      // dV: dO^T; dK: Q^T), in ring slot i % (PFD + 1)
+      vec8<E> opa[PFD + 1], opb[PFD + 1];
+      auto fetch = [&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        constexpr int sl = i % (PFD + 1);
+        if constexpr (i < NC) {
+          opa[sl] = ld8<E>(qr + a_off[i]);
+          opb[sl] = k_frag(i);
+        } else if constexpr (i < 2 * NC) {
+          opa[sl] = ld8<E>(gr + a_off[i - NC]);
+          opb[sl] = v_frag(i - NC);
+        } else if constexpr (i < 2 * NC + NO) {
+          constexpr int o = i - 2 * NC, hh = o / (D / 32), d = o % (D / 32);
+          opa[sl] = load_tr_pair<E>(do_st(stc) + rb0 + 16 * hh * D, t_off.lo(d), t_off.hi(d));
+        } else {
+          constexpr int o = i - 2 * NC - NO, hh = o / (D / 32), d = o % (D / 32);
+          opa[sl] = load_tr_pair<E>(q_st(stc) + rb0 + 16 * hh * D, t_off.lo(d), t_off.hi(d));
+        }
+      };
+      // before MFMA i: its operands (PFD = 0) or those of MFMA i + PFD
+      auto ahead = [&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        if constexpr (i + PFD < NM) fetch(std::integral_constant<int, i + PFD>{});
+      };
+      static_for<PFD>([&](auto ic) { fetch(ic); });
       static_for<NC>([&](auto ic) {
         constexpr int cc = decltype(ic)::value;
-        sacc = mfma32(ld8<E>(qr + a_off[cc]), k_frag(cc), sacc);
+        ahead(ic);
+        sacc = mfma32(opa[cc % (PFD + 1)], opb[cc % (PFD + 1)], sacc);
       });
       if (cr != 1.0f) {
 #pragma unroll
@@ -764,14 +797,15 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
       floatx16 p;
       vec8<E> pf[2];
       static_for<NC>([&](auto ic) {
-        constexpr int cc = decltype(ic)::value;
-        dpacc = mfma32(ld8<E>(gr + a_off[cc]), v_frag(cc), dpacc);
+        constexpr int cc = decltype(ic)::value, i = NC + cc;
+        ahead(std::integral_constant<int, i>{});
+        dpacc = mfma32(opa[i % (PFD + 1)], opb[i % (PFD + 1)], dpacc);
         if constexpr (cc >= 1) {
           constexpr int i0 = (cc - 1) * 16 / (NC - 1), i1 = cc * 16 / (NC - 1);
           static_for<i1 - i0>([&](auto kc) {
-            constexpr int i = i0 + decltype(kc)::value;
-            p[i] = fast_exp2(sacc[i]);
-            pf[i >> 3][i & 7] = (E)p[i];
+            constexpr int e = i0 + decltype(kc)::value;
+            p[e] = fast_exp2(sacc[e]);
+            pf[e >> 3][e & 7] = (E)p[e];
           });
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -780,18 +814,17 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
       // here on) and its max in NO - 1 slices
       floatx16 &ds = p;
       float mk = 0.0f;
-      const int rb0 = (32 * qs) * D;
       static_for<NO>([&](auto io) {
-        constexpr int o = decltype(io)::value;
+        constexpr int o = decltype(io)::value, i = 2 * NC + o;
         constexpr int hh = o / (D / 32), d = o % (D / 32);
-        dv[d] = mfma32(load_tr_pair<E>(do_st(stc) + rb0 + 16 * hh * D, t_off.lo(d), t_off.hi(d)),
-                       pf[hh], dv[d]);
+        ahead(std::integral_constant<int, i>{});
+        dv[d] = mfma32(opa[i % (PFD + 1)], pf[hh], dv[d]);
         if constexpr (o >= 1) {
           constexpr int i0 = (o - 1) * 16 / (NO - 1), i1 = o * 16 / (NO - 1);
           static_for<i1 - i0>([&](auto kc) {
-            constexpr int i = i0 + decltype(kc)::value;
-            ds[i] *= dpacc[i];
-            mk = fmaxf(mk, fabsf(ds[i]));
+            constexpr int e = i0 + decltype(kc)::value;
+            ds[e] *= dpacc[e];
+            mk = fmaxf(mk, fabsf(ds[e]));
           });
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -813,9 +846,9 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
 #pragma unroll
         for (int j = 0; j < 8; ++j) dsf[hh][j] = (E)(ds[8 * hh + j] * sc.mul);
         static_for<D / 32>([&](auto id) {
-          constexpr int d = decltype(id)::value;
-          dk[d] = mfma32(load_tr_pair<E>(q_st(stc) + rb0 + 16 * hh * D, t_off.lo(d), t_off.hi(d)),
-                         dsf[hh], dk[d]);
+          constexpr int d = decltype(id)::value, i = 2 * NC + NO + hh * (D / 32) + d;
+          ahead(std::integral_constant<int, i>{});
+          dk[d] = mfma32(opa[i % (PFD + 1)], dsf[hh], dk[d]);
         });
         __builtin_amdgcn_sched_barrier(0);
       });
