@@ -591,10 +591,6 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
       if constexpr (decltype(qc)::value & 1) l1 = dot2_acc(pr, l1);
       else l0 = dot2_acc(pr, l0);
     };
-    // Software-pipelined slices: -1 to -2.5 % on the forward configs
-    // measured, except the D = 64 key-split kernel (+1 %), which keeps the
-    // plain order.
-    constexpr bool SWP = !(D == 64 && KSPLIT == 2);
     constexpr int MAXP = (NPAIR + M - 1) / M;   // pairs per slice, at most
     floatx2 eh[MAXP];                           // exp2s awaiting conversion
     // operands read this many MFMAs ahead (3 at D = 128: -1 to -2 % there;
@@ -620,35 +616,28 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
         const int sb = j / (2 * (D / 32)), hh = (j / (D / 32)) % 2, d = j % (D / 32);
         oacc[d] = mfma32(op[i % (PF + 1)], p_prev[sb][hh], oacc[d]);
       }
-      // softmax pairs [i * NPAIR / M, (i + 1) * NPAIR / M) of tile t.  SWP:
-      // their exp2s now, their conversion and sum in the next slice (the
+      // softmax pairs [i * NPAIR / M, (i + 1) * NPAIR / M) of tile t: their
+      // exp2s now, their conversion and sum in the next slice (the
       // previous slice's pairs are converted first and summed last), so no
       // instruction waits on the result of the one before it
       constexpr int b_cur = i * NPAIR / M, n_cur = (i + 1) * NPAIR / M - b_cur;
-      if constexpr (SWP) {
-        constexpr int b_prv = i > 0 ? (i - 1) * NPAIR / M : 0, n_prv = i > 0 ? b_cur - b_prv : 0;
-        vec2<E> pr[MAXP];
-        static_for<n_prv>([&](auto kc) {
-          constexpr int k = decltype(kc)::value;
-          pr[k] = pair_store(std::integral_constant<int, b_prv + k>{}, eh[k]);
-        });
-        static_for<n_cur>([&](auto kc) {
-          constexpr int k = decltype(kc)::value;
-          eh[k] = pair_exp(std::integral_constant<int, b_cur + k>{});
-        });
-        static_for<n_prv>([&](auto kc) {
-          constexpr int k = decltype(kc)::value;
-          pair_sum(std::integral_constant<int, b_prv + k>{}, pr[k]);
-        });
-      } else {
-        static_for<n_cur>([&](auto kc) {
-          constexpr auto q = std::integral_constant<int, b_cur + decltype(kc)::value>{};
-          pair_sum(q, pair_store(q, pair_exp(q)));
-        });
-      }
+      constexpr int b_prv = i > 0 ? (i - 1) * NPAIR / M : 0, n_prv = i > 0 ? b_cur - b_prv : 0;
+      vec2<E> pr[MAXP];
+      static_for<n_prv>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        pr[k] = pair_store(std::integral_constant<int, b_prv + k>{}, eh[k]);
+      });
+      static_for<n_cur>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        eh[k] = pair_exp(std::integral_constant<int, b_cur + k>{});
+      });
+      static_for<n_prv>([&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        pair_sum(std::integral_constant<int, b_prv + k>{}, pr[k]);
+      });
       __builtin_amdgcn_sched_barrier(0);
     });
-    if constexpr (SWP) {
+    {
       constexpr int b_last = (M - 1) * NPAIR / M;
       static_for<NPAIR - b_last>([&](auto kc) {
         constexpr int k = decltype(kc)::value;
