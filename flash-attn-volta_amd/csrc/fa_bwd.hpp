@@ -724,7 +724,9 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
       constexpr int NC = D / 16;          // S / dP MFMAs (K-dim chunks of 16)
       constexpr int NO = 2 * (D / 32);    // dV / dK MFMAs (2 query halves x D / 32)
       constexpr int NM = 2 * NC + 2 * NO;
-      constexpr int PFD = T::PF_OPS;      // operand reads this many MFMAs ahead
+      // S / dP operand reads this many MFMAs ahead (the non-causal variant
+      // would spill)
+      constexpr int PFD = CAUSAL ? T::PF_OPS : 0;
       const int qs = NSUB * qh + sb;
       floatx16 sacc, dpacc;
 #pragma unroll
@@ -776,10 +778,16 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
           opa[sl] = load_tr_pair<E>(q_st(stc) + rb0 + 16 * hh * D, t_off.lo(d), t_off.hi(d));
         }
       };
-      // before MFMA i: its operands (PFD = 0) or those of MFMA i + PFD
+      // before MFMA i: the S / dP operands of MFMA i + PFD (PFD = 0: its
+      // own), the dV / dK operand of MFMA i itself (reading those ahead
+      // too spills a register)
       auto ahead = [&](auto ic) {
         constexpr int i = decltype(ic)::value;
-        if constexpr (i + PFD < NM) fetch(std::integral_constant<int, i + PFD>{});
+        if constexpr (i < 2 * NC) {
+          if constexpr (i + PFD < 2 * NC) fetch(std::integral_constant<int, i + PFD>{});
+        } else {
+          fetch(ic);
+        }
       };
       static_for<PFD>([&](auto ic) { fetch(ic); });
       static_for<NC>([&](auto ic) {
@@ -1113,24 +1121,18 @@ void fa_bwd_dq_kernel(BwdArgs a) {
       const int ns = sub_n(sb);
       return !(CAUSAL && ns > wq0 + 31 + off) && ns < Sk;
     };
-    // S^T = K Q^T (PRE: c s - LSE') and dP^T = V dO^T for sub-block sb;
-    // each pair of K / V operands is read from LDS one MFMA pair ahead
+    // S^T = K Q^T (PRE: c s - LSE') and dP^T = V dO^T for sub-block sb
     auto s_dp = [&](int sb, floatx16 &sacc, floatx16 &dpacc) {
       const int ks = NSUB * kh + sb;
       const f16 *kr = k_st(stc) + 32 * ks * D;
       const f16 *vr = v_st(stc) + 32 * ks * D;
-      vec8<E> ko[2], vo[2];
-      ko[0] = ld8<E>(kr + a_off[0]);
-      vo[0] = ld8<E>(vr + a_off[0]);
-      static_for<D / 16>([&](auto ic) {
-        constexpr int cc = decltype(ic)::value;
-        if constexpr (cc + 1 < D / 16) {
-          ko[(cc + 1) & 1] = ld8<E>(kr + a_off[cc + 1]);
-          vo[(cc + 1) & 1] = ld8<E>(vr + a_off[cc + 1]);
-        }
-        sacc = mfma32(ko[cc & 1], qf[cc], cc == 0 ? s_seed : sacc);
-        dpacc = mfma32(vo[cc & 1], gf[cc], cc == 0 ? dl_seed : dpacc);
-      });
+      sacc = mfma32(ld8<E>(kr + a_off[0]), qf[0], s_seed);
+      dpacc = mfma32(ld8<E>(vr + a_off[0]), gf[0], dl_seed);
+#pragma unroll
+      for (int cc = 1; cc < D / 16; ++cc) {
+        sacc = mfma32(ld8<E>(kr + a_off[cc]), qf[cc], sacc);
+        dpacc = mfma32(ld8<E>(vr + a_off[cc]), gf[cc], dpacc);
+      }
     };
     auto grad = [&](int sb, floatx16 &sacc, const floatx16 &dpacc) {
       const int ks = NSUB * kh + sb;
