@@ -456,7 +456,9 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   if constexpr (T::KV_LDS) {
     const int sk = swz<D, kKvSwizzle>(l32);
 #pragma unroll
-    for (int cc = 0; cc < D / 16; ++cc) kv_off[cc] = l32 * D + (((2 * cc + g) ^ sk) << 3);
+    for (int cc = 0; cc < D / 16; ++cc)
+      kv_off[cc] = (kKvSwizzle == SW_P8 && cc >= 4) ? kv_off[cc - 4] + 64
+                                                    : l32 * D + (((2 * cc + g) ^ sk) << 3);
   }
   vec8<E> kf[NKF], vf[NKF];
   const float ck = std::is_same<E, f16>::value ? fminf(a.c, 1.0f) : 1.0f;
@@ -569,8 +571,12 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   TrOffsets<D, kDkdvSwizzle> t_off;
   {
     const int sa = swz<D, kDkdvSwizzle>(l32);
+    // SW_P8 permutes only a chunk index's low 3 bits, so chunks 8-15 (D =
+    // 128) sit 64 elements after chunks 0-7: an immediate, not a register
+    static_assert(kDkdvSwizzle == SW_P8, "offsets below assume a 3-bit swizzle");
 #pragma unroll
-    for (int cc = 0; cc < D / 16; ++cc) a_off[cc] = l32 * D + (((2 * cc + g) ^ sa) << 3);
+    for (int cc = 0; cc < D / 16; ++cc)
+      a_off[cc] = cc < 4 ? l32 * D + (((2 * cc + g) ^ sa) << 3) : a_off[cc - 4] + 64;
     t_off.init(lane);
   }
 
