@@ -202,14 +202,14 @@ bool fwd_prescaled(const fa::FwdArgs &a) {
   return std::is_same<E, fa::f16>::value && a.c <= 1.0f;
 }
 
-template <typename E, int D, bool CAUSAL, int KSPLIT, bool PRE>
+template <typename E, int D, bool CAUSAL, int KSPLIT, bool PRE, int NW = 4>
 int launch_fwd_split(const fa::FwdArgs &args, hipStream_t stream) {
-  using T = fa::FwdTile<D, KSPLIT>;
+  using T = fa::FwdTile<D, KSPLIT, NW>;
   fa::FwdArgs a = args;
   a.n_qtiles = (a.Sq + T::BM - 1) / T::BM;
   const int64_t grid = (int64_t)a.n_qtiles * a.B * a.H;
   if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
-  constexpr auto kernel = fa::fa_fwd_kernel<E, D, CAUSAL, KSPLIT, false, PRE>;
+  constexpr auto kernel = fa::fa_fwd_kernel<E, D, CAUSAL, KSPLIT, false, PRE, false, NW>;
   a.zigzag = CAUSAL ? zigzag_order(grid, a.n_qtiles, resident_per_cu<kernel>(T::NT)) : 0;
   hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(T::NT), 0, stream, a);
   return launch_status();
@@ -217,6 +217,17 @@ int launch_fwd_split(const fa::FwdArgs &args, hipStream_t stream) {
 
 template <typename E, int D, bool CAUSAL, int KSPLIT>
 int launch_fwd_mode(const fa::FwdArgs &a, hipStream_t stream) {
+  // Non-causal D = 64 grids of at least one 256-query tile per CU: eight
+  // waves, 256 queries per workgroup sharing each K / V tile (half the
+  // tile DMAs per query).
+  if constexpr (D == 64 && !CAUSAL && KSPLIT == 1) {
+    if ((int64_t)((a.Sq + 255) / 256) * a.B * a.H >= device_cus()) {
+      if constexpr (std::is_same<E, fa::f16>::value) {
+        if (fwd_prescaled<E>(a)) return launch_fwd_split<E, D, CAUSAL, 1, true, 8>(a, stream);
+      }
+      return launch_fwd_split<E, D, CAUSAL, 1, false, 8>(a, stream);
+    }
+  }
   // (not the unsplit D = 128 layout: the -max seed's 16 registers would
   // push it past 256 VGPRs, measured +3-4 % on the grids that use it)
   if constexpr (std::is_same<E, fa::f16>::value && !(D == 128 && KSPLIT == 1)) {

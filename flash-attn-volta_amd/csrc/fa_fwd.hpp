@@ -143,14 +143,16 @@ __device__ __forceinline__ BalItem fa_fwd_bal_item(const FwdArgs &a, int u, int 
 // for an odd middle tile.
 __host__ __device__ constexpr int bal_items(int nb) { return 3 * (nb >> 1) + (nb & 1); }
 
-template <int D, int KSPLIT>
+template <int D, int KSPLIT, int NW = 4>
 struct FwdTile {
   static_assert(KSPLIT == 1 || KSPLIT == 2, "key split is 1 or 2");
-  static constexpr int NQG = 4 / KSPLIT;   // query groups of 32 per workgroup
+  static_assert(NW == 4 || (NW == 8 && KSPLIT == 1 && D >= 64),
+                "eight waves: 256 queries, no key split, D >= 64");
+  static constexpr int NQG = NW / KSPLIT;  // query groups of 32 per workgroup
   static constexpr int NSUB = 2 / KSPLIT;  // 32-key sub-blocks per wave per tile
   static constexpr int BM = 32 * NQG;      // queries per workgroup
   static constexpr int BN = 64;            // keys per tile
-  static constexpr int NT = 256;           // 4 waves
+  static constexpr int NT = 64 * NW;       // NW waves
   static constexpr int LDS_TILE = BN * D;  // swizzled, unpadded (fa_common.hpp)
   // O^T partial sums of a key-half wave handed over for the final merge
   static_assert(64 * (D / 2) * 4 <= LDS_TILE * 2, "a merge buffer must fit in one K slot");
@@ -174,11 +176,11 @@ struct FwdTile {
 // writes its rows' normalised O and log2-domain LSE over that range to
 // part_o / part_lse, which fa_fwd_combine_kernel merges.
 template <typename E, int D, bool CAUSAL, int KSPLIT, bool SPLITKV = false, bool PRE = false,
-          bool BAL = false>
-__global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
+          bool BAL = false, int NW = 4>
+__global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
   static_assert(!PRE || std::is_same<E, f16>::value, "the pre-scaled mode is fp16 only");
   static_assert(!BAL || (CAUSAL && !SPLITKV), "the balanced schedule is for causal grids");
-  using T = FwdTile<D, KSPLIT>;
+  using T = FwdTile<D, KSPLIT, NW>;
   constexpr int NSUB = T::NSUB;
   constexpr int BM = T::BM, BN = T::BN;
   // One LDS object per slot, so the compiler sees that a DMA into one slot
@@ -253,8 +255,8 @@ __global__ __launch_bounds__(256) void fa_fwd_kernel(FwdArgs a) {
 
   // ---- K and V tiles go straight to LDS (fa_common.hpp DmaStager): both
   // in kperm row order, chunks swizzled; rows past Sk read as zeros.
-  DmaStager<D, SW_A> stk;   // K: read only as A operands
-  DmaStager<D, SW_T> stv;   // V: read only transposed
+  DmaStager<D, SW_A, 64, NW> stk;   // K: read only as A operands
+  DmaStager<D, SW_T, 64, NW> stv;   // V: read only transposed
   stk.init(w, lane, a.k.ss);
   stv.init(w, lane, a.v.ss);
   auto load_k = [&](int n0, auto sc) { stk.load(k_sl(sc), kb, a.k.ss, n0, Sk, w); };

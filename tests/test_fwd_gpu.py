@@ -143,7 +143,8 @@ def test_forward_argument_errors():
 
 # The launcher splits each tile's keys across two waves only when the grid of
 # 128-query workgroups is small (< 2 per CU, < 4 causal; 256 CUs on MI355X).
-# These ragged shapes are large enough to run the unsplit variant; the shapes
+# These ragged shapes are large enough to run the unsplit variant (the
+# non-causal D = 64 one as eight-wave, 256-query workgroups); the shapes
 # above run the split one.
 @pytest.mark.parametrize("shape,causal", [((4, 1000, 32, 64), False), ((8, 1000, 32, 64), True),
                                           ((4, 777, 32, 128), False), ((8, 520, 32, 32), True)])
