@@ -228,6 +228,17 @@ int launch_fwd_mode(const fa::FwdArgs &a, hipStream_t stream) {
       return launch_fwd_split<E, D, CAUSAL, 1, false, 8>(a, stream);
     }
   }
+  // Non-causal D = 128 key-split grids of at least one 128-query tile per
+  // CU: eight waves (four query groups x two key halves) sharing each K / V
+  // tile.
+  if constexpr (D == 128 && !CAUSAL && KSPLIT == 2) {
+    if ((int64_t)((a.Sq + 127) / 128) * a.B * a.H >= device_cus()) {
+      if constexpr (std::is_same<E, fa::f16>::value) {
+        if (fwd_prescaled<E>(a)) return launch_fwd_split<E, D, CAUSAL, 2, true, 8>(a, stream);
+      }
+      return launch_fwd_split<E, D, CAUSAL, 2, false, 8>(a, stream);
+    }
+  }
   // (not the unsplit D = 128 layout: the -max seed's 16 registers would
   // push it past 256 VGPRs, measured +3-4 % on the grids that use it)
   if constexpr (std::is_same<E, fa::f16>::value && !(D == 128 && KSPLIT == 1)) {

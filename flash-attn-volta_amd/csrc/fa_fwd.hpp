@@ -146,8 +146,7 @@ __host__ __device__ constexpr int bal_items(int nb) { return 3 * (nb >> 1) + (nb
 template <int D, int KSPLIT, int NW = 4>
 struct FwdTile {
   static_assert(KSPLIT == 1 || KSPLIT == 2, "key split is 1 or 2");
-  static_assert(NW == 4 || (NW == 8 && KSPLIT == 1 && D >= 64),
-                "eight waves: 256 queries, no key split, D >= 64");
+  static_assert(NW == 4 || (NW == 8 && D >= 64), "eight waves need D >= 64");
   static constexpr int NQG = NW / KSPLIT;  // query groups of 32 per workgroup
   static constexpr int NSUB = 2 / KSPLIT;  // 32-key sub-blocks per wave per tile
   static constexpr int BM = 32 * NQG;      // queries per workgroup
@@ -187,7 +186,8 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
   // cannot alias reads of another and does not wait for it early.
   __shared__ __attribute__((aligned(16))) f16 sk0[T::LDS_TILE], sk1[T::LDS_TILE];
   __shared__ __attribute__((aligned(16))) f16 sv0[T::LDS_TILE], sv1[T::LDS_TILE];
-  __shared__ __attribute__((aligned(16))) float s_ml[2][2][64];   // merge: m, l per query group
+  // merge: m, l per query group (key-split layouts)
+  __shared__ __attribute__((aligned(16))) float s_ml[KSPLIT == 2 ? T::NQG : 1][2][64];
   auto k_sl = [&](auto sc) -> f16 * { return decltype(sc)::value ? sk1 : sk0; };
   auto v_sl = [&](auto sc) -> f16 * { return decltype(sc)::value ? sv1 : sv0; };
 
@@ -674,10 +674,14 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
     else pv(C0{}, Check{}, nl, p_a);
   }
 
-  // ---- merge the two key halves of each query group (K slots reused; the
-  // loop's last barrier ordered every read of them before these writes)
+  // ---- merge the two key halves of each query group, through one LDS
+  // slot per group: K slots (the loop's last barrier ordered every read of
+  // them before these writes), and with four groups the V slots too, which
+  // the last tile's P V above still reads until the barrier here
   if (KSPLIT == 2) {
-    float *mbuf = reinterpret_cast<float *>(qg ? sk1 : sk0);
+    if constexpr (T::NQG > 2) __syncthreads();
+    f16 *slot = qg == 0 ? sk0 : (qg == 1 ? sk1 : (qg == 2 ? sv0 : sv1));
+    float *mbuf = reinterpret_cast<float *>(slot);
     if (kh == 1) {
       s_ml[qg][0][lane] = m_run;
       s_ml[qg][1][lane] = l_run;

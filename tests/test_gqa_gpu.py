@@ -169,6 +169,7 @@ BF16_CASES = [
     (1, 4096, 4096, 16, 16, 64, True),        # the C4a shape
     (1, 600, 600, 64, 64, 128, False),        # grid for the eight-wave D = 128 dK/dV
     (1, 2100, 2100, 32, 8, 64, False),        # eight-wave forward (256 queries), ragged
+    (1, 2100, 2100, 16, 4, 128, False),       # eight-wave key-split forward, ragged
 ]
 
 
