@@ -289,15 +289,15 @@ int launch_dkdv_split(const fa::BwdArgs &args, hipStream_t stream) {
   return launch_status();
 }
 
-template <typename E, int D, bool CAUSAL, int SPLIT, bool PRE>
+template <typename E, int D, bool CAUSAL, int SPLIT, bool PRE, int NW = 4>
 int launch_dq_split(const fa::BwdArgs &args, hipStream_t stream) {
-  using T = fa::DqTile<D, SPLIT>;
+  using T = fa::DqTile<D, SPLIT, NW>;
   fa::BwdArgs a = args;
   a.n_blocks = (a.Sq + T::BM - 1) / T::BM;
   // a split query block takes two workgroups
   const int64_t grid = ((int64_t)a.n_blocks + a.dq_split) * a.B * a.H;
   if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
-  constexpr auto kernel = fa::fa_bwd_dq_kernel<E, D, CAUSAL, SPLIT, PRE>;
+  constexpr auto kernel = fa::fa_bwd_dq_kernel<E, D, CAUSAL, SPLIT, PRE, NW>;
   a.zigzag = CAUSAL ? zigzag_order(grid, a.n_blocks, resident_per_cu<kernel>(T::NT)) : 0;
   hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(T::NT), 0, stream, a);
   return launch_status();
@@ -321,6 +321,21 @@ int launch_dkdv(const fa::BwdArgs &a, hipStream_t stream) {
 template <typename E, int D, bool CAUSAL>
 int launch_dq(const fa::BwdArgs &a, hipStream_t stream) {
   const bool split = row_split(a.Sq, (int64_t)a.B * a.H, CAUSAL);
+  // Non-causal grids of at least one eight-wave workgroup per CU: eight
+  // waves sharing each K / V tile, as in the forward (D = 64: 256 queries,
+  // no key split; D = 128 where the key split is chosen: 128 queries)
+  if constexpr (!CAUSAL && D == 64) {
+    if (!split && (int64_t)((a.Sq + 255) / 256) * a.B * a.H >= device_cus()) {
+      if constexpr (std::is_same<E, fa::f16>::value) {
+        if (a.c <= 1.0f) return launch_dq_split<E, D, CAUSAL, 1, true, 8>(a, stream);
+      }
+      return launch_dq_split<E, D, CAUSAL, 1, false, 8>(a, stream);
+    }
+  }
+  if constexpr (!CAUSAL && D == 128) {
+    if (split && (int64_t)((a.Sq + 127) / 128) * a.B * a.H >= device_cus())
+      return launch_dq_split<E, D, CAUSAL, 2, false, 8>(a, stream);
+  }
   // the pre-scaled mode under the forward's condition (fp16, c <= 1); not at
   // D = 128, where its seed registers would cost the second wave per SIMD
   if constexpr (std::is_same<E, fa::f16>::value && D <= 64) {

@@ -935,14 +935,15 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
 // LDS as K and V (kperm row order).  (The dK/dV kernel's 128-row tiles with
 // early S/dP issue measured 12 % slower here: the second score set costs
 // the third wave per SIMD.)
-template <int D, int SPLIT>
+template <int D, int SPLIT, int NW = 4>
 struct DqTile {
   static_assert(SPLIT == 1 || SPLIT == 2, "split is 1 or 2");
-  static constexpr int NQG = 4 / SPLIT;
+  static_assert(NW == 4 || (NW == 8 && D >= 64), "eight waves need D >= 64");
+  static constexpr int NQG = NW / SPLIT;   // query groups of 32
   static constexpr int NSUB = 2 / SPLIT;
   static constexpr int BM = 32 * NQG;
   static constexpr int BN = 64;
-  static constexpr int NT = 256;
+  static constexpr int NT = 64 * NW;
   static constexpr int LDS_TILE = BN * D;   // swizzled, unpadded (fa_common.hpp)
   static_assert(64 * (D / 2) * 4 <= LDS_TILE * 2, "a merge buffer must fit in one K stage");
 };
@@ -951,11 +952,14 @@ struct DqTile {
 // rounded to fp16, as in the forward's pre-scaled mode, and the S^T MFMAs
 // start from -LSE * log2(e), so they produce c s - LSE' and P is one exp2
 // per score, no FMA.
-template <typename E, int D, bool CAUSAL, int SPLIT, bool PRE = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3 : 1)))
+// NW = 8 (non-causal grids, chosen by the launcher): twice the query groups
+// share each K / V tile.
+template <typename E, int D, bool CAUSAL, int SPLIT, bool PRE = false, int NW = 4>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3 : 1)))
 void fa_bwd_dq_kernel(BwdArgs a) {
   static_assert(!PRE || std::is_same<E, f16>::value, "the pre-scaled mode is fp16 only");
-  using T = DqTile<D, SPLIT>;
+  static_assert(NW == 4 || !CAUSAL, "eight-wave dQ workgroups are for non-causal grids");
+  using T = DqTile<D, SPLIT, NW>;
   constexpr int BM = T::BM, BN = T::BN, NSUB = T::NSUB;
   // One LDS object per stage (see the dK/dV kernel).
   __shared__ __attribute__((aligned(16))) f16 s_k0[T::LDS_TILE], s_k1[T::LDS_TILE];
@@ -968,7 +972,7 @@ void fa_bwd_dq_kernel(BwdArgs a) {
   const int bid = blockIdx.x;
   // zero the split counters of the dK/dV launch that follows on the stream
   if (a.cnt_zero != nullptr && bid == 0) {
-    for (int i = threadIdx.x; i < a.n_cnt_zero; i += 256) a.cnt_zero[i] = 0u;
+    for (int i = threadIdx.x; i < a.n_cnt_zero; i += T::NT) a.cnt_zero[i] = 0u;
   }
   const int bh = bid % BH;
   const int rank = bid / BH;
@@ -1012,7 +1016,7 @@ void fa_bwd_dq_kernel(BwdArgs a) {
   const float c = a.c;
 
   // K and V tiles go straight to LDS (fa_common.hpp DmaStager).
-  DmaStager<D, SW_AT, BN> stk, stv;
+  DmaStager<D, SW_AT, BN, NW> stk, stv;
   stk.init(w, lane, a.k.ss);
   stv.init(w, lane, a.v.ss);
   auto load_tile = [&](int n0, auto stc) {
@@ -1193,7 +1197,9 @@ void fa_bwd_dq_kernel(BwdArgs a) {
   if (SPLIT == 2) {
     // the loop's last barrier ordered every tile read before these writes;
     // both key halves of a query carry the same scale
-    merge_pair<D>(reinterpret_cast<float *>(qg ? s_k1 : s_k0), kh == 1, dq, DsScale{}, lane);
+    // one K / V stage buffer per query group (up to four)
+    f16 *buf = qg == 0 ? s_k0 : (qg == 1 ? s_k1 : (qg == 2 ? s_v0 : s_v1));
+    merge_pair<D>(reinterpret_cast<float *>(buf), kh == 1, dq, DsScale{}, lane);
     if (kh == 1) return;
   }
   if (split) {
