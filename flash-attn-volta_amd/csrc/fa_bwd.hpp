@@ -48,9 +48,13 @@
 
 namespace fa {
 
-// Swizzle of the dK/dV kernel's tiles: SW_P8 (fa_common.hpp), not SW_AT,
-// whose second-read offsets would spill its registers.
-constexpr int kDkdvSwizzle = SW_P8;
+// Swizzle of the dK/dV kernel's query tiles (read both ways): the padded
+// SW_PD (fa_common.hpp) at D = 128, SW_P8 below -- not SW_AT, whose
+// second-read offsets would spill its registers.  Measured at D = 128:
+// LDS bank conflicts 45 % of LDS-active cycles with SW_P8, 0 with SW_PD;
+// the backward -3.2 to -3.8 % at (1,4096,8,128) and (1,4096,16,128).
+template <int D>
+constexpr int kDkdvSwizzle = D >= 128 ? SW_PD : SW_P8;
 
 struct BwdArgs {
   TensorDesc q, k, v, dout;   // q, dout: (B, Sq, H, D); k, v: (B, Sk, Hk, D)
@@ -381,8 +385,14 @@ struct DkdvTile {
   static constexpr int NT = 64 * NW;
   // waves per SIMD the register allocation is held to
   static constexpr int WAVES_PER_EU = (D == 64 && KV_LDS) ? 3 : (WIDE ? 2 : 1);
-  static constexpr int LDS_TILE = BQ * D;   // swizzled, unpadded (fa_common.hpp)
-  static constexpr int LDS_KV = KV_LDS ? BK * D : 8;   // K (or V) tile, kperm rows
+  // K and V staged in LDS are read only as B operands, row by row like an
+  // A operand: at D = 64 they take SW_A (conflict-free for those reads,
+  // with offsets of their own), at D = 128 the query tiles' SW_PD
+  // (conflict-free both ways, 4 offset registers where SW_A takes 8)
+  static constexpr int QSW = kDkdvSwizzle<D>;
+  static constexpr int KVSW = (KV_LDS && D == 64) ? SW_A : QSW;
+  static constexpr int LDS_TILE = lds_row<D, QSW>(BQ);   // one stage (fa_common.hpp)
+  static constexpr int LDS_KV = KV_LDS ? lds_row<D, KVSW>(BK) : 8;   // K (or V), kperm rows
   // operand reads of sdp_grad's MFMAs this many MFMAs ahead (0: each just
   // before its MFMA)
   static constexpr int PF_OPS = (D == 64 && KV_LDS) ? 1 : 0;
@@ -447,19 +457,22 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   // unscaled (ck = 1: a second bf16 rounding would cost 8-bit accuracy),
   // only its sign follows sm_scale.
   constexpr int NKF = T::KV_LDS ? 1 : D / 16;
-  // K and V staged in LDS are read only as B operands, row by row like an
-  // A operand: at D = 64 they take SW_A (conflict-free for those reads)
-  // and offsets of their own; the D = 128 layout, out of registers, keeps
-  // the query tiles' swizzle and offsets.
-  constexpr int kKvSwizzle = (T::KV_LDS && D == 64) ? SW_A : kDkdvSwizzle;
-  int kv_off[T::KV_LDS ? D / 16 : 1];
-  if constexpr (T::KV_LDS) {
-    const int sk = swz<D, kKvSwizzle>(l32);
+  constexpr int QSW = T::QSW, KVSW = T::KVSW;
+  // Element offset of A-operand row l32, chunk 2cc + g, of a tile laid out
+  // with swizzle SW.  SW_PD (D = 128) permutes a chunk index's bits 2-3
+  // only, so chunk 2cc + 2 + g sits 16 elements after chunk 2cc + g (cc
+  // even): an immediate, not a register.
+  auto row_offsets = [&](auto swc, int (&off)[D / 16]) {
+    constexpr int SW = decltype(swc)::value;
+    const int s = swz<D, SW>(l32);
 #pragma unroll
-    for (int cc = 0; cc < D / 16; ++cc)
-      kv_off[cc] = (kKvSwizzle == SW_P8 && cc >= 4) ? kv_off[cc - 4] + 64
-                                                    : l32 * D + (((2 * cc + g) ^ sk) << 3);
-  }
+    for (int cc = 0; cc < D / 16; ++cc) {
+      if (SW == SW_PD && (cc & 1)) off[cc] = off[cc - 1] + 16;
+      else off[cc] = lds_row<D, SW>(l32) + (((2 * cc + g) ^ s) << 3);
+    }
+  };
+  int kv_off[T::KV_LDS ? D / 16 : 1];
+  if constexpr (T::KV_LDS) row_offsets(std::integral_constant<int, KVSW>{}, kv_off);
   vec8<E> kf[NKF], vf[NKF];
   const float ck = std::is_same<E, f16>::value ? fminf(a.c, 1.0f) : 1.0f;
   const float cr = a.c / ck;
@@ -468,7 +481,7 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   // first query tile's loads are issued too (one memory latency for both)
   if constexpr (T::KV_LDS) {
     // the workgroup's BK keys into LDS (zeros past Sk)
-    DmaStager<D, kKvSwizzle, BK, T::NW> stk, stv;
+    DmaStager<D, KVSW, BK, T::NW> stk, stv;
     stk.init(w, lane, a.k.ss);
     stv.init(w, lane, a.v.ss);
     stk.load(s_k, a.k.head(b, hk), a.k.ss, k0, Sk, w);
@@ -480,11 +493,11 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   // B operands of S and dP: K^T / V^T fragments K[key][16cc + 8g .. +7]
   // (registers, or LDS rows 32kg + l32 read like the query tiles' A rows)
   auto k_frag = [&](int cc) -> vec8<E> {
-    if constexpr (T::KV_LDS) return ld8<E>(s_k + 32 * kg * D + kv_off[cc]);
+    if constexpr (T::KV_LDS) return ld8<E>(s_k + lds_row<D, KVSW>(32 * kg) + kv_off[cc]);
     else return kf[cc];
   };
   auto v_frag = [&](int cc) -> vec8<E> {
-    if constexpr (T::KV_LDS) return ld8<E>(s_v + 32 * kg * D + kv_off[cc]);
+    if constexpr (T::KV_LDS) return ld8<E>(s_v + lds_row<D, KVSW>(32 * kg) + kv_off[cc]);
     else return vf[cc];
   };
 
@@ -513,7 +526,7 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   // seeds: s_lse = -LSE * log2(e) / cr (-inf past S, so P = 0 there) and
   // s_dl = -delta.  Seeding the S and dP MFMAs with them yields
   // ck * s - LSE' and dP - delta with no per-score VALU work.
-  DmaStager<D, kDkdvSwizzle, BQ, T::NW> stq, stg;
+  DmaStager<D, QSW, BQ, T::NW> stq, stg;
   stq.init(w, lane, a.q.ss);
   stg.init(w, lane, a.dout.ss);
   const float lse_mul = -kLog2e / cr;
@@ -568,17 +581,9 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   // 2cc + g; transposed reads: rows 4g + (l16 >> 2), column chunk
   // 4d + 2((lane >> 4) & 1) + ((l16 >> 1) & 1), half 4 * (l16 & 1).
   int a_off[D / 16];
-  TrOffsets<D, kDkdvSwizzle> t_off;
-  {
-    const int sa = swz<D, kDkdvSwizzle>(l32);
-    // SW_P8 permutes only a chunk index's low 3 bits, so chunks 8-15 (D =
-    // 128) sit 64 elements after chunks 0-7: an immediate, not a register
-    static_assert(kDkdvSwizzle == SW_P8, "offsets below assume a 3-bit swizzle");
-#pragma unroll
-    for (int cc = 0; cc < D / 16; ++cc)
-      a_off[cc] = cc < 4 ? l32 * D + (((2 * cc + g) ^ sa) << 3) : a_off[cc - 4] + 64;
-    t_off.init(lane);
-  }
+  TrOffsets<D, QSW> t_off;
+  row_offsets(std::integral_constant<int, QSW>{}, a_off);
+  t_off.init(lane);
 
   if (n_tiles > 0) load_tile(cur_h, cur_m0, std::integral_constant<int, 0>{});
   __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): K, V and the first tile resident
@@ -588,7 +593,7 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
     __syncthreads();
     if (kmul != 1.0f) {
 #pragma unroll
-      for (int ch = tid; ch < BK * D / 8; ch += T::NT) {
+      for (int ch = tid; ch < T::LDS_KV / 8; ch += T::NT) {   // padding too
         vec8<E> x = ld8<E>(s_k + 8 * ch);
 #pragma unroll
         for (int j = 0; j < 8; ++j) x[j] = (E)((float)x[j] * kmul);
@@ -650,8 +655,8 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
           dpacc[8 * hh + 4 + j] = d_hi[j];
         }
       }
-      const f16 *qr = q_st(stc) + 32 * qs * D;
-      const f16 *gr = do_st(stc) + 32 * qs * D;
+      const f16 *qr = q_st(stc) + lds_row<D, QSW>(32 * qs);
+      const f16 *gr = do_st(stc) + lds_row<D, QSW>(32 * qs);
 #pragma unroll
       for (int cc = 0; cc < D / 16; ++cc) {
         sacc = mfma32(ld8<E>(qr + a_off[cc]), k_frag(cc), sacc);
@@ -705,7 +710,7 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         // kperm rows 32qs + 16hh + 4g + (0..3) and +8: this 8-query slice
-        const int rb = (32 * qs + 16 * hh) * D;
+        const int rb = lds_row<D, QSW>(32 * qs + 16 * hh);
 #pragma unroll
         for (int d = 0; d < D / 32; ++d) {
           dv[d] = mfma32(load_tr_pair<E>(do_st(stc) + rb, t_off.lo(d), t_off.hi(d)), pf[hh], dv[d]);
@@ -729,7 +734,6 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
     auto sdp_grad = [&](int sb) {
       constexpr int NC = D / 16;          // S / dP MFMAs (K-dim chunks of 16)
       constexpr int NO = 2 * (D / 32);    // dV / dK MFMAs (2 query halves x D / 32)
-      constexpr int NM = 2 * NC + 2 * NO;
       // S / dP operand reads this many MFMAs ahead (the non-causal variant
       // would spill)
       constexpr int PFD = CAUSAL ? T::PF_OPS : 0;
@@ -761,9 +765,9 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
         for (int i = 0; i < 16; ++i)
           sacc[i] = (slot_row(i, 0) >= lo && slot_row(i, 0) < hi) ? sacc[i] : kNegInf;
       }
-      const f16 *qr = q_st(stc) + 32 * qs * D;
-      const f16 *gr = do_st(stc) + 32 * qs * D;
-      const int rb0 = (32 * qs) * D;
+      const f16 *qr = q_st(stc) + lds_row<D, QSW>(32 * qs);
+      const f16 *gr = do_st(stc) + lds_row<D, QSW>(32 * qs);
+      const int rb0 = lds_row<D, QSW>(32 * qs);
       // LDS operands of MFMA i of the block (S: Q and K^T; dP: dO and V^T;
       // dV: dO^T; dK: Q^T), in ring slot i % (PFD + 1)
       vec8<E> opa[PFD + 1], opb[PFD + 1];
@@ -778,10 +782,12 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
           opb[sl] = v_frag(i - NC);
         } else if constexpr (i < 2 * NC + NO) {
           constexpr int o = i - 2 * NC, hh = o / (D / 32), d = o % (D / 32);
-          opa[sl] = load_tr_pair<E>(do_st(stc) + rb0 + 16 * hh * D, t_off.lo(d), t_off.hi(d));
+          opa[sl] = load_tr_pair<E>(do_st(stc) + rb0 + lds_row<D, QSW>(16 * hh), t_off.lo(d),
+                                    t_off.hi(d));
         } else {
           constexpr int o = i - 2 * NC - NO, hh = o / (D / 32), d = o % (D / 32);
-          opa[sl] = load_tr_pair<E>(q_st(stc) + rb0 + 16 * hh * D, t_off.lo(d), t_off.hi(d));
+          opa[sl] = load_tr_pair<E>(q_st(stc) + rb0 + lds_row<D, QSW>(16 * hh), t_off.lo(d),
+                                    t_off.hi(d));
         }
       };
       // before MFMA i: the S / dP operands of MFMA i + PFD (PFD = 0: its

@@ -217,8 +217,8 @@ __device__ __forceinline__ int wave_id() {
 // ---------------------------------------------------------------------------
 // Swizzled tiles staged straight from global memory into LDS.
 //
-// A tile is ROWS rows x D fp16, unpadded (row stride 2*D bytes), with 32-row
-// blocks in kperm row order.  Each row's 16-byte chunks are XOR-permuted:
+// A tile is ROWS rows x D fp16, row stride 2*D bytes (unpadded except
+// SW_PD's 16 bytes per KiB), with 32-row blocks in kperm row order.  Each row's 16-byte chunks are XOR-permuted:
 // physical chunk = logical chunk ^ swz(row).  The LDS serves a wave's read
 // in groups of lanes (gfx950: 64 banks of 4 bytes; 16 lanes of a 128-bit
 // read, 32 lanes of a 64-bit transposed read per cycle), so a read is
@@ -242,13 +242,25 @@ __device__ __forceinline__ int wave_id() {
 //   SW_P8 (tiles read both ways where the registers of those extra offsets
 //         would cost occupancy): period 8, the 8-lane form of the first
 //         property and the second at D <= 64.
-enum { SW_A = 0, SW_T = 1, SW_AT = 2, SW_P8 = 3 };
+//   SW_PD (tiles read both ways, D = 128): both properties with period 4
+//         in the row, on a tile padded with 16 bytes after every KiB
+//         (lds_row).  Rows 8 apart then share the chunk permutation (the
+//         second transposed read is the first's address plus an immediate,
+//         lds_row(8)) but sit 32 bytes apart in the bank window, which
+//         gives 16 consecutive rows 16 distinct groups.  A tile costs 1/64
+//         more LDS.  (The D = 64 analogue -- period 8, rows 8 apart 16 bytes
+//         apart -- measured as many conflicts as SW_P8 on the query tiles
+//         and more than SW_A on row-read tiles, so the model above is not
+//         the whole story at D = 64; it is not used.)
+enum { SW_A = 0, SW_T = 1, SW_AT = 2, SW_P8 = 3, SW_PD = 4 };
 template <int D, int SW>
 __device__ __forceinline__ constexpr int swz(int r) {
+  static_assert(SW != SW_PD || D >= 128, "SW_PD is the D = 128 layout");
   if (SW == SW_A)
     return D >= 128 ? (r & 15)
          : D == 64  ? (((r >> 1) & 3) | (((r ^ (r >> 3)) & 1) << 2))
                     : (((r >> 2) & 1) | ((((r >> 1) ^ (r >> 3)) & 1) << 1));
+  if (SW == SW_PD) return (r & 3) << 2;
   if (SW == SW_P8)
     return D >= 64 ? (((r & 3) << 1) | ((r >> 2) & 1)) : ((((r >> 1) & 1) << 1) | ((r >> 2) & 1));
   if (SW == SW_T)
@@ -259,6 +271,15 @@ __device__ __forceinline__ constexpr int swz(int r) {
        : D == 64  ? (((r >> 1) & 1) | (((r ^ (r >> 2)) & 1) << 1) |
                      (((r ^ (r >> 1) ^ (r >> 3)) & 1) << 2))
                   : (((r >> 2) & 1) | ((((r >> 1) ^ (r >> 3)) & 1) << 1));
+}
+
+// Element offset of row r of a tile in LDS (rows of D fp16; an SW_PD tile
+// has 8 elements of padding after every 512).  Linear in r over multiples
+// of 4 rows at D = 128, so sub-block bases stay immediates.  lds_row(ROWS)
+// is a tile's size.
+template <int D, int SW>
+__host__ __device__ __forceinline__ constexpr int lds_row(int r) {
+  return SW == SW_PD ? r * D + 8 * ((r * D) >> 9) : r * D;
 }
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -293,8 +314,10 @@ struct DmaStager {
     load(slot, rows_rsrc(head, ss, r0, S, D), w);
   }
   __device__ __forceinline__ void load(f16 *slot, __amdgpu_buffer_rsrc_t rs, int w) const {
+    // one KiB per instruction, plus SW_PD's 16 bytes after each
+    constexpr int kStride = lds_row<D, SW>(512 / D);
 #pragma unroll
-    for (int j = 0; j < PER_WAVE; ++j) lds_dma16(rs, slot + (w * PER_WAVE + j) * 512, off[j]);
+    for (int j = 0; j < PER_WAVE; ++j) lds_dma16(rs, slot + (w * PER_WAVE + j) * kStride, off[j]);
   }
 };
 
@@ -322,9 +345,10 @@ __device__ __forceinline__ vec8<E> load_tr_pair(const f16 *base, int lo, int hi)
 // column block d (32 columns), rows 4g + (l16 >> 2) (`lo`) and 8 rows
 // further (`hi`), column chunk 4d + 2((lane >> 4) & 1) + ((l16 >> 1) & 1),
 // half 4 * (l16 & 1).  Row offsets that are multiples of 16 (sub-blocks of
-// 32 rows, the 16-row halves) keep the swizzle.  With SW_T the swizzle
-// repeats every 8 rows and hi(d) is lo(d) + 8 D, an immediate; with SW_AT
-// the two reads take different chunk permutations and hi is a register.
+// 32 rows, the 16-row halves; lds_row of them) keep the swizzle.  With
+// SW_T, SW_P8 and SW_PD the swizzle repeats every 8 rows and hi(d) is
+// lo(d) + lds_row(8), an immediate; with SW_AT the two reads take
+// different chunk permutations and hi is a register.
 template <int D, int SW>
 struct TrOffsets {
   static constexpr bool SPLIT = SW == SW_A || SW == SW_AT;
@@ -336,14 +360,14 @@ struct TrOffsets {
 #pragma unroll
     for (int d = 0; d < D / 32; ++d) {
       const int c = 4 * d + 2 * ((lane >> 4) & 1) + ((l16 >> 1) & 1);
-      lo_[d] = tr * D + ((c ^ swz<D, SW>(tr)) << 3) + half;
+      lo_[d] = lds_row<D, SW>(tr) + ((c ^ swz<D, SW>(tr)) << 3) + half;
       if constexpr (SPLIT) hi_[d] = (tr + 8) * D + ((c ^ swz<D, SW>(tr + 8)) << 3) + half;
     }
   }
   __device__ __forceinline__ int lo(int d) const { return lo_[d]; }
   __device__ __forceinline__ int hi(int d) const {
     if constexpr (SPLIT) return hi_[d];
-    else return lo_[d] + 8 * D;
+    else return lo_[d] + lds_row<D, SW>(8);
   }
 };
 
