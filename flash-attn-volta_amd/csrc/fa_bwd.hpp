@@ -394,8 +394,15 @@ struct DkdvTile {
   static constexpr int LDS_TILE = lds_row<D, QSW>(BQ);   // one stage (fa_common.hpp)
   static constexpr int LDS_KV = KV_LDS ? lds_row<D, KVSW>(BK) : 8;   // K (or V), kperm rows
   // operand reads of sdp_grad's MFMAs this many MFMAs ahead (0: each just
-  // before its MFMA)
-  static constexpr int PF_OPS = (D == 64 && KV_LDS) ? 1 : 0;
+  // before its MFMA), for the S / dP MFMAs, and with PF_ALL for the dV / dK
+  // MFMAs too.  At D = 128 (two waves per SIMD) every MFMA otherwise waits
+  // on its own LDS reads: the backward -1 to -2.4 % with the S / dP
+  // operands ahead, and another -1 to -2.4 % with all of them (measured at
+  // (1,4096,8,128), (1,4096,16,128), (1,8192,8,128) causal and non-causal;
+  // two MFMAs ahead: +-0.8 %).  At D = 64 (three waves per SIMD, 168 VGPRs)
+  // the dV / dK operands ahead would spill.
+  static constexpr int PF_OPS = KV_LDS ? 1 : 0;
+  static constexpr bool PF_ALL = WIDE;
   // layouts that implement the causal key-block split (BwdArgs::split_kt)
   static constexpr bool KEY_SPLIT = WIDE || (D == 64 && SPLIT == 2);
   static_assert(64 * (D / 2) * 4 <= LDS_TILE * 2, "a merge buffer must fit in one stage");
@@ -734,9 +741,10 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
     auto sdp_grad = [&](int sb) {
       constexpr int NC = D / 16;          // S / dP MFMAs (K-dim chunks of 16)
       constexpr int NO = 2 * (D / 32);    // dV / dK MFMAs (2 query halves x D / 32)
-      // S / dP operand reads this many MFMAs ahead (the non-causal variant
+      // operand reads this many MFMAs ahead (the non-causal D = 64 variant
       // would spill)
-      constexpr int PFD = CAUSAL ? T::PF_OPS : 0;
+      constexpr int PFD = (CAUSAL || T::WIDE) ? T::PF_OPS : 0;
+      constexpr int NM = 2 * NC + 2 * NO;
       const int qs = NSUB * qh + sb;
       floatx16 sacc, dpacc;
 #pragma unroll
@@ -790,12 +798,14 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
                                     t_off.hi(d));
         }
       };
-      // before MFMA i: the S / dP operands of MFMA i + PFD (PFD = 0: its
-      // own), the dV / dK operand of MFMA i itself (reading those ahead
-      // too spills a register)
+      // before MFMA i: the operands of MFMA i + PFD (PFD = 0: its own); at
+      // D = 64 the dV / dK operand of MFMA i itself (reading those ahead
+      // too spills a register there)
       auto ahead = [&](auto ic) {
         constexpr int i = decltype(ic)::value;
-        if constexpr (i < 2 * NC) {
+        if constexpr (T::PF_ALL) {
+          if constexpr (i + PFD < NM) fetch(std::integral_constant<int, i + PFD>{});
+        } else if constexpr (i < 2 * NC) {
           if constexpr (i + PFD < 2 * NC) fetch(std::integral_constant<int, i + PFD>{});
         } else {
           fetch(ic);
