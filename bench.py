@@ -582,6 +582,60 @@ def run_configs(steps, warmup, with_cpu, prewarm_s=0.0):
               f"{r.get('cpu_fwd_tflops', '-')} | {r.get('cpu_fwd_bwd_tflops', '-')} |")
 
 
+# Grids several rounds of workgroups deep, for --large: (B, S, H, D, causal)
+LARGE_TABLE = [
+    (4, 4096, 16, 64, False),
+    (4, 4096, 16, 64, True),
+    (4, 4096, 16, 128, False),
+    (4, 4096, 16, 128, True),
+    (1, 16384, 16, 128, True),
+]
+
+
+def run_large(steps, warmup, prewarm_s=0.0):
+    """Forward and backward calls (flash_attn_forward with LSE,
+    flash_attn_backward) on grids that fill the GPU several times over,
+    inputs N(0, 1) * 0.5, pre-warmed, HIP events.  TFLOP/s in the metric's
+    convention (forward 4*B*H*S^2*D, backward 4x that, dense when causal);
+    `issued_pct` is the share of the MFMA peak spent on the work the kernels
+    issue: half the scores when causal, and 7 GEMMs of 2*S^2*D per head in
+    the backward (S and dP recomputed by both backward kernels), 3.5x the
+    forward's 2.  One JSON line per shape, then a markdown table."""
+    import torch
+    from flash_attn_volta import flash_attn_backward, flash_attn_forward
+    rows = []
+    for b, s, h, d, causal in LARGE_TABLE:
+        g = torch.Generator(device="cpu").manual_seed(0)
+        q, k, v, do = (torch.randn((b, s, h, d), generator=g).half().mul_(0.5).cuda()
+                       for _ in range(4))
+        o, lse = flash_attn_forward(q, k, v, causal=causal, return_softmax_lse=True)
+
+        def fwd():
+            flash_attn_forward(q, k, v, causal=causal, return_softmax_lse=True)
+
+        def bwd():
+            flash_attn_backward(do, q, k, v, o, lse, causal=causal)
+        flops = fwd_flops(b, s, h, d)
+        useful = 0.5 if causal else 1.0
+        row = {"shape": [b, s, h, d], "causal": causal}
+        for name, fn, counted, issued in (("fwd", fwd, 1.0, 1.0), ("bwd", bwd, 4.0, 3.5)):
+            prewarm(fn, prewarm_s)
+            t = time_loop(fn, steps, warmup)[1]
+            row[f"{name}_us"] = round(t * 1e6, 2)
+            row[f"{name}_tflops"] = round(counted * flops / t / 1e12, 1)
+            row[f"{name}_issued_pct"] = round(
+                100 * issued * useful * flops / t / 1e12 / PEAK_FP16_TFLOPS, 1)
+        rows.append(row)
+        print(json.dumps(row), flush=True)
+    print("| (B,S,H,D) | fwd us | fwd TFLOP/s (issued % of peak) | bwd us | "
+          "bwd TFLOP/s (issued % of peak) |")
+    print("|---|---:|---:|---:|---:|")
+    for r in rows:
+        print(f"| {tuple(r['shape'])}{' causal' if r['causal'] else ' non-causal'} | "
+              f"{r['fwd_us']} | {r['fwd_tflops']} ({r['fwd_issued_pct']} %) | "
+              f"{r['bwd_us']} | {r['bwd_tflops']} ({r['bwd_issued_pct']} %) |")
+
+
 # Fused-prologue workloads: (name, B, S, H, Hk, D, qk_norm, dtype name)
 ROPE_TABLE = [
     ("C5-llama", 1, 4096, 16, 16, 128, False, "fp16"),
@@ -942,6 +996,9 @@ def main():
                     help="instead of the benchmark line, time every BASELINE config (GPU "
                          "fwd and fwd+bwd, plus the CPU baseline unless --no-cpu) and print "
                          "a table")
+    ap.add_argument("--large", action="store_true",
+                    help="instead of the benchmark line, time the forward and backward calls "
+                         "on grids several rounds of workgroups deep and print a table")
     ap.add_argument("--rope", action="store_true",
                     help="instead of the benchmark line, time the fused QK-norm + rotary "
                          "prologue against transformers' eager one and print a table")
@@ -996,6 +1053,10 @@ def main():
     if args.decode:
         torch.cuda.set_device(0)
         run_decode(args.steps, args.warmup)
+        return
+    if args.large:
+        torch.cuda.set_device(0)
+        run_large(args.steps, args.warmup, args.prewarm_seconds)
         return
     if args.llama:
         torch.cuda.set_device(0)
