@@ -125,13 +125,59 @@ int launch_status() {
   return e == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
 }
 
-// Compute units of the current device (cached per device; 256 on MI355X).
+// Device of `stream`: kernels run on the device their stream belongs to,
+// which need not be the host thread's current device.  The NULL stream (or
+// a stream the runtime cannot place) means the current device.
+int stream_device(hipStream_t stream) {
+  int dev = -1;
+  if (stream != nullptr) {
+    if (hipStreamGetDevice(stream, &dev) == hipSuccess && dev >= 0) return dev;
+    (void)hipGetLastError();   // not a launch error of the call
+  }
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return -1;
+  }
+  return dev;
+}
+
+// The stream the current entry point launches on, per host thread: set by
+// LaunchDevice at the top of each launching path (nested paths keep the
+// outer one's), so the launch decisions below follow the stream's device
+// without the stream passed through every helper.  The device is looked up
+// on first use, after the arguments have been validated.
+struct LaunchTarget {
+  bool active = false;
+  void *stream = nullptr;
+  int dev = -2;   // -2: not looked up yet
+};
+thread_local LaunchTarget t_launch;
+
+struct LaunchDevice {
+  LaunchTarget saved;
+  explicit LaunchDevice(void *stream) : saved(t_launch) {
+    if (!t_launch.active || t_launch.stream != stream) t_launch = LaunchTarget{true, stream, -2};
+  }
+  ~LaunchDevice() { t_launch = saved; }
+  LaunchDevice(const LaunchDevice &) = delete;
+  LaunchDevice &operator=(const LaunchDevice &) = delete;
+};
+
+int launch_device() {
+  if (t_launch.active) {
+    if (t_launch.dev == -2) t_launch.dev = stream_device(static_cast<hipStream_t>(t_launch.stream));
+    return t_launch.dev;
+  }
+  return stream_device(nullptr);
+}
+
+// Compute units of the launch device (cached per device; 256 on MI355X).
 // The cache is atomic: entry points may be called from several host
 // threads at once (they all store the same value).
 int device_cus() {
   static std::atomic<int> cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  const int dev = launch_device();
+  if (dev < 0 || dev >= 64) return 256;
   int n = cache[dev].load(std::memory_order_relaxed);
   if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
@@ -249,6 +295,18 @@ int launch_fwd_mode(const fa::FwdArgs &a, hipStream_t stream) {
 
 template <typename E, int D, bool CAUSAL>
 int launch_fwd(const fa::FwdArgs &a, hipStream_t stream) {
+  // Non-causal grids of at most one 64-query workgroup per CU, where the
+  // four-wave key-split layout would run one wave per SIMD: eight waves per
+  // workgroup, each query group's keys in four parts of 128-key tiles --
+  // twice the waves in flight on the same grid.
+  if constexpr (!CAUSAL && D >= 64) {
+    if ((int64_t)((a.Sq + 63) / 64) * a.B * a.H <= device_cus()) {
+      if constexpr (std::is_same<E, fa::f16>::value) {
+        if (fwd_prescaled<E>(a)) return launch_fwd_split<E, D, CAUSAL, 4, true, 8>(a, stream);
+      }
+      return launch_fwd_split<E, D, CAUSAL, 4, false, 8>(a, stream);
+    }
+  }
   return row_split(a.Sq, (int64_t)a.B * a.H, CAUSAL) ? launch_fwd_mode<E, D, CAUSAL, 2>(a, stream)
                                                      : launch_fwd_mode<E, D, CAUSAL, 1>(a, stream);
 }
@@ -333,12 +391,17 @@ int launch_dq(const fa::BwdArgs &a, hipStream_t stream) {
     }
   }
   if constexpr (!CAUSAL && D == 128) {
-    if (split && (int64_t)((a.Sq + 127) / 128) * a.B * a.H >= device_cus())
+    if (split && (int64_t)((a.Sq + 127) / 128) * a.B * a.H >= device_cus()) {
+      if constexpr (std::is_same<E, fa::f16>::value) {
+        if (a.c <= 1.0f) return launch_dq_split<E, D, CAUSAL, 2, true, 8>(a, stream);
+      }
       return launch_dq_split<E, D, CAUSAL, 2, false, 8>(a, stream);
+    }
   }
-  // the pre-scaled mode under the forward's condition (fp16, c <= 1); not at
-  // D = 128, where its seed registers would cost the second wave per SIMD
-  if constexpr (std::is_same<E, fa::f16>::value && D <= 64) {
+  // the pre-scaled mode under the forward's condition (fp16, c <= 1), at
+  // every D (at D = 128 its 16 seed registers fit beside two waves per SIMD
+  // since the LDS offsets stopped taking a register per array and stage)
+  if constexpr (std::is_same<E, fa::f16>::value) {
     if (a.c <= 1.0f)
       return split ? launch_dq_split<E, D, CAUSAL, 2, true>(a, stream)
                    : launch_dq_split<E, D, CAUSAL, 1, true>(a, stream);
@@ -485,6 +548,7 @@ fa::FwdArgs fwd_args(const void *q, const void *k, const void *v, void *o, float
 int run_fwd(const void *q, const void *k, const void *v, void *o, float *lse, const Shape &s,
             const int64_t *q_st, const int64_t *k_st, const int64_t *v_st, const int64_t *o_st,
             float sm_scale, int causal, void *stream) {
+  const LaunchDevice launch_dev(stream);
   int rc = check_fwd(q, k, v, o, lse, s, q_st, k_st, v_st, o_st, sm_scale);
   if (rc) return rc;
   const fa::FwdArgs a = fwd_args(q, k, v, o, lse, s, q_st, k_st, v_st, o_st, sm_scale);
@@ -496,6 +560,7 @@ int run_fwd_splitkv(const void *q, const void *k, const void *v, void *o, float 
                     void *workspace, size_t workspace_bytes, const Shape &s, const int64_t *q_st,
                     const int64_t *k_st, const int64_t *v_st, const int64_t *o_st, float sm_scale,
                     int causal, void *stream) {
+  const LaunchDevice launch_dev(stream);
   int rc = check_fwd(q, k, v, o, lse, s, q_st, k_st, v_st, o_st, sm_scale);
   if (rc) return rc;
   const SplitPlan plan = splitkv_plan(s);
@@ -624,6 +689,7 @@ int run_fwd_ws(const void *q, const void *k, const void *v, void *o, float *lse,
                size_t workspace_bytes, const Shape &s, const int64_t *q_st, const int64_t *k_st,
                const int64_t *v_st, const int64_t *o_st, float sm_scale, int causal,
                void *stream) {
+  const LaunchDevice launch_dev(stream);
   int rc = check_fwd(q, k, v, o, lse, s, q_st, k_st, v_st, o_st, sm_scale);
   if (rc) return rc;
   // less than the schedule's workspace (none included): the plain forward
@@ -657,6 +723,7 @@ int run_fwd_ws(const void *q, const void *k, const void *v, void *o, float *lse,
 
 int run_pre(const void *o, const void *dout, float *delta, const Shape &s, const int64_t *o_st,
             const int64_t *do_st, void *stream) {
+  const LaunchDevice launch_dev(stream);
   int rc = check_shape(s);
   if (rc) return rc;
   if ((rc = check_q_like(o, o_st, s))) return rc;
@@ -856,6 +923,7 @@ int run_dkdv(const void *dout, const void *q, const void *k, const void *v, cons
              const int64_t *dv_st, float sm_scale, int causal, void *stream, int split_kt = 0,
              unsigned *cnt = nullptr, float *part = nullptr, const DqSplit *dqs = nullptr,
              float *dq_part = nullptr, void *dq = nullptr, const int64_t *dq_st = nullptr) {
+  const LaunchDevice launch_dev(stream);
   fa::BwdArgs a;
   int rc = bwd_common(dout, q, k, v, lse, delta, s, do_st, q_st, k_st, v_st, sm_scale, &a);
   if (rc) return rc;
@@ -894,6 +962,7 @@ int run_dq(const void *dout, const void *q, const void *k, const void *v, const 
            int causal, void *stream, const void *o = nullptr, const int64_t *o_st = nullptr,
            unsigned *cnt_zero = nullptr, int n_cnt_zero = 0, int dq_split = 0,
            float *dq_part = nullptr) {
+  const LaunchDevice launch_dev(stream);
   fa::BwdArgs a;
   int rc = bwd_common(dout, q, k, v, lse, delta, s, do_st, q_st, k_st, v_st, sm_scale, &a);
   if (rc) return rc;
@@ -949,6 +1018,7 @@ int run_bwd(const void *dout, const void *q, const void *k, const void *v, const
             size_t workspace_bytes, const Shape &s, const int64_t *do_st, const int64_t *q_st,
             const int64_t *k_st, const int64_t *v_st, const int64_t *o_st, const int64_t *dq_st,
             const int64_t *dk_st, const int64_t *dv_st, float sm_scale, int causal, void *stream) {
+  const LaunchDevice launch_dev(stream);
   int rc = check_bwd(dout, q, k, v, o, lse, dq, dk, dv, s, do_st, q_st, k_st, v_st, o_st, dq_st,
                      dk_st, dv_st, sm_scale);
   if (rc) return rc;
@@ -1093,6 +1163,7 @@ int run_rope_fwd(const void *q, const void *k, void *q_out, void *k_out, const v
                  const void *sin, const void *wq, const void *wk, float eps, const RopeShape &s,
                  const int64_t *q_st, const int64_t *k_st, const int64_t *qo_st,
                  const int64_t *ko_st, const int64_t *cs_st, void *stream) {
+  const LaunchDevice launch_dev(stream);
   int rc = check_rope_shape(s);
   if (rc) return rc;
   if ((rc = check_tensor(q, q_st, s.B, s.S, s.H, s.D, false, 0))) return rc;
@@ -1135,6 +1206,7 @@ int run_rope_bwd(const void *dq_out, const void *dk_out, const void *q, const vo
                  size_t workspace_bytes, const RopeShape &s, const int64_t *dqo_st,
                  const int64_t *dko_st, const int64_t *q_st, const int64_t *k_st,
                  const int64_t *dq_st, const int64_t *dk_st, const int64_t *cs_st, void *stream) {
+  const LaunchDevice launch_dev(stream);
   int rc = check_rope_shape(s);
   if (rc) return rc;
   if ((rc = check_tensor(dq_out, dqo_st, s.B, s.S, s.H, s.D, false, 0))) return rc;
@@ -1214,14 +1286,24 @@ namespace {
 constexpr int kScratchDevices = 64;
 std::atomic<uintptr_t> g_scratch_addr[kScratchDevices];
 
-int scratch_on_current_device(void **out) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return FA_ERR_LAUNCH;
-  const bool cached = dev >= 0 && dev < kScratchDevices;
+// The scratch array's address on the device of `stream` (stream_device):
+// looked up with that device current, which is restored afterwards.
+int scratch_for_stream(void *stream, void **out) {
+  const int dev = stream_device(static_cast<hipStream_t>(stream));
+  if (dev < 0) return FA_ERR_LAUNCH;
+  const bool cached = dev < kScratchDevices;
   uintptr_t p = cached ? g_scratch_addr[dev].load(std::memory_order_relaxed) : 0;
   if (p == 0) {
+    int cur = dev;
+    if (hipGetDevice(&cur) != hipSuccess) cur = dev;
+    if (cur != dev && hipSetDevice(dev) != hipSuccess) {
+      (void)hipGetLastError();
+      return FA_ERR_LAUNCH;
+    }
     void *addr = nullptr;
-    if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || addr == nullptr) {
+    const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (e != hipSuccess || addr == nullptr) {
       (void)hipGetLastError();   // not a launch error of the next call
       return FA_ERR_LAUNCH;
     }
@@ -1382,7 +1464,7 @@ int fa_bwd_gqa_noalloc(const void *dout, const void *q, const void *k, const voi
   if (rc) return rc;
   if (delta_bytes(B, Sq, H) > (size_t)FA_NOALLOC_SCRATCH_BYTES) return FA_ERR_SCRATCH;
   void *ws = nullptr;
-  if ((rc = scratch_on_current_device(&ws))) return rc;
+  if ((rc = scratch_for_stream(stream, &ws))) return rc;
   return run_bwd(dout, q, k, v, o, lse, dq, dk, dv, ws, FA_NOALLOC_SCRATCH_BYTES, s, do_strides,
                  q_strides, k_strides, v_strides, o_strides, dq_strides, dk_strides, dv_strides,
                  sm_scale, causal, stream);

@@ -1,22 +1,27 @@
 // fa_bwd.hpp -- backward FlashAttention kernels for gfx950.
 //
-// FlashAttention backward (Dao et al. 2022, Algorithm 4) as three launches,
-// the same split as the reference (flash_attn_volta/triton_fa_bwd.py:636-700):
-//   1. fa_bwd_preprocess_kernel : delta = rowsum(dO * O) in fp32
-//                                 (reference: torch op at triton_fa_bwd.py:650)
-//   2. fa_bwd_dkdv_kernel       : one workgroup per key block, sweeping query
-//                                 tiles; dV = P^T dO, dK = scale * dS^T Q
-//                                 (reference: _fa_bwd_dkdv_kernel_*, :319-580)
-//   3. fa_bwd_dq_kernel         : one workgroup per query block, sweeping key
-//                                 tiles; dQ = scale * dS K
-//                                 (reference: _fa_bwd_dq_kernel_*, :73-307)
-// with P = exp(scale * Q K^T - LSE) recomputed from the forward LSE and
+// FlashAttention backward (Dao et al. 2022, Algorithm 4).  The reference
+// (flash_attn_volta/triton_fa_bwd.py:636-700) runs a delta op and two
+// kernels; fa_bwd here runs two launches, in this order on one stream:
+//   1. fa_bwd_dq_kernel   : one workgroup per query block, sweeping key
+//                           tiles; dQ = scale * dS K, and delta =
+//                           rowsum(dO * O) in fp32 from the rows its lanes
+//                           hold, written for the next launch (reference:
+//                           _fa_bwd_dq_kernel_*, :73-307, and the torch op
+//                           at :650)
+//   2. fa_bwd_dkdv_kernel : one workgroup per key block, sweeping query
+//                           tiles; dV = P^T dO, dK = scale * dS^T Q
+//                           (reference: _fa_bwd_dkdv_kernel_*, :319-580)
+// The standalone entry points fa_bwd_preprocess / fa_bwd_dq / fa_bwd_dkdv
+// run fa_bwd_preprocess_kernel (delta alone) and each kernel by itself.
+// P = exp(scale * Q K^T - LSE) is recomputed from the forward LSE and
 // dS = P * (dO V^T - delta).  No floating-point atomics and no S x S
 // buffer: every output element is written once by one lane, so results are
 // bit-reproducible and a causal query row's dQ never reads a key block it
-// cannot see.  (The one integer atomic, in the causal key-block split of
-// the eight-wave D = 128 dK/dV kernel, only decides which of two
-// workgroups adds their two fp32 partials; the sum is the same either way.)
+// cannot see.  (The one integer atomic, in the causal key-block split --
+// of the eight-wave D = 128 dK/dV layout and of the D = 64 query-split
+// layout, DkdvTile::KEY_SPLIT -- only decides which of two workgroups adds
+// their two fp32 partials; the sum is the same either way.)
 //
 // Fragment layouts follow fa_common.hpp.  The dK/dV kernel computes S = Q K^T
 // with queries as the (kperm-ordered) A rows, so a lane owns one key and its
@@ -54,7 +59,7 @@ namespace fa {
 // LDS bank conflicts 45 % of LDS-active cycles with SW_P8, 0 with SW_PD;
 // the backward -3.2 to -3.8 % at (1,4096,8,128) and (1,4096,16,128).
 template <int D>
-constexpr int kDkdvSwizzle = D >= 128 ? SW_PD : SW_P8;
+constexpr int kDkdvSwizzle = D >= 128 ? SW_PD : (D == 64 ? SW_AT : SW_P8);
 
 struct BwdArgs {
   TensorDesc q, k, v, dout;   // q, dout: (B, Sq, H, D); k, v: (B, Sk, Hk, D)
@@ -402,7 +407,7 @@ struct DkdvTile {
   // two MFMAs ahead: +-0.8 %).  At D = 64 (three waves per SIMD, 168 VGPRs)
   // the dV / dK operands ahead would spill.
   static constexpr int PF_OPS = KV_LDS ? 1 : 0;
-  static constexpr bool PF_ALL = WIDE;
+  static constexpr bool PF_ALL = WIDE || (D == 64 && KV_LDS);
   // layouts that implement the causal key-block split (BwdArgs::split_kt)
   static constexpr bool KEY_SPLIT = WIDE || (D == 64 && SPLIT == 2);
   static_assert(64 * (D / 2) * 4 <= LDS_TILE * 2, "a merge buffer must fit in one stage");
@@ -469,17 +474,37 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   // with swizzle SW.  SW_PD (D = 128) permutes a chunk index's bits 2-3
   // only, so chunk 2cc + 2 + g sits 16 elements after chunk 2cc + g (cc
   // even): an immediate, not a register.
-  auto row_offsets = [&](auto swc, int (&off)[D / 16]) {
+  // Offsets are in bytes and carry the wave's first row in the tile
+  // (`base`, elements: a multiple of 32 rows); tile_step hides them from
+  // loop-invariant code motion (opaque()), so each read is one offset
+  // register plus an immediate (array, stage, sub-block).  Under SW_PD only
+  // the even chunks' offsets are kept (odd = even + 32 bytes).
+  auto row_offsets = [&](auto swc, int (&off)[D / 16], int base) {
     constexpr int SW = decltype(swc)::value;
     const int s = swz<D, SW>(l32);
 #pragma unroll
-    for (int cc = 0; cc < D / 16; ++cc) {
-      if (SW == SW_PD && (cc & 1)) off[cc] = off[cc - 1] + 16;
-      else off[cc] = lds_row<D, SW>(l32) + (((2 * cc + g) ^ s) << 3);
-    }
+    for (int cc = 0; cc < D / 16; ++cc)
+      off[cc] = 2 * (base + lds_row<D, SW>(l32) + (((2 * cc + g) ^ s) << 3));
   };
+  auto row_off = [&](auto swc, const int (&off)[D / 16], int cc) -> int {
+    constexpr int SW = decltype(swc)::value;
+    return (SW == SW_PD && (cc & 1)) ? off[cc - 1] + 32 : off[cc];
+  };
+  auto hide_offsets = [&](auto swc, int (&off)[D / 16]) {
+    constexpr int SW = decltype(swc)::value;
+#pragma unroll
+    for (int cc = 0; cc < D / 16; ++cc)
+      if (!(SW == SW_PD && (cc & 1))) opaque<16>(off[cc]);
+  };
+  // The eight-wave D = 128 layout keeps the wave's rows out of the offsets
+  // and unhidden (FOLD false: the wave part is added to the array address,
+  // as a scalar): folded and hidden there, the backward measured 1-1.5 %
+  // slower at every D = 128 shape, with the same instruction counts.
+  constexpr bool FOLD = !T::WIDE;
+  const int kw = FOLD ? 0 : lds_row<D, KVSW>(32 * kg);   // elements
   int kv_off[T::KV_LDS ? D / 16 : 1];
-  if constexpr (T::KV_LDS) row_offsets(std::integral_constant<int, KVSW>{}, kv_off);
+  if constexpr (T::KV_LDS)
+    row_offsets(std::integral_constant<int, KVSW>{}, kv_off, FOLD ? lds_row<D, KVSW>(32 * kg) : 0);
   vec8<E> kf[NKF], vf[NKF];
   const float ck = std::is_same<E, f16>::value ? fminf(a.c, 1.0f) : 1.0f;
   const float cr = a.c / ck;
@@ -500,11 +525,11 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   // B operands of S and dP: K^T / V^T fragments K[key][16cc + 8g .. +7]
   // (registers, or LDS rows 32kg + l32 read like the query tiles' A rows)
   auto k_frag = [&](int cc) -> vec8<E> {
-    if constexpr (T::KV_LDS) return ld8<E>(s_k + lds_row<D, KVSW>(32 * kg) + kv_off[cc]);
+    if constexpr (T::KV_LDS) return ld8_b<E>(s_k + kw, row_off(std::integral_constant<int, KVSW>{}, kv_off, cc));
     else return kf[cc];
   };
   auto v_frag = [&](int cc) -> vec8<E> {
-    if constexpr (T::KV_LDS) return ld8<E>(s_v + lds_row<D, KVSW>(32 * kg) + kv_off[cc]);
+    if constexpr (T::KV_LDS) return ld8_b<E>(s_v + kw, row_off(std::integral_constant<int, KVSW>{}, kv_off, cc));
     else return vf[cc];
   };
 
@@ -587,10 +612,22 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   // A-operand rows (Q, dO of this wave's 32-query sub-block): row l32, chunk
   // 2cc + g; transposed reads: rows 4g + (l16 >> 2), column chunk
   // 4d + 2((lane >> 4) & 1) + ((l16 >> 1) & 1), half 4 * (l16 & 1).
+  // All in bytes, carrying the wave's first query row in the tile
+  // (32 * NSUB * qh), as does the LSE / delta seed offset `s_row` (row
+  // 32 * NSUB * qh + 8g of s_lse / s_dl).
+  // (FOLD false: on the array addresses instead, qw and sw.)
+  const int qbase = lds_row<D, QSW>(32 * NSUB * qh);
+  const int qw = FOLD ? 0 : qbase, sw = FOLD ? 0 : 32 * NSUB * qh;
   int a_off[D / 16];
-  TrOffsets<D, QSW> t_off;
-  row_offsets(std::integral_constant<int, QSW>{}, a_off);
-  t_off.init(lane);
+  TrOffsetsB<D, QSW> t_off;
+  row_offsets(std::integral_constant<int, QSW>{}, a_off, FOLD ? qbase : 0);
+  t_off.init(lane, FOLD ? qbase : 0);
+  int s_row = 4 * (8 * g + (FOLD ? 32 * NSUB * qh : 0));
+  auto a_at = [&](int cc) { return row_off(std::integral_constant<int, QSW>{}, a_off, cc); };
+  // seed rows r .. r + 3 (r a compile-time multiple of 4) of a stage
+  auto seed4 = [&](const float *arr, int r) {
+    return *reinterpret_cast<const floatx4 *>(reinterpret_cast<const char *>(arr + sw) + s_row + 4 * r);
+  };
 
   if (n_tiles > 0) load_tile(cur_h, cur_m0, std::integral_constant<int, 0>{});
   __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): K, V and the first tile resident
@@ -620,6 +657,12 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   // is unrolled by two) so every LDS address is a base plus an immediate.
   auto tile_step = [&](auto stc, int t) {
     constexpr int st = decltype(stc)::value;
+    if constexpr (FOLD) {
+      hide_offsets(std::integral_constant<int, QSW>{}, a_off);
+      if constexpr (T::KV_LDS) hide_offsets(std::integral_constant<int, KVSW>{}, kv_off);
+      t_off.hide();
+      opaque<32>(s_row);
+    }
     const int m0 = cur_m0;
     const bool more = t + 1 < n_tiles;
     int nxt_h = cur_h, nxt_m0 = cur_m0;
@@ -646,14 +689,13 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
     // 32qs + 16hh + 8g + j; slot i <-> query ms + slot_row(i, g), lane <->
     // key).
     auto s_dp = [&](int sb, floatx16 &sacc, floatx16 &dpacc) {
-      const int qs = NSUB * qh + sb;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        const int r = 32 * qs + 16 * hh + 8 * g;
-        const floatx4 l_lo = *(const floatx4 *)&s_lse[st][r];
-        const floatx4 l_hi = *(const floatx4 *)&s_lse[st][r + 4];
-        const floatx4 d_lo = *(const floatx4 *)&s_dl[st][r];
-        const floatx4 d_hi = *(const floatx4 *)&s_dl[st][r + 4];
+        const int r = 32 * sb + 16 * hh;
+        const floatx4 l_lo = seed4(s_lse[st], r);
+        const floatx4 l_hi = seed4(s_lse[st], r + 4);
+        const floatx4 d_lo = seed4(s_dl[st], r);
+        const floatx4 d_hi = seed4(s_dl[st], r + 4);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           sacc[8 * hh + j] = l_lo[j];
@@ -662,17 +704,16 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
           dpacc[8 * hh + 4 + j] = d_hi[j];
         }
       }
-      const f16 *qr = q_st(stc) + lds_row<D, QSW>(32 * qs);
-      const f16 *gr = do_st(stc) + lds_row<D, QSW>(32 * qs);
+      const f16 *qr = q_st(stc) + qw + lds_row<D, QSW>(32 * sb);
+      const f16 *gr = do_st(stc) + qw + lds_row<D, QSW>(32 * sb);
 #pragma unroll
       for (int cc = 0; cc < D / 16; ++cc) {
-        sacc = mfma32(ld8<E>(qr + a_off[cc]), k_frag(cc), sacc);
-        dpacc = mfma32(ld8<E>(gr + a_off[cc]), v_frag(cc), dpacc);
+        sacc = mfma32(ld8_b<E>(qr, a_at(cc)), k_frag(cc), sacc);
+        dpacc = mfma32(ld8_b<E>(gr, a_at(cc)), v_frag(cc), dpacc);
       }
     };
     // Softmax-gradient of sub-block sb and its dV / dK MFMAs.
     auto grad = [&](int sb, floatx16 &sacc, const floatx16 &dpacc) {
-      const int qs = NSUB * qh + sb;
       const int ms = sub_m(sb);
       // Invisible scores become -inf (P = 0) in one pass, taken only by
       // diagonal and ragged sub-blocks, so the softmax below is branch-free.
@@ -717,11 +758,11 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         // kperm rows 32qs + 16hh + 4g + (0..3) and +8: this 8-query slice
-        const int rb = lds_row<D, QSW>(32 * qs + 16 * hh);
+        const int rb = qw + lds_row<D, QSW>(32 * sb + 16 * hh);
 #pragma unroll
         for (int d = 0; d < D / 32; ++d) {
-          dv[d] = mfma32(load_tr_pair<E>(do_st(stc) + rb, t_off.lo(d), t_off.hi(d)), pf[hh], dv[d]);
-          dk[d] = mfma32(load_tr_pair<E>(q_st(stc) + rb, t_off.lo(d), t_off.hi(d)), dsf[hh], dk[d]);
+          dv[d] = mfma32(load_tr_pair_b<E>(do_st(stc) + rb, t_off.lo(d), t_off.hi(d)), pf[hh], dv[d]);
+          dk[d] = mfma32(load_tr_pair_b<E>(q_st(stc) + rb, t_off.lo(d), t_off.hi(d)), dsf[hh], dk[d]);
         }
       }
     };
@@ -743,17 +784,16 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
       constexpr int NO = 2 * (D / 32);    // dV / dK MFMAs (2 query halves x D / 32)
       // operand reads this many MFMAs ahead (the non-causal D = 64 variant
       // would spill)
-      constexpr int PFD = (CAUSAL || T::WIDE) ? T::PF_OPS : 0;
+      constexpr int PFD = T::PF_OPS;
       constexpr int NM = 2 * NC + 2 * NO;
-      const int qs = NSUB * qh + sb;
       floatx16 sacc, dpacc;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        const int r = 32 * qs + 16 * hh + 8 * g;
-        const floatx4 l_lo = *(const floatx4 *)&s_lse[st][r];
-        const floatx4 l_hi = *(const floatx4 *)&s_lse[st][r + 4];
-        const floatx4 d_lo = *(const floatx4 *)&s_dl[st][r];
-        const floatx4 d_hi = *(const floatx4 *)&s_dl[st][r + 4];
+        const int r = 32 * sb + 16 * hh;
+        const floatx4 l_lo = seed4(s_lse[st], r);
+        const floatx4 l_hi = seed4(s_lse[st], r + 4);
+        const floatx4 d_lo = seed4(s_dl[st], r);
+        const floatx4 d_hi = seed4(s_dl[st], r + 4);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           sacc[8 * hh + j] = l_lo[j];
@@ -773,9 +813,9 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
         for (int i = 0; i < 16; ++i)
           sacc[i] = (slot_row(i, 0) >= lo && slot_row(i, 0) < hi) ? sacc[i] : kNegInf;
       }
-      const f16 *qr = q_st(stc) + lds_row<D, QSW>(32 * qs);
-      const f16 *gr = do_st(stc) + lds_row<D, QSW>(32 * qs);
-      const int rb0 = lds_row<D, QSW>(32 * qs);
+      const f16 *qr = q_st(stc) + qw + lds_row<D, QSW>(32 * sb);
+      const f16 *gr = do_st(stc) + qw + lds_row<D, QSW>(32 * sb);
+      const int rb0 = qw + lds_row<D, QSW>(32 * sb);
       // LDS operands of MFMA i of the block (S: Q and K^T; dP: dO and V^T;
       // dV: dO^T; dK: Q^T), in ring slot i % (PFD + 1)
       vec8<E> opa[PFD + 1], opb[PFD + 1];
@@ -783,18 +823,18 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
         constexpr int i = decltype(ic)::value;
         constexpr int sl = i % (PFD + 1);
         if constexpr (i < NC) {
-          opa[sl] = ld8<E>(qr + a_off[i]);
+          opa[sl] = ld8_b<E>(qr, a_at(i));
           opb[sl] = k_frag(i);
         } else if constexpr (i < 2 * NC) {
-          opa[sl] = ld8<E>(gr + a_off[i - NC]);
+          opa[sl] = ld8_b<E>(gr, a_at(i - NC));
           opb[sl] = v_frag(i - NC);
         } else if constexpr (i < 2 * NC + NO) {
           constexpr int o = i - 2 * NC, hh = o / (D / 32), d = o % (D / 32);
-          opa[sl] = load_tr_pair<E>(do_st(stc) + rb0 + lds_row<D, QSW>(16 * hh), t_off.lo(d),
+          opa[sl] = load_tr_pair_b<E>(do_st(stc) + rb0 + lds_row<D, QSW>(16 * hh), t_off.lo(d),
                                     t_off.hi(d));
         } else {
           constexpr int o = i - 2 * NC - NO, hh = o / (D / 32), d = o % (D / 32);
-          opa[sl] = load_tr_pair<E>(q_st(stc) + rb0 + lds_row<D, QSW>(16 * hh), t_off.lo(d),
+          opa[sl] = load_tr_pair_b<E>(q_st(stc) + rb0 + lds_row<D, QSW>(16 * hh), t_off.lo(d),
                                     t_off.hi(d));
         }
       };
@@ -1120,16 +1160,20 @@ void fa_bwd_dq_kernel(BwdArgs a) {
     s_seed[i] = PRE ? shift : 0.0f;
   }
 
-  // Per-lane LDS element offsets inside a stage (as in the dK/dV kernel):
+  // Per-lane LDS byte offsets inside a stage (as in the dK/dV kernel):
   // A-operand rows l32, chunk 2cc + g; transposed reads of K rows
-  // 4g + (l16 >> 2).
+  // 4g + (l16 >> 2); both carrying the wave's first key row in the tile
+  // (32 * NSUB * kh) and hidden from loop-invariant code motion at every
+  // step (fa_common.hpp opaque()).
+  const int wrow = 32 * NSUB * kh * D;
   int a_off[D / 16];
-  TrOffsets<D, SW_AT> t_off;
+  TrOffsetsB<D, SW_AT> t_off;
   {
     const int sa = swz<D, SW_AT>(l32);
 #pragma unroll
-    for (int cc = 0; cc < D / 16; ++cc) a_off[cc] = l32 * D + (((2 * cc + g) ^ sa) << 3);
-    t_off.init(lane);
+    for (int cc = 0; cc < D / 16; ++cc)
+      a_off[cc] = 2 * (wrow + l32 * D + (((2 * cc + g) ^ sa) << 3));
+    t_off.init(lane, wrow);
   }
 
   __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): rows, LSE, delta and the first tile resident
@@ -1137,6 +1181,9 @@ void fa_bwd_dq_kernel(BwdArgs a) {
 
   auto tile_step = [&](auto stc, int t) {
     constexpr int st = decltype(stc)::value;
+#pragma unroll
+    for (int cc = 0; cc < D / 16; ++cc) opaque<16>(a_off[cc]);
+    t_off.hide();
     const int n0 = t * BN;
     const bool more = t + 1 < t_hi;
     if (more) load_next(std::integral_constant<int, st ^ 1>{});   // tile t + 1
@@ -1149,19 +1196,17 @@ void fa_bwd_dq_kernel(BwdArgs a) {
     };
     // S^T = K Q^T (PRE: c s - LSE') and dP^T = V dO^T for sub-block sb
     auto s_dp = [&](int sb, floatx16 &sacc, floatx16 &dpacc) {
-      const int ks = NSUB * kh + sb;
-      const f16 *kr = k_st(stc) + 32 * ks * D;
-      const f16 *vr = v_st(stc) + 32 * ks * D;
-      sacc = mfma32(ld8<E>(kr + a_off[0]), qf[0], s_seed);
-      dpacc = mfma32(ld8<E>(vr + a_off[0]), gf[0], dl_seed);
+      const f16 *kr = k_st(stc) + 32 * sb * D;
+      const f16 *vr = v_st(stc) + 32 * sb * D;
+      sacc = mfma32(ld8_b<E>(kr, a_off[0]), qf[0], s_seed);
+      dpacc = mfma32(ld8_b<E>(vr, a_off[0]), gf[0], dl_seed);
 #pragma unroll
       for (int cc = 1; cc < D / 16; ++cc) {
-        sacc = mfma32(ld8<E>(kr + a_off[cc]), qf[cc], sacc);
-        dpacc = mfma32(ld8<E>(vr + a_off[cc]), gf[cc], dpacc);
+        sacc = mfma32(ld8_b<E>(kr, a_off[cc]), qf[cc], sacc);
+        dpacc = mfma32(ld8_b<E>(vr, a_off[cc]), gf[cc], dpacc);
       }
     };
     auto grad = [&](int sb, floatx16 &sacc, const floatx16 &dpacc) {
-      const int ks = NSUB * kh + sb;
       const int ns = sub_n(sb);
       // invisible scores -> -inf (P = 0), diagonal / ragged sub-blocks only
       if ((CAUSAL && ns + 31 > wq0 + off) || (ns + 31 >= Sk)) {
@@ -1184,11 +1229,12 @@ void fa_bwd_dq_kernel(BwdArgs a) {
       for (int i = 0; i < 16; ++i) dsf[i >> 3][i & 7] = (E)ds[i];
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        // kperm rows 32ks + 16hh + 4g + (0..3) and +8: this 8-key slice
-        const int rb = (32 * ks + 16 * hh) * D;
+        // kperm rows 32(NSUB kh + sb) + 16hh + 4g + (0..3) and +8: this
+        // 8-key slice
+        const int rb = (32 * sb + 16 * hh) * D;
 #pragma unroll
         for (int d = 0; d < D / 32; ++d)
-          dq[d] = mfma32(load_tr_pair<E>(k_st(stc) + rb, t_off.lo(d), t_off.hi(d)), dsf[hh], dq[d]);
+          dq[d] = mfma32(load_tr_pair_b<E>(k_st(stc) + rb, t_off.lo(d), t_off.hi(d)), dsf[hh], dq[d]);
       }
     };
 

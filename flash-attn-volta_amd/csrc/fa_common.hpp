@@ -214,6 +214,24 @@ __device__ __forceinline__ int wave_id() {
   return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 }
 
+// Per-lane LDS offsets inside a tile loop.  An LDS read's address is
+// VGPR + 16-bit immediate, and the addresses of one lane's reads differ by
+// compile-time constants (LDS array, stage, sub-block, 8-row step) once the
+// lane's offset carries the wave-uniform part (its query or key group).  But
+// LLVM hoists every (array + offset) sum out of the loop as a loop invariant,
+// each into a VGPR of its own: one register per array, stage and chunk
+// (measured: 34 address VGPRs in the D = 64 dK/dV loop, against 11 offsets).
+// Passing the offsets through an empty asm at the top of every iteration
+// makes those sums loop-variant, so each read takes the offset register plus
+// an immediate.  No instruction is emitted.
+// The offsets are kept in bytes (an element offset would need a shift per
+// use) and ALIGN states what the reads may assume of them.
+template <int ALIGN>
+__device__ __forceinline__ void opaque(int &x) {
+  asm volatile("" : "+v"(x));
+  __builtin_assume((x & (ALIGN - 1)) == 0);
+}
+
 // ---------------------------------------------------------------------------
 // Swizzled tiles staged straight from global memory into LDS.
 //
@@ -341,6 +359,19 @@ __device__ __forceinline__ vec8<E> load_tr_pair(const f16 *base, int lo, int hi)
   return __builtin_bit_cast(vec8<E>, r);
 }
 
+// load_tr_pair at byte offsets lo, hi from base.
+template <typename E>
+__device__ __forceinline__ vec8<E> load_tr_pair_b(const f16 *base, int lo, int hi) {
+  typedef __fp16 h4 __attribute__((vector_size(8)));
+  typedef __attribute__((address_space(3))) h4 lds_h4;
+  const char *b = reinterpret_cast<const char *>(base);
+  h4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_h4 *)(b + lo));
+  h4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_h4 *)(b + hi));
+  const u32x2 x = __builtin_bit_cast(u32x2, a0), y = __builtin_bit_cast(u32x2, a1);
+  const u32x4 r = {x[0], x[1], y[0], y[1]};
+  return __builtin_bit_cast(vec8<E>, r);
+}
+
 // Per-lane element offsets of the transposed reads of a swizzled tile: for
 // column block d (32 columns), rows 4g + (l16 >> 2) (`lo`) and 8 rows
 // further (`hi`), column chunk 4d + 2((lane >> 4) & 1) + ((l16 >> 1) & 1),
@@ -371,10 +402,47 @@ struct TrOffsets {
   }
 };
 
+// TrOffsets in bytes, hidden from loop-invariant code motion by hide() (see
+// opaque()): for loops whose LDS arrays and stages are compile-time
+// constants, so every transposed read is one register plus an immediate.
+template <int D, int SW>
+struct TrOffsetsB {
+  static constexpr bool SPLIT = TrOffsets<D, SW>::SPLIT;
+  int lo_[D / 32];
+  int hi_[SPLIT ? D / 32 : 1];
+  __device__ __forceinline__ void init(int lane, int base) {
+    TrOffsets<D, SW> t;
+    t.init(lane);
+#pragma unroll
+    for (int d = 0; d < D / 32; ++d) {
+      lo_[d] = 2 * (t.lo(d) + base);
+      if constexpr (SPLIT) hi_[d] = 2 * (t.hi(d) + base);
+    }
+  }
+  __device__ __forceinline__ int lo(int d) const { return lo_[d]; }
+  __device__ __forceinline__ int hi(int d) const {
+    if constexpr (SPLIT) return hi_[d];
+    else return lo_[d] + 2 * lds_row<D, SW>(8);
+  }
+  __device__ __forceinline__ void hide() {
+#pragma unroll
+    for (int d = 0; d < D / 32; ++d) {
+      opaque<8>(lo_[d]);
+      if constexpr (SPLIT) opaque<8>(hi_[d]);
+    }
+  }
+};
+
 // 8 consecutive 16-bit values at p (16-byte aligned), as an E vector.
 template <typename E>
 __device__ __forceinline__ vec8<E> ld8(const f16 *p) {
   return *reinterpret_cast<const vec8<E> *>(p);
+}
+
+// The same at a byte offset from p.
+template <typename E>
+__device__ __forceinline__ vec8<E> ld8_b(const f16 *p, int byte_off) {
+  return *reinterpret_cast<const vec8<E> *>(reinterpret_cast<const char *>(p) + byte_off);
 }
 
 // Kernel arguments shared by the forward and backward launches. Strides are

@@ -145,25 +145,33 @@ __host__ __device__ constexpr int bal_items(int nb) { return 3 * (nb >> 1) + (nb
 
 template <int D, int KSPLIT, int NW = 4>
 struct FwdTile {
-  static_assert(KSPLIT == 1 || KSPLIT == 2, "key split is 1 or 2");
+  static_assert(KSPLIT == 1 || KSPLIT == 2 || KSPLIT == 4, "key split is 1, 2 or 4");
   static_assert(NW == 4 || (NW == 8 && D >= 64), "eight waves need D >= 64");
+  static_assert(NW % KSPLIT == 0, "every query group takes all key parts");
   static constexpr int NQG = NW / KSPLIT;  // query groups of 32 per workgroup
-  static constexpr int NSUB = 2 / KSPLIT;  // 32-key sub-blocks per wave per tile
+  static constexpr int NSUB = KSPLIT == 1 ? 2 : 1;   // 32-key sub-blocks per wave per tile
   static constexpr int BM = 32 * NQG;      // queries per workgroup
-  static constexpr int BN = 64;            // keys per tile
+  static constexpr int BN = 32 * NSUB * KSPLIT;   // keys per tile: 64, or 128 with four parts
   static constexpr int NT = 64 * NW;       // NW waves
   static constexpr int LDS_TILE = BN * D;  // swizzled, unpadded (fa_common.hpp)
-  // O^T partial sums of a key-half wave handed over for the final merge
-  static_assert(64 * (D / 2) * 4 <= LDS_TILE * 2, "a merge buffer must fit in one K slot");
+  // O^T partial sums of a key-part wave handed over for the final merge:
+  // one buffer per (query group, key part > 0), in the four K / V slots
+  // (one per slot with two parts, two per slot with four)
+  static constexpr int MERGE_FLOATS = 64 * (D / 2);
+  static constexpr int MERGE_PER_SLOT = KSPLIT == 4 ? 2 : 1;
+  static_assert(MERGE_FLOATS * 4 * MERGE_PER_SLOT <= LDS_TILE * 2, "merge buffers must fit a slot");
+  static_assert(NQG * (KSPLIT - 1) <= 4 * MERGE_PER_SLOT, "the merge buffers must fit the slots");
 };
 
-// Workgroup = 4 waves.  KSPLIT = 1: each wave owns 32 queries (BM = 128)
+// Workgroup = NW waves (4 or 8).  KSPLIT = 1: each wave owns 32 queries
 // and both 32-key halves of every 64-key tile.  KSPLIT = 2: wave w owns
-// query group qg = w / 2 (BM = 64) and key half kh = w % 2 of every tile;
-// each wave runs its own online softmax over its key half and the two halves
-// of a query group merge through LDS at the end (lane l of both waves holds
-// the same query and the same O^T rows, so the merge is element-wise).
-// Splitting keys halves each wave's work per tile and doubles the waves in
+// query group qg = w / 2 and key half kh = w % 2 of every tile; each wave
+// runs its own online softmax over its key half and the two halves of a
+// query group merge through LDS at the end (lane l of both waves holds the
+// same query and the same O^T rows, so the merge is element-wise).
+// KSPLIT = 4: 128-key tiles, wave w owns query group w / 4 and the 32-key
+// quarter w % 4 of every tile; the quarters merge the same way.  Splitting
+// keys divides each wave's work per tile and multiplies the waves in
 // flight: it pays when the grid is too small to fill the GPU, and for
 // causal attention, whose last query tile walks every key tile.  The
 // launcher picks KSPLIT from the grid size.
@@ -179,6 +187,7 @@ template <typename E, int D, bool CAUSAL, int KSPLIT, bool SPLITKV = false, bool
 __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
   static_assert(!PRE || std::is_same<E, f16>::value, "the pre-scaled mode is fp16 only");
   static_assert(!BAL || (CAUSAL && !SPLITKV), "the balanced schedule is for causal grids");
+  static_assert(KSPLIT <= 2 || (!BAL && !SPLITKV), "four key parts: the plain schedule only");
   using T = FwdTile<D, KSPLIT, NW>;
   constexpr int NSUB = T::NSUB;
   constexpr int BM = T::BM, BN = T::BN;
@@ -187,7 +196,7 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
   __shared__ __attribute__((aligned(16))) f16 sk0[T::LDS_TILE], sk1[T::LDS_TILE];
   __shared__ __attribute__((aligned(16))) f16 sv0[T::LDS_TILE], sv1[T::LDS_TILE];
   // merge: m, l per query group (key-split layouts)
-  __shared__ __attribute__((aligned(16))) float s_ml[KSPLIT == 2 ? T::NQG : 1][2][64];
+  __shared__ __attribute__((aligned(16))) float s_ml[KSPLIT >= 2 ? T::NQG * (KSPLIT - 1) : 1][2][64];
   auto k_sl = [&](auto sc) -> f16 * { return decltype(sc)::value ? sk1 : sk0; };
   auto v_sl = [&](auto sc) -> f16 * { return decltype(sc)::value ? sv1 : sv0; };
 
@@ -225,8 +234,8 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
   const int hk = SPLITKV ? bh % hx : h / grp;        // key/value head
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = wave_id();
-  const int qg = KSPLIT == 2 ? (w >> 1) : w;
-  const int kh = KSPLIT == 2 ? (w & 1) : 0;
+  const int qg = w / KSPLIT;
+  const int kh = w % KSPLIT;
   const int g = lane >> 5, l32 = lane & 31;
   const int q0 = qt * BM;
   const int wq0 = q0 + 32 * qg;   // first row of this wave
@@ -255,8 +264,8 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
 
   // ---- K and V tiles go straight to LDS (fa_common.hpp DmaStager): both
   // in kperm row order, chunks swizzled; rows past Sk read as zeros.
-  DmaStager<D, SW_A, 64, NW> stk;   // K: read only as A operands
-  DmaStager<D, SW_T, 64, NW> stv;   // V: read only transposed
+  DmaStager<D, SW_A, BN, NW> stk;   // K: read only as A operands
+  DmaStager<D, SW_T, BN, NW> stv;   // V: read only transposed
   stk.init(w, lane, a.k.ss);
   stv.init(w, lane, a.v.ss);
   auto load_k = [&](int n0, auto sc) { stk.load(k_sl(sc), kb, a.k.ss, n0, Sk, w); };
@@ -276,17 +285,27 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
     cv.advance();
   };
 
-  // Per-lane LDS element offsets inside a slot: K rows l32 (A operand of
+  // Per-lane LDS byte offsets inside a slot: K rows l32 (A operand of
   // S^T = K Q^T), chunk 2cc + g; V^T transpose reads of rows 4g + (l16 >> 2)
-  // (and + 8), i.e. natural V rows 8g + (l16 >> 2) (and + 4).
+  // (and + 8), i.e. natural V rows 8g + (l16 >> 2) (and + 4).  Both carry
+  // the wave's first key row in the tile (32 * NSUB * kh) and are hidden
+  // from loop-invariant code motion at every step (fa_common.hpp opaque()),
+  // so a read is one offset register plus an immediate (slot, sub-block).
+  const int wrow = 32 * NSUB * kh * D;
   int a_off[D / 16];
-  TrOffsets<D, SW_T> t_off;
+  TrOffsetsB<D, SW_T> t_off;
   {
     const int sa = swz<D, SW_A>(l32);
 #pragma unroll
-    for (int cc = 0; cc < D / 16; ++cc) a_off[cc] = l32 * D + (((2 * cc + g) ^ sa) << 3);
-    t_off.init(lane);
+    for (int cc = 0; cc < D / 16; ++cc)
+      a_off[cc] = 2 * (wrow + l32 * D + (((2 * cc + g) ^ sa) << 3));
+    t_off.init(lane, wrow);
   }
+  auto hide_offsets = [&]() {
+#pragma unroll
+    for (int cc = 0; cc < D / 16; ++cc) opaque<16>(a_off[cc]);
+    t_off.hide();
+  };
 
   // Sub-block sb (32 keys) of this wave in the tile at n0 starts at key
   // n0 + 32 * (NSUB * kh + sb); it is dead when it lies entirely above the
@@ -328,10 +347,10 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
 #pragma unroll
     for (int sb = 0; sb < NSUB; ++sb) {
       if (decltype(checkc)::value && dead(n0, sb)) continue;
-      const f16 *kr = k_sl(sc) + 32 * (NSUB * kh + sb) * D;
-      floatx16 acc = mfma32(ld8<E>(kr + a_off[0]), qf[0], negm);
+      const f16 *kr = k_sl(sc) + 32 * sb * D;
+      floatx16 acc = mfma32(ld8_b<E>(kr, a_off[0]), qf[0], negm);
 #pragma unroll
-      for (int cc = 1; cc < D / 16; ++cc) acc = mfma32(ld8<E>(kr + a_off[cc]), qf[cc], acc);
+      for (int cc = 1; cc < D / 16; ++cc) acc = mfma32(ld8_b<E>(kr, a_off[cc]), qf[cc], acc);
       s[sb] = acc;
     }
   };
@@ -347,10 +366,10 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         // kperm rows 32 * (sub-block) + 16hh + 4g (+8): keys 16hh + 8g + 0..7
-        const int rb = (32 * (NSUB * kh + sb) + 16 * hh) * D;
+        const int rb = (32 * sb + 16 * hh) * D;
 #pragma unroll
         for (int d = 0; d < D / 32; ++d)
-          oacc[d] = mfma32(load_tr_pair<E>(v_sl(sc) + rb, t_off.lo(d), t_off.hi(d)), pf[sb][hh],
+          oacc[d] = mfma32(load_tr_pair_b<E>(v_sl(sc) + rb, t_off.lo(d), t_off.hi(d)), pf[sb][hh],
                            oacc[d]);
       }
     }
@@ -500,6 +519,7 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
     constexpr int pc = decltype(pcc)::value;
     using CP = std::integral_constant<int, pc>;
     using CQ = std::integral_constant<int, pc ^ 1>;
+    hide_offsets();
     const int n0 = t * BN;
     if (t + 2 < n_tiles) load_k_next(CP{});   // K(t + 2)
     if (!v0_early || t > 0) load_v_next(CP{});   // V(t) (V(0) at D = 128: the prologue)
@@ -536,6 +556,7 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
     constexpr int pc = decltype(pcc)::value;
     using CP = std::integral_constant<int, pc>;
     using CQ = std::integral_constant<int, pc ^ 1>;
+    hide_offsets();
     // The block in issue order: MQ S^T MFMAs (K slot pc ^ 1) and MP P V
     // MFMAs (V slot pc ^ 1), alternating while both remain, each followed
     // by its share of tile t's softmax (NPAIR pairs of scores: two FMAs, two
@@ -562,10 +583,10 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
       kind_index(i, is_q, j);
       if (is_q) {
         const int sb = j / (D / 16), cc = j % (D / 16);
-        return ld8<E>(ks + 32 * (NSUB * kh + sb) * D + a_off[cc]);
+        return ld8_b<E>(ks + 32 * sb * D, a_off[cc]);
       }
       const int sb = j / (2 * (D / 32)), hh = (j / (D / 32)) % 2, d = j % (D / 32);
-      return load_tr_pair<E>(vs + (32 * (NSUB * kh + sb) + 16 * hh) * D, t_off.lo(d), t_off.hi(d));
+      return load_tr_pair_b<E>(vs + (32 * sb + 16 * hh) * D, t_off.lo(d), t_off.hi(d));
     };
     const float c_ = c, neg_m = -m_run;
     float l0 = 0.0f, l1 = 0.0f;
@@ -678,6 +699,52 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FwdArgs a) {
   // slot per group: K slots (the loop's last barrier ordered every read of
   // them before these writes), and with four groups the V slots too, which
   // the last tile's P V above still reads until the barrier here
+  if constexpr (KSPLIT == 4) {
+    // key parts 1..3 of query group qg hand over (m, l, O^T) in buffer
+    // qg * 3 + kh - 1 (two per LDS slot, the V slots too: the barrier
+    // first ends the last tile's P V reads); part 0 merges them in order
+    __syncthreads();
+    auto mbuf_of = [&](int i) -> float * {
+      const int sl = i >> 1;
+      f16 *slot = sl == 0 ? sk0 : (sl == 1 ? sk1 : (sl == 2 ? sv0 : sv1));
+      return reinterpret_cast<float *>(slot) + (i & 1) * T::MERGE_FLOATS;
+    };
+    if (kh > 0) {
+      const int i = qg * 3 + kh - 1;
+      float *mbuf = mbuf_of(i);
+      s_ml[i][0][lane] = m_run;
+      s_ml[i][1][lane] = l_run;
+#pragma unroll
+      for (int d = 0; d < D / 32; ++d)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) mbuf[(16 * d + j) * 64 + lane] = oacc[d][j];
+    }
+    __syncthreads();
+    if (kh > 0) return;
+    float mp[3], m = m_run;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      mp[k] = s_ml[qg * 3 + k][0][lane];
+      m = fmaxf(m, mp[k]);
+    }
+    const float f0 = (m == kNegInf) ? 0.0f : fast_exp2(m_run - m);
+    l_run *= f0;
+#pragma unroll
+    for (int d = 0; d < D / 32; ++d)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) oacc[d][j] *= f0;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      const float fk = (m == kNegInf) ? 0.0f : fast_exp2(mp[k] - m);
+      const float *mbuf = mbuf_of(qg * 3 + k);
+      l_run += s_ml[qg * 3 + k][1][lane] * fk;
+#pragma unroll
+      for (int d = 0; d < D / 32; ++d)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) oacc[d][j] += mbuf[(16 * d + j) * 64 + lane] * fk;
+    }
+    m_run = m;
+  }
   if (KSPLIT == 2) {
     if constexpr (T::NQG > 2) __syncthreads();
     f16 *slot = qg == 0 ? sk0 : (qg == 1 ? sk1 : (qg == 2 ? sv0 : sv1));

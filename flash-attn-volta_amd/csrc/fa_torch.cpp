@@ -174,6 +174,18 @@ std::optional<Tensor> attn(int64_t handle, const Tensor &q, const Tensor &k, con
 }  // namespace
 
 PYBIND11_MODULE(_fa_torch, m) {
+  // This module calls the library's entry points with the argument lists of
+  // the header it was compiled against; a library built from another ABI
+  // version (the two .so files are built separately) would take them
+  // without an error.  Refuse to load then: the Python autograd path, which
+  // checks the version itself, takes over.
+  if (fa_abi_version() != FA_ABI_VERSION) {
+    PyErr_Format(PyExc_ImportError,
+                 "_fa_torch was built for libfa_mi355x ABI %d, the loaded library has ABI %d: "
+                 "rebuild both (flash_attn_volta.build)",
+                 (int)FA_ABI_VERSION, (int)fa_abi_version());
+    throw pybind11::error_already_set();
+  }
   m.doc() = "C++ autograd node of flash_attn_volta's flash_attn / flash_attn_gqa";
   m.def("make_plan", &make_plan, "register a launch plan (ints, sm_scale) -> handle");
   m.def("attn", &attn, "forward of a plan, recording the C++ backward node");

@@ -11,6 +11,7 @@ that.
 """
 from __future__ import annotations
 
+import collections
 import ctypes
 
 import torch
@@ -95,8 +96,13 @@ def convert(name: str, first: int, values) -> tuple:
 # (stream order keeps one call's use of it before the next one's), grown
 # when a call needs more.  A call made while its stream is being captured
 # into a graph gets a fresh tensor instead: the graph keeps the addresses it
-# recorded, which a later growth here would free.
-_WS: dict = {}
+# recorded, which a later growth here would free.  At most
+# MAX_CACHED_STREAMS streams keep one (least recently used dropped first),
+# so threads drawing streams from a pool cannot pin a workspace each (up to
+# ~64 MiB for the split schedule of a small causal grid); the memory of a
+# dropped one goes back to torch's caching allocator.
+MAX_CACHED_STREAMS = 4
+_WS: "collections.OrderedDict" = collections.OrderedDict()
 
 
 def workspace(nbytes: int, device: torch.device, stream: int) -> torch.Tensor:
@@ -107,6 +113,10 @@ def workspace(nbytes: int, device: torch.device, stream: int) -> torch.Tensor:
     if ws is None or ws.numel() < nbytes:
         _WS.pop(key, None)
         ws = _WS[key] = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        while len(_WS) > MAX_CACHED_STREAMS:
+            _WS.popitem(last=False)
+    else:
+        _WS.move_to_end(key)
     return ws
 
 

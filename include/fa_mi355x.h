@@ -14,6 +14,11 @@
  *   lse, delta                 : (B, H, S) fp32, contiguous.
  * Strides are in elements and given per tensor as {b, s, h, d}.
  * All launches are asynchronous on `stream`; no call synchronises the host.
+ * Kernels run on the device `stream` belongs to (the current device for
+ * the NULL stream), whichever device is current in the calling thread, and
+ * every pointer must be memory of that device; launch decisions (the
+ * device's CU count) and fa_bwd_gqa_noalloc's scratch buffer follow that
+ * device too.
  *
  * Status codes: 0 on success, a negative FA_ERR_* otherwise. Argument
  * validation runs before any HIP call, so it behaves the same on a machine
@@ -265,7 +270,11 @@ int fa_bwd_gqa(const void *dout, const void *q, const void *k, const void *v,
  *
  * Every call on a GPU shares that GPU's buffer, so calls that overlap on
  * one GPU (concurrent streams, or host threads without ordering) race and
- * must be serialised by the caller.
+ * must be serialised by the caller.  The buffer used is that of the
+ * stream's device; its address is looked up on the first call per device
+ * (hipGetSymbolAddress, which allocates nothing), so a caller that
+ * captures this call into a HIP graph makes one eager call on the device
+ * first.
  *
  * No counterpart in the reference (its backward allocates through torch,
  * flash_attn_volta/triton_fa_bwd.py:650-654).

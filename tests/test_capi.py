@@ -445,3 +445,55 @@ def test_torch_node_module_loads():
         import torch
         t = torch.zeros(8)
         _fa_torch.attn(12345, t, t, t, True)
+
+
+_STUB_LIB = r"""
+#include <stddef.h>
+int fa_abi_version(void) { return %d; }
+const char *fa_strerror(int s) { (void)s; return "stub"; }
+int fa_fwd(void) { return -9; }
+int fa_fwd_gqa(void) { return -9; }
+int fa_fwd_ws(void) { return -9; }
+int fa_bwd(void) { return -9; }
+int fa_bwd_gqa(void) { return -9; }
+"""
+
+
+def test_torch_node_refuses_a_library_of_another_abi(tmp_path):
+    """_fa_torch calls the library with the argument lists of the header it
+    was compiled against, so it must not load beside a libfa_mi355x.so of
+    another ABI version (the two are built separately).  A copy of the built
+    module next to a stub library that reports another version (rpath
+    $ORIGIN picks the stub) raises ImportError on import (pybind11 chains
+    the module's own message as its cause) -- the error that autograd.py
+    turns into the Python autograd path -- while the real pair imports."""
+    import shutil
+    import subprocess
+    import sys
+
+    pkg = os.path.dirname(os.path.abspath(_capi.__file__))
+    ext = os.path.join(pkg, "_fa_torch.so")
+    if not os.path.exists(ext):
+        pytest.skip("_fa_torch.so is not built")
+    src = tmp_path / "stub.c"
+    src.write_text(_STUB_LIB % (_capi.ABI_VERSION + 1000))
+    subprocess.run(["gcc", "-shared", "-fPIC", str(src), "-o", str(tmp_path / "libfa_mi355x.so")],
+                   check=True)
+    shutil.copy(ext, tmp_path / "_fa_torch.so")
+    probe = (
+        "import importlib.util, sys, torch\n"
+        "spec = importlib.util.spec_from_file_location('_fa_torch', sys.argv[1])\n"
+        "m = importlib.util.module_from_spec(spec)\n"
+        "try:\n"
+        "    spec.loader.exec_module(m)\n"
+        "except ImportError as e:\n"
+        "    print('IMPORT_ERROR', e, e.__cause__)\n"
+        "else:\n"
+        "    print('LOADED', m.PLAN_INTS)\n")
+    bad = subprocess.run([sys.executable, "-c", probe, str(tmp_path / "_fa_torch.so")],
+                         capture_output=True, text=True, timeout=300)
+    assert "IMPORT_ERROR" in bad.stdout, bad.stdout + bad.stderr
+    assert f"ABI {_capi.ABI_VERSION}" in bad.stdout and "rebuild" in bad.stdout
+    good = subprocess.run([sys.executable, "-c", probe, ext], capture_output=True, text=True,
+                          timeout=300)
+    assert "LOADED 36" in good.stdout, good.stdout + good.stderr

@@ -76,6 +76,26 @@ def test_forward_ragged(S, D, causal):
     assert max_abs(lse, lse_ref) < TOL
 
 
+# Non-causal grids of at most one 64-query workgroup per CU take the
+# eight-wave layout whose query groups split each 128-key tile in four
+# (fa_api.hip launch_fwd); the first shape sits at that bound (256
+# workgroups), the second just past it (the two-part layout), the others
+# are ragged in both lengths and use both head dims, a tile count that is
+# not a multiple of the unroll and fewer keys than one tile.
+@pytest.mark.parametrize("shape", [(2, 1024, 8, 64), (1, 1024, 17, 64), (3, 777, 5, 64),
+                                   (1, 1000, 4, 128), (2, 100, 2, 64), (1, 1, 3, 128)])
+def test_forward_four_part_layout(shape):
+    B, S, H, D = shape
+    print(f"[case] fwd four-part {shape}", flush=True)
+    (q, k, v, _), o_ref, lse_ref = _oracle_fwd(B, S, H, D, False, None, 1.0, 7)
+    out, lse = _run(q, k, v, False, None)
+    e_o, e_l = max_abs(out, o_ref), max_abs(lse, lse_ref)
+    report(f"fwd four-part {shape}", out=e_o, lse=e_l)
+    assert e_o < TOL and e_l < TOL
+    out2, lse2 = _run(q, k, v, False, None)
+    assert torch.equal(out, out2) and torch.equal(lse, lse2)
+
+
 @pytest.mark.parametrize("sm_scale", [-0.125, 0.0, 0.01, 0.5])
 def test_forward_signed_and_zero_scale(sm_scale):
     B, S, H, D = 1, 300, 2, 64
