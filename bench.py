@@ -245,6 +245,22 @@ def useful_fraction(s, causal):
     return (s + 1) / (2.0 * s) if causal else 1.0
 
 
+# GEMMs of 2*B*H*S^2*D each that attention needs at the least: the forward's
+# two (S = QK^T, O = PV) and a backward's five (S and dP recomputed once,
+# dV, dK, dQ; the reference's PLAN_BACKWARD.md:8-15).  This build's backward
+# issues seven: the dQ kernel and the dK/dV kernel each recompute S and dP,
+# the price of writing every gradient once, without atomics.  Per backward
+# kernel the shared S and dP are charged to dK/dV (S, dP, dV, dK), the dQ
+# kernel keeps only its own dQ GEMM.
+MINIMAL_GEMMS = {"fwd": 2, "bwd": 5, "step": 7, "bwd_dkdv": 4, "bwd_dq": 1}
+
+
+def minimal_flops(b, s, h, d, causal, part):
+    """FLOPs of the minimal algorithm for `part` (MINIMAL_GEMMS), causal half
+    (with the diagonal) when causal: the basis of every `*minimal*` figure."""
+    return MINIMAL_GEMMS[part] * 2.0 * b * h * s * s * d * useful_fraction(s, causal)
+
+
 def profiled_counters(kernel_sym):
     """Counter-derived figures for the kernel whose symbol starts with
     `kernel_sym`, from the committed rocprofv3 PMC summaries
@@ -543,10 +559,18 @@ def run_configs(steps, warmup, with_cpu, prewarm_s=0.0):
         row = {"config": name, "shape": [b, s, h, d], "causal": causal,
                "gpu_fwd_us": round(t_f * 1e6, 2), "gpu_fwd_tflops": round(flops / t_f / 1e12, 2),
                "gpu_fwd_pct_peak": round(100 * flops / t_f / 1e12 / PEAK_FP16_TFLOPS, 2)}
+        useful = useful_fraction(s, causal)
+        row["gpu_fwd_issued_pct"] = round(100 * useful * flops / t_f / 1e12 / PEAK_FP16_TFLOPS, 2)
         if with_bwd:
             row.update({"gpu_fwd_bwd_us": round(t_fb * 1e6, 2),
                         "gpu_fwd_bwd_tflops": round(5 * flops / t_fb / 1e12, 2),
                         "gpu_fwd_bwd_pct_peak": round(100 * 5 * flops / t_fb / 1e12 / PEAK_FP16_TFLOPS, 2),
+                        # 9 GEMMs issued (2 fwd + 7 bwd), 7 minimal, causal half
+                        "gpu_fwd_bwd_issued_pct": round(
+                            100 * 4.5 * useful * flops / t_fb / 1e12 / PEAK_FP16_TFLOPS, 2),
+                        "gpu_fwd_bwd_minimal_pct": round(
+                            100 * minimal_flops(b, s, h, d, causal, "step") / t_fb / 1e12
+                            / PEAK_FP16_TFLOPS, 2),
                         "gpu_fwd_bwd_graph_us": round(t_fbg * 1e6, 2),
                         "gpu_fwd_bwd_graph_tflops": round(5 * flops / t_fbg / 1e12, 2),
                         "peak_extra_mb": round(mem[True] / 1e6, 2),
@@ -567,18 +591,20 @@ def run_configs(steps, warmup, with_cpu, prewarm_s=0.0):
                 row["cpu_fwd_bwd_tflops"] = round(5 * flops / t_cfb / 1e12, 4)
         rows.append(row)
         print(json.dumps(row), flush=True)
-    hdr = ("| config | shape | GPU fwd us | GPU fwd TFLOP/s (% peak) | GPU fwd+bwd us | "
-           "GPU fwd+bwd TFLOP/s (% peak) | fwd+bwd graph replay us (TFLOP/s) | peak extra MB "
-           "(no split) | CPU fwd TFLOP/s | CPU fwd+bwd TFLOP/s |")
+    hdr = ("| config | shape | GPU fwd us | GPU fwd TFLOP/s (% peak; % issued) | GPU fwd+bwd us | "
+           "GPU fwd+bwd TFLOP/s (% peak; % issued; % minimal) | fwd+bwd graph replay us (TFLOP/s) | "
+           "peak extra MB (no split) | CPU fwd TFLOP/s | CPU fwd+bwd TFLOP/s |")
     print(hdr)
     print("|---|---|---:|---:|---:|---:|---:|---:|---:|---:|")
     for r in rows:
-        fb = (f"{r['gpu_fwd_bwd_us']} | {r['gpu_fwd_bwd_tflops']} ({r['gpu_fwd_bwd_pct_peak']} %) | "
+        fb = (f"{r['gpu_fwd_bwd_us']} | {r['gpu_fwd_bwd_tflops']} ({r['gpu_fwd_bwd_pct_peak']} %; "
+              f"{r['gpu_fwd_bwd_issued_pct']} %; {r['gpu_fwd_bwd_minimal_pct']} %) | "
               f"{r['gpu_fwd_bwd_graph_us']} ({r['gpu_fwd_bwd_graph_tflops']}) | "
               f"{r['peak_extra_mb']} ({r['peak_extra_mb_no_split']})"
               if "gpu_fwd_bwd_us" in r else "n/a | n/a | n/a | n/a")
         print(f"| {r['config']} | {tuple(r['shape'])}{' causal' if r['causal'] else ''} | "
-              f"{r['gpu_fwd_us']} | {r['gpu_fwd_tflops']} ({r['gpu_fwd_pct_peak']} %) | {fb} | "
+              f"{r['gpu_fwd_us']} | {r['gpu_fwd_tflops']} ({r['gpu_fwd_pct_peak']} %; "
+              f"{r['gpu_fwd_issued_pct']} %) | {fb} | "
               f"{r.get('cpu_fwd_tflops', '-')} | {r.get('cpu_fwd_bwd_tflops', '-')} |")
 
 
@@ -625,15 +651,18 @@ def run_large(steps, warmup, prewarm_s=0.0):
             row[f"{name}_tflops"] = round(counted * flops / t / 1e12, 1)
             row[f"{name}_issued_pct"] = round(
                 100 * issued * useful * flops / t / 1e12 / PEAK_FP16_TFLOPS, 1)
+            row[f"{name}_minimal_pct"] = round(
+                100 * minimal_flops(b, s, h, d, causal, name) / t / 1e12 / PEAK_FP16_TFLOPS, 1)
         rows.append(row)
         print(json.dumps(row), flush=True)
     print("| (B,S,H,D) | fwd us | fwd TFLOP/s (issued % of peak) | bwd us | "
-          "bwd TFLOP/s (issued % of peak) |")
+          "bwd TFLOP/s (issued % of peak; minimal 5-GEMM % of peak) |")
     print("|---|---:|---:|---:|---:|")
     for r in rows:
         print(f"| {tuple(r['shape'])}{' causal' if r['causal'] else ' non-causal'} | "
               f"{r['fwd_us']} | {r['fwd_tflops']} ({r['fwd_issued_pct']} %) | "
-              f"{r['bwd_us']} | {r['bwd_tflops']} ({r['bwd_issued_pct']} %) |")
+              f"{r['bwd_us']} | {r['bwd_tflops']} ({r['bwd_issued_pct']} %; "
+              f"{r['bwd_minimal_pct']} %) |")
 
 
 # Fused-prologue workloads: (name, B, S, H, Hk, D, qk_norm, dtype name)
@@ -1143,6 +1172,10 @@ def main():
                 "flops_per_launch": d["flops"],
                 "mfma_busy_counter": counters.get("mfma_busy") if counters else None,
                 "counters_source": counters_src}
+    if dom in MINIMAL_GEMMS:
+        roofline["frac_minimal"] = round(
+            minimal_flops(B, S, H, D, CAUSAL, dom) / t_in / 1e12 / PEAK_FP16_TFLOPS, 4)
+        roofline["minimal_gemms"] = MINIMAL_GEMMS[dom]
     all_kernels = {}
     for n, r in kt.items():
         sym_n = profiled_traffic(r["kernel"])[2]
@@ -1154,6 +1187,10 @@ def main():
             row.update({"avg_us_in_step": round(r["avg_us_in_step"], 3),
                         "frac_mfma_in_step": round(tf / PEAK_FP16_TFLOPS, 4),
                         "frac_useful_in_step": round(useful * tf / PEAK_FP16_TFLOPS, 4)})
+            if n in MINIMAL_GEMMS:
+                mf = minimal_flops(B, S, H, D, CAUSAL, n)
+                row["frac_minimal_in_step"] = round(
+                    mf / (r["avg_us_in_step"] * 1e-6) / 1e12 / PEAK_FP16_TFLOPS, 4)
             c, _ = profiled_counters(sym_n)
             if c:
                 row["mfma_busy_counter"] = c.get("mfma_busy")
@@ -1182,6 +1219,10 @@ def main():
                    "B": B, "S": S, "H": H, "D": D, "causal": CAUSAL, "sm_scale": 1.0 / math.sqrt(D),
                    "flops_convention": "fwd 4*B*H*S^2*D dense-counted, fwd+bwd 5x"},
         "pct_peak": round(100.0 * value / PEAK_FP16_TFLOPS, 2),
+        "frac_minimal": round(minimal_flops(B, S, H, D, CAUSAL, "step") / t_step / 1e12
+                              / PEAK_FP16_TFLOPS, 4),
+        "frac_minimal_note": "share of the dense MFMA peak spent on the minimal algorithm's "
+                             "work: 2 forward + 5 backward GEMMs of 2*B*H*S^2*D, causal half",
         "fwd": {"value": round(fwd_tf, 3), "unit": "TFLOP/s", "ms": round(t_fwd * 1e3, 4),
                 "pct_peak": round(100.0 * fwd_tf / PEAK_FP16_TFLOPS, 2),
                 "vs_baseline": round(fwd_tf / REF_FWD_TFLOPS, 3),
