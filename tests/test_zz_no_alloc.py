@@ -76,3 +76,49 @@ def test_noalloc_matches_fa_bwd_gqa_bitwise():
             assert torch.isfinite(a.float()).all(), name
             assert torch.equal(a, b), f"call {i}: {name} differs from fa_bwd_gqa " \
                 f"(max-abs {(a.float() - b.float()).abs().max().item():.3e})"
+
+
+def test_noalloc_under_graph_capture_matches_eager():
+    """The callers fa_bwd_gqa_noalloc is for capture it into HIP graphs: one
+    eager call on the device first (it looks up the scratch buffer's device
+    address, which the header asks to happen before capture), then the call
+    captured into a torch.cuda.CUDAGraph and replayed twice with unrelated
+    eager work between the replays; every replay's gradients must equal the
+    eager fa_bwd_gqa's bitwise (split causal D = 128 problem: the split
+    counters are zeroed by a kernel, no memset is recorded)."""
+    from flash_attn_volta import _capi, flash_attn_forward_gqa
+    from flash_attn_volta.forward import kernel_strides
+    lib = _capi.load()
+    B, Sq, Sk, H, Hk, D, dtype, causal = CASES[0]
+    print(f"[case] noalloc graph capture: B={B} Sq={Sq} H={H} D={D} causal={causal}", flush=True)
+    q, k, v, do = _inputs(B, Sq, Sk, H, Hk, D, dtype, seed=31)
+    o, lse = flash_attn_forward_gqa(q, k, v, causal=causal, return_softmax_lse=True)
+    full = lib.fa_bwd_gqa_workspace_bytes(B, Sq, Sk, H, Hk, D, int(causal))
+    ws = torch.full((min(full, _capi.NOALLOC_SCRATCH_BYTES),), 0x5A, dtype=torch.uint8,
+                    device="cuda")
+    ref = _call(lib, "fa_bwd_gqa", do, q, k, v, o, lse, causal, ws)
+    _call(lib, "fa_bwd_gqa_noalloc", do, q, k, v, o, lse, causal)   # the eager first call
+
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    st = tuple(kernel_strides(t) for t in (do, q, k, v, o, dq, dk, dv))
+    ptrs = (do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+            lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr())
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g):
+            rc = lib.fa_bwd_gqa_noalloc(*ptrs, B, Sq, Sk, H, Hk, D, *st, 1.0 / math.sqrt(D),
+                                        int(causal), _capi.FA_DTYPE_F16,
+                                        torch.cuda.current_stream().cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    _capi.check(rc, "fa_bwd_gqa_noalloc (captured)")
+    for rep in range(2):
+        for t in (dq, dk, dv):
+            t.fill_(float("nan"))
+        noise = torch.randn(1 << 20, device="cuda").sum()   # unrelated eager kernels
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.isfinite(noise)
+        for name, a, b in zip(("dq", "dk", "dv"), (dq, dk, dv), ref):
+            assert torch.equal(a, b), f"replay {rep}: {name} differs from eager fa_bwd_gqa"
