@@ -261,14 +261,17 @@ def minimal_flops(b, s, h, d, causal, part):
     return MINIMAL_GEMMS[part] * 2.0 * b * h * s * s * d * useful_fraction(s, causal)
 
 
-def profiled_counters(kernel_sym):
+def profiled_counters(kernel_sym, prefer="c4a_causal"):
     """Counter-derived figures for the kernel whose symbol starts with
     `kernel_sym`, from the committed rocprofv3 PMC summaries
-    (profiles/*_counters.md, JSON block written by `bench.py --pmc-summary`).
+    (profiles/*_counters.md, JSON block written by `bench.py --pmc-summary`),
+    the benchmark workload's file (`prefer` in its name) first: the same
+    kernel instantiation runs at several configs.
     Returns (dict, source) or (None, None)."""
     import glob
     import re
-    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", "*_counters.md"))):
+    paths = sorted(glob.glob(os.path.join(ROOT, "profiles", "*_counters.md")))
+    for path in sorted(paths, key=lambda p: prefer not in os.path.basename(p)):
         text = open(path).read()
         m = re.search(r"```json\s*(\{.*?\})\s*```", text, re.S)
         if not m:
@@ -870,11 +873,13 @@ def run_decode(steps, warmup):
               f"({100 * r['splitkv_frac_hbm']:.1f} %) | {r['speedup']}x |")
 
 
-def run_profile_config(name, steps, warmup):
+def run_profile_config(name, steps, warmup, prewarm_s=0.0):
     """The training step's kernels for one BASELINE config, as the program
     that rocprofv3 counter passes run: `warmup` + `steps` rounds of
     flash_attn_forward (with LSE) and flash_attn_backward on the same
-    inputs as --configs, nothing else on the GPU in between."""
+    inputs as --configs, nothing else on the GPU in between (with
+    `prewarm_s` > 0, first that long of the same rounds, so that a kernel
+    trace's averages are dominated by launches at ramped clocks)."""
     import torch
     from flash_attn_volta import flash_attn_backward, flash_attn_forward
     rows = [r for r in CONFIG_TABLE if r[0] == name]
@@ -884,9 +889,13 @@ def run_profile_config(name, steps, warmup):
     g = torch.Generator(device="cpu").manual_seed(0)
     q, k, v = (((torch.randn((b, s, h, d), generator=g)).half() * in_scale).cuda() for _ in range(3))
     do = torch.randn((b, s, h, d), generator=torch.Generator(device="cpu").manual_seed(1)).half().cuda()
-    for _ in range(warmup + steps):
+    def rnd():
         o, lse = flash_attn_forward(q, k, v, causal=causal, sm_scale=sc, return_softmax_lse=True)
         flash_attn_backward(do, q, k, v, o, lse, causal=causal, sm_scale=sc)
+    if prewarm_s > 0:
+        prewarm(rnd, prewarm_s)
+    for _ in range(warmup + steps):
+        rnd()
     torch.cuda.synchronize()
     log(f"[bench] profiled {name} ({b},{s},{h},{d}) causal={causal}: {warmup + steps} steps")
 
@@ -935,7 +944,8 @@ PMC_PASSES = {
          "SQ_ACTIVE_INST_VALU SQ_VALU_MFMA_COEXEC_CYCLES SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE",
 }
 XCDS = 8            # MI355X: GRBM_GUI_ACTIVE comes back summed over the 8 XCDs
-SIMDS = 4 * 256     # 256 CUs x 4 SIMDs
+CUS = 256
+SIMDS = 4 * CUS     # 256 CUs x 4 SIMDs
 
 
 def pmc_summary(dirs):
@@ -999,10 +1009,23 @@ def pmc_summary(dirs):
                     row[k] = round(av[c] / wc, 4)
         if av.get("SQ_VALU_MFMA_BUSY_CYCLES") and "SQ_VALU_MFMA_COEXEC_CYCLES" in av:
             row["mfma_coexec"] = round(av["SQ_VALU_MFMA_COEXEC_CYCLES"] / av["SQ_VALU_MFMA_BUSY_CYCLES"], 4)
+        # the texture / LDS pass (one TA and one TD per CU; LDS load
+        # bandwidth in 64-byte units, summed over the CUs)
+        if cyc:
+            if "TA_TA_BUSY" in av:
+                row["ta_busy"] = round(av["TA_TA_BUSY"] / (cyc * CUS), 4)
+            if "TD_TD_BUSY" in av:
+                row["td_busy"] = round(av["TD_TD_BUSY"] / (cyc * CUS), 4)
+            if "TD_TC_STALL" in av:
+                row["td_tc_stall"] = round(av["TD_TC_STALL"] / (cyc * CUS), 4)
+            if "SQ_INSTS_LDS_LOAD_BANDWIDTH" in av:
+                row["lds_load_b_per_clk_cu"] = round(64.0 * av["SQ_INSTS_LDS_LOAD_BANDWIDTH"] / (cyc * CUS), 1)
         out[key] = row
     cols = ["cycles", "mfma_busy", "valu_per_mfma", "salu_per_mfma", "lds_per_mfma", "trans_per_mfma",
             "lds_bank_conflict", "waves_per_simd", "wait_any", "wait_issue", "active", "mfma_coexec",
+            "ta_busy", "td_busy", "td_tc_stall", "lds_load_b_per_clk_cu",
             "lds_bytes", "grid", "workgroup"]
+    cols = [c for c in cols if any(c in r for r in out.values())]
     print("| kernel | " + " | ".join(cols) + " |")
     print("|---|" + "---:|" * len(cols))
     for key, row in out.items():
@@ -1010,6 +1033,98 @@ def pmc_summary(dirs):
     print("\n```json")
     print(json.dumps({"kernels": out, "xcds": XCDS, "simds": SIMDS}, indent=1))
     print("```")
+
+
+def traffic_summary(dirs):
+    """HBM bytes per launch from four rocprofv3 --pmc output directories:
+    FETCH_SIZE and WRITE_SIZE over the benchmark's kernels, then the same two
+    counters over --copy-calibration's plain device copies, whose known
+    traffic (read n + write n bytes per dispatch) gives the scale of each
+    counter.  Prints the per-kernel table and the JSON block that
+    profiled_traffic() reads back (profiles/*_hbm_traffic.md)."""
+    import collections
+    import csv
+    import glob
+
+    def per_kernel(dr, counter):
+        vals = collections.defaultdict(list)
+        for path in glob.glob(os.path.join(dr, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(path)):
+                if r["Counter_Name"] == counter:
+                    vals[r["Kernel_Name"]].append(float(r["Counter_Value"]))
+        return {k: statistics.mean(v) for k, v in vals.items()}
+
+    fetch, write = per_kernel(dirs[0], "FETCH_SIZE"), per_kernel(dirs[1], "WRITE_SIZE")
+    cfetch, cwrite = per_kernel(dirs[2], "FETCH_SIZE"), per_kernel(dirs[3], "WRITE_SIZE")
+    copy = [k for k in cfetch if "copyBuffer" in k or "copy" in k.lower()]
+    if not copy:
+        raise SystemExit("no copy kernel in the calibration runs")
+    # the calibration copy reads and writes n bytes; WRITE_SIZE counts the
+    # write exactly (scale 1), FETCH_SIZE is scaled to the same n
+    n_kib = cwrite[copy[0]]
+    f_scale = n_kib / cfetch[copy[0]]
+    w_scale = n_kib / cwrite[copy[0]]
+    print(f"Calibration: the copy writes {n_kib:.1f} KiB per dispatch: FETCH_SIZE reads "
+          f"{cfetch[copy[0]]:.1f} KiB, WRITE_SIZE {cwrite[copy[0]]:.1f} KiB -> scale factors fetch "
+          f"x{f_scale:.3f}, write x{w_scale:.3f}.\n")
+    print(f"| kernel | FETCH_SIZE (KiB) | WRITE_SIZE (KiB) | traffic = fetch*{f_scale:.3f} + "
+          f"write*{w_scale:.3f} (MiB) |")
+    print("|---|---:|---:|---:|")
+    table = {}
+    for k in sorted(fetch):
+        if "fa_" not in k:
+            continue
+        b = (fetch[k] * f_scale + write.get(k, 0.0) * w_scale) * 1024.0
+        table[demangle_fa(k)] = int(round(b))
+        print(f"| `{demangle_fa(k)}` | {fetch[k]:.1f} | {write.get(k, 0.0):.1f} | {b / 2**20:.2f} |")
+    print("\n```json")
+    print(json.dumps({"traffic_bytes_per_launch": table}))
+    print("```")
+
+
+def trace_summary(dirs):
+    """Per-kernel launch statistics of rocprofv3 --kernel-trace --stats
+    output directories (`*_kernel_stats.csv`, one directory per run) for
+    the fa:: kernels: calls, average / min / max duration and share of the
+    run's GPU time, as a markdown table per directory.  Durations of a
+    --profile-config run are those of back-to-back training-step launches
+    without a pre-warm, i.e. with the clocks still ramping."""
+    import csv
+    import glob
+    for dr in dirs:
+        rows = []
+        for path in glob.glob(os.path.join(dr, "**", "*kernel_stats.csv"), recursive=True):
+            for r in csv.DictReader(open(path)):
+                rows.append(r)
+        print(f"{dr}:\n")
+        print("| kernel | calls | avg (us) | min (us) | max (us) | % of GPU time |")
+        print("|---|---:|---:|---:|---:|---:|")
+        for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"])):
+            print(f"| `{demangle_fa(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                  f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | "
+                  f"{float(r['Percentage']):.2f} |")
+        print()
+        # the training step's launches: every run of consecutive fwd -> dQ ->
+        # dK/dV dispatches, per kernel, and the last 20 such sequences (the
+        # benchmark's clean in-step loop runs last)
+        disp = []
+        for path in glob.glob(os.path.join(dr, "**", "*kernel_trace.csv"), recursive=True):
+            for r in csv.DictReader(open(path)):
+                disp.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]),
+                             demangle_fa(r["Kernel_Name"])))
+        disp.sort()
+        kind = [("fwd" if n.startswith("fa_fwd_kernel") else "dq" if n.startswith("fa_bwd_dq_kernel")
+                 else "dkdv" if n.startswith("fa_bwd_dkdv_kernel") else "") for _, _, n in disp]
+        seqs = [i for i in range(len(disp) - 2) if kind[i:i + 3] == ["fwd", "dq", "dkdv"]]
+        if seqs:
+            print("| kernel (in-step launches: fwd -> dQ -> dK/dV sequences) | launches | mean (us) | "
+                  "median (us) | mean of the last 20 (us) |")
+            print("|---|---:|---:|---:|---:|")
+            for j, name in enumerate(("fwd", "dq", "dkdv")):
+                d = [(disp[i + j][1] - disp[i + j][0]) / 1e3 for i in seqs]
+                print(f"| {name} (`{disp[seqs[-1] + j][2]}`) | {len(d)} | {statistics.mean(d):.2f} | "
+                      f"{statistics.median(d):.2f} | {statistics.mean(d[-20:]):.2f} |")
+            print()
 
 
 def main():
@@ -1048,7 +1163,23 @@ def main():
     ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
                     help="summarise rocprofv3 --pmc output directories (one per counter pass) "
                          "into per-kernel counter figures and exit (no GPU needed)")
+    ap.add_argument("--profile-prewarm", type=float, default=0.0, metavar="SECONDS",
+                    help="with --profile-config: run the same rounds this long first")
+    ap.add_argument("--traffic-summary", nargs=4,
+                    metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
+                    help="summarise four rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE over the "
+                         "benchmark, then over --copy-calibration) into HBM bytes per launch and "
+                         "exit (no GPU needed)")
+    ap.add_argument("--trace-summary", nargs="+", metavar="DIR",
+                    help="summarise rocprofv3 --kernel-trace --stats output directories into "
+                         "per-kernel launch tables and exit (no GPU needed)")
     args = ap.parse_args()
+    if args.trace_summary:
+        trace_summary(args.trace_summary)
+        return
+    if args.traffic_summary:
+        traffic_summary(args.traffic_summary)
+        return
     if args.pmc_summary:
         pmc_summary(args.pmc_summary)
         return
@@ -1073,7 +1204,7 @@ def main():
         return
     if args.profile_config:
         torch.cuda.set_device(0)
-        run_profile_config(args.profile_config, args.steps, args.warmup)
+        run_profile_config(args.profile_config, args.steps, args.warmup, args.profile_prewarm)
         return
     if args.configs:
         torch.cuda.set_device(0)
