@@ -43,6 +43,9 @@ METRIC = "fwd & fwd+bwd TFLOP/s + % fp16 MFMA peak at (1,4096,16,64) causal fp16
 PEAK_FP16_TFLOPS = 2516.6        # MI355X dense fp16 MFMA: 256 CU * 2.4 GHz * 4096 FLOP/clk
 PEAK_HBM_GBS = 8000.0
 B, S, H, D, CAUSAL = 1, 4096, 16, 64, True
+# fa_bwd's form for this workload: causal D <= 64 backwards run the delta
+# pre-pass and one fused launch of every dK/dV and dQ block
+FUSED_BWD = CAUSAL and D <= 64
 # Reference's published fwd+bwd figure for this exact shape and metric
 # (V100-SXM2, results/backward_bench.json:65-70).
 REF_FWD_BWD_TFLOPS = 61.83
@@ -141,6 +144,13 @@ def kernel_times(q, k, v, do, steps, warmup, prewarm_s=0.0):
                                   B, S, H, D, st["do"], st["q"], st["k"], st["v"], st["dq"],
                                   scale, int(CAUSAL), stream), "fa_bwd_dq")
 
+    def blocks():
+        _capi.check(lib.fa_bwd_blocks(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                      lse.data_ptr(), delta.data_ptr(), dq.data_ptr(),
+                                      dk.data_ptr(), dv.data_ptr(), B, S, H, D, st["do"],
+                                      st["q"], st["k"], st["v"], st["dq"], st["dk"], st["dv"],
+                                      scale, int(CAUSAL), stream), "fa_bwd_blocks")
+
     pre()
     base = 2.0 * B * H * S * S * D          # one dense S x S x D GEMM
     io = B * S * H * D * 2                  # bytes of one fp16 (B,S,H,D) tensor
@@ -155,6 +165,10 @@ def kernel_times(q, k, v, do, steps, warmup, prewarm_s=0.0):
         ("bwd_dkdv", dkdv, f"fa_bwd_dkdv_kernel<_Float16, {D}, {cb}, ", 4 * base, 6 * io + 2 * rows),
         ("bwd_dq", dqk, f"fa_bwd_dq_kernel<_Float16, {D}, {cb}, ", 3 * base, 5 * io + 2 * rows),
     ]
+    if FUSED_BWD:
+        # the fused launch of every dK/dV and every dQ block (fa_bwd_blocks)
+        table.append(("bwd_fused", blocks, f"fa_bwd_fused_kernel<_Float16, {D}, {cb}, ",
+                      7 * base, 7 * io + 2 * rows))
     res = {}
     for name, fn, sym, flops, nbytes in table:
         prewarm(fn, 0.5 * prewarm_s)
@@ -162,16 +176,21 @@ def kernel_times(q, k, v, do, steps, warmup, prewarm_s=0.0):
         res[name] = {"kernel": sym, "avg_us": ev * 1e6, "flops": flops, "bytes": nbytes,
                      "tflops": flops / ev / 1e12, "gbs": nbytes / ev / 1e9}
 
-    # The same kernels in the training step's order (forward, dQ, dK/dV)
-    # with an event between consecutive launches, so each kernel is timed
-    # in the step's context (clock and cache state) rather than in a loop
-    # of its own.  The step's dQ launch also computes delta; here delta
-    # comes from the pre-pass above, otherwise the launches are the step's.
+    # The same kernels in the training step's order with an event between
+    # consecutive launches, so each kernel is timed in the step's context
+    # (clock and cache state) rather than in a loop of its own: the
+    # forward, then fa_bwd's launches -- the delta pre-pass and the fused
+    # launch (causal D <= 64: exactly the step's launches), or the dQ and
+    # dK/dV kernels (the step's dQ launch also computes delta; here delta
+    # comes from the pre-pass above).
     def fwd_lse():
         _capi.check(lib.fa_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                                lse.data_ptr(), B, S, H, D, st["q"], st["k"], st["v"], st["o"],
                                scale, int(CAUSAL), stream), "fa_fwd")
-    seq = (("fwd", fwd_lse), ("bwd_dq", dqk), ("bwd_dkdv", dkdv))
+    if FUSED_BWD:
+        seq = (("fwd", fwd_lse), ("bwd_preprocess", pre), ("bwd_fused", blocks))
+    else:
+        seq = (("fwd", fwd_lse), ("bwd_dq", dqk), ("bwd_dkdv", dkdv))
 
     def seq_step():
         for _, fn in seq:
@@ -251,8 +270,9 @@ def useful_fraction(s, causal):
 # issues seven: the dQ kernel and the dK/dV kernel each recompute S and dP,
 # the price of writing every gradient once, without atomics.  Per backward
 # kernel the shared S and dP are charged to dK/dV (S, dP, dV, dK), the dQ
-# kernel keeps only its own dQ GEMM.
-MINIMAL_GEMMS = {"fwd": 2, "bwd": 5, "step": 7, "bwd_dkdv": 4, "bwd_dq": 1}
+# kernel keeps only its own dQ GEMM; the fused launch of both is charged the
+# whole backward's five.
+MINIMAL_GEMMS = {"fwd": 2, "bwd": 5, "step": 7, "bwd_dkdv": 4, "bwd_dq": 1, "bwd_fused": 5}
 
 
 def minimal_flops(b, s, h, d, causal, part):
@@ -1104,23 +1124,29 @@ def trace_summary(dirs):
                   f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | "
                   f"{float(r['Percentage']):.2f} |")
         print()
-        # the training step's launches: every run of consecutive fwd -> dQ ->
-        # dK/dV dispatches, per kernel, and the last 20 such sequences (the
-        # benchmark's clean in-step loop runs last)
+        # the training step's launches: every run of consecutive fwd ->
+        # pre-pass -> fused (or fwd -> dQ -> dK/dV) dispatches, per kernel,
+        # and the last 20 such sequences (the benchmark's clean in-step loop
+        # runs last)
         disp = []
         for path in glob.glob(os.path.join(dr, "**", "*kernel_trace.csv"), recursive=True):
             for r in csv.DictReader(open(path)):
                 disp.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]),
                              demangle_fa(r["Kernel_Name"])))
         disp.sort()
-        kind = [("fwd" if n.startswith("fa_fwd_kernel") else "dq" if n.startswith("fa_bwd_dq_kernel")
-                 else "dkdv" if n.startswith("fa_bwd_dkdv_kernel") else "") for _, _, n in disp]
-        seqs = [i for i in range(len(disp) - 2) if kind[i:i + 3] == ["fwd", "dq", "dkdv"]]
-        if seqs:
-            print("| kernel (in-step launches: fwd -> dQ -> dK/dV sequences) | launches | mean (us) | "
+        prefixes = (("fwd", "fa_fwd_kernel"), ("pre", "fa_bwd_preprocess_kernel"),
+                    ("fused", "fa_bwd_fused_kernel"), ("dq", "fa_bwd_dq_kernel"),
+                    ("dkdv", "fa_bwd_dkdv_kernel"))
+        kind = [next((k for k, p in prefixes if n.startswith(p)), "") for _, _, n in disp]
+        for order, title in ((("fwd", "pre", "fused"), "fwd -> pre-pass -> fused dK/dV + dQ"),
+                             (("fwd", "dq", "dkdv"), "fwd -> dQ -> dK/dV")):
+            seqs = [i for i in range(len(disp) - 2) if tuple(kind[i:i + 3]) == order]
+            if not seqs:
+                continue
+            print(f"| kernel (in-step launches: {title} sequences) | launches | mean (us) | "
                   "median (us) | mean of the last 20 (us) |")
             print("|---|---:|---:|---:|---:|")
-            for j, name in enumerate(("fwd", "dq", "dkdv")):
+            for j, name in enumerate(order):
                 d = [(disp[i + j][1] - disp[i + j][0]) / 1e3 for i in seqs]
                 print(f"| {name} (`{disp[seqs[-1] + j][2]}`) | {len(d)} | {statistics.mean(d):.2f} | "
                       f"{statistics.median(d):.2f} | {statistics.mean(d[-20:]):.2f} |")
@@ -1278,9 +1304,11 @@ def main():
     value = 5.0 * flops_f / t_step / 1e12
     fwd_tf = flops_f / t_fwd / 1e12
 
-    # the training step launches fwd, then fa_bwd = dQ (which also computes
-    # delta) and dK/dV; the pre-pass kernel is timed only as a standalone
-    step_kernels = ("bwd_dkdv", "bwd_dq", "fwd")
+    # the training step launches fwd, then fa_bwd = the pre-pass and the
+    # fused launch (causal D <= 64), or dQ (which also computes delta) and
+    # dK/dV
+    step_kernels = (("bwd_fused", "bwd_preprocess", "fwd") if FUSED_BWD
+                    else ("bwd_dkdv", "bwd_dq", "fwd"))
     dom = max(step_kernels, key=lambda n: kt[n]["avg_us_in_step"])
     d = kt[dom]
     traffic, traffic_src, sym = profiled_traffic(d["kernel"])
@@ -1370,8 +1398,11 @@ def main():
                                  "note": "same step captured once into a HIP graph and replayed"},
         "roofline": roofline,
         "kernels": all_kernels,
-        "step_launches": ["fa_fwd_kernel", "fa_bwd_dq_kernel (also computes delta)",
-                          "fa_bwd_dkdv_kernel"],
+        "step_launches": (["fa_fwd_kernel", "fa_bwd_preprocess_kernel",
+                           "fa_bwd_fused_kernel (every dK/dV block, then every dQ block)"]
+                          if FUSED_BWD else
+                          ["fa_fwd_kernel", "fa_bwd_dq_kernel (also computes delta)",
+                           "fa_bwd_dkdv_kernel"]),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -313,7 +313,7 @@ int launch_fwd(const fa::FwdArgs &a, hipStream_t stream) {
 
 template <typename E, int D>
 int launch_pre(const fa::PreArgs &a, hipStream_t stream) {
-  constexpr int RPB = 256 / (D / 8);
+  constexpr int RPB = 128;   // two lanes per row
   const int64_t rows = (int64_t)a.B * a.H * a.S;
   const int64_t grid = (rows + RPB - 1) / RPB;
   if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
@@ -408,6 +408,61 @@ int launch_dq(const fa::BwdArgs &a, hipStream_t stream) {
   }
   return split ? launch_dq_split<E, D, CAUSAL, 2, false>(a, stream)
                : launch_dq_split<E, D, CAUSAL, 1, false>(a, stream);
+}
+
+// Fused causal backward (fa::fa_bwd_fused_kernel, D <= 64): the pre-pass,
+// which computes delta and zeroes the key-block split's counters, then
+// one launch of every dK/dV block followed by every dQ block.
+struct FusedBwd {
+  fa::BwdArgs akv, aq;   // the dK/dV and dQ blocks' arguments
+  fa::PreArgs pre;
+  bool with_pre;         // launch the pre-pass first (false: delta is given)
+  bool kv_split2;        // dK/dV layout: the query-split kernel (SPLIT = 2)
+  bool q_split2;         // dQ layout: the key-split kernel (SPLIT = 2)
+};
+
+template <typename E, int D, bool CAUSAL, int KVS, int QS>
+int launch_bwd_fused_as(FusedBwd f, hipStream_t stream) {
+  using T = fa::DkdvTile<D, KVS>;
+  using Q = fa::DqTile<D, QS, 4>;
+  f.akv.n_blocks = (f.akv.Sk + T::BK - 1) / T::BK;
+  f.aq.n_blocks = (f.aq.Sq + Q::BM - 1) / Q::BM;
+  const int64_t n_kv = ((int64_t)f.akv.n_blocks + f.akv.split_kt) * f.akv.B * f.akv.Hk;
+  const int64_t n_q = (int64_t)f.aq.n_blocks * f.aq.B * f.aq.H;
+  if (n_kv + n_q > 0x7fffffff) return FA_ERR_TOO_LARGE;
+  // heaviest blocks first in both parts: the last workgroups dispatched
+  // are the lightest dQ blocks
+  f.akv.zigzag = 0;
+  f.aq.zigzag = 0;
+  if (f.with_pre) {
+    const int rc = launch_pre<E, D>(f.pre, stream);
+    if (rc) return rc;
+  }
+  if constexpr (std::is_same<E, fa::f16>::value) {
+    if (f.aq.c <= 1.0f) {
+      hipLaunchKernelGGL((fa::fa_bwd_fused_kernel<E, D, CAUSAL, KVS, QS, true>),
+                         dim3((unsigned)(n_kv + n_q)), dim3(256), 0, stream, f.akv, f.aq, (int)n_kv);
+      return launch_status();
+    }
+  }
+  hipLaunchKernelGGL((fa::fa_bwd_fused_kernel<E, D, CAUSAL, KVS, QS, false>),
+                     dim3((unsigned)(n_kv + n_q)), dim3(256), 0, stream, f.akv, f.aq, (int)n_kv);
+  return launch_status();
+}
+
+template <typename E, int D, bool CAUSAL>
+int launch_bwd_fused(const FusedBwd &f, hipStream_t stream) {
+  if constexpr (D <= 64 && CAUSAL) {
+    if (f.kv_split2)
+      return f.q_split2 ? launch_bwd_fused_as<E, D, CAUSAL, 2, 2>(f, stream)
+                        : launch_bwd_fused_as<E, D, CAUSAL, 2, 1>(f, stream);
+    return f.q_split2 ? launch_bwd_fused_as<E, D, CAUSAL, 1, 2>(f, stream)
+                      : launch_bwd_fused_as<E, D, CAUSAL, 1, 1>(f, stream);
+  } else {
+    (void)f;
+    (void)stream;
+    return FA_ERR_HEAD_DIM;   // run_bwd picks the fused path for causal D <= 64 only
+  }
 }
 
 // (dtype, D, causal) -> one instantiation of launcher L<E, D, CAUSAL>.
@@ -917,14 +972,14 @@ size_t split_bytes(const DkdvSplit &p) {
   return p.split_kt > 0 ? split_cnt_bytes(p) + split_part_bytes(p) : 0;
 }
 
-int run_dkdv(const void *dout, const void *q, const void *k, const void *v, const float *lse,
-             const float *delta, void *dk, void *dv, const Shape &s, const int64_t *do_st,
-             const int64_t *q_st, const int64_t *k_st, const int64_t *v_st, const int64_t *dk_st,
-             const int64_t *dv_st, float sm_scale, int causal, void *stream, int split_kt = 0,
-             unsigned *cnt = nullptr, float *part = nullptr, const DqSplit *dqs = nullptr,
-             float *dq_part = nullptr, void *dq = nullptr, const int64_t *dq_st = nullptr) {
-  const LaunchDevice launch_dev(stream);
-  fa::BwdArgs a;
+// The dK/dV kernel's arguments (every check of run_dkdv).
+int dkdv_args(const void *dout, const void *q, const void *k, const void *v, const float *lse,
+              const float *delta, void *dk, void *dv, const Shape &s, const int64_t *do_st,
+              const int64_t *q_st, const int64_t *k_st, const int64_t *v_st,
+              const int64_t *dk_st, const int64_t *dv_st, float sm_scale, int split_kt,
+              unsigned *cnt, float *part, const DqSplit *dqs, float *dq_part, void *dq,
+              const int64_t *dq_st, fa::BwdArgs *out) {
+  fa::BwdArgs &a = *out;
   int rc = bwd_common(dout, q, k, v, lse, delta, s, do_st, q_st, k_st, v_st, sm_scale, &a);
   if (rc) return rc;
   if ((rc = check_kv_like(dk, dk_st, s, true))) return rc;
@@ -950,20 +1005,31 @@ int run_dkdv(const void *dout, const void *q, const void *k, const void *v, cons
   a.dv_sb = dv_st[0];
   a.dv_ss = dv_st[1];
   a.dv_sh = dv_st[2];
+  return FA_OK;
+}
+
+int run_dkdv(const void *dout, const void *q, const void *k, const void *v, const float *lse,
+             const float *delta, void *dk, void *dv, const Shape &s, const int64_t *do_st,
+             const int64_t *q_st, const int64_t *k_st, const int64_t *v_st, const int64_t *dk_st,
+             const int64_t *dv_st, float sm_scale, int causal, void *stream, int split_kt = 0,
+             unsigned *cnt = nullptr, float *part = nullptr, const DqSplit *dqs = nullptr,
+             float *dq_part = nullptr, void *dq = nullptr, const int64_t *dq_st = nullptr) {
+  const LaunchDevice launch_dev(stream);
+  fa::BwdArgs a;
+  int rc = dkdv_args(dout, q, k, v, lse, delta, dk, dv, s, do_st, q_st, k_st, v_st, dk_st, dv_st,
+                     sm_scale, split_kt, cnt, part, dqs, dq_part, dq, dq_st, &a);
+  if (rc) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   FA_DISPATCH(launch_dkdv, s, causal, a, st);
 }
 
-// dQ; with `o` given (the full backward), the kernel also computes delta
-// from O and dO and writes it to `delta` instead of reading it.
-int run_dq(const void *dout, const void *q, const void *k, const void *v, const float *lse,
-           const float *delta, void *dq, const Shape &s, const int64_t *do_st, const int64_t *q_st,
-           const int64_t *k_st, const int64_t *v_st, const int64_t *dq_st, float sm_scale,
-           int causal, void *stream, const void *o = nullptr, const int64_t *o_st = nullptr,
-           unsigned *cnt_zero = nullptr, int n_cnt_zero = 0, int dq_split = 0,
-           float *dq_part = nullptr) {
-  const LaunchDevice launch_dev(stream);
-  fa::BwdArgs a;
+// The dQ kernel's arguments (every check of run_dq).
+int dq_args(const void *dout, const void *q, const void *k, const void *v, const float *lse,
+            const float *delta, void *dq, const Shape &s, const int64_t *do_st,
+            const int64_t *q_st, const int64_t *k_st, const int64_t *v_st, const int64_t *dq_st,
+            float sm_scale, const void *o, const int64_t *o_st, unsigned *cnt_zero,
+            int n_cnt_zero, int dq_split, float *dq_part, fa::BwdArgs *out) {
+  fa::BwdArgs &a = *out;
   int rc = bwd_common(dout, q, k, v, lse, delta, s, do_st, q_st, k_st, v_st, sm_scale, &a);
   if (rc) return rc;
   if ((rc = check_q_like(dq, dq_st, s, true))) return rc;
@@ -980,6 +1046,22 @@ int run_dq(const void *dout, const void *q, const void *k, const void *v, const 
   a.dq_sb = dq_st[0];
   a.dq_ss = dq_st[1];
   a.dq_sh = dq_st[2];
+  return FA_OK;
+}
+
+// dQ; with `o` given (the full backward), the kernel also computes delta
+// from O and dO and writes it to `delta` instead of reading it.
+int run_dq(const void *dout, const void *q, const void *k, const void *v, const float *lse,
+           const float *delta, void *dq, const Shape &s, const int64_t *do_st, const int64_t *q_st,
+           const int64_t *k_st, const int64_t *v_st, const int64_t *dq_st, float sm_scale,
+           int causal, void *stream, const void *o = nullptr, const int64_t *o_st = nullptr,
+           unsigned *cnt_zero = nullptr, int n_cnt_zero = 0, int dq_split = 0,
+           float *dq_part = nullptr) {
+  const LaunchDevice launch_dev(stream);
+  fa::BwdArgs a;
+  int rc = dq_args(dout, q, k, v, lse, delta, dq, s, do_st, q_st, k_st, v_st, dq_st, sm_scale, o,
+                   o_st, cnt_zero, n_cnt_zero, dq_split, dq_part, &a);
+  if (rc) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   FA_DISPATCH(launch_dq, s, causal, a, st);
 }
@@ -1011,6 +1093,13 @@ int check_bwd(const void *dout, const void *q, const void *k, const void *v, con
   if (!aligned16(lse)) return FA_ERR_ALIGNMENT;
   if (!isfinite(sm_scale)) return FA_ERR_SCALE;
   return FA_OK;
+}
+
+// The fused backward launch (fa::fa_bwd_fused_kernel) for causal
+// D = 32 / 64 backwards without the dQ split (whose halves the dK/dV
+// kernel adds after the dQ kernel).
+bool bwd_fused(const Shape &s, int causal, const DqSplit &qplan) {
+  return causal && s.D <= 64 && qplan.split == 0;
 }
 
 int run_bwd(const void *dout, const void *q, const void *k, const void *v, const void *o,
@@ -1046,6 +1135,29 @@ int run_bwd(const void *dout, const void *q, const void *k, const void *v, const
   }
   float *dq_part =
       qplan.split > 0 ? reinterpret_cast<float *>(ws + dbytes + split_bytes(plan)) : nullptr;
+  if (bwd_fused(s, causal, qplan)) {
+    FusedBwd f{};
+    if ((rc = dkdv_args(dout, q, k, v, lse, delta, dk, dv, s, do_st, q_st, k_st, v_st, dk_st,
+                        dv_st, sm_scale, plan.split_kt, cnt, part, nullptr, nullptr, nullptr,
+                        nullptr, &f.akv)))
+      return rc;
+    if ((rc = dq_args(dout, q, k, v, lse, delta, dq, s, do_st, q_st, k_st, v_st, dq_st, sm_scale,
+                      nullptr, nullptr, nullptr, 0, 0, nullptr, &f.aq)))
+      return rc;
+    f.pre.o = desc(o, o_st, s.Sq);
+    f.pre.dout = desc(dout, do_st, s.Sq);
+    f.pre.delta = delta;
+    f.pre.B = s.B;
+    f.pre.S = s.Sq;
+    f.pre.H = s.H;
+    f.pre.cnt_zero = cnt;
+    f.pre.n_cnt_zero = (int)plan.slots;
+    f.with_pre = true;
+    f.kv_split2 = plan.split_kt > 0 || row_split(s.Sk, (int64_t)s.B * s.Hk, true, 2);
+    f.q_split2 = row_split(s.Sq, (int64_t)s.B * s.H, true);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    FA_DISPATCH(launch_bwd_fused, s, causal, f, st);
+  }
   // dQ first: it computes delta (the pre-pass, folded in) for the dK/dV
   // kernel, which runs after it on the same stream, zeroes the key-block
   // split's counters and leaves its split query blocks' halves for the
@@ -1055,6 +1167,38 @@ int run_bwd(const void *dout, const void *q, const void *k, const void *v, const
     return rc;
   return run_dkdv(dout, q, k, v, lse, delta, dk, dv, s, do_st, q_st, k_st, v_st, dk_st, dv_st,
                   sm_scale, causal, stream, plan.split_kt, cnt, part, &qplan, dq_part, dq, dq_st);
+}
+
+// Both gradient launches given delta (fa_bwd without its delta step):
+// the fused launch where fa_bwd uses it (without a key-block split: there
+// is no workspace), else the dQ kernel reading delta, then the dK/dV
+// kernel.
+int run_bwd_blocks(const void *dout, const void *q, const void *k, const void *v,
+                   const float *lse, const float *delta, void *dq, void *dk, void *dv,
+                   const Shape &s, const int64_t *do_st, const int64_t *q_st,
+                   const int64_t *k_st, const int64_t *v_st, const int64_t *dq_st,
+                   const int64_t *dk_st, const int64_t *dv_st, float sm_scale, int causal,
+                   void *stream) {
+  const LaunchDevice launch_dev(stream);
+  if (!bwd_fused(s, causal, DqSplit{})) {
+    const int rc = run_dq(dout, q, k, v, lse, delta, dq, s, do_st, q_st, k_st, v_st, dq_st,
+                          sm_scale, causal, stream);
+    if (rc) return rc;
+    return run_dkdv(dout, q, k, v, lse, delta, dk, dv, s, do_st, q_st, k_st, v_st, dk_st, dv_st,
+                    sm_scale, causal, stream);
+  }
+  FusedBwd f{};
+  int rc = dkdv_args(dout, q, k, v, lse, delta, dk, dv, s, do_st, q_st, k_st, v_st, dk_st, dv_st,
+                     sm_scale, 0, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, &f.akv);
+  if (rc) return rc;
+  if ((rc = dq_args(dout, q, k, v, lse, delta, dq, s, do_st, q_st, k_st, v_st, dq_st, sm_scale,
+                    nullptr, nullptr, nullptr, 0, 0, nullptr, &f.aq)))
+    return rc;
+  f.with_pre = false;
+  f.kv_split2 = row_split(s.Sk, (int64_t)s.B * s.Hk, true, 2);
+  f.q_split2 = row_split(s.Sq, (int64_t)s.B * s.H, true);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  FA_DISPATCH(launch_bwd_fused, s, causal, f, st);
 }
 
 Shape square(int B, int S, int H, int D) { return Shape{B, S, S, H, H, D, FA_DTYPE_F16}; }
@@ -1490,6 +1634,19 @@ int fa_bwd_dq(const void *dout, const void *q, const void *k, const void *v,
               float sm_scale, int causal, void *stream) {
   return run_dq(dout, q, k, v, lse, delta, dq, square(B, S, H, D), do_strides, q_strides,
                 k_strides, v_strides, dq_strides, sm_scale, causal, stream);
+}
+
+int fa_bwd_blocks(const void *dout, const void *q, const void *k, const void *v,
+                  const float *lse, const float *delta, void *dq, void *dk, void *dv,
+                  int B, int S, int H, int D,
+                  const int64_t do_strides[4], const int64_t q_strides[4],
+                  const int64_t k_strides[4], const int64_t v_strides[4],
+                  const int64_t dq_strides[4], const int64_t dk_strides[4],
+                  const int64_t dv_strides[4],
+                  float sm_scale, int causal, void *stream) {
+  return run_bwd_blocks(dout, q, k, v, lse, delta, dq, dk, dv, square(B, S, H, D), do_strides,
+                        q_strides, k_strides, v_strides, dq_strides, dk_strides, dv_strides,
+                        sm_scale, causal, stream);
 }
 
 size_t fa_rope_qk_workspace_bytes(int B, int S, int H, int Hk, int D) {

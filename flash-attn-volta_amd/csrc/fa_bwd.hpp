@@ -2,18 +2,27 @@
 //
 // FlashAttention backward (Dao et al. 2022, Algorithm 4).  The reference
 // (flash_attn_volta/triton_fa_bwd.py:636-700) runs a delta op and two
-// kernels; fa_bwd here runs two launches, in this order on one stream:
-//   1. fa_bwd_dq_kernel   : one workgroup per query block, sweeping key
-//                           tiles; dQ = scale * dS K, and delta =
-//                           rowsum(dO * O) in fp32 from the rows its lanes
-//                           hold, written for the next launch (reference:
-//                           _fa_bwd_dq_kernel_*, :73-307, and the torch op
-//                           at :650)
-//   2. fa_bwd_dkdv_kernel : one workgroup per key block, sweeping query
-//                           tiles; dV = P^T dO, dK = scale * dS^T Q
-//                           (reference: _fa_bwd_dkdv_kernel_*, :319-580)
-// The standalone entry points fa_bwd_preprocess / fa_bwd_dq / fa_bwd_dkdv
-// run fa_bwd_preprocess_kernel (delta alone) and each kernel by itself.
+// kernels.  The work is split the same way, into two kinds of workgroup
+// ("blocks"):
+//   dQ block   (dq_block)  : one query block, sweeping key tiles; dQ =
+//                            scale * dS K (reference: _fa_bwd_dq_kernel_*,
+//                            :73-307)
+//   dK/dV block (dkdv_block): one key block, sweeping query tiles; dV =
+//                            P^T dO, dK = scale * dS^T Q (reference:
+//                            _fa_bwd_dkdv_kernel_*, :319-580)
+// and delta = rowsum(dO * O) in fp32 (the torch op at :650).  fa_bwd runs
+// them as
+//   causal, D <= 64: fa_bwd_preprocess_kernel (delta), then ONE launch of
+//                    fa_bwd_fused_kernel, every dK/dV block and then every
+//                    dQ block in one grid: the dQ blocks fill the slots the
+//                    causal sweeps of unequal length leave idle;
+//   otherwise:       fa_bwd_dq_kernel, whose blocks also compute delta from
+//                    the rows their lanes hold and write it, then
+//                    fa_bwd_dkdv_kernel.
+// Both ways compute delta with the same fp32 operations in the same order,
+// so the gradients are the same bits.  The standalone entry points
+// fa_bwd_preprocess / fa_bwd_dq / fa_bwd_dkdv run fa_bwd_preprocess_kernel
+// and each block kernel by itself.
 // P = exp(scale * Q K^T - LSE) is recomputed from the forward LSE and
 // dS = P * (dO V^T - delta).  No floating-point atomics and no S x S
 // buffer: every output element is written once by one lane, so results are
@@ -54,10 +63,13 @@
 namespace fa {
 
 // Swizzle of the dK/dV kernel's query tiles (read both ways): the padded
-// SW_PD (fa_common.hpp) at D = 128, SW_P8 below -- not SW_AT, whose
-// second-read offsets would spill its registers.  Measured at D = 128:
-// LDS bank conflicts 45 % of LDS-active cycles with SW_P8, 0 with SW_PD;
-// the backward -3.2 to -3.8 % at (1,4096,8,128) and (1,4096,16,128).
+// SW_PD (fa_common.hpp) at D = 128, SW_AT at D = 64 (conflict-free both
+// ways; its offsets fit since they are byte offsets hidden from
+// loop-invariant code motion at each tile step), SW_P8 at D = 32.
+// Measured at D = 128: LDS bank conflicts 45 % of LDS-active cycles with
+// SW_P8, 0 with SW_PD; the backward -3.2 to -3.8 % at (1,4096,8,128) and
+// (1,4096,16,128).  At D = 64 SW_AT took the conflicts from 0.03-0.08 to
+// 0.
 template <int D>
 constexpr int kDkdvSwizzle = D >= 128 ? SW_PD : (D == 64 ? SW_AT : SW_P8);
 
@@ -109,33 +121,52 @@ struct PreArgs {
   TensorDesc o, dout;
   float *delta;
   int B, S, H;
+  // when non-NULL, workgroup 0 zeroes cnt_zero[0 .. n_cnt_zero) (the
+  // key-block split counters of the fused backward launch that follows)
+  unsigned *cnt_zero;
+  int n_cnt_zero;
 };
 
 // ---------------------------------------------------------------------------
-// delta[b,h,s] = sum_d O * dO.  Each group of D/8 lanes reduces one row from
-// 16-byte loads; rows are enumerated in (b, h, s) order so delta writes are
-// contiguous.
+// delta[b,h,s] = sum_d O * dO.  Two lanes per row, rows in (b, h, s) order
+// (delta writes contiguous).  Lane g of a pair sums its half of the row in
+// the dQ kernel's fragment order -- chunks 16c + 8g .. +7, c ascending, one
+// fp32 FMA per element -- then the pair adds its two sums: the same fp32
+// operations, in the same order, as the dQ kernel's own delta (BwdArgs::
+// delta_out), so every backward path sees bit-identical delta.  (dP - delta
+// cancels exactly in exact arithmetic for a query with one visible key; in
+// fp32 it leaves a few ulps of delta in dS, and which few depends on this
+// order.)
 template <typename E, int D>
 __global__ __launch_bounds__(256) void fa_bwd_preprocess_kernel(PreArgs a) {
-  constexpr int LPR = D / 8;               // lanes per row
-  constexpr int RPB = 256 / LPR;           // rows per block
+  constexpr int RPB = 128;   // rows per block
   const int tid = threadIdx.x;
-  const int64_t row = (int64_t)blockIdx.x * RPB + tid / LPR;
-  const int part = tid % LPR;
+  if (a.cnt_zero != nullptr && blockIdx.x == 0) {
+    for (int i = tid; i < a.n_cnt_zero; i += 256) a.cnt_zero[i] = 0u;
+  }
+  const int64_t row = (int64_t)blockIdx.x * RPB + (tid >> 1);
+  const int g = tid & 1;
   const int64_t total = (int64_t)a.B * a.H * a.S;
   float acc = 0.0f;
   if (row < total) {
     const int s = (int)(row % a.S);
     const int64_t bh = row / a.S;
     const int h = (int)(bh % a.H), b = (int)(bh / a.H);
-    const vec8<E> ov = ld8<E>(a.o.head(b, h) + (int64_t)s * a.o.ss + 8 * part);
-    const vec8<E> gv = ld8<E>(a.dout.head(b, h) + (int64_t)s * a.dout.ss + 8 * part);
+    const f16 *po = a.o.head(b, h) + (int64_t)s * a.o.ss + 8 * g;
+    const f16 *pg = a.dout.head(b, h) + (int64_t)s * a.dout.ss + 8 * g;
+    vec8<E> ov[D / 16], gv[D / 16];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc = __builtin_fmaf((float)ov[j], (float)gv[j], acc);
+    for (int c = 0; c < D / 16; ++c) {
+      ov[c] = ld8<E>(po + 16 * c);
+      gv[c] = ld8<E>(pg + 16 * c);
+    }
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc = __builtin_fmaf((float)ov[c][j], (float)gv[c][j], acc);
   }
-#pragma unroll
-  for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-  if (row < total && part == 0) a.delta[row] = acc;
+  acc += __shfl_xor(acc, 1, 64);
+  if (row < total && g == 0) a.delta[row] = acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -413,19 +444,28 @@ struct DkdvTile {
   static_assert(64 * (D / 2) * 4 <= LDS_TILE * 2, "a merge buffer must fit in one stage");
 };
 
+// The LDS arrays of one dK/dV workgroup.  One LDS object per stage: the
+// compiler then sees that the DMA into one stage cannot alias reads of the
+// other and does not wait for it early.  Declared by the kernel that runs
+// the block (the dK/dV kernel, or the fused backward kernel, whose dQ
+// blocks reuse the four tile stages) and passed in by pointer: the block
+// functions are inlined, so every access still names its own object.
+#define FA_DKDV_LDS(T)                                                                 \
+  __shared__ __attribute__((aligned(16))) f16 s_q0[T::LDS_TILE], s_q1[T::LDS_TILE];   \
+  __shared__ __attribute__((aligned(16))) f16 s_do0[T::LDS_TILE], s_do1[T::LDS_TILE]; \
+  __shared__ __attribute__((aligned(16))) float s_lse[2][T::BQ];                      \
+  __shared__ __attribute__((aligned(16))) float s_dl[2][T::BQ];                       \
+  __shared__ __attribute__((aligned(16))) f16 s_k[T::LDS_KV], s_v[T::LDS_KV]
+
+// One dK/dV block (workgroup `bid` of the dK/dV grid).
 template <typename E, int D, bool CAUSAL, int SPLIT>
-__global__ __launch_bounds__((DkdvTile<D, SPLIT>::NT))
-__attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_bwd_dkdv_kernel(
-    BwdArgs a) {
+__device__ __forceinline__ void dkdv_block(const BwdArgs &a, const int bid, f16 *s_q0, f16 *s_q1,
+                                           f16 *s_do0, f16 *s_do1,
+                                           float (*s_lse)[DkdvTile<D, SPLIT>::BQ],
+                                           float (*s_dl)[DkdvTile<D, SPLIT>::BQ], f16 *s_k,
+                                           f16 *s_v) {
   using T = DkdvTile<D, SPLIT>;
   constexpr int BK = T::BK, BQ = T::BQ, NSUB = T::NSUB;
-  // One LDS object per stage: the compiler then sees that the DMA into one
-  // stage cannot alias reads of the other and does not wait for it early.
-  __shared__ __attribute__((aligned(16))) f16 s_q0[T::LDS_TILE], s_q1[T::LDS_TILE];
-  __shared__ __attribute__((aligned(16))) f16 s_do0[T::LDS_TILE], s_do1[T::LDS_TILE];
-  __shared__ __attribute__((aligned(16))) float s_lse[2][BQ];
-  __shared__ __attribute__((aligned(16))) float s_dl[2][BQ];
-  __shared__ __attribute__((aligned(16))) f16 s_k[T::LDS_KV], s_v[T::LDS_KV];
   auto q_st = [&](auto stc) -> f16 * { return decltype(stc)::value ? s_q1 : s_q0; };
   auto do_st = [&](auto stc) -> f16 * { return decltype(stc)::value ? s_do1 : s_do0; };
 
@@ -434,7 +474,6 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
 
   const int Sq = a.Sq, Sk = a.Sk, off = a.off;
   const int BHk = a.B * a.Hk;
-  const int bid = blockIdx.x;
   const int bhk = bid % BHk;
   const int rank = bid / BHk;
   // Causal: low key blocks see the most queries.  Blocks go heaviest
@@ -982,6 +1021,15 @@ __attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_b
   }
 }
 
+template <typename E, int D, bool CAUSAL, int SPLIT>
+__global__ __launch_bounds__((DkdvTile<D, SPLIT>::NT))
+__attribute__((amdgpu_waves_per_eu(DkdvTile<D, SPLIT>::WAVES_PER_EU))) void fa_bwd_dkdv_kernel(
+    BwdArgs a) {
+  using T = DkdvTile<D, SPLIT>;
+  FA_DKDV_LDS(T);
+  dkdv_block<E, D, CAUSAL, SPLIT>(a, blockIdx.x, s_q0, s_q1, s_do0, s_do1, s_lse, s_dl, s_k, s_v);
+}
+
 // ---------------------------------------------------------------------------
 // dQ: workgroup = 4 waves.  SPLIT = 1: wave w owns 32 queries (BM = 128)
 // and both 32-key sub-blocks of every 64-key tile.  SPLIT = 2: wave w owns
@@ -1010,22 +1058,21 @@ struct DqTile {
 // per score, no FMA.
 // NW = 8 (non-causal grids, chosen by the launcher): twice the query groups
 // share each K / V tile.
-template <typename E, int D, bool CAUSAL, int SPLIT, bool PRE = false, int NW = 4>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3 : 1)))
-void fa_bwd_dq_kernel(BwdArgs a) {
+// One dQ block (workgroup `bid` of the dQ grid) on four LDS stages of at
+// least DqTile::LDS_TILE elements each: K and V, double-buffered (one LDS
+// object per stage, as in the dK/dV block).
+template <typename E, int D, bool CAUSAL, int SPLIT, bool PRE, int NW>
+__device__ __forceinline__ void dq_block(const BwdArgs &a, const int bid, f16 *s_k0, f16 *s_k1,
+                                         f16 *s_v0, f16 *s_v1) {
   static_assert(!PRE || std::is_same<E, f16>::value, "the pre-scaled mode is fp16 only");
   static_assert(NW == 4 || !CAUSAL, "eight-wave dQ workgroups are for non-causal grids");
   using T = DqTile<D, SPLIT, NW>;
   constexpr int BM = T::BM, BN = T::BN, NSUB = T::NSUB;
-  // One LDS object per stage (see the dK/dV kernel).
-  __shared__ __attribute__((aligned(16))) f16 s_k0[T::LDS_TILE], s_k1[T::LDS_TILE];
-  __shared__ __attribute__((aligned(16))) f16 s_v0[T::LDS_TILE], s_v1[T::LDS_TILE];
   auto k_st = [&](auto stc) -> f16 * { return decltype(stc)::value ? s_k1 : s_k0; };
   auto v_st = [&](auto stc) -> f16 * { return decltype(stc)::value ? s_v1 : s_v0; };
 
   const int Sq = a.Sq, Sk = a.Sk, off = a.off;
   const int BH = a.B * a.H;
-  const int bid = blockIdx.x;
   // zero the split counters of the dK/dV launch that follows on the stream
   if (a.cnt_zero != nullptr && bid == 0) {
     for (int i = threadIdx.x; i < a.n_cnt_zero; i += T::NT) a.cnt_zero[i] = 0u;
@@ -1272,6 +1319,41 @@ void fa_bwd_dq_kernel(BwdArgs a) {
   }
   if (qrow < Sq)
     store_row<E, D>(a.dq + b * a.dq_sb + h * a.dq_sh + (int64_t)qrow * a.dq_ss, dq, dq_mul, g);
+}
+
+template <typename E, int D, bool CAUSAL, int SPLIT, bool PRE = false, int NW = 4>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(D <= 64 ? 3 : 1)))
+void fa_bwd_dq_kernel(BwdArgs a) {
+  using T = DqTile<D, SPLIT, NW>;
+  __shared__ __attribute__((aligned(16))) f16 s_k0[T::LDS_TILE], s_k1[T::LDS_TILE];
+  __shared__ __attribute__((aligned(16))) f16 s_v0[T::LDS_TILE], s_v1[T::LDS_TILE];
+  dq_block<E, D, CAUSAL, SPLIT, PRE, NW>(a, blockIdx.x, s_k0, s_k1, s_v0, s_v1);
+}
+
+// ---------------------------------------------------------------------------
+// Fused backward (causal, D <= 64): the dK/dV blocks and the dQ blocks of
+// one backward in one grid -- workgroups [0, n_kv) run dkdv_block with
+// `akv`, the rest dq_block with `aq` -- so that the dQ blocks, dispatched
+// after every dK/dV block, fill the slots the causal sweeps of unequal
+// length leave idle, and no kernel boundary drains the GPU between the
+// two.  Both read only the inputs and delta (the pre-pass computes it and
+// zeroes the key-block split's counters first) and write disjoint outputs,
+// so no workgroup waits for another.  The dQ blocks run in the dK/dV
+// blocks' four tile stages.
+template <typename E, int D, bool CAUSAL, int KVSPLIT, int QSPLIT, bool PRE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+void fa_bwd_fused_kernel(BwdArgs akv, BwdArgs aq, int n_kv) {
+  using T = DkdvTile<D, KVSPLIT>;
+  using Q = DqTile<D, QSPLIT, 4>;
+  static_assert(T::NT == 256 && Q::NT == 256, "both blocks take four waves");
+  static_assert(D <= 64, "three waves per SIMD for both blocks");
+  static_assert(T::LDS_TILE >= Q::LDS_TILE, "a dQ stage fits in a dK/dV tile stage");
+  FA_DKDV_LDS(T);
+  const int bid = blockIdx.x;
+  if (bid < n_kv)
+    dkdv_block<E, D, CAUSAL, KVSPLIT>(akv, bid, s_q0, s_q1, s_do0, s_do1, s_lse, s_dl, s_k, s_v);
+  else
+    dq_block<E, D, CAUSAL, QSPLIT, PRE, 4>(aq, bid - n_kv, s_q0, s_q1, s_do0, s_do1);
 }
 
 }  // namespace fa

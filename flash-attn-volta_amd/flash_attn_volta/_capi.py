@@ -56,6 +56,7 @@ EXPORTED_SYMBOLS = (
     "fa_bwd_gqa_noalloc",
     "fa_bwd_dkdv",
     "fa_bwd_dq",
+    "fa_bwd_blocks",
     "fa_rope_qk_fwd",
     "fa_rope_qk_workspace_bytes",
     "fa_rope_qk_bwd",
@@ -147,6 +148,11 @@ def _declare(lib):
                               _ci, _ci, _ci, _ci,
                               _i64x4, _i64x4, _i64x4, _i64x4, _i64x4,
                               ctypes.c_float, _ci, _vp]
+    lib.fa_bwd_blocks.restype = _ci
+    lib.fa_bwd_blocks.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                  _ci, _ci, _ci, _ci,
+                                  _i64x4, _i64x4, _i64x4, _i64x4, _i64x4, _i64x4, _i64x4,
+                                  ctypes.c_float, _ci, _vp]
     _i64x2 = ctypes.POINTER(ctypes.c_int64)
     lib.fa_rope_qk_fwd.restype = _ci
     lib.fa_rope_qk_fwd.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_float,

@@ -211,12 +211,16 @@ size_t fa_bwd_gqa_workspace_bytes(int B, int Sq, int Sk, int H, int Hk, int D, i
 
 /*
  * Backward attention: (dq, dk, dv) of L = <o, dout> with o = fa_fwd(q,k,v),
- * given the forward's `lse`. Two launches: the dQ kernel (one workgroup
- * per query block), which also computes delta = rowsum(o * dout) -- what
- * fa_bwd_preprocess computes -- into the workspace, then the dK/dV kernel
- * (one workgroup per key block, or two for the longest causal blocks when
- * the workspace has room: fa_bwd_gqa_workspace_bytes). No floating-point
- * atomics: results are bit-reproducible.
+ * given the forward's `lse`. Two launches. Causal with D = 32 or 64:
+ * fa_bwd_preprocess's kernel (delta = rowsum(o * dout) into the
+ * workspace), then one launch running every dK/dV workgroup (one per key
+ * block, or two for the longest blocks when the workspace has room:
+ * fa_bwd_gqa_workspace_bytes) and then every dQ workgroup (one per query
+ * block). Otherwise: the dQ kernel, which also computes delta into the
+ * workspace, then the dK/dV kernel. No floating-point atomics: results
+ * are bit-reproducible and, with the fa_bwd_workspace_bytes workspace (no
+ * split), bit-identical to the three separate calls fa_bwd_preprocess,
+ * fa_bwd_dq, fa_bwd_dkdv.
  *
  * Replaces flash_attn_volta/triton_fa_bwd.py:587-700 (flash_attn_backward
  * and _run_bwd_kernels, launching _fa_bwd_dq_kernel_* and
@@ -315,6 +319,27 @@ int fa_bwd_dq(const void *dout, const void *q, const void *k, const void *v,
               const int64_t k_strides[4], const int64_t v_strides[4],
               const int64_t dq_strides[4],
               float sm_scale, int causal, void *stream);
+
+/*
+ * Both gradient launches of fa_bwd given delta (the fa_bwd_preprocess
+ * output), i.e. fa_bwd without its delta step and without a workspace (so
+ * without the key-block split): for causal D = 32 / 64 the one fused
+ * launch of every dK/dV and every dQ workgroup, otherwise fa_bwd_dq then
+ * fa_bwd_dkdv.  Bit-identical to fa_bwd with the fa_bwd_workspace_bytes
+ * workspace.  For callers that time or schedule the gradient launches
+ * apart from the delta step.
+ *
+ * Replaces the two kernel launches of _run_bwd_kernels, which take delta
+ * from the torch op before them (flash_attn_volta/triton_fa_bwd.py:667-695).
+ */
+int fa_bwd_blocks(const void *dout, const void *q, const void *k, const void *v,
+                  const float *lse, const float *delta, void *dq, void *dk, void *dv,
+                  int B, int S, int H, int D,
+                  const int64_t do_strides[4], const int64_t q_strides[4],
+                  const int64_t k_strides[4], const int64_t v_strides[4],
+                  const int64_t dq_strides[4], const int64_t dk_strides[4],
+                  const int64_t dv_strides[4],
+                  float sm_scale, int causal, void *stream);
 
 /*
  * Fused attention prologue for q and k: optional per-head RMSNorm (QK-norm)

@@ -313,3 +313,95 @@ def test_backward_causal_key_block_split(B, Sq, Sk, H, Hk, D, dtype):
     # bit-reproducible whatever the workspace held before
     for a, b in zip(split, again):
         assert torch.equal(a, b)
+
+
+def _bwd_three_launches(do, q, k, v, o, lse, causal, sm_scale):
+    """The three separate entry points fa_bwd_preprocess, fa_bwd_dq and
+    fa_bwd_dkdv (the reference's three backward launches), fp16."""
+    from flash_attn_volta import _capi
+    from flash_attn_volta.forward import kernel_strides
+    lib = _capi.load()
+    B, S, H, D = q.shape
+    stream = torch.cuda.current_stream().cuda_stream
+    delta = torch.empty((B, H, S), dtype=torch.float32, device="cuda")
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    st = {n: kernel_strides(t) for n, t in dict(do=do, q=q, k=k, v=v, o=o, dq=dq, dk=dk,
+                                                   dv=dv).items()}
+    _capi.check(lib.fa_bwd_preprocess(o.data_ptr(), do.data_ptr(), delta.data_ptr(), B, S, H, D,
+                                      st["o"], st["do"], stream), "fa_bwd_preprocess")
+    _capi.check(lib.fa_bwd_dq(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                              lse.data_ptr(), delta.data_ptr(), dq.data_ptr(), B, S, H, D,
+                              st["do"], st["q"], st["k"], st["v"], st["dq"], sm_scale,
+                              int(causal), stream), "fa_bwd_dq")
+    _capi.check(lib.fa_bwd_dkdv(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                lse.data_ptr(), delta.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                B, S, H, D, st["do"], st["q"], st["k"], st["v"], st["dk"],
+                                st["dv"], sm_scale, int(causal), stream), "fa_bwd_dkdv")
+    torch.cuda.synchronize()
+    # fa_bwd_blocks: both gradient launches of fa_bwd, given the same delta
+    bq, bk, bv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    _capi.check(lib.fa_bwd_blocks(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                  lse.data_ptr(), delta.data_ptr(), bq.data_ptr(), bk.data_ptr(),
+                                  bv.data_ptr(), B, S, H, D, st["do"], st["q"], st["k"], st["v"],
+                                  st["dq"], st["dk"], st["dv"], sm_scale, int(causal), stream),
+                "fa_bwd_blocks")
+    torch.cuda.synchronize()
+    return (dq, dk, dv), (bq, bk, bv)
+
+
+# The causal D = 32 / 64 backward runs as the pre-pass and one fused launch
+# (every dK/dV block, then every dQ block, in one grid); the three separate
+# entry points run the same block code in three launches, so the gradients
+# must be bit-identical; so must fa_bwd_blocks (the fused launch alone,
+# given delta).  Shapes: both layout pairs the launcher picks for H = Hk
+# (dK/dV query-split with dQ key-split on grids under a round, both
+# unsplit above), a ragged length, and a scale above ln 2 (the dQ block's
+# unscaled mode).
+@pytest.mark.parametrize("B,S,H,D,sm_scale,in_scale", [
+    (1, 4096, 16, 64, None, 0.5),
+    (4, 2048, 16, 64, None, 1.0),
+    (2, 1000, 8, 64, 1.0, 0.35),
+    (4, 512, 4, 32, None, 1.0),
+    (8, 1024, 32, 32, None, 1.0),
+])
+def test_backward_fused_launch_matches_three_launches(B, S, H, D, sm_scale, in_scale):
+    from flash_attn_volta import flash_attn_backward, flash_attn_forward
+    print(f"[case] bwd fused vs three launches B={B} S={S} H={H} D={D} scale={sm_scale}",
+          flush=True)
+    q, k, v, do = (t.cuda() for t in orc.make_inputs(B, S, H, D, seed=21, scale=in_scale))
+    sc = default_scale(D, sm_scale)
+    o, lse = flash_attn_forward(q, k, v, causal=True, sm_scale=sc, return_softmax_lse=True)
+    fused = flash_attn_backward(do, q, k, v, o, lse, causal=True, sm_scale=sc)
+    three, blocks = _bwd_three_launches(do, q, k, v, o, lse, True, sc)
+    for name, a, b, c in zip(("dq", "dk", "dv"), fused, three, blocks):
+        assert torch.isfinite(a.float()).all(), name
+        assert torch.equal(a, b), f"{name} differs (max-abs {max_abs(a, b.float()):.3e})"
+        assert torch.equal(a, c), f"fa_bwd_blocks {name} differs"
+
+
+# The two mixed layout pairs, which need H != Hk or Sq != Sk (so the three
+# square entry points cannot run them): dK/dV query-split beside unsplit dQ
+# (many query heads per key/value head), and unsplit dK/dV beside the
+# key-split dQ (a short query block against a long key range, bottom-right
+# causal); against the float64 oracle, fp16 and bf16.
+@pytest.mark.parametrize("B,Sq,Sk,H,Hk,D,dtype", [
+    (32, 128, 128, 32, 4, 32, torch.float16),
+    (32, 128, 128, 32, 4, 32, torch.bfloat16),
+    (4, 128, 1024, 32, 32, 64, torch.float16),
+])
+def test_backward_fused_launch_mixed_layouts(B, Sq, Sk, H, Hk, D, dtype):
+    from flash_attn_volta import flash_attn_backward_gqa, flash_attn_forward_gqa
+    print(f"[case] bwd fused mixed layouts B={B} Sq={Sq} Sk={Sk} H={H} Hk={Hk} D={D} {dtype}",
+          flush=True)
+    q, k, v, do = orc.make_inputs_gqa(B, Sq, Sk, H, Hk, D, seed=23, dtype=dtype)
+    sc = default_scale(D, None)
+    o_ref, _ = orc.attention_fwd_gqa(q, k, v, True, sc)
+    dq_ref, dk_ref, dv_ref, _ = orc.attention_bwd_gqa(do, q, k, v, True, sc, o=o_ref)
+    qd, kd, vd, dod = (t.cuda() for t in (q, k, v, do))
+    o, lse = flash_attn_forward_gqa(qd, kd, vd, causal=True, return_softmax_lse=True)
+    dq, dk, dv = flash_attn_backward_gqa(dod, qd, kd, vd, o, lse, causal=True)
+    tol = TOL if dtype == torch.float16 else 4e-2
+    errs = dict(dq=max_abs(dq, dq_ref), dk=max_abs(dk, dk_ref), dv=max_abs(dv, dv_ref))
+    report(f"bwd fused mixed {B},{Sq},{Sk},{H},{Hk},{D}", **errs)
+    for key, e in errs.items():
+        assert e < tol, f"{key} max-abs {e:.3e} >= {tol}"
