@@ -117,6 +117,7 @@ def kernel_times(q, k, v, do, steps, warmup, prewarm_s=0.0):
     lib = _capi.load()
     out, lse = flash_attn_forward(q, k, v, causal=CAUSAL, return_softmax_lse=True)
     delta = torch.empty((B, H, S), dtype=torch.float32, device=q.device)
+    rowmax = torch.empty(lib.fa_bwd_rowmax_bytes(B, S, H) // 4, dtype=torch.float32, device=q.device)
     dq, dk, dv = (torch.empty_like(q) for _ in range(3))
     st = {name: kernel_strides(t) for name, t in
           (("q", q), ("k", k), ("v", v), ("do", do), ("o", out), ("dq", dq), ("dk", dk), ("dv", dv))}
@@ -129,12 +130,14 @@ def kernel_times(q, k, v, do, steps, warmup, prewarm_s=0.0):
                                stream), "fa_fwd")
 
     def pre():
-        _capi.check(lib.fa_bwd_preprocess(out.data_ptr(), do.data_ptr(), delta.data_ptr(), B, S, H, D,
-                                          st["o"], st["do"], stream), "fa_bwd_preprocess")
+        _capi.check(lib.fa_bwd_preprocess(out.data_ptr(), do.data_ptr(), delta.data_ptr(),
+                                          rowmax.data_ptr(), B, S, H, D, st["o"], st["do"], stream),
+                    "fa_bwd_preprocess")
 
     def dkdv():
         _capi.check(lib.fa_bwd_dkdv(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                    lse.data_ptr(), delta.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                    lse.data_ptr(), delta.data_ptr(), rowmax.data_ptr(),
+                                    dk.data_ptr(), dv.data_ptr(),
                                     B, S, H, D, st["do"], st["q"], st["k"], st["v"], st["dk"], st["dv"],
                                     scale, int(CAUSAL), stream), "fa_bwd_dkdv")
 
@@ -146,8 +149,9 @@ def kernel_times(q, k, v, do, steps, warmup, prewarm_s=0.0):
 
     def blocks():
         _capi.check(lib.fa_bwd_blocks(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                      lse.data_ptr(), delta.data_ptr(), dq.data_ptr(),
-                                      dk.data_ptr(), dv.data_ptr(), B, S, H, D, st["do"],
+                                      lse.data_ptr(), delta.data_ptr(), rowmax.data_ptr(),
+                                      dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), B, S, H, D,
+                                      st["do"],
                                       st["q"], st["k"], st["v"], st["dq"], st["dk"], st["dv"],
                                       scale, int(CAUSAL), stream), "fa_bwd_blocks")
 
@@ -155,20 +159,21 @@ def kernel_times(q, k, v, do, steps, warmup, prewarm_s=0.0):
     base = 2.0 * B * H * S * S * D          # one dense S x S x D GEMM
     io = B * S * H * D * 2                  # bytes of one fp16 (B,S,H,D) tensor
     rows = B * H * S * 4                    # bytes of one fp32 (B,H,S) vector
+    rmax = rows // 16                       # the row-group maxima: 2 fp32 per 32 rows
     cb = "true" if CAUSAL else "false"
     table = [
         # name, fn, kernel symbol prefix (the last template argument, the
         # in-workgroup split, is chosen by the launcher from the grid size),
         # algorithmic dense FLOPs per launch, algorithmic HBM bytes
         ("fwd", fwd, f"fa_fwd_kernel<_Float16, {D}, {cb}, ", 2 * base, 4 * io),
-        ("bwd_preprocess", pre, f"fa_bwd_preprocess_kernel<_Float16, {D}>", 2.0 * B * H * S * D, 2 * io + rows),
-        ("bwd_dkdv", dkdv, f"fa_bwd_dkdv_kernel<_Float16, {D}, {cb}, ", 4 * base, 6 * io + 2 * rows),
+        ("bwd_preprocess", pre, f"fa_bwd_preprocess_kernel<_Float16, {D}>", 2.0 * B * H * S * D, 2 * io + rows + rmax),
+        ("bwd_dkdv", dkdv, f"fa_bwd_dkdv_kernel<_Float16, {D}, {cb}, ", 4 * base, 6 * io + 2 * rows + rmax),
         ("bwd_dq", dqk, f"fa_bwd_dq_kernel<_Float16, {D}, {cb}, ", 3 * base, 5 * io + 2 * rows),
     ]
     if FUSED_BWD:
         # the fused launch of every dK/dV and every dQ block (fa_bwd_blocks)
         table.append(("bwd_fused", blocks, f"fa_bwd_fused_kernel<_Float16, {D}, {cb}, ",
-                      7 * base, 7 * io + 2 * rows))
+                      7 * base, 7 * io + 2 * rows + rmax))
     res = {}
     for name, fn, sym, flops, nbytes in table:
         prewarm(fn, 0.5 * prewarm_s)

@@ -120,6 +120,13 @@ float kernel_scale(float sm_scale) {
   return c < 1e-30f ? 1e-30f : c;
 }
 
+// fa::BwdArgs::lse_mul for kernel scale c: the dK/dV kernel's own
+// definition of cr, in the same IEEE operations
+float lse_seed_mul(float c, int dtype) {
+  const float ck = dtype == FA_DTYPE_F16 ? fminf(c, 1.0f) : 1.0f;
+  return -fa::kLog2e / (c / ck);
+}
+
 int launch_status() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? FA_OK : FA_ERR_LAUNCH;
@@ -313,9 +320,8 @@ int launch_fwd(const fa::FwdArgs &a, hipStream_t stream) {
 
 template <typename E, int D>
 int launch_pre(const fa::PreArgs &a, hipStream_t stream) {
-  constexpr int RPB = 128;   // two lanes per row
-  const int64_t rows = (int64_t)a.B * a.H * a.S;
-  const int64_t grid = (rows + RPB - 1) / RPB;
+  constexpr int RPB = 128;   // two lanes per row, 128 rows of one (b, h) per workgroup
+  const int64_t grid = (int64_t)a.B * a.H * ((a.S + RPB - 1) / RPB);
   if (grid > 0x7fffffff) return FA_ERR_TOO_LARGE;
   hipLaunchKernelGGL((fa::fa_bwd_preprocess_kernel<E, D>), dim3((unsigned)grid), dim3(256), 0,
                      stream, a);
@@ -776,19 +782,32 @@ int run_fwd_ws(const void *q, const void *k, const void *v, void *o, float *lse,
   FA_DISPATCH(launch_fwd_bal, s, causal, L, st);
 }
 
-int run_pre(const void *o, const void *dout, float *delta, const Shape &s, const int64_t *o_st,
-            const int64_t *do_st, void *stream) {
+// Backward workspace pieces: delta, then the row-group maxima.
+size_t delta_bytes(int B, int Sq, int H) {
+  const size_t n = (size_t)B * (size_t)H * (size_t)Sq * sizeof(float);
+  return (n + 255) & ~(size_t)255;
+}
+
+// Row-group maxima (fa::BwdArgs::rmax): (B, H, ceil(Sq / 32), 2) fp32.
+size_t rmax_bytes(int B, int Sq, int H) {
+  const size_t n = (size_t)B * (size_t)H * (size_t)fa::row_groups(Sq) * 2 * sizeof(float);
+  return (n + 255) & ~(size_t)255;
+}
+
+int run_pre(const void *o, const void *dout, float *delta, float *rmax, const Shape &s,
+            const int64_t *o_st, const int64_t *do_st, void *stream) {
   const LaunchDevice launch_dev(stream);
   int rc = check_shape(s);
   if (rc) return rc;
   if ((rc = check_q_like(o, o_st, s))) return rc;
   if ((rc = check_q_like(dout, do_st, s))) return rc;
   if (delta == nullptr) return FA_ERR_NULL_POINTER;
-  if (!aligned16(delta)) return FA_ERR_ALIGNMENT;
+  if (!aligned16(delta) || (rmax != nullptr && !aligned16(rmax))) return FA_ERR_ALIGNMENT;
   fa::PreArgs a{};
   a.o = desc(o, o_st, s.Sq);
   a.dout = desc(dout, do_st, s.Sq);
   a.delta = delta;
+  a.rmax = rmax;
   a.B = s.B;
   a.S = s.Sq;
   a.H = s.H;
@@ -830,6 +849,7 @@ int bwd_common(const void *dout, const void *q, const void *k, const void *v, co
   a.grp = s.H / s.Hk;
   a.off = s.Sk - s.Sq;
   a.c = kernel_scale(sm_scale);
+  a.lse_mul = lse_seed_mul(a.c, s.dtype);
   a.sm_scale = sm_scale;
   a.neg = sm_scale < 0.0f;
   *out = a;
@@ -974,16 +994,19 @@ size_t split_bytes(const DkdvSplit &p) {
 
 // The dK/dV kernel's arguments (every check of run_dkdv).
 int dkdv_args(const void *dout, const void *q, const void *k, const void *v, const float *lse,
-              const float *delta, void *dk, void *dv, const Shape &s, const int64_t *do_st,
-              const int64_t *q_st, const int64_t *k_st, const int64_t *v_st,
-              const int64_t *dk_st, const int64_t *dv_st, float sm_scale, int split_kt,
-              unsigned *cnt, float *part, const DqSplit *dqs, float *dq_part, void *dq,
-              const int64_t *dq_st, fa::BwdArgs *out) {
+              const float *delta, const float *rmax, void *dk, void *dv, const Shape &s,
+              const int64_t *do_st, const int64_t *q_st, const int64_t *k_st,
+              const int64_t *v_st, const int64_t *dk_st, const int64_t *dv_st, float sm_scale,
+              int split_kt, unsigned *cnt, float *part, const DqSplit *dqs, float *dq_part,
+              void *dq, const int64_t *dq_st, fa::BwdArgs *out) {
   fa::BwdArgs &a = *out;
   int rc = bwd_common(dout, q, k, v, lse, delta, s, do_st, q_st, k_st, v_st, sm_scale, &a);
   if (rc) return rc;
   if ((rc = check_kv_like(dk, dk_st, s, true))) return rc;
   if ((rc = check_kv_like(dv, dv_st, s, true))) return rc;
+  if (rmax == nullptr) return FA_ERR_NULL_POINTER;
+  if (!aligned16(rmax)) return FA_ERR_ALIGNMENT;
+  a.rmax = rmax;
   a.split_kt = split_kt;
   a.cnt = cnt;
   a.part = part;
@@ -1009,15 +1032,16 @@ int dkdv_args(const void *dout, const void *q, const void *k, const void *v, con
 }
 
 int run_dkdv(const void *dout, const void *q, const void *k, const void *v, const float *lse,
-             const float *delta, void *dk, void *dv, const Shape &s, const int64_t *do_st,
+             const float *delta, const float *rmax, void *dk, void *dv, const Shape &s,
+             const int64_t *do_st,
              const int64_t *q_st, const int64_t *k_st, const int64_t *v_st, const int64_t *dk_st,
              const int64_t *dv_st, float sm_scale, int causal, void *stream, int split_kt = 0,
              unsigned *cnt = nullptr, float *part = nullptr, const DqSplit *dqs = nullptr,
              float *dq_part = nullptr, void *dq = nullptr, const int64_t *dq_st = nullptr) {
   const LaunchDevice launch_dev(stream);
   fa::BwdArgs a;
-  int rc = dkdv_args(dout, q, k, v, lse, delta, dk, dv, s, do_st, q_st, k_st, v_st, dk_st, dv_st,
-                     sm_scale, split_kt, cnt, part, dqs, dq_part, dq, dq_st, &a);
+  int rc = dkdv_args(dout, q, k, v, lse, delta, rmax, dk, dv, s, do_st, q_st, k_st, v_st, dk_st,
+                     dv_st, sm_scale, split_kt, cnt, part, dqs, dq_part, dq, dq_st, &a);
   if (rc) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   FA_DISPATCH(launch_dkdv, s, causal, a, st);
@@ -1028,15 +1052,18 @@ int dq_args(const void *dout, const void *q, const void *k, const void *v, const
             const float *delta, void *dq, const Shape &s, const int64_t *do_st,
             const int64_t *q_st, const int64_t *k_st, const int64_t *v_st, const int64_t *dq_st,
             float sm_scale, const void *o, const int64_t *o_st, unsigned *cnt_zero,
-            int n_cnt_zero, int dq_split, float *dq_part, fa::BwdArgs *out) {
+            int n_cnt_zero, int dq_split, float *dq_part, float *rmax_out,
+            fa::BwdArgs *out) {
   fa::BwdArgs &a = *out;
   int rc = bwd_common(dout, q, k, v, lse, delta, s, do_st, q_st, k_st, v_st, sm_scale, &a);
   if (rc) return rc;
   if ((rc = check_q_like(dq, dq_st, s, true))) return rc;
   if (o != nullptr) {
+    // the full backward: delta and the row-group maxima computed here
     if ((rc = check_q_like(o, o_st, s))) return rc;
     a.o = desc(o, o_st, s.Sq);
     a.delta_out = const_cast<float *>(delta);
+    a.rmax_out = rmax_out;
   }
   a.cnt_zero = cnt_zero;
   a.n_cnt_zero = n_cnt_zero;
@@ -1056,20 +1083,16 @@ int run_dq(const void *dout, const void *q, const void *k, const void *v, const 
            const int64_t *k_st, const int64_t *v_st, const int64_t *dq_st, float sm_scale,
            int causal, void *stream, const void *o = nullptr, const int64_t *o_st = nullptr,
            unsigned *cnt_zero = nullptr, int n_cnt_zero = 0, int dq_split = 0,
-           float *dq_part = nullptr) {
+           float *dq_part = nullptr, float *rmax_out = nullptr) {
   const LaunchDevice launch_dev(stream);
   fa::BwdArgs a;
   int rc = dq_args(dout, q, k, v, lse, delta, dq, s, do_st, q_st, k_st, v_st, dq_st, sm_scale, o,
-                   o_st, cnt_zero, n_cnt_zero, dq_split, dq_part, &a);
+                   o_st, cnt_zero, n_cnt_zero, dq_split, dq_part, rmax_out, &a);
   if (rc) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   FA_DISPATCH(launch_dq, s, causal, a, st);
 }
 
-size_t delta_bytes(int B, int Sq, int H) {
-  const size_t n = (size_t)B * (size_t)H * (size_t)Sq * sizeof(float);
-  return (n + 255) & ~(size_t)255;
-}
 
 
 // Every check of the full backward but the workspace's: a call that passes
@@ -1111,17 +1134,21 @@ int run_bwd(const void *dout, const void *q, const void *k, const void *v, const
   int rc = check_bwd(dout, q, k, v, o, lse, dq, dk, dv, s, do_st, q_st, k_st, v_st, o_st, dq_st,
                      dk_st, dv_st, sm_scale);
   if (rc) return rc;
-  if (workspace == nullptr || workspace_bytes < delta_bytes(s.B, s.Sq, s.H))
+  const size_t rbytes = rmax_bytes(s.B, s.Sq, s.H);
+  if (workspace == nullptr || workspace_bytes < delta_bytes(s.B, s.Sq, s.H) + rbytes)
     return FA_ERR_WORKSPACE;
   if (!aligned16(workspace)) return FA_ERR_ALIGNMENT;
   float *delta = static_cast<float *>(workspace);
   // The key-block split runs when the workspace has room for it (see
   // fa_bwd_gqa_workspace_bytes): counters, then the fp32 partials.
-  // Layout: delta, then the dK/dV split's counters and partials, then the
-  // dQ split's partials -- both splits or neither, by workspace size.
+  // Layout: delta, the row-group maxima, then the dK/dV split's counters
+  // and partials, then the dQ split's partials -- both splits or neither,
+  // by workspace size.  (`dbytes` below covers delta and the maxima.)
   DkdvSplit plan = dkdv_split_plan(s, causal);
   DqSplit qplan = dq_split_plan(s, causal);
-  const size_t dbytes = delta_bytes(s.B, s.Sq, s.H);
+  float *rmax = reinterpret_cast<float *>(static_cast<char *>(workspace) +
+                                          delta_bytes(s.B, s.Sq, s.H));
+  const size_t dbytes = delta_bytes(s.B, s.Sq, s.H) + rbytes;
   if (workspace_bytes < dbytes + split_bytes(plan) + dq_split_bytes(qplan)) {
     plan = DkdvSplit{};
     qplan = DqSplit{};
@@ -1137,16 +1164,17 @@ int run_bwd(const void *dout, const void *q, const void *k, const void *v, const
       qplan.split > 0 ? reinterpret_cast<float *>(ws + dbytes + split_bytes(plan)) : nullptr;
   if (bwd_fused(s, causal, qplan)) {
     FusedBwd f{};
-    if ((rc = dkdv_args(dout, q, k, v, lse, delta, dk, dv, s, do_st, q_st, k_st, v_st, dk_st,
-                        dv_st, sm_scale, plan.split_kt, cnt, part, nullptr, nullptr, nullptr,
-                        nullptr, &f.akv)))
+    if ((rc = dkdv_args(dout, q, k, v, lse, delta, rmax, dk, dv, s, do_st, q_st, k_st, v_st,
+                        dk_st, dv_st, sm_scale, plan.split_kt, cnt, part, nullptr, nullptr,
+                        nullptr, nullptr, &f.akv)))
       return rc;
     if ((rc = dq_args(dout, q, k, v, lse, delta, dq, s, do_st, q_st, k_st, v_st, dq_st, sm_scale,
-                      nullptr, nullptr, nullptr, 0, 0, nullptr, &f.aq)))
+                      nullptr, nullptr, nullptr, 0, 0, nullptr, nullptr, &f.aq)))
       return rc;
     f.pre.o = desc(o, o_st, s.Sq);
     f.pre.dout = desc(dout, do_st, s.Sq);
     f.pre.delta = delta;
+    f.pre.rmax = rmax;
     f.pre.B = s.B;
     f.pre.S = s.Sq;
     f.pre.H = s.H;
@@ -1158,15 +1186,16 @@ int run_bwd(const void *dout, const void *q, const void *k, const void *v, const
     hipStream_t st = static_cast<hipStream_t>(stream);
     FA_DISPATCH(launch_bwd_fused, s, causal, f, st);
   }
-  // dQ first: it computes delta (the pre-pass, folded in) for the dK/dV
-  // kernel, which runs after it on the same stream, zeroes the key-block
-  // split's counters and leaves its split query blocks' halves for the
-  // dK/dV kernel to add.
+  // dQ first: it computes delta and the row-group maxima (the pre-pass,
+  // folded in) for the dK/dV kernel, which runs after it on the same
+  // stream, zeroes the key-block split's counters and leaves its split
+  // query blocks' halves for the dK/dV kernel to add.
   if ((rc = run_dq(dout, q, k, v, lse, delta, dq, s, do_st, q_st, k_st, v_st, dq_st, sm_scale,
-                   causal, stream, o, o_st, cnt, (int)plan.slots, qplan.split, dq_part)))
+                   causal, stream, o, o_st, cnt, (int)plan.slots, qplan.split, dq_part, rmax)))
     return rc;
-  return run_dkdv(dout, q, k, v, lse, delta, dk, dv, s, do_st, q_st, k_st, v_st, dk_st, dv_st,
-                  sm_scale, causal, stream, plan.split_kt, cnt, part, &qplan, dq_part, dq, dq_st);
+  return run_dkdv(dout, q, k, v, lse, delta, rmax, dk, dv, s, do_st, q_st, k_st, v_st, dk_st,
+                  dv_st, sm_scale, causal, stream, plan.split_kt, cnt, part, &qplan, dq_part, dq,
+                  dq_st);
 }
 
 // Both gradient launches given delta (fa_bwd without its delta step):
@@ -1174,25 +1203,32 @@ int run_bwd(const void *dout, const void *q, const void *k, const void *v, const
 // is no workspace), else the dQ kernel reading delta, then the dK/dV
 // kernel.
 int run_bwd_blocks(const void *dout, const void *q, const void *k, const void *v,
-                   const float *lse, const float *delta, void *dq, void *dk, void *dv,
-                   const Shape &s, const int64_t *do_st, const int64_t *q_st,
+                   const float *lse, const float *delta, const float *rmax, void *dq, void *dk,
+                   void *dv, const Shape &s, const int64_t *do_st, const int64_t *q_st,
                    const int64_t *k_st, const int64_t *v_st, const int64_t *dq_st,
                    const int64_t *dk_st, const int64_t *dv_st, float sm_scale, int causal,
                    void *stream) {
   const LaunchDevice launch_dev(stream);
   if (!bwd_fused(s, causal, DqSplit{})) {
-    const int rc = run_dq(dout, q, k, v, lse, delta, dq, s, do_st, q_st, k_st, v_st, dq_st,
-                          sm_scale, causal, stream);
+    // every check before the first launch
+    fa::BwdArgs chk;
+    int rc = dkdv_args(dout, q, k, v, lse, delta, rmax, dk, dv, s, do_st, q_st, k_st, v_st,
+                       dk_st, dv_st, sm_scale, 0, nullptr, nullptr, nullptr, nullptr, nullptr,
+                       nullptr, &chk);
     if (rc) return rc;
-    return run_dkdv(dout, q, k, v, lse, delta, dk, dv, s, do_st, q_st, k_st, v_st, dk_st, dv_st,
-                    sm_scale, causal, stream);
+    rc = run_dq(dout, q, k, v, lse, delta, dq, s, do_st, q_st, k_st, v_st, dq_st, sm_scale,
+                causal, stream);
+    if (rc) return rc;
+    return run_dkdv(dout, q, k, v, lse, delta, rmax, dk, dv, s, do_st, q_st, k_st, v_st, dk_st,
+                    dv_st, sm_scale, causal, stream);
   }
   FusedBwd f{};
-  int rc = dkdv_args(dout, q, k, v, lse, delta, dk, dv, s, do_st, q_st, k_st, v_st, dk_st, dv_st,
-                     sm_scale, 0, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, &f.akv);
+  int rc = dkdv_args(dout, q, k, v, lse, delta, rmax, dk, dv, s, do_st, q_st, k_st, v_st, dk_st,
+                     dv_st, sm_scale, 0, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                     &f.akv);
   if (rc) return rc;
   if ((rc = dq_args(dout, q, k, v, lse, delta, dq, s, do_st, q_st, k_st, v_st, dq_st, sm_scale,
-                    nullptr, nullptr, nullptr, 0, 0, nullptr, &f.aq)))
+                    nullptr, nullptr, nullptr, 0, 0, nullptr, nullptr, &f.aq)))
     return rc;
   f.with_pre = false;
   f.kv_split2 = row_split(s.Sk, (int64_t)s.B * s.Hk, true, 2);
@@ -1485,7 +1521,8 @@ const char *fa_strerror(int status) {
       return "the HIP runtime reported an error (a kernel launch, or the device address of "
              "the no-alloc scratch buffer)";
     case FA_ERR_SCRATCH:
-      return "fa_bwd_gqa_noalloc: delta (4 * B * H * Sq bytes) exceeds the static scratch "
+      return "fa_bwd_gqa_noalloc: delta and the row-group maxima (fa_bwd_workspace_bytes) "
+             "exceed the static scratch "
              "buffer (FA_NOALLOC_SCRATCH_BYTES)";
     case FA_ERR_DTYPE: return "unsupported dtype (supported: FA_DTYPE_F16, FA_DTYPE_BF16)";
     case FA_ERR_EPS: return "norm eps is negative or not finite";
@@ -1544,22 +1581,27 @@ int fa_fwd_ws(const void *q, const void *k, const void *v, void *o, float *lse,
                     q_strides, k_strides, v_strides, o_strides, sm_scale, causal, stream);
 }
 
-int fa_bwd_preprocess(const void *o, const void *dout, float *delta,
+int fa_bwd_preprocess(const void *o, const void *dout, float *delta, float *rowmax,
                       int B, int S, int H, int D,
                       const int64_t o_strides[4], const int64_t do_strides[4],
                       void *stream) {
-  return run_pre(o, dout, delta, square(B, S, H, D), o_strides, do_strides, stream);
+  return run_pre(o, dout, delta, rowmax, square(B, S, H, D), o_strides, do_strides, stream);
 }
 
 size_t fa_bwd_workspace_bytes(int B, int S, int H, int D) {
   if (check_shape(square(B, S, H, D)) != FA_OK) return 0;
-  return delta_bytes(B, S, H);
+  return delta_bytes(B, S, H) + rmax_bytes(B, S, H);
+}
+
+size_t fa_bwd_rowmax_bytes(int B, int S, int H) {
+  if (B <= 0 || S <= 0 || H <= 0) return 0;
+  return rmax_bytes(B, S, H);
 }
 
 size_t fa_bwd_gqa_workspace_bytes(int B, int Sq, int Sk, int H, int Hk, int D, int causal) {
   const Shape s{B, Sq, Sk, H, Hk, D, FA_DTYPE_F16};
   if (check_shape(s) != FA_OK) return 0;
-  return delta_bytes(B, Sq, H) + split_bytes(dkdv_split_plan(s, causal)) +
+  return delta_bytes(B, Sq, H) + rmax_bytes(B, Sq, H) + split_bytes(dkdv_split_plan(s, causal)) +
          dq_split_bytes(dq_split_plan(s, causal));
 }
 
@@ -1606,7 +1648,8 @@ int fa_bwd_gqa_noalloc(const void *dout, const void *q, const void *k, const voi
   int rc = check_bwd(dout, q, k, v, o, lse, dq, dk, dv, s, do_strides, q_strides, k_strides,
                      v_strides, o_strides, dq_strides, dk_strides, dv_strides, sm_scale);
   if (rc) return rc;
-  if (delta_bytes(B, Sq, H) > (size_t)FA_NOALLOC_SCRATCH_BYTES) return FA_ERR_SCRATCH;
+  if (delta_bytes(B, Sq, H) + rmax_bytes(B, Sq, H) > (size_t)FA_NOALLOC_SCRATCH_BYTES)
+    return FA_ERR_SCRATCH;
   void *ws = nullptr;
   if ((rc = scratch_for_stream(stream, &ws))) return rc;
   return run_bwd(dout, q, k, v, o, lse, dq, dk, dv, ws, FA_NOALLOC_SCRATCH_BYTES, s, do_strides,
@@ -1615,14 +1658,15 @@ int fa_bwd_gqa_noalloc(const void *dout, const void *q, const void *k, const voi
 }
 
 int fa_bwd_dkdv(const void *dout, const void *q, const void *k, const void *v,
-                const float *lse, const float *delta, void *dk, void *dv,
+                const float *lse, const float *delta, const float *rowmax, void *dk, void *dv,
                 int B, int S, int H, int D,
                 const int64_t do_strides[4], const int64_t q_strides[4],
                 const int64_t k_strides[4], const int64_t v_strides[4],
                 const int64_t dk_strides[4], const int64_t dv_strides[4],
                 float sm_scale, int causal, void *stream) {
-  return run_dkdv(dout, q, k, v, lse, delta, dk, dv, square(B, S, H, D), do_strides, q_strides,
-                  k_strides, v_strides, dk_strides, dv_strides, sm_scale, causal, stream);
+  return run_dkdv(dout, q, k, v, lse, delta, rowmax, dk, dv, square(B, S, H, D), do_strides,
+                  q_strides, k_strides, v_strides, dk_strides, dv_strides, sm_scale, causal,
+                  stream);
 }
 
 int fa_bwd_dq(const void *dout, const void *q, const void *k, const void *v,
@@ -1637,16 +1681,16 @@ int fa_bwd_dq(const void *dout, const void *q, const void *k, const void *v,
 }
 
 int fa_bwd_blocks(const void *dout, const void *q, const void *k, const void *v,
-                  const float *lse, const float *delta, void *dq, void *dk, void *dv,
-                  int B, int S, int H, int D,
+                  const float *lse, const float *delta, const float *rowmax, void *dq, void *dk,
+                  void *dv, int B, int S, int H, int D,
                   const int64_t do_strides[4], const int64_t q_strides[4],
                   const int64_t k_strides[4], const int64_t v_strides[4],
                   const int64_t dq_strides[4], const int64_t dk_strides[4],
                   const int64_t dv_strides[4],
                   float sm_scale, int causal, void *stream) {
-  return run_bwd_blocks(dout, q, k, v, lse, delta, dq, dk, dv, square(B, S, H, D), do_strides,
-                        q_strides, k_strides, v_strides, dq_strides, dk_strides, dv_strides,
-                        sm_scale, causal, stream);
+  return run_bwd_blocks(dout, q, k, v, lse, delta, rowmax, dq, dk, dv, square(B, S, H, D),
+                        do_strides, q_strides, k_strides, v_strides, dq_strides, dk_strides,
+                        dv_strides, sm_scale, causal, stream);
 }
 
 size_t fa_rope_qk_workspace_bytes(int B, int S, int H, int Hk, int D) {

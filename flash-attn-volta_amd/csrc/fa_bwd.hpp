@@ -46,9 +46,22 @@
 // |dS| ~ 1e-9 deep in a network), where fp16 would flush it to zero.  Each
 // lane therefore scales its output row's dS by a power of two 2^e and
 // divides the result by 2^e at the end.  In dK (lane = key, summing over
-// queries) e is a running scale chosen from the largest |dS| the lane has
-// produced, so that scaled values stay in [2^10, 2^15], with the fp32
-// accumulator rescaled exactly whenever e changes.  In dQ (lane = query) e
+// queries) e is settled per query tile, before the tile's MFMAs, from a
+// bound on the lane's |dS| over the tile: |dS| = P |dO . V_k - delta| <=
+// max|dO| ||V_k||_1 + max|delta| (P <= 1), with max|dO| and max|delta| over
+// the tile's rows from the row-group maxima (BwdArgs::rmax) that the delta
+// pass writes; e keeps the scaled bound in [2^8, 2^15] (re-settled to
+// [2^14, 2^15) when it leaves), so no scaled dS passes fp16's 65504, with
+// the fp32 accumulator rescaled exactly whenever e changes.  The maxima
+// come in through the scalar cache with the tile's loads, and the check for
+// tile t + 1 runs at the end of tile t, under its last MFMAs.  (Settling
+// from the bound replaced a per-32x32-block maximum of the computed |dS| on
+// the MFMAs' path: the backward -1.2 to -4.3 % at (1,4096,16,64),
+// (1,4096,8,128), (1,4096,16,128), (2,2048,16,64), (1,8192,16,64) and
+// (4,4096,16,64), causal and not; +-0.5 % at (2,1024,8,64) and
+// (1,2048,16,64); +6.5 % at (4,512,4,32), whose sweeps of at most four
+// tiles pay the per-block set-up -- ||V_k||_1, the first settle -- and a
+// pre-pass that also writes the maxima.)  In dQ (lane = query) e
 // is fixed per query before the sweep, from the query's dO row: dO and
 // delta are scaled so that the row's largest |dO| lies in [2^-4, 2^-3),
 // which bounds |dS * 2^e| by 2^-2 D max|V| and needs no per-tile checks.
@@ -73,6 +86,9 @@ namespace fa {
 template <int D>
 constexpr int kDkdvSwizzle = D >= 128 ? SW_PD : (D == 64 ? SW_AT : SW_P8);
 
+// 32-row groups of S rows (the row-group maxima's second-to-last extent)
+__host__ __device__ __forceinline__ int row_groups(int S) { return (S + 31) >> 5; }
+
 struct BwdArgs {
   TensorDesc q, k, v, dout;   // q, dout: (B, Sq, H, D); k, v: (B, Sk, Hk, D)
   const float *lse;     // (B, H, Sq) natural log
@@ -81,6 +97,13 @@ struct BwdArgs {
   // and dO and written here (the pre-pass folded into the dQ kernel)
   float *delta_out;
   TensorDesc o;         // (B, Sq, H, D), read when delta_out is set
+  // Row-group maxima: for every 32-query-row group of each (b, h), the
+  // largest max_d |dO| and the largest |delta| over its rows, (B, H,
+  // row_groups(Sq), 2) fp32.  The dK/dV blocks read them (rmax: the bound
+  // that fixes their dS scale per query tile); the dQ kernel writes them
+  // beside delta_out when rmax_out is set.
+  const float *rmax;
+  float *rmax_out;
   f16 *dq, *dk, *dv;    // dq: (B, Sq, H, D); dk, dv: (B, Sk, Hk, D)
   int64_t dq_sb, dq_ss, dq_sh;
   int64_t dk_sb, dk_ss, dk_sh;
@@ -90,6 +113,10 @@ struct BwdArgs {
   int off;              // causal: query i sees keys j <= i + off (off = Sk - Sq)
   int n_blocks;         // query blocks (dQ) or key blocks (dK/dV)
   float c;              // |sm_scale| * log2(e), clamped away from 0
+  // dK/dV blocks: the LSE seed factor -log2(e) / cr, cr = c / ck (ck =
+  // min(c, 1) for fp16, 1 for bf16), from the host: a uniform value that
+  // a VGPR would hold for the whole sweep
+  float lse_mul;
   float sm_scale;       // signed scale applied to dQ and dK
   int neg;              // 1 when sm_scale < 0 (K or Q negated in S recompute)
   int zigzag;           // causal block order: 1 zigzag heavy / light, 0 heaviest first
@@ -120,6 +147,7 @@ struct BwdArgs {
 struct PreArgs {
   TensorDesc o, dout;
   float *delta;
+  float *rmax;   // row-group maxima (BwdArgs::rmax), (B, H, G, 2); NULL: not written
   int B, S, H;
   // when non-NULL, workgroup 0 zeroes cnt_zero[0 .. n_cnt_zero) (the
   // key-block split counters of the fused backward launch that follows)
@@ -128,29 +156,32 @@ struct PreArgs {
 };
 
 // ---------------------------------------------------------------------------
-// delta[b,h,s] = sum_d O * dO.  Two lanes per row, rows in (b, h, s) order
-// (delta writes contiguous).  Lane g of a pair sums its half of the row in
-// the dQ kernel's fragment order -- chunks 16c + 8g .. +7, c ascending, one
-// fp32 FMA per element -- then the pair adds its two sums: the same fp32
-// operations, in the same order, as the dQ kernel's own delta (BwdArgs::
-// delta_out), so every backward path sees bit-identical delta.  (dP - delta
-// cancels exactly in exact arithmetic for a query with one visible key; in
-// fp32 it leaves a few ulps of delta in dS, and which few depends on this
-// order.)
+// delta[b,h,s] = sum_d O * dO.  Two lanes per row; a workgroup covers 128
+// rows of one (b, h), a wave 32 of them (delta writes contiguous).  Lane g
+// of a pair sums its half of the row in the dQ kernel's fragment order --
+// chunks 16c + 8g .. +7, c ascending, one fp32 FMA per element -- then the
+// pair adds its two sums: the same fp32 operations, in the same order, as
+// the dQ kernel's own delta (BwdArgs::delta_out), so every backward path
+// sees bit-identical delta.  (dP - delta cancels exactly in exact
+// arithmetic for a query with one visible key; in fp32 it leaves a few
+// ulps of delta in dS, and which few depends on this order.)  With rmax
+// set, each wave also writes its 32 rows' group maxima (max |dO|, max
+// |delta|: BwdArgs::rmax), which maxima alone make exact whatever the order.
 template <typename E, int D>
 __global__ __launch_bounds__(256) void fa_bwd_preprocess_kernel(PreArgs a) {
-  constexpr int RPB = 128;   // rows per block
+  constexpr int RPB = 128;   // rows per block, all of one (b, h)
   const int tid = threadIdx.x;
   if (a.cnt_zero != nullptr && blockIdx.x == 0) {
     for (int i = tid; i < a.n_cnt_zero; i += 256) a.cnt_zero[i] = 0u;
   }
-  const int64_t row = (int64_t)blockIdx.x * RPB + (tid >> 1);
+  const int nchunk = (a.S + RPB - 1) / RPB;
+  const int64_t bh = blockIdx.x / nchunk;
+  const int s0 = (int)(blockIdx.x % nchunk) * RPB;
+  const int s = s0 + (tid >> 1);
   const int g = tid & 1;
-  const int64_t total = (int64_t)a.B * a.H * a.S;
-  float acc = 0.0f;
-  if (row < total) {
-    const int s = (int)(row % a.S);
-    const int64_t bh = row / a.S;
+  const bool valid = s < a.S;
+  float acc = 0.0f, om = 0.0f;
+  if (valid) {
     const int h = (int)(bh % a.H), b = (int)(bh / a.H);
     const f16 *po = a.o.head(b, h) + (int64_t)s * a.o.ss + 8 * g;
     const f16 *pg = a.dout.head(b, h) + (int64_t)s * a.dout.ss + 8 * g;
@@ -163,44 +194,59 @@ __global__ __launch_bounds__(256) void fa_bwd_preprocess_kernel(PreArgs a) {
 #pragma unroll
     for (int c = 0; c < D / 16; ++c)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc = __builtin_fmaf((float)ov[c][j], (float)gv[c][j], acc);
+      for (int j = 0; j < 8; ++j) {
+        acc = __builtin_fmaf((float)ov[c][j], (float)gv[c][j], acc);
+        om = fmaxf(om, fabsf((float)gv[c][j]));
+      }
   }
-  acc += __shfl_xor(acc, 1, 64);
-  if (row < total && g == 0) a.delta[row] = acc;
+  acc += xor1(acc);   // the row's other half
+  if (valid && g == 0) a.delta[bh * a.S + s] = acc;
+  if (a.rmax != nullptr) {
+    // the wave's 32 rows (64 lanes, rows past S contribute 0), maxima in
+    // lane 63
+    const unsigned dm = max_wave_nonneg(om);
+    const unsigned am = max_wave_nonneg(valid ? fabsf(acc) : 0.0f);
+    const int sw = s0 + 32 * (tid >> 6);   // the wave's first row
+    if ((tid & 63) == 63 && sw < a.S) {
+      float *p = a.rmax + (bh * row_groups(a.S) + sw / 32) * 2;
+      p[0] = __uint_as_float(dm);
+      p[1] = __uint_as_float(am);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
-// Running power-of-two scale of one dK lane's dS column (see the header).
+// Power-of-two scale of one dK lane's dS column (see the header), settled
+// per query tile from a bound on the lane's |dS| over that tile.
 struct DsScale {
-  int e = 0;
-  float mul = 1.0f;   // 2^e
+  float mul = 1.0f;   // 2^e, |e| <= 100 (a normal float)
 
-  // `m` = largest unscaled |dS| of the current block over this lane and its
-  // lane^32 partner (same output row).  Returns the factor by which the
-  // lane's accumulator must be multiplied (1 when e is unchanged).
-  // Straight-line selects (no per-lane branch, so no exec-mask juggling in
-  // the loop that calls it).
-  __device__ __forceinline__ float update(float m) {
-    const float sm = m * mul;
-    // bitwise, not short-circuit: && / || would become branches again
-    const bool need = (m > 0.0f) & ((sm > 32768.0f) | (sm < 1024.0f));
-    // m = f * 2^x, f in [0.5, 1): new e puts m * 2^e in [2^13, 2^14)
-    int en = 14 - __builtin_amdgcn_frexp_expf(m);
+  // e, from mul alone (one register per lane for the state)
+  __device__ __forceinline__ int exp() const { return __builtin_amdgcn_frexp_expf(mul) - 1; }
+
+  // Whether settle(bnd) would change the scale: bnd > 0 and bnd * 2^e
+  // outside [2^8, 2^15].  When it is false in every lane, settle() would
+  // return 1 everywhere and leave the state as it is.
+  __device__ __forceinline__ bool stale(float bnd) const {
+    const float sb = bnd * mul;
+    // bitwise, not short-circuit: && / || would become branches
+    return (bnd > 0.0f) & ((sb > 32768.0f) | (sb < 256.0f));
+  }
+  // New scale for a tile whose dS obey |dS| <= bnd: when stale, e := 15 -
+  // exponent(bnd), so bnd * 2^e lies in [2^14, 2^15) (bnd = f * 2^x, f in
+  // [0.5, 1)) and no scaled dS can pass fp16's 65504.  Returns the factor
+  // by which the lane's accumulator must be multiplied (1 when e is
+  // unchanged).  Straight-line selects, no per-lane branch.
+  __device__ __forceinline__ float settle(float bnd) {
+    const int e = exp();
+    int en = 15 - __builtin_amdgcn_frexp_expf(bnd);
     en = en > 100 ? 100 : (en < -100 ? -100 : en);
-    en = need ? en : e;
+    en = stale(bnd) ? en : e;
     const float f = __builtin_amdgcn_ldexpf(1.0f, en - e);
-    e = en;
     mul = __builtin_amdgcn_ldexpf(1.0f, en);
     return f;
   }
 };
-
-__device__ __forceinline__ float absmax16(const floatx16 &x) {
-  float m = fabsf(x[0]);
-#pragma unroll
-  for (int i = 1; i < 16; ++i) m = fmaxf(m, fabsf(x[i]));
-  return m;
-}
 
 // Store a D^T x 32 accumulator set (lane = row `row`, slots = columns) as
 // row `row` of a (.., D) tensor of element type E, scaled by `mul`.
@@ -281,7 +327,7 @@ __device__ __forceinline__ void load_row_frags(vec8<E> (&f)[D / 16], const f16 *
 template <int D>
 __device__ __forceinline__ void merge_pair(float *buf, bool writer, floatx16 (&acc)[D / 32],
                                            const DsScale &sc, int lane) {
-  const float inv = __builtin_amdgcn_ldexpf(1.0f, -sc.e);
+  const float inv = __builtin_amdgcn_ldexpf(1.0f, -sc.exp());
   if (writer) {
 #pragma unroll
     for (int d = 0; d < D / 32; ++d)
@@ -453,8 +499,8 @@ struct DkdvTile {
 #define FA_DKDV_LDS(T)                                                                 \
   __shared__ __attribute__((aligned(16))) f16 s_q0[T::LDS_TILE], s_q1[T::LDS_TILE];   \
   __shared__ __attribute__((aligned(16))) f16 s_do0[T::LDS_TILE], s_do1[T::LDS_TILE]; \
-  __shared__ __attribute__((aligned(16))) float s_lse[2][T::BQ];                      \
-  __shared__ __attribute__((aligned(16))) float s_dl[2][T::BQ];                       \
+  __shared__ __attribute__((aligned(16))) float s_lse[2][T::BQ];                     \
+  __shared__ __attribute__((aligned(16))) float s_dl[2][T::BQ];                      \
   __shared__ __attribute__((aligned(16))) f16 s_k[T::LDS_KV], s_v[T::LDS_KV]
 
 // One dK/dV block (workgroup `bid` of the dK/dV grid).
@@ -600,7 +646,7 @@ __device__ __forceinline__ void dkdv_block(const BwdArgs &a, const int bid, f16 
   DmaStager<D, QSW, BQ, T::NW> stq, stg;
   stq.init(w, lane, a.q.ss);
   stg.init(w, lane, a.dout.ss);
-  const float lse_mul = -kLog2e / cr;
+  const float lse_mul = a.lse_mul;
   float lse_r = 0.0f, dl_r = 0.0f;   // raw LSE / delta of row m0 + tid
   // Q and dO go straight to LDS stage `st`; LSE / delta through VGPRs.
   // (cur_h, cur_m0) is tile t's query head and first row; advance()
@@ -624,6 +670,15 @@ __device__ __forceinline__ void dkdv_block(const BwdArgs &a, const int bid, f16 
     cg.init(a.dout.head(b, h), a.dout.ss, m0, Sq, D, BQ);
   };
   aim(cur_h, cur_m0);
+  // The tile's row-group maxima (BwdArgs::rmax: max |dO| and max |delta|
+  // of each 32 rows), for the bound |dS| <= P (|dO . V_k| + |delta|) <=
+  // max|dO| ||V_k||_1 + max|delta| (P <= 1) that settles each lane's dS
+  // scale before the tile's MFMAs: uniform loads through the scalar cache
+  // (constant address space; no launch writes the maxima while this one
+  // reads them), issued with the tile's other loads and held in SGPRs, so
+  // that the settle at the tile's start waits on nothing.
+  typedef const __attribute__((address_space(4))) float kfloat;
+  float nx_rm[2 * (BQ / 32)];
   auto load_tile = [&](int h, int m0, auto stc) {
     stq.load(q_st(stc), cq.rsrc(), w);
     stg.load(do_st(stc), cg.rsrc(), w);
@@ -633,6 +688,15 @@ __device__ __forceinline__ void dkdv_block(const BwdArgs &a, const int bid, f16 
       // rows past Sq: +inf LSE, so the seed below is -inf and P = 0
       lse_r = (m < Sq) ? a.lse[row] : kPosInf;
       dl_r = (m < Sq) ? a.delta[row] : 0.0f;
+    }
+    const int ng = row_groups(Sq);
+    kfloat *rm = (kfloat *)(a.rmax + (((int64_t)b * a.H + h) * ng + m0 / 32) * 2);
+#pragma unroll
+    for (int i = 0; i < BQ / 32; ++i) {
+      // groups past Sq (a ragged last tile) bound nothing
+      const bool in = m0 / 32 + i < ng;
+      nx_rm[2 * i] = in ? rm[2 * i] : 0.0f;
+      nx_rm[2 * i + 1] = in ? rm[2 * i + 1] : 0.0f;
     }
   };
   // Publishing a stage: its LSE / delta rows go to LDS, then every DMA of
@@ -691,6 +755,42 @@ __device__ __forceinline__ void dkdv_block(const BwdArgs &a, const int bid, f16 
   }
   if (n_tiles > 0) store_tile(std::integral_constant<int, 0>{});
   __syncthreads();
+
+  // ||V_k||_1 of this lane's key (its half row and lane ^ 32's; fp32)
+  float nv = 0.0f;
+#pragma unroll
+  for (int cc = 0; cc < D / 16; ++cc) {
+    const vec8<E> x = v_frag(cc);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) nv += fabsf((float)x[j]);
+  }
+  nv += xor32(nv);
+  // A query tile's dS scale from the bound on its |dS| (the maxima loaded
+  // with the tile): settled (and the dK accumulators rescaled by the
+  // factor) only when some lane's scale must change -- a wave-uniform
+  // branch, rarely taken once the sweep has found its range.  The first
+  // tile's in the prologue, every later one's at the end of the tile
+  // before it, where the check issues under that tile's last MFMAs.
+  auto settle_scale = [&]() {
+    // (non-negative: unsigned maxima of the bit patterns, scalar ops)
+    unsigned mdo = __float_as_uint(nx_rm[0]), mdl = __float_as_uint(nx_rm[1]);
+#pragma unroll
+    for (int i = 1; i < BQ / 32; ++i) {
+      mdo = max(mdo, __float_as_uint(nx_rm[2 * i]));
+      mdl = max(mdl, __float_as_uint(nx_rm[2 * i + 1]));
+    }
+    const float bnd = __builtin_fmaf(__uint_as_float(mdo), nv, __uint_as_float(mdl));
+    if (__any(sc.stale(bnd))) {
+      const float f = sc.settle(bnd);
+      if (__any(f != 1.0f)) {
+#pragma unroll
+        for (int d = 0; d < D / 32; ++d)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) dk[d][i] *= f;
+      }
+    }
+  };
+  if (n_tiles > 0) settle_scale();   // the first tile's scale
 
   // One query tile; the LDS stage is a compile-time constant (the loop below
   // is unrolled by two) so every LDS address is a base plus an immediate.
@@ -776,17 +876,7 @@ __device__ __forceinline__ void dkdv_block(const BwdArgs &a, const int bid, f16 
         p[i] = fast_exp2(sacc[i]);
         ds[i] = p[i] * dpacc[i];
       }
-      // adaptive power-of-two scale of this key's dS column
-      const float mk = absmax16(ds);
-      {
-        const float f = sc.update(max_xor32(mk));
-        if (__any(f != 1.0f)) {
-#pragma unroll
-          for (int d = 0; d < D / 32; ++d)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) dk[d][i] *= f;
-        }
-      }
+      // dS in E at the tile's power-of-two scale
       vec8<E> pf[2], dsf[2];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
@@ -920,35 +1010,25 @@ __device__ __forceinline__ void dkdv_block(const BwdArgs &a, const int bid, f16 
         __builtin_amdgcn_sched_barrier(0);
       });
       // dV^T += dO^T P, with dS = P dP (into p: P is needed as E only from
-      // here on) and its max in NO - 1 slices
+      // here on) in NO - 1 slices, and the tile's dS bound under the first
       floatx16 &ds = p;
-      float mk = 0.0f;
+      float bnd = 0.0f;
       static_for<NO>([&](auto io) {
         constexpr int o = decltype(io)::value, i = 2 * NC + o;
         constexpr int hh = o / (D / 32), d = o % (D / 32);
         ahead(std::integral_constant<int, i>{});
         dv[d] = mfma32(opa[i % (PFD + 1)], pf[hh], dv[d]);
+
         if constexpr (o >= 1) {
           constexpr int i0 = (o - 1) * 16 / (NO - 1), i1 = o * 16 / (NO - 1);
           static_for<i1 - i0>([&](auto kc) {
             constexpr int e = i0 + decltype(kc)::value;
             ds[e] *= dpacc[e];
-            mk = fmaxf(mk, fabsf(ds[e]));
           });
         }
         __builtin_amdgcn_sched_barrier(0);
       });
-      // adaptive power-of-two scale of this key's dS column (as grad())
-      {
-        const float f = sc.update(max_xor32(mk));
-        if (__any(f != 1.0f)) {
-#pragma unroll
-          for (int d = 0; d < D / 32; ++d)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) dk[d][i] *= f;
-        }
-      }
-      // dK^T += Q^T dS: each query half's 8 conversions before its MFMAs
+      // dK^T += Q^T dS, dS in E at the tile's power-of-two scale: each query half's 8 conversions before its MFMAs
       vec8<E> dsf[2];
       static_for<2>([&](auto ih) {
         constexpr int hh = decltype(ih)::value;
@@ -977,7 +1057,10 @@ __device__ __forceinline__ void dkdv_block(const BwdArgs &a, const int bid, f16 
       }
     }
 
-    if (more) store_tile(std::integral_constant<int, st ^ 1>{});
+    if (more) {
+      settle_scale();   // tile t + 1's scale, under this tile's last MFMAs
+      store_tile(std::integral_constant<int, st ^ 1>{});
+    }
     cur_h = nxt_h;
     cur_m0 = nxt_m0;
     __syncthreads();
@@ -1184,6 +1267,18 @@ __device__ __forceinline__ void dq_block(const BwdArgs &a, const int bid, f16 *s
 #pragma unroll
     for (int j = 0; j < 8; ++j) gm = fmaxf(gm, fabsf((float)gf[c][j]));
   gm = max_xor32(gm);   // the row's other half is in lane ^ 32
+  if (a.rmax_out != nullptr && kh == 0 && seg == 0) {
+    // the wave's 32 rows' group maxima, beside delta (BwdArgs::rmax); the
+    // two lane halves hold the same rows (the low half's maxima end in
+    // lane 31), rows past Sq contribute 0
+    const unsigned dm = max_halves_nonneg(qrow < Sq ? gm : 0.0f);
+    const unsigned am = max_halves_nonneg(fabsf(dl));
+    if (lane == 31 && wq0 < Sq) {
+      float *p = a.rmax_out + ((int64_t)bh * row_groups(a.Sq) + wq0 / 32) * 2;
+      p[0] = __uint_as_float(dm);
+      p[1] = __uint_as_float(am);
+    }
+  }
   int ge = 0;
   if (gm > 0.0f && gm < kPosInf) {
     ge = -3 - __builtin_amdgcn_frexp_expf(gm);

@@ -84,8 +84,18 @@ __device__ __forceinline__ float fast_log2(float x) {
 }
 
 // Value held by lane (lane ^ 32): the other half-wave owns the same query.
+// v_permlane32_swap (below) leaves each lane {own, partner}; their bitwise
+// xor with own is the partner, whichever order they come in (no LDS
+// round trip).
 __device__ __forceinline__ float xor32(float x) {
-  return __shfl_xor(x, 32, 64);
+  const unsigned u = __float_as_uint(x);
+  auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(r[0] ^ r[1] ^ u);
+}
+
+// Value held by lane (lane ^ 1) (DPP quad_perm [1, 0, 3, 2]).
+__device__ __forceinline__ float xor1(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xF, 0xF, false));
 }
 
 // max(x, value of lane ^ 32) without an LDS round trip.  v_permlane32_swap
@@ -95,6 +105,35 @@ __device__ __forceinline__ float xor32(float x) {
 __device__ __forceinline__ float max_xor32(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(x, fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])));
+}
+
+// Cross-lane maxima of non-negative floats, compared as unsigned bit
+// patterns (they order non-negative floats as the floats do: one v_max_u32
+// per step, no NaN canonicalisation), through DPP row operations instead
+// of LDS-crossbar permutes.  One step: max with the lane DPP control CTRL
+// names, in the rows of ROWS (other rows keep their value).
+template <int CTRL, int ROWS>
+__device__ __forceinline__ unsigned dpp_umax(unsigned m) {
+  return max(m, (unsigned)__builtin_amdgcn_update_dpp((int)m, (int)m, CTRL, ROWS, 0xF, false));
+}
+
+// Maximum of x >= 0 over each 32-lane half of the wave, in the half's last
+// lane (31, 63): within quads (lane ^ 1, lane ^ 2), 8-lane groups
+// (row_half_mirror), 16-lane rows (row_mirror), then row 0's into row 1
+// and row 2's into row 3 (row_bcast:15).
+__device__ __forceinline__ unsigned max_halves_nonneg(float x) {
+  unsigned m = __float_as_uint(x);
+  m = dpp_umax<0xB1, 0xF>(m);    // quad_perm [1, 0, 3, 2]
+  m = dpp_umax<0x4E, 0xF>(m);    // quad_perm [2, 3, 0, 1]
+  m = dpp_umax<0x141, 0xF>(m);   // row_half_mirror
+  m = dpp_umax<0x140, 0xF>(m);   // row_mirror
+  return dpp_umax<0x142, 0xA>(m);   // row_bcast:15
+}
+
+// Maximum of x >= 0 over the wave, in lane 63 (row_bcast:31 brings lane
+// 31's half maximum into rows 2 and 3).
+__device__ __forceinline__ unsigned max_wave_nonneg(float x) {
+  return dpp_umax<0x143, 0xC>(max_halves_nonneg(x));
 }
 
 // Sum of the two 16-bit values of `p` accumulated into fp32 `acc`

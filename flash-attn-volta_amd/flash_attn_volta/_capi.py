@@ -14,7 +14,7 @@ import threading
 LIB_NAME = "libfa_mi355x.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # status codes (enum fa_status)
 FA_OK = 0
@@ -49,6 +49,7 @@ EXPORTED_SYMBOLS = (
     "fa_fwd_ws",
     "fa_fwd_workspace_bytes",
     "fa_bwd_preprocess",
+    "fa_bwd_rowmax_bytes",
     "fa_bwd_workspace_bytes",
     "fa_bwd_gqa_workspace_bytes",
     "fa_bwd",
@@ -110,7 +111,9 @@ def _declare(lib):
     lib.fa_fwd_workspace_bytes.restype = ctypes.c_size_t
     lib.fa_fwd_workspace_bytes.argtypes = [_ci, _ci, _ci, _ci, _ci, _ci, _ci]
     lib.fa_bwd_preprocess.restype = _ci
-    lib.fa_bwd_preprocess.argtypes = [_vp, _vp, _vp, _ci, _ci, _ci, _ci, _i64x4, _i64x4, _vp]
+    lib.fa_bwd_preprocess.argtypes = [_vp, _vp, _vp, _vp, _ci, _ci, _ci, _ci, _i64x4, _i64x4, _vp]
+    lib.fa_bwd_rowmax_bytes.restype = ctypes.c_size_t
+    lib.fa_bwd_rowmax_bytes.argtypes = [_ci, _ci, _ci]
     lib.fa_bwd_workspace_bytes.restype = ctypes.c_size_t
     lib.fa_bwd_workspace_bytes.argtypes = [_ci, _ci, _ci, _ci]
     lib.fa_bwd_gqa_workspace_bytes.restype = ctypes.c_size_t
@@ -139,7 +142,7 @@ def _declare(lib):
                                        _i64x4, _i64x4, _i64x4, _i64x4,
                                        ctypes.c_float, _ci, _ci, _vp]
     lib.fa_bwd_dkdv.restype = _ci
-    lib.fa_bwd_dkdv.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+    lib.fa_bwd_dkdv.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                 _ci, _ci, _ci, _ci,
                                 _i64x4, _i64x4, _i64x4, _i64x4, _i64x4, _i64x4,
                                 ctypes.c_float, _ci, _vp]
@@ -149,7 +152,7 @@ def _declare(lib):
                               _i64x4, _i64x4, _i64x4, _i64x4, _i64x4,
                               ctypes.c_float, _ci, _vp]
     lib.fa_bwd_blocks.restype = _ci
-    lib.fa_bwd_blocks.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+    lib.fa_bwd_blocks.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                   _ci, _ci, _ci, _ci,
                                   _i64x4, _i64x4, _i64x4, _i64x4, _i64x4, _i64x4, _i64x4,
                                   ctypes.c_float, _ci, _vp]

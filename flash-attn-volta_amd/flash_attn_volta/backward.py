@@ -276,7 +276,7 @@ def bwd_preprocess(o: torch.Tensor, do: torch.Tensor) -> torch.Tensor:
     o, do = _kernel_ready(o), _kernel_ready(do)
     delta = torch.empty((B, H, N), dtype=torch.float32, device=o.device)
     with _on_device(o.device):
-        rc = lib.fa_bwd_preprocess(o.data_ptr(), do.data_ptr(), delta.data_ptr(), B, N, H, D,
-                                   kernel_strides(o), kernel_strides(do), _stream_ptr(o.device))
+        rc = lib.fa_bwd_preprocess(o.data_ptr(), do.data_ptr(), delta.data_ptr(), None, B, N, H,
+                                   D, kernel_strides(o), kernel_strides(do), _stream_ptr(o.device))
     _capi.check(rc, "fa_bwd_preprocess")
     return delta

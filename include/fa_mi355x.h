@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define FA_ABI_VERSION 8
+#define FA_ABI_VERSION 9
 
 /* Size of the static device scratch buffer that fa_bwd_gqa_noalloc uses as
  * its workspace (one per GPU, held for the life of the process). */
@@ -181,13 +181,25 @@ size_t fa_fwd_workspace_bytes(int B, int Sq, int Sk, int H, int Hk, int D, int c
 /*
  * Backward pre-pass: delta[b,h,s] = sum_d o[b,s,h,d] * do[b,s,h,d] in fp32.
  * Replaces the torch expression at flash_attn_volta/triton_fa_bwd.py:649-650.
+ *
+ * With `rowmax` non-NULL it also writes the row-group maxima the dK/dV
+ * kernel reads (fa_bwd_dkdv, fa_bwd_blocks): for every group of 32 query
+ * rows of each (b, h), rowmax[b][h][g][0] = max over the group's rows and
+ * d of |do[b, s, h, d]| and rowmax[b][h][g][1] = max |delta[b, h, s]|,
+ * fp32, g < ceil(S / 32), fa_bwd_rowmax_bytes(B, S, H) bytes, 16-byte
+ * aligned.  (No reference counterpart: they bound |dS| so that the dK/dV
+ * kernel fixes its fp16 dS scale per query tile; see fa_bwd.)
  */
-int fa_bwd_preprocess(const void *o, const void *dout, float *delta,
+int fa_bwd_preprocess(const void *o, const void *dout, float *delta, float *rowmax,
                       int B, int S, int H, int D,
                       const int64_t o_strides[4], const int64_t do_strides[4],
                       void *stream);
 
-/* Bytes of device workspace fa_bwd needs for these sizes (0 on bad sizes). */
+/* Bytes of the row-group maxima of fa_bwd_preprocess (0 on bad sizes). */
+size_t fa_bwd_rowmax_bytes(int B, int S, int H);
+
+/* Bytes of device workspace fa_bwd needs for these sizes (0 on bad sizes):
+ * delta and the row-group maxima. */
 size_t fa_bwd_workspace_bytes(int B, int S, int H, int D);
 
 /*
@@ -199,7 +211,7 @@ size_t fa_bwd_workspace_bytes(int B, int S, int H, int D);
  * each, fp32 partials added by whichever finishes second) and, when the
  * dQ grid is at most half a round, for the query-block split of the dQ
  * kernel (its longest query blocks swept by two workgroups, fp32 halves
- * added by the dK/dV kernel); at most 80 MiB + 4 KiB in all.
+ * added by the dK/dV kernel): at most 80 MiB + 4 KiB more.
  * Any workspace of at least the minimum is valid: with less than this
  * size the backward runs unsplit.  Split and unsplit results differ in
  * rounding only; each is bit-reproducible.
@@ -212,12 +224,17 @@ size_t fa_bwd_gqa_workspace_bytes(int B, int Sq, int Sk, int H, int Hk, int D, i
 /*
  * Backward attention: (dq, dk, dv) of L = <o, dout> with o = fa_fwd(q,k,v),
  * given the forward's `lse`. Two launches. Causal with D = 32 or 64:
- * fa_bwd_preprocess's kernel (delta = rowsum(o * dout) into the
- * workspace), then one launch running every dK/dV workgroup (one per key
- * block, or two for the longest blocks when the workspace has room:
- * fa_bwd_gqa_workspace_bytes) and then every dQ workgroup (one per query
- * block). Otherwise: the dQ kernel, which also computes delta into the
- * workspace, then the dK/dV kernel. No floating-point atomics: results
+ * fa_bwd_preprocess's kernel (delta = rowsum(o * dout) and the row-group
+ * maxima into the workspace), then one launch running every dK/dV
+ * workgroup (one per key block, or two for the longest blocks when the
+ * workspace has room: fa_bwd_gqa_workspace_bytes) and then every dQ
+ * workgroup (one per query block). Otherwise: the dQ kernel, which also
+ * computes delta and the maxima into the workspace, then the dK/dV kernel.
+ * dS is rounded to fp16 for the MFMAs at a power-of-two scale per key,
+ * settled per 32- to 128-query tile from the bound |dS| <= max|do| *
+ * ||v_key||_1 + max|delta| over the tile's rows (so no scaled dS can
+ * overflow fp16, and tiny upstream gradients keep fp16 precision), and
+ * unscaled in fp32 at the end. No floating-point atomics: results
  * are bit-reproducible and, with the fa_bwd_workspace_bytes workspace (no
  * split), bit-identical to the three separate calls fa_bwd_preprocess,
  * fa_bwd_dq, fa_bwd_dkdv.
@@ -297,7 +314,8 @@ int fa_bwd_gqa_noalloc(const void *dout, const void *q, const void *k, const voi
  * The two main backward kernels as separate steps (fa_bwd runs the dQ
  * kernel, computing delta on the way, then the dK/dV kernel; called
  * separately they take delta from fa_bwd_preprocess).  `delta` is the
- * fa_bwd_preprocess output, (B, H, S) fp32 contiguous.
+ * fa_bwd_preprocess output, (B, H, S) fp32 contiguous, and fa_bwd_dkdv's
+ * `rowmax` (not NULL) its row-group maxima for the same o and dout.
  *
  * fa_bwd_dkdv replaces the launch of _fa_bwd_dkdv_kernel_{d64,d128}
  * (flash_attn_volta/triton_fa_bwd.py:682-695): dK, dV per key block.
@@ -305,7 +323,7 @@ int fa_bwd_gqa_noalloc(const void *dout, const void *q, const void *k, const voi
  * (triton_fa_bwd.py:667-679): dQ per query block.
  */
 int fa_bwd_dkdv(const void *dout, const void *q, const void *k, const void *v,
-                const float *lse, const float *delta, void *dk, void *dv,
+                const float *lse, const float *delta, const float *rowmax, void *dk, void *dv,
                 int B, int S, int H, int D,
                 const int64_t do_strides[4], const int64_t q_strides[4],
                 const int64_t k_strides[4], const int64_t v_strides[4],
@@ -321,8 +339,9 @@ int fa_bwd_dq(const void *dout, const void *q, const void *k, const void *v,
               float sm_scale, int causal, void *stream);
 
 /*
- * Both gradient launches of fa_bwd given delta (the fa_bwd_preprocess
- * output), i.e. fa_bwd without its delta step and without a workspace (so
+ * Both gradient launches of fa_bwd given delta and the row-group maxima
+ * (the fa_bwd_preprocess outputs, `rowmax` not NULL), i.e. fa_bwd without
+ * its delta step and without a workspace (so
  * without the key-block split): for causal D = 32 / 64 the one fused
  * launch of every dK/dV and every dQ workgroup, otherwise fa_bwd_dq then
  * fa_bwd_dkdv.  Bit-identical to fa_bwd with the fa_bwd_workspace_bytes
@@ -333,8 +352,8 @@ int fa_bwd_dq(const void *dout, const void *q, const void *k, const void *v,
  * from the torch op before them (flash_attn_volta/triton_fa_bwd.py:667-695).
  */
 int fa_bwd_blocks(const void *dout, const void *q, const void *k, const void *v,
-                  const float *lse, const float *delta, void *dq, void *dk, void *dv,
-                  int B, int S, int H, int D,
+                  const float *lse, const float *delta, const float *rowmax, void *dq,
+                  void *dk, void *dv, int B, int S, int H, int D,
                   const int64_t do_strides[4], const int64_t q_strides[4],
                   const int64_t k_strides[4], const int64_t v_strides[4],
                   const int64_t dq_strides[4], const int64_t dk_strides[4],

@@ -324,24 +324,29 @@ def _bwd_three_launches(do, q, k, v, o, lse, causal, sm_scale):
     B, S, H, D = q.shape
     stream = torch.cuda.current_stream().cuda_stream
     delta = torch.empty((B, H, S), dtype=torch.float32, device="cuda")
+    rowmax = torch.empty(lib.fa_bwd_rowmax_bytes(B, S, H) // 4, dtype=torch.float32, device="cuda")
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     st = {n: kernel_strides(t) for n, t in dict(do=do, q=q, k=k, v=v, o=o, dq=dq, dk=dk,
                                                    dv=dv).items()}
-    _capi.check(lib.fa_bwd_preprocess(o.data_ptr(), do.data_ptr(), delta.data_ptr(), B, S, H, D,
-                                      st["o"], st["do"], stream), "fa_bwd_preprocess")
+    _capi.check(lib.fa_bwd_preprocess(o.data_ptr(), do.data_ptr(), delta.data_ptr(),
+                                      rowmax.data_ptr(), B, S, H, D, st["o"], st["do"], stream),
+                "fa_bwd_preprocess")
     _capi.check(lib.fa_bwd_dq(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
                               lse.data_ptr(), delta.data_ptr(), dq.data_ptr(), B, S, H, D,
                               st["do"], st["q"], st["k"], st["v"], st["dq"], sm_scale,
                               int(causal), stream), "fa_bwd_dq")
     _capi.check(lib.fa_bwd_dkdv(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                lse.data_ptr(), delta.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                lse.data_ptr(), delta.data_ptr(), rowmax.data_ptr(),
+                                dk.data_ptr(), dv.data_ptr(),
                                 B, S, H, D, st["do"], st["q"], st["k"], st["v"], st["dk"],
                                 st["dv"], sm_scale, int(causal), stream), "fa_bwd_dkdv")
     torch.cuda.synchronize()
     # fa_bwd_blocks: both gradient launches of fa_bwd, given the same delta
+    # and row-group maxima
     bq, bk, bv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     _capi.check(lib.fa_bwd_blocks(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                  lse.data_ptr(), delta.data_ptr(), bq.data_ptr(), bk.data_ptr(),
+                                  lse.data_ptr(), delta.data_ptr(), rowmax.data_ptr(),
+                                  bq.data_ptr(), bk.data_ptr(),
                                   bv.data_ptr(), B, S, H, D, st["do"], st["q"], st["k"], st["v"],
                                   st["dq"], st["dk"], st["dv"], sm_scale, int(causal), stream),
                 "fa_bwd_blocks")
@@ -374,6 +379,73 @@ def test_backward_fused_launch_matches_three_launches(B, S, H, D, sm_scale, in_s
     fused = flash_attn_backward(do, q, k, v, o, lse, causal=True, sm_scale=sc)
     three, blocks = _bwd_three_launches(do, q, k, v, o, lse, True, sc)
     for name, a, b, c in zip(("dq", "dk", "dv"), fused, three, blocks):
+        assert torch.isfinite(a.float()).all(), name
+        assert torch.equal(a, b), f"{name} differs (max-abs {max_abs(a, b.float()):.3e})"
+        assert torch.equal(a, c), f"fa_bwd_blocks {name} differs"
+
+
+# fa_bwd's dK/dV blocks read row-group maxima -- max |dO| and max |delta|
+# over every 32 query rows of each (b, h), which bound |dS| and so fix each
+# query tile's dS scale -- written by the dQ kernel on the unfused shapes
+# (the pre-pass folded into it) and by the pre-pass on the fused causal
+# D <= 64 ones.  Both must equal the maxima of dO and of the delta the
+# same call wrote (bitwise: a max is exact; groups past S hold nothing),
+# fa_bwd_preprocess must write the same delta and maxima, and the three
+# separate launches, which read the pre-pass's maxima, must reproduce
+# fa_bwd bit for bit.  dO rows span 2^-6 .. 2^2, so a group boundary off
+# by a row changes a maximum.
+@pytest.mark.parametrize("B,S,H,D,causal", [
+    (1, 1000, 4, 128, True),    # unfused causal, ragged last group
+    (2, 777, 3, 64, False),     # unfused non-causal
+    (1, 1024, 8, 128, False),
+    (2, 300, 2, 32, False),
+    (2, 1000, 8, 64, True),     # fused: the pre-pass writes them
+])
+def test_backward_row_maxima(B, S, H, D, causal):
+    from flash_attn_volta import _capi, flash_attn_forward
+    from flash_attn_volta.forward import kernel_strides
+    print(f"[case] bwd row maxima B={B} S={S} H={H} D={D} causal={causal}", flush=True)
+    lib = _capi.load()
+    q, k, v, do = (t.cuda() for t in orc.make_inputs(B, S, H, D, seed=31))
+    g = torch.Generator("cpu").manual_seed(32)
+    e = torch.randint(-6, 3, (1, S, 1, 1), generator=g).float().cuda()
+    do = (do.float() * torch.exp2(e)).half()
+    sc = default_scale(D, None)
+    o, lse = flash_attn_forward(q, k, v, causal=causal, sm_scale=sc, return_softmax_lse=True)
+    G = (S + 31) // 32
+    r_bytes = lib.fa_bwd_rowmax_bytes(B, S, H)
+    ws_bytes = lib.fa_bwd_workspace_bytes(B, S, H, D)
+    d_bytes = ws_bytes - r_bytes
+    assert r_bytes >= B * H * G * 8 and d_bytes >= B * H * S * 4
+    ws = torch.full((ws_bytes,), 0xFF, dtype=torch.uint8, device="cuda")
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    st = tuple(kernel_strides(t) for t in (do, q, k, v, o, dq, dk, dv))
+    stream = torch.cuda.current_stream().cuda_stream
+    _capi.check(lib.fa_bwd(do.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                           lse.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                           ws.data_ptr(), ws_bytes, B, S, H, D, *st, sc, int(causal), stream),
+                "fa_bwd")
+    torch.cuda.synchronize()
+    delta = ws[:d_bytes].view(torch.float32)[:B * H * S].view(B, H, S)
+    rmax = ws[d_bytes:].view(torch.float32)[:B * H * G * 2].view(B, H, G, 2)
+    pad = G * 32 - S
+    mdo = do.float().abs().amax(-1).permute(0, 2, 1)                # (B, H, S)
+    mdo = torch.nn.functional.pad(mdo, (0, pad)).view(B, H, G, 32).amax(-1)
+    mdl = torch.nn.functional.pad(delta.abs(), (0, pad)).view(B, H, G, 32).amax(-1)
+    assert torch.equal(rmax[..., 0], mdo), "max |dO| per group"
+    assert torch.equal(rmax[..., 1], mdl), "max |delta| per group"
+    ref_delta = (o.double() * do.double()).sum(-1).permute(0, 2, 1)
+    assert max_abs(delta, ref_delta) < 1e-3
+    # the pre-pass's delta and maxima, and the three launches
+    d2 = torch.empty((B, H, S), dtype=torch.float32, device="cuda")
+    r2 = torch.full((r_bytes // 4,), float("nan"), dtype=torch.float32, device="cuda")
+    _capi.check(lib.fa_bwd_preprocess(o.data_ptr(), do.data_ptr(), d2.data_ptr(), r2.data_ptr(),
+                                      B, S, H, D, st[4], st[0], stream), "fa_bwd_preprocess")
+    torch.cuda.synchronize()
+    assert torch.equal(d2, delta)
+    assert torch.equal(r2[:B * H * G * 2].view(B, H, G, 2), rmax)
+    three, blocks = _bwd_three_launches(do, q, k, v, o, lse, causal, sc)
+    for name, a, b, c in zip(("dq", "dk", "dv"), (dq, dk, dv), three, blocks):
         assert torch.isfinite(a.float()).all(), name
         assert torch.equal(a, b), f"{name} differs (max-abs {max_abs(a, b.float()):.3e})"
         assert torch.equal(a, c), f"fa_bwd_blocks {name} differs"

@@ -46,7 +46,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.fa_abi_version() == _capi.ABI_VERSION == 8
+    assert lib.fa_abi_version() == _capi.ABI_VERSION == 9
 
 
 def test_noalloc_scratch_size_matches_header():
@@ -95,14 +95,21 @@ def _bwd(lib, ws=P, ws_bytes=None, lse=P, B=1, S=128, H=2, D=64, scale=0.125, dq
 
 
 def test_workspace_bytes(lib):
-    assert lib.fa_bwd_workspace_bytes(1, 4096, 16, 64) == 4 * 4096 * 16
-    assert lib.fa_bwd_workspace_bytes(1, 3, 1, 64) == 256          # rounded to 256 B
+    # delta (4 B per row), then the row-group maxima (2 fp32 per 32 rows),
+    # each rounded up to 256 B
+    assert lib.fa_bwd_workspace_bytes(1, 4096, 16, 64) == 4 * 4096 * 16 + 8 * 128 * 16
+    assert lib.fa_bwd_rowmax_bytes(1, 4096, 16) == 8 * 128 * 16
+    assert lib.fa_bwd_rowmax_bytes(2, 100, 3) == 256               # 2 x 3 x 4 groups x 8 B -> 256
+    assert lib.fa_bwd_rowmax_bytes(1, 33, 40) == 768               # 40 x 2 groups x 8 B = 640 -> 768
+    assert lib.fa_bwd_rowmax_bytes(0, 33, 40) == 0
+    assert lib.fa_bwd_workspace_bytes(1, 3, 1, 64) == 512          # 256 + 256
     assert lib.fa_bwd_workspace_bytes(1, 3, 1, 48) == 0            # bad D
     assert lib.fa_bwd_workspace_bytes(0, 3, 1, 64) == 0            # bad B
 
 
 def test_split_workspace_bytes(lib):
-    """fa_bwd_gqa_workspace_bytes: the delta minimum, plus room for the
+    """fa_bwd_gqa_workspace_bytes: the minimum (delta and the row-group
+    maxima), plus room for the
     causal key-block (dK/dV) and query-block (dQ) splits only for D = 64 /
     128 causal grids of at most one
     round of resident workgroups (one per CU at D = 128, three at D = 64;
@@ -159,10 +166,27 @@ def test_bwd_validation(lib):
 
 def test_preprocess_validation(lib):
     s = _st(1, 64, 1, 64)
-    assert lib.fa_bwd_preprocess(P, P, None, 1, 64, 1, 64, s, s, None) == _capi.FA_ERR_NULL_POINTER
-    assert lib.fa_bwd_preprocess(P, P, BAD, 1, 64, 1, 64, s, s, None) == _capi.FA_ERR_ALIGNMENT
-    assert lib.fa_bwd_preprocess(P, None, P, 1, 64, 1, 64, s, s, None) == _capi.FA_ERR_NULL_POINTER
-    assert lib.fa_bwd_preprocess(P, P, P, 1, 64, 1, 40, s, s, None) == _capi.FA_ERR_HEAD_DIM
+    pre = lib.fa_bwd_preprocess
+    assert pre(P, P, None, P, 1, 64, 1, 64, s, s, None) == _capi.FA_ERR_NULL_POINTER
+    assert pre(P, P, BAD, P, 1, 64, 1, 64, s, s, None) == _capi.FA_ERR_ALIGNMENT
+    assert pre(P, P, P, BAD, 1, 64, 1, 64, s, s, None) == _capi.FA_ERR_ALIGNMENT   # row maxima
+    assert pre(P, None, P, P, 1, 64, 1, 64, s, s, None) == _capi.FA_ERR_NULL_POINTER
+    assert pre(P, P, P, None, 1, 64, 1, 40, s, s, None) == _capi.FA_ERR_HEAD_DIM
+
+
+def test_standalone_dkdv_needs_row_maxima(lib):
+    """fa_bwd_dkdv and fa_bwd_blocks read the pre-pass's row-group maxima
+    (their dS bound): NULL or misaligned is refused before any launch."""
+    s = _st(1, 64, 1, 64)
+    dkdv = lib.fa_bwd_dkdv
+    assert dkdv(P, P, P, P, P, P, None, P, P, 1, 64, 1, 64, s, s, s, s, s, s, 0.125, 1,
+                None) == _capi.FA_ERR_NULL_POINTER
+    assert dkdv(P, P, P, P, P, P, BAD, P, P, 1, 64, 1, 64, s, s, s, s, s, s, 0.125, 1,
+                None) == _capi.FA_ERR_ALIGNMENT
+    blocks = lib.fa_bwd_blocks
+    for causal in (0, 1):
+        assert blocks(P, P, P, P, P, P, None, P, P, P, 1, 64, 1, 64, s, s, s, s, s, s, s, 0.125,
+                      causal, None) == _capi.FA_ERR_NULL_POINTER
 
 
 def _fwd_gqa(lib, B=1, Sq=100, Sk=300, H=8, Hk=2, D=64, q=P, k=P, v=P, o=P, lse=None,
