@@ -413,15 +413,20 @@ __device__ __forceinline__ void split_finish(const BwdArgs &a, floatx16 (&dk)[D 
   __syncthreads();
   if (s_order == 0) return;   // the other segment finishes this block
   if (holder && in_range) {
+    // dK added and stored before dV's partial is loaded: both partials in
+    // flight beside dK and dV would pass 256 VGPRs at D = 128 (spills)
     float *other = a.part + ((size_t)slot * 2 + (seg ^ 1)) * (2 * HALF * LANES) + pl;
 #pragma unroll
     for (int d = 0; d < D / 32; ++d)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
+      for (int i = 0; i < 16; ++i)
         dk[d][i] = mul_then_add(dk[d][i], a.sm_scale, load_agent(other + (16 * d + i) * LANES));
-        dv[d][i] = mul_then_add(dv[d][i], 1.0f, load_agent(other + (HALF + 16 * d + i) * LANES));
-      }
     store_row<E, D>(dk_row, dk, 1.0f, g);
+#pragma unroll
+    for (int d = 0; d < D / 32; ++d)
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        dv[d][i] = mul_then_add(dv[d][i], 1.0f, load_agent(other + (HALF + 16 * d + i) * LANES));
     store_row<E, D>(dv_row, dv, 1.0f, g);
   }
 }
@@ -756,13 +761,14 @@ __device__ __forceinline__ void dkdv_block(const BwdArgs &a, const int bid, f16 
   if (n_tiles > 0) store_tile(std::integral_constant<int, 0>{});
   __syncthreads();
 
-  // ||V_k||_1 of this lane's key (its half row and lane ^ 32's; fp32)
+  // ||V_k||_1 of this lane's key (its half row and lane ^ 32's): sign bits
+  // cleared two values at a time, pairs summed by v_dot2 against (1, 1)
   float nv = 0.0f;
 #pragma unroll
   for (int cc = 0; cc < D / 16; ++cc) {
-    const vec8<E> x = v_frag(cc);
+    const u32x4 x = __builtin_bit_cast(u32x4, v_frag(cc)) & 0x7fff7fffu;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) nv += fabsf((float)x[j]);
+    for (int j = 0; j < 4; ++j) nv = dot2_acc(__builtin_bit_cast(vec2<E>, x[j]), nv);
   }
   nv += xor32(nv);
   // A query tile's dS scale from the bound on its |dS| (the maxima loaded
