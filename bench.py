@@ -987,7 +987,15 @@ def pmc_summary(dirs):
       wait_any, wait_issue, active = SQ_WAIT_ANY, SQ_WAIT_INST_ANY,
                     SQ_ACTIVE_INST_ANY as shares of SQ_WAVE_CYCLES;
       mfma_coexec = SQ_VALU_MFMA_COEXEC_CYCLES / SQ_VALU_MFMA_BUSY_CYCLES
-                    (share of MFMA-busy cycles in which a VALU op issued).
+                    (share of MFMA-busy cycles in which a VALU op issued);
+      lds_latency, vmem_latency = rocprofiler's LdsLatency / VmemLatency
+                    (in-flight instruction level accumulated per cycle over
+                    the instruction count: mean cycles from issue to data);
+      iss_valu, iss_lds, iss_sca, iss_misc, iss_vmem, wait_lds =
+                    SQ_ACTIVE_INST_{VALU,LDS,SCA,MISC,VMEM} and
+                    SQ_WAIT_INST_LDS as shares of SQ_WAVE_CYCLES (VALU
+                    includes the MFMAs; SCA = SALU + SMEM; MISC = branches,
+                    barriers and messages).
 
     Prints a markdown table and the JSON block that bench.py reads back
     (profiles/*_counters.md)."""
@@ -1032,6 +1040,15 @@ def pmc_summary(dirs):
                          ("SQ_ACTIVE_INST_ANY", "active")):
                 if c in av:
                     row[k] = round(av[c] / wc, 4)
+        if wc:
+            for c, k in (("SQ_ACTIVE_INST_VALU", "iss_valu"), ("SQ_ACTIVE_INST_LDS", "iss_lds"),
+                         ("SQ_ACTIVE_INST_SCA", "iss_sca"), ("SQ_ACTIVE_INST_MISC", "iss_misc"),
+                         ("SQ_ACTIVE_INST_VMEM", "iss_vmem"), ("SQ_WAIT_INST_LDS", "wait_lds")):
+                if c in av:
+                    row[k] = round(av[c] / wc, 4)
+        for c, k in (("LdsLatency", "lds_latency"), ("VmemLatency", "vmem_latency")):
+            if c in av:
+                row[k] = round(av[c], 1)
         if av.get("SQ_VALU_MFMA_BUSY_CYCLES") and "SQ_VALU_MFMA_COEXEC_CYCLES" in av:
             row["mfma_coexec"] = round(av["SQ_VALU_MFMA_COEXEC_CYCLES"] / av["SQ_VALU_MFMA_BUSY_CYCLES"], 4)
         # the texture / LDS pass (one TA and one TD per CU; LDS load
@@ -1049,6 +1066,8 @@ def pmc_summary(dirs):
     cols = ["cycles", "mfma_busy", "valu_per_mfma", "salu_per_mfma", "lds_per_mfma", "trans_per_mfma",
             "lds_bank_conflict", "waves_per_simd", "wait_any", "wait_issue", "active", "mfma_coexec",
             "ta_busy", "td_busy", "td_tc_stall", "lds_load_b_per_clk_cu",
+            "iss_valu", "iss_lds", "iss_sca", "iss_misc", "iss_vmem", "wait_lds",
+            "lds_latency", "vmem_latency",
             "lds_bytes", "grid", "workgroup"]
     cols = [c for c in cols if any(c in r for r in out.values())]
     print("| kernel | " + " | ".join(cols) + " |")
