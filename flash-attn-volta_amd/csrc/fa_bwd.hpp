@@ -76,15 +76,19 @@
 namespace fa {
 
 // Swizzle of the dK/dV kernel's query tiles (read both ways): the padded
-// SW_PD (fa_common.hpp) at D = 128, SW_AT at D = 64 (conflict-free both
-// ways; its offsets fit since they are byte offsets hidden from
-// loop-invariant code motion at each tile step), SW_P8 at D = 32.
+// SW_PD (fa_common.hpp) at D = 128, SW_AT at D = 64 and 32 (conflict-free
+// both ways; its offsets fit since they are byte offsets hidden from
+// loop-invariant code motion at each tile step).  At D = 32 (4 chunks a
+// row) any chunk permutation serves the transposed reads; the row reads
+// need rows r, r + 4, r + 8, r + 12 permuted apart, which SW_P8's period
+// of 8 cannot do (12 % of the D = 32 fused launch's LDS cycles
+// conflicted).
 // Measured at D = 128: LDS bank conflicts 45 % of LDS-active cycles with
 // SW_P8, 0 with SW_PD; the backward -3.2 to -3.8 % at (1,4096,8,128) and
 // (1,4096,16,128).  At D = 64 SW_AT took the conflicts from 0.03-0.08 to
 // 0.
 template <int D>
-constexpr int kDkdvSwizzle = D >= 128 ? SW_PD : (D == 64 ? SW_AT : SW_P8);
+constexpr int kDkdvSwizzle = D >= 128 ? SW_PD : SW_AT;
 
 // 32-row groups of S rows (the row-group maxima's second-to-last extent)
 __host__ __device__ __forceinline__ int row_groups(int S) { return (S + 31) >> 5; }
@@ -668,11 +672,16 @@ __device__ __forceinline__ void dkdv_block(const BwdArgs &a, const int bid, f16 
     }
   };
   // Q / dO descriptors of the tile to load, walked by cursors: re-aimed at
-  // a new query head, advanced by BQ rows otherwise.
+  // a new query head, advanced by BQ rows otherwise; likewise the head's
+  // row-group maxima (below).
+  typedef const __attribute__((address_space(4))) float kfloat;
+  const int ng = row_groups(Sq);
   RowCursor cq, cg;
+  kfloat *rm_h;
   auto aim = [&](int h, int m0) {
     cq.init(a.q.head(b, h), a.q.ss, m0, Sq, D, BQ);
     cg.init(a.dout.head(b, h), a.dout.ss, m0, Sq, D, BQ);
+    rm_h = (kfloat *)(a.rmax + ((int64_t)b * a.H + h) * ng * 2);
   };
   aim(cur_h, cur_m0);
   // The tile's row-group maxima (BwdArgs::rmax: max |dO| and max |delta|
@@ -682,7 +691,6 @@ __device__ __forceinline__ void dkdv_block(const BwdArgs &a, const int bid, f16 
   // (constant address space; no launch writes the maxima while this one
   // reads them), issued with the tile's other loads and held in SGPRs, so
   // that the settle at the tile's start waits on nothing.
-  typedef const __attribute__((address_space(4))) float kfloat;
   float nx_rm[2 * (BQ / 32)];
   auto load_tile = [&](int h, int m0, auto stc) {
     stq.load(q_st(stc), cq.rsrc(), w);
@@ -694,14 +702,13 @@ __device__ __forceinline__ void dkdv_block(const BwdArgs &a, const int bid, f16 
       lse_r = (m < Sq) ? a.lse[row] : kPosInf;
       dl_r = (m < Sq) ? a.delta[row] : 0.0f;
     }
-    const int ng = row_groups(Sq);
-    kfloat *rm = (kfloat *)(a.rmax + (((int64_t)b * a.H + h) * ng + m0 / 32) * 2);
 #pragma unroll
     for (int i = 0; i < BQ / 32; ++i) {
-      // groups past Sq (a ragged last tile) bound nothing
-      const bool in = m0 / 32 + i < ng;
-      nx_rm[2 * i] = in ? rm[2 * i] : 0.0f;
-      nx_rm[2 * i + 1] = in ? rm[2 * i + 1] : 0.0f;
+      // a ragged last tile's groups past Sq read the head's last group
+      // again, which the tile holds (tiles start below Sq): same bound
+      const int gi = min((m0 >> 5) + i, ng - 1);
+      nx_rm[2 * i] = rm_h[2 * gi];
+      nx_rm[2 * i + 1] = rm_h[2 * gi + 1];
     }
   };
   // Publishing a stage: its LSE / delta rows go to LDS, then every DMA of
