@@ -311,9 +311,10 @@ int fa_bwd_gqa_noalloc(const void *dout, const void *q, const void *k, const voi
                        float sm_scale, int causal, int dtype, void *stream);
 
 /*
- * The two main backward kernels as separate steps (fa_bwd runs the dQ
- * kernel, computing delta on the way, then the dK/dV kernel; called
- * separately they take delta from fa_bwd_preprocess).  `delta` is the
+ * The two main backward kernels as separate steps (outside its causal
+ * D = 32 / 64 fused launch, fa_bwd runs the dQ kernel, computing delta
+ * and the maxima on the way, then the dK/dV kernel; called separately they
+ * take both from fa_bwd_preprocess).  `delta` is the
  * fa_bwd_preprocess output, (B, H, S) fp32 contiguous, and fa_bwd_dkdv's
  * `rowmax` (not NULL) its row-group maxima for the same o and dout.
  *
