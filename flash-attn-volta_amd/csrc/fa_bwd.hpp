@@ -913,8 +913,8 @@ __device__ __forceinline__ void dkdv_block(const BwdArgs &a, const int bid, f16 
     // in program order, so the VALU work issues under MFMAs it does not
     // depend on --
     //   S MFMAs;  dP MFMAs, with exp2 of S (P, rounded to E) between them;
-    //   dV MFMAs (they need only P), with dS = P (dP - delta) and its max
-    //   between them;  dK MFMAs, with dS's scaled conversion between.
+    //   dV MFMAs (they need only P), with dS = P (dP - delta) between
+    //   them;  dK MFMAs, with dS's scaled conversion between.
     // A MFMA runs ~32 cycles in the matrix pipe while the wave issues the
     // VALU slice after it; sched_barrier(0) keeps the compiler from
     // regrouping the slices.  Invisible scores (diagonal and ragged
@@ -1023,9 +1023,8 @@ __device__ __forceinline__ void dkdv_block(const BwdArgs &a, const int bid, f16 
         __builtin_amdgcn_sched_barrier(0);
       });
       // dV^T += dO^T P, with dS = P dP (into p: P is needed as E only from
-      // here on) in NO - 1 slices, and the tile's dS bound under the first
+      // here on) in NO - 1 slices
       floatx16 &ds = p;
-      float bnd = 0.0f;
       static_for<NO>([&](auto io) {
         constexpr int o = decltype(io)::value, i = 2 * NC + o;
         constexpr int hh = o / (D / 32), d = o % (D / 32);
@@ -1444,8 +1443,9 @@ void fa_bwd_dq_kernel(BwdArgs a) {
 // `akv`, the rest dq_block with `aq` -- so that the dQ blocks, dispatched
 // after every dK/dV block, fill the slots the causal sweeps of unequal
 // length leave idle, and no kernel boundary drains the GPU between the
-// two.  Both read only the inputs and delta (the pre-pass computes it and
-// zeroes the key-block split's counters first) and write disjoint outputs,
+// two.  Both read only the inputs, delta and the row-group maxima (the
+// pre-pass computes them and zeroes the key-block split's counters first)
+// and write disjoint outputs,
 // so no workgroup waits for another.  The dQ blocks run in the dK/dV
 // blocks' four tile stages.
 template <typename E, int D, bool CAUSAL, int KVSPLIT, int QSPLIT, bool PRE>
