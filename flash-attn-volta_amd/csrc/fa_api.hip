@@ -370,10 +370,13 @@ int launch_dq_split(const fa::BwdArgs &args, hipStream_t stream) {
 template <typename E, int D, bool CAUSAL>
 int launch_dkdv(const fa::BwdArgs &a, hipStream_t stream) {
   // the key-block split runs in the eight-wave D = 128 kernel and in the
-  // D = 64 query-split kernel (dkdv_split_plan)
-  if constexpr (D == 128 && CAUSAL) {
-    if (a.split_kt > 0) return launch_dkdv_split<E, D, CAUSAL, 1>(a, stream);
-  }
+  // D = 64 query-split kernel (dkdv_split_plan).  Causal D = 128 takes the
+  // eight-wave layout on every grid: the layout of fa_bwd's fused launch,
+  // so the separate launches give the same bits (the fused launch in this
+  // layout ran the (1,2048,16,128) causal backward 19 % faster than the
+  // dQ kernel and the four-wave query-split dK/dV kernel, one wave per
+  // SIMD, that this grid used to take)
+  if constexpr (D == 128 && CAUSAL) return launch_dkdv_split<E, D, CAUSAL, 1>(a, stream);
   if constexpr (D == 64 && CAUSAL) {
     if (a.split_kt > 0) return launch_dkdv_split<E, D, CAUSAL, 2>(a, stream);
   }
@@ -430,7 +433,7 @@ struct FusedBwd {
 template <typename E, int D, bool CAUSAL, int KVS, int QS>
 int launch_bwd_fused_as(FusedBwd f, hipStream_t stream) {
   using T = fa::DkdvTile<D, KVS>;
-  using Q = fa::DqTile<D, QS, 4>;
+  using Q = fa::DqTile<D, QS, T::NW>;
   f.akv.n_blocks = (f.akv.Sk + T::BK - 1) / T::BK;
   f.aq.n_blocks = (f.aq.Sq + Q::BM - 1) / Q::BM;
   const int64_t n_kv = ((int64_t)f.akv.n_blocks + f.akv.split_kt) * f.akv.B * f.akv.Hk;
@@ -447,12 +450,12 @@ int launch_bwd_fused_as(FusedBwd f, hipStream_t stream) {
   if constexpr (std::is_same<E, fa::f16>::value) {
     if (f.aq.c <= 1.0f) {
       hipLaunchKernelGGL((fa::fa_bwd_fused_kernel<E, D, CAUSAL, KVS, QS, true>),
-                         dim3((unsigned)(n_kv + n_q)), dim3(256), 0, stream, f.akv, f.aq, (int)n_kv);
+                         dim3((unsigned)(n_kv + n_q)), dim3(T::NT), 0, stream, f.akv, f.aq, (int)n_kv);
       return launch_status();
     }
   }
   hipLaunchKernelGGL((fa::fa_bwd_fused_kernel<E, D, CAUSAL, KVS, QS, false>),
-                     dim3((unsigned)(n_kv + n_q)), dim3(256), 0, stream, f.akv, f.aq, (int)n_kv);
+                     dim3((unsigned)(n_kv + n_q)), dim3(T::NT), 0, stream, f.akv, f.aq, (int)n_kv);
   return launch_status();
 }
 
@@ -464,10 +467,14 @@ int launch_bwd_fused(const FusedBwd &f, hipStream_t stream) {
                         : launch_bwd_fused_as<E, D, CAUSAL, 2, 1>(f, stream);
     return f.q_split2 ? launch_bwd_fused_as<E, D, CAUSAL, 1, 2>(f, stream)
                       : launch_bwd_fused_as<E, D, CAUSAL, 1, 1>(f, stream);
+  } else if constexpr (D == 128 && CAUSAL) {
+    // the eight-wave dK/dV layout beside eight-wave dQ blocks
+    return f.q_split2 ? launch_bwd_fused_as<E, D, CAUSAL, 1, 2>(f, stream)
+                      : launch_bwd_fused_as<E, D, CAUSAL, 1, 1>(f, stream);
   } else {
     (void)f;
     (void)stream;
-    return FA_ERR_HEAD_DIM;   // run_bwd picks the fused path for causal D <= 64 only
+    return FA_ERR_HEAD_DIM;   // run_bwd picks the fused path for causal grids only
   }
 }
 
@@ -1119,10 +1126,24 @@ int check_bwd(const void *dout, const void *q, const void *k, const void *v, con
 }
 
 // The fused backward launch (fa::fa_bwd_fused_kernel) for causal
-// D = 32 / 64 backwards without the dQ split (whose halves the dK/dV
-// kernel adds after the dQ kernel).
-bool bwd_fused(const Shape &s, int causal, const DqSplit &qplan) {
-  return causal && s.D <= 64 && qplan.split == 0;
+// backwards without the dQ split (whose halves the dK/dV kernel adds after
+// the dQ kernel): every D = 32 / 64 one, and the D = 128 ones below.
+// `plan` is the key-block split that will run (none without the
+// workspace for it), so fa_bwd_blocks, which never splits, takes the path
+// fa_bwd takes with the minimum workspace.
+bool bwd_fused(const Shape &s, int causal, const DqSplit &qplan, const DkdvSplit &plan) {
+  if (!causal || qplan.split != 0) return false;
+  if (s.D <= 64) return true;
+  // D = 128: where no key-block split runs and the eight-wave dK/dV grid
+  // is at most three rounds (one workgroup per CU).  Measured against the
+  // dQ kernel (delta folded in) then the dK/dV kernel: (1,2048,16,128)
+  // -19.5 %, (2,1100,32,128) -2.8 %, (1,4096,16,128) -1.4 %; with the
+  // key split ((1,4096,8,128)) +1.7 %, and on (4,4096,16,128) (eight
+  // rounds) +1.8 %, where the separate pre-pass over O and dO costs more
+  // than the fusion saves.
+  using T = fa::DkdvTile<128, 1>;
+  const int64_t blocks = (s.Sk + T::BK - 1) / T::BK * ((int64_t)s.B * s.Hk);
+  return plan.split_kt == 0 && blocks <= 3 * (int64_t)device_cus();
 }
 
 int run_bwd(const void *dout, const void *q, const void *k, const void *v, const void *o,
@@ -1162,7 +1183,7 @@ int run_bwd(const void *dout, const void *q, const void *k, const void *v, const
   }
   float *dq_part =
       qplan.split > 0 ? reinterpret_cast<float *>(ws + dbytes + split_bytes(plan)) : nullptr;
-  if (bwd_fused(s, causal, qplan)) {
+  if (bwd_fused(s, causal, qplan, plan)) {
     FusedBwd f{};
     if ((rc = dkdv_args(dout, q, k, v, lse, delta, rmax, dk, dv, s, do_st, q_st, k_st, v_st,
                         dk_st, dv_st, sm_scale, plan.split_kt, cnt, part, nullptr, nullptr,
@@ -1209,7 +1230,7 @@ int run_bwd_blocks(const void *dout, const void *q, const void *k, const void *v
                    const int64_t *dk_st, const int64_t *dv_st, float sm_scale, int causal,
                    void *stream) {
   const LaunchDevice launch_dev(stream);
-  if (!bwd_fused(s, causal, DqSplit{})) {
+  if (!bwd_fused(s, causal, DqSplit{}, DkdvSplit{})) {
     // every check before the first launch
     fa::BwdArgs chk;
     int rc = dkdv_args(dout, q, k, v, lse, delta, rmax, dk, dv, s, do_st, q_st, k_st, v_st,

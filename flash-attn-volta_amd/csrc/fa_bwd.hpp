@@ -1160,7 +1160,6 @@ template <typename E, int D, bool CAUSAL, int SPLIT, bool PRE, int NW>
 __device__ __forceinline__ void dq_block(const BwdArgs &a, const int bid, f16 *s_k0, f16 *s_k1,
                                          f16 *s_v0, f16 *s_v1) {
   static_assert(!PRE || std::is_same<E, f16>::value, "the pre-scaled mode is fp16 only");
-  static_assert(NW == 4 || !CAUSAL, "eight-wave dQ workgroups are for non-causal grids");
   using T = DqTile<D, SPLIT, NW>;
   constexpr int BM = T::BM, BN = T::BN, NSUB = T::NSUB;
   auto k_st = [&](auto stc) -> f16 * { return decltype(stc)::value ? s_k1 : s_k0; };
@@ -1449,19 +1448,20 @@ void fa_bwd_dq_kernel(BwdArgs a) {
 // so no workgroup waits for another.  The dQ blocks run in the dK/dV
 // blocks' four tile stages.
 template <typename E, int D, bool CAUSAL, int KVSPLIT, int QSPLIT, bool PRE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+__global__ __launch_bounds__((DkdvTile<D, KVSPLIT>::NT))
+__attribute__((amdgpu_waves_per_eu(D <= 64 ? 3 : 2)))
 void fa_bwd_fused_kernel(BwdArgs akv, BwdArgs aq, int n_kv) {
   using T = DkdvTile<D, KVSPLIT>;
-  using Q = DqTile<D, QSPLIT, 4>;
-  static_assert(T::NT == 256 && Q::NT == 256, "both blocks take four waves");
-  static_assert(D <= 64, "three waves per SIMD for both blocks");
+  using Q = DqTile<D, QSPLIT, T::NW>;
+  static_assert(T::NT == Q::NT, "both blocks take the same waves");
+  static_assert(D <= 64 ? T::NW == 4 : T::WIDE, "four-wave blocks at D <= 64, eight at D = 128");
   static_assert(T::LDS_TILE >= Q::LDS_TILE, "a dQ stage fits in a dK/dV tile stage");
   FA_DKDV_LDS(T);
   const int bid = blockIdx.x;
   if (bid < n_kv)
     dkdv_block<E, D, CAUSAL, KVSPLIT>(akv, bid, s_q0, s_q1, s_do0, s_do1, s_lse, s_dl, s_k, s_v);
   else
-    dq_block<E, D, CAUSAL, QSPLIT, PRE, 4>(aq, bid - n_kv, s_q0, s_q1, s_do0, s_do1);
+    dq_block<E, D, CAUSAL, QSPLIT, PRE, T::NW>(aq, bid - n_kv, s_q0, s_q1, s_do0, s_do1);
 }
 
 }  // namespace fa

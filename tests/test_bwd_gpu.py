@@ -354,20 +354,26 @@ def _bwd_three_launches(do, q, k, v, o, lse, causal, sm_scale):
     return (dq, dk, dv), (bq, bk, bv)
 
 
-# The causal D = 32 / 64 backward runs as the pre-pass and one fused launch
-# (every dK/dV block, then every dQ block, in one grid); the three separate
-# entry points run the same block code in three launches, so the gradients
-# must be bit-identical; so must fa_bwd_blocks (the fused launch alone,
-# given delta).  Shapes: both layout pairs the launcher picks for H = Hk
-# (dK/dV query-split with dQ key-split on grids under a round, both
-# unsplit above), a ragged length, and a scale above ln 2 (the dQ block's
-# unscaled mode).
+# The causal backward runs as the pre-pass and one fused launch (every
+# dK/dV block, then every dQ block, in one grid: four-wave blocks at
+# D = 32 / 64, eight-wave ones at D = 128); the three separate entry points
+# run the same block code in three launches, so the gradients must be
+# bit-identical; so must fa_bwd_blocks (the fused launch alone, given
+# delta).  Shapes: both layout pairs the launcher picks for H = Hk at
+# D = 64 (dK/dV query-split with dQ key-split on grids under a round, both
+# unsplit above), a ragged length, a scale above ln 2 (the dQ block's
+# unscaled mode), and D = 128 grids on which flash_attn_backward's
+# workspace enables no key-block split (a split sums two fp32 partials, a
+# different rounding; its own test is test_backward_causal_key_block_split).
 @pytest.mark.parametrize("B,S,H,D,sm_scale,in_scale", [
     (1, 4096, 16, 64, None, 0.5),
     (4, 2048, 16, 64, None, 1.0),
     (2, 1000, 8, 64, 1.0, 0.35),
     (4, 512, 4, 32, None, 1.0),
     (8, 1024, 32, 32, None, 1.0),
+    (1, 4096, 16, 128, None, 0.5),
+    (2, 1100, 32, 128, None, 1.0),
+    (1, 2048, 16, 128, 1.0, 0.35),
 ])
 def test_backward_fused_launch_matches_three_launches(B, S, H, D, sm_scale, in_scale):
     from flash_attn_volta import flash_attn_backward, flash_attn_forward
