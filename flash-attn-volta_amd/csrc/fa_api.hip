@@ -419,7 +419,7 @@ int launch_dq(const fa::BwdArgs &a, hipStream_t stream) {
                : launch_dq_split<E, D, CAUSAL, 1, false>(a, stream);
 }
 
-// Fused causal backward (fa::fa_bwd_fused_kernel, D <= 64): the pre-pass,
+// Fused causal backward (fa::fa_bwd_fused_kernel; bwd_fused decides): the pre-pass,
 // which computes delta and zeroes the key-block split's counters, then
 // one launch of every dK/dV block followed by every dQ block.
 struct FusedBwd {

@@ -12,7 +12,9 @@
 //                            _fa_bwd_dkdv_kernel_*, :319-580)
 // and delta = rowsum(dO * O) in fp32 (the torch op at :650).  fa_bwd runs
 // them as
-//   causal, D <= 64: fa_bwd_preprocess_kernel (delta), then ONE launch of
+//   causal, D <= 64, and causal D = 128 on grids of at most three rounds
+//   without the key-block split:
+//                    fa_bwd_preprocess_kernel (delta), then ONE launch of
 //                    fa_bwd_fused_kernel, every dK/dV block and then every
 //                    dQ block in one grid: the dQ blocks fill the slots the
 //                    causal sweeps of unequal length leave idle;
@@ -1437,7 +1439,8 @@ void fa_bwd_dq_kernel(BwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Fused backward (causal, D <= 64): the dK/dV blocks and the dQ blocks of
+// Fused backward (causal; four-wave blocks at D <= 64, the eight-wave dK/dV
+// layout with eight-wave dQ blocks at D = 128): the dK/dV blocks and the dQ blocks of
 // one backward in one grid -- workgroups [0, n_kv) run dkdv_block with
 // `akv`, the rest dq_block with `aq` -- so that the dQ blocks, dispatched
 // after every dK/dV block, fill the slots the causal sweeps of unequal

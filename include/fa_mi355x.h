@@ -223,7 +223,9 @@ size_t fa_bwd_gqa_workspace_bytes(int B, int Sq, int Sk, int H, int Hk, int D, i
 
 /*
  * Backward attention: (dq, dk, dv) of L = <o, dout> with o = fa_fwd(q,k,v),
- * given the forward's `lse`. Two launches. Causal with D = 32 or 64:
+ * given the forward's `lse`. Two launches. Causal with D = 32 or 64, and
+ * causal D = 128 when no key-block split runs and the grid is at most
+ * three workgroups of eight waves per compute unit:
  * fa_bwd_preprocess's kernel (delta = rowsum(o * dout) and the row-group
  * maxima into the workspace), then one launch running every dK/dV
  * workgroup (one per key block, or two for the longest blocks when the
@@ -311,8 +313,8 @@ int fa_bwd_gqa_noalloc(const void *dout, const void *q, const void *k, const voi
                        float sm_scale, int causal, int dtype, void *stream);
 
 /*
- * The two main backward kernels as separate steps (outside its causal
- * D = 32 / 64 fused launch, fa_bwd runs the dQ kernel, computing delta
+ * The two main backward kernels as separate steps (outside its fused
+ * causal launch, fa_bwd runs the dQ kernel, computing delta
  * and the maxima on the way, then the dK/dV kernel; called separately they
  * take both from fa_bwd_preprocess).  `delta` is the
  * fa_bwd_preprocess output, (B, H, S) fp32 contiguous, and fa_bwd_dkdv's
@@ -343,9 +345,9 @@ int fa_bwd_dq(const void *dout, const void *q, const void *k, const void *v,
  * Both gradient launches of fa_bwd given delta and the row-group maxima
  * (the fa_bwd_preprocess outputs, `rowmax` not NULL), i.e. fa_bwd without
  * its delta step and without a workspace (so
- * without the key-block split): for causal D = 32 / 64 the one fused
- * launch of every dK/dV and every dQ workgroup, otherwise fa_bwd_dq then
- * fa_bwd_dkdv.  Bit-identical to fa_bwd with the fa_bwd_workspace_bytes
+ * without the key-block split): where fa_bwd takes its fused launch
+ * (above), that launch of every dK/dV and every dQ workgroup, otherwise
+ * fa_bwd_dq then fa_bwd_dkdv.  Bit-identical to fa_bwd with the fa_bwd_workspace_bytes
  * workspace.  For callers that time or schedule the gradient launches
  * apart from the delta step.
  *
