@@ -981,6 +981,30 @@ DqSplit dq_split_plan(const Shape &s, int causal) {
   return p;
 }
 
+// Causal D = 128 backwards that run as the fused launch (bwd_fused): no
+// dQ split and an eight-wave dK/dV grid of at most three rounds, unsplit.
+// Measured against the dQ kernel (delta folded in) then the dK/dV kernel:
+// (1,2048,16,128) -18.6 %, (2,1100,32,128) -2.7 %, (1,4096,16,128) -1.6 %,
+// and against the key-block split that (1,4096,8,128) (C4b), (1,8192,4,128)
+// and (2,4096,4,128) took before: -10.0, -9.0 and -10.3 % (the dQ blocks
+// fill the idle slots of the unequal sweeps the split evened out, without
+// its partials); on (4,4096,16,128) (eight rounds) the separate pre-pass
+// over O and dO costs more than the fusion saves (+1.8 %).
+bool fused128(const Shape &s, int causal, const DqSplit &qplan) {
+  if (!causal || s.D != 128 || qplan.split != 0) return false;
+  using T = fa::DkdvTile<128, 1>;
+  const int64_t blocks = (s.Sk + T::BK - 1) / T::BK * ((int64_t)s.B * s.Hk);
+  return blocks <= 3 * (int64_t)device_cus();
+}
+
+// Both backward splits for these sizes (what fa_bwd_gqa_workspace_bytes
+// makes room for): the dQ split, and the key-block split except where
+// the fused D = 128 launch runs, unsplit.
+void bwd_plans(const Shape &s, int causal, DkdvSplit &plan, DqSplit &qplan) {
+  qplan = dq_split_plan(s, causal);
+  plan = fused128(s, causal, qplan) ? DkdvSplit{} : dkdv_split_plan(s, causal);
+}
+
 // two segments x BM rows x D fp32 per split query block
 size_t dq_split_bytes(const DqSplit &p) {
   return p.split > 0 ? (size_t)p.slots * 2 * (size_t)p.bm * (size_t)p.d * sizeof(float) : 0;
@@ -1127,23 +1151,12 @@ int check_bwd(const void *dout, const void *q, const void *k, const void *v, con
 
 // The fused backward launch (fa::fa_bwd_fused_kernel) for causal
 // backwards without the dQ split (whose halves the dK/dV kernel adds after
-// the dQ kernel): every D = 32 / 64 one, and the D = 128 ones below.
-// `plan` is the key-block split that will run (none without the
+// the dQ kernel): every D = 32 / 64 one, and the D = 128 ones of
+// fused128.  `qplan` is the dQ split that will run (none without the
 // workspace for it), so fa_bwd_blocks, which never splits, takes the path
 // fa_bwd takes with the minimum workspace.
-bool bwd_fused(const Shape &s, int causal, const DqSplit &qplan, const DkdvSplit &plan) {
-  if (!causal || qplan.split != 0) return false;
-  if (s.D <= 64) return true;
-  // D = 128: where no key-block split runs and the eight-wave dK/dV grid
-  // is at most three rounds (one workgroup per CU).  Measured against the
-  // dQ kernel (delta folded in) then the dK/dV kernel: (1,2048,16,128)
-  // -19.5 %, (2,1100,32,128) -2.8 %, (1,4096,16,128) -1.4 %; with the
-  // key split ((1,4096,8,128)) +1.7 %, and on (4,4096,16,128) (eight
-  // rounds) +1.8 %, where the separate pre-pass over O and dO costs more
-  // than the fusion saves.
-  using T = fa::DkdvTile<128, 1>;
-  const int64_t blocks = (s.Sk + T::BK - 1) / T::BK * ((int64_t)s.B * s.Hk);
-  return plan.split_kt == 0 && blocks <= 3 * (int64_t)device_cus();
+bool bwd_fused(const Shape &s, int causal, const DqSplit &qplan) {
+  return causal && qplan.split == 0 && (s.D <= 64 || fused128(s, causal, qplan));
 }
 
 int run_bwd(const void *dout, const void *q, const void *k, const void *v, const void *o,
@@ -1165,8 +1178,9 @@ int run_bwd(const void *dout, const void *q, const void *k, const void *v, const
   // Layout: delta, the row-group maxima, then the dK/dV split's counters
   // and partials, then the dQ split's partials -- both splits or neither,
   // by workspace size.  (`dbytes` below covers delta and the maxima.)
-  DkdvSplit plan = dkdv_split_plan(s, causal);
-  DqSplit qplan = dq_split_plan(s, causal);
+  DkdvSplit plan;
+  DqSplit qplan;
+  bwd_plans(s, causal, plan, qplan);
   float *rmax = reinterpret_cast<float *>(static_cast<char *>(workspace) +
                                           delta_bytes(s.B, s.Sq, s.H));
   const size_t dbytes = delta_bytes(s.B, s.Sq, s.H) + rbytes;
@@ -1183,7 +1197,7 @@ int run_bwd(const void *dout, const void *q, const void *k, const void *v, const
   }
   float *dq_part =
       qplan.split > 0 ? reinterpret_cast<float *>(ws + dbytes + split_bytes(plan)) : nullptr;
-  if (bwd_fused(s, causal, qplan, plan)) {
+  if (bwd_fused(s, causal, qplan)) {
     FusedBwd f{};
     if ((rc = dkdv_args(dout, q, k, v, lse, delta, rmax, dk, dv, s, do_st, q_st, k_st, v_st,
                         dk_st, dv_st, sm_scale, plan.split_kt, cnt, part, nullptr, nullptr,
@@ -1230,7 +1244,7 @@ int run_bwd_blocks(const void *dout, const void *q, const void *k, const void *v
                    const int64_t *dk_st, const int64_t *dv_st, float sm_scale, int causal,
                    void *stream) {
   const LaunchDevice launch_dev(stream);
-  if (!bwd_fused(s, causal, DqSplit{}, DkdvSplit{})) {
+  if (!bwd_fused(s, causal, DqSplit{})) {
     // every check before the first launch
     fa::BwdArgs chk;
     int rc = dkdv_args(dout, q, k, v, lse, delta, rmax, dk, dv, s, do_st, q_st, k_st, v_st,
@@ -1622,8 +1636,10 @@ size_t fa_bwd_rowmax_bytes(int B, int S, int H) {
 size_t fa_bwd_gqa_workspace_bytes(int B, int Sq, int Sk, int H, int Hk, int D, int causal) {
   const Shape s{B, Sq, Sk, H, Hk, D, FA_DTYPE_F16};
   if (check_shape(s) != FA_OK) return 0;
-  return delta_bytes(B, Sq, H) + rmax_bytes(B, Sq, H) + split_bytes(dkdv_split_plan(s, causal)) +
-         dq_split_bytes(dq_split_plan(s, causal));
+  DkdvSplit plan;
+  DqSplit qplan;
+  bwd_plans(s, causal, plan, qplan);
+  return delta_bytes(B, Sq, H) + rmax_bytes(B, Sq, H) + split_bytes(plan) + dq_split_bytes(qplan);
 }
 
 int fa_bwd(const void *dout, const void *q, const void *k, const void *v,

@@ -13,7 +13,7 @@
 // and delta = rowsum(dO * O) in fp32 (the torch op at :650).  fa_bwd runs
 // them as
 //   causal, D <= 64, and causal D = 128 on grids of at most three rounds
-//   without the key-block split:
+//   without the dQ split:
 //                    fa_bwd_preprocess_kernel (delta), then ONE launch of
 //                    fa_bwd_fused_kernel, every dK/dV block and then every
 //                    dQ block in one grid: the dQ blocks fill the slots the

@@ -114,18 +114,18 @@ def test_split_workspace_bytes(lib):
     128 causal grids of at most one
     round of resident workgroups (one per CU at D = 128, three at D = 64;
     256 CUs here: without a GPU the count defaults to MI355X's) whose
-    longest sweep has at least 32 query tiles."""
+    longest sweep has at least 32 query tiles -- at D = 128 only beside the
+    dQ split (without it the fused launch runs, unsplit)."""
     mini = lib.fa_bwd_workspace_bytes(1, 4096, 8, 128)
-    # (1,4096,8,128) causal: 32 key blocks x 8 heads; blocks with > 4 of
-    # their 64-query tiles (kt < 30) split: 240 slots, 2 x 2 x 128 x 128
-    # fp32 each, plus 240 counters rounded up to 1 KiB
-    slots = 30 * 8
-    assert lib.fa_bwd_gqa_workspace_bytes(1, 4096, 4096, 8, 8, 128, 1) == \
-        mini + 1024 + slots * 2 * 2 * 128 * 128 * 4
-    # (1,4096,4,128): the same key-block split over 4 heads (120 slots, 480 B
-    # of counters rounded to 512), and the dQ grid (64-row blocks x 4 heads,
-    # half a round at two per CU) splits its last blocks with more than
-    # 64 / 3 = 21 key tiles (43 of 64): 2 x 64 x 128 fp32 each
+    # (1,4096,8,128) causal: no dQ split (64 blocks x 8 heads is a full
+    # round), so the fused D = 128 launch, unsplit: the minimum
+    assert lib.fa_bwd_gqa_workspace_bytes(1, 4096, 4096, 8, 8, 128, 1) == mini
+    # (1,4096,4,128): the dQ grid (64-row blocks x 4 heads, half a round at
+    # two per CU) splits its last blocks with more than 64 / 3 = 21 key
+    # tiles (43 of 64): 2 x 64 x 128 fp32 each; beside it the key-block
+    # split: 32 key blocks x 4 heads, those with > 4 of their 64-query
+    # tiles (kt < 30) split, 120 slots of 2 x 2 x 128 x 128 fp32, and 480 B
+    # of counters rounded to 512
     assert lib.fa_bwd_gqa_workspace_bytes(1, 4096, 4096, 4, 4, 128, 1) == \
         lib.fa_bwd_workspace_bytes(1, 4096, 4, 128) + 512 + 30 * 4 * 2 * 2 * 128 * 128 * 4 + \
         43 * 4 * 2 * 64 * 128 * 4
@@ -146,8 +146,12 @@ def test_split_workspace_bytes(lib):
         lib.fa_bwd_workspace_bytes(1, 4096, 16, 128)                               # 512 blocks
     assert lib.fa_bwd_gqa_workspace_bytes(1, 1024, 1024, 16, 16, 128, 1) == \
         lib.fa_bwd_workspace_bytes(1, 1024, 16, 128)                               # 16 tiles
-    # grouped heads: tiles count over the 4 query heads of each key head
-    assert lib.fa_bwd_gqa_workspace_bytes(1, 700, 1000, 8, 2, 128, 1) > \
+    # grouped heads: tiles count over the 2 query heads of each key head
+    # (beside the dQ split, as every D = 128 key split); without the dQ
+    # split the fused launch runs unsplit
+    assert lib.fa_bwd_gqa_workspace_bytes(1, 2100, 2400, 4, 2, 128, 1) > \
+        lib.fa_bwd_workspace_bytes(1, 2100, 4, 128)
+    assert lib.fa_bwd_gqa_workspace_bytes(1, 700, 1000, 8, 2, 128, 1) == \
         lib.fa_bwd_workspace_bytes(1, 700, 8, 128)
     assert lib.fa_bwd_gqa_workspace_bytes(1, 700, 1000, 8, 3, 128, 1) == 0       # H % Hk
     assert lib.fa_bwd_gqa_workspace_bytes(1, 700, 1000, 8, 2, 96, 1) == 0        # bad D
