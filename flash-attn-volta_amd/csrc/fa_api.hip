@@ -981,28 +981,37 @@ DqSplit dq_split_plan(const Shape &s, int causal) {
   return p;
 }
 
-// Causal D = 128 backwards that run as the fused launch (bwd_fused): no
-// dQ split and an eight-wave dK/dV grid of at most three rounds, unsplit.
-// Measured against the dQ kernel (delta folded in) then the dK/dV kernel:
-// (1,2048,16,128) -18.6 %, (2,1100,32,128) -2.7 %, (1,4096,16,128) -1.6 %,
-// and against the key-block split that (1,4096,8,128) (C4b), (1,8192,4,128)
-// and (2,4096,4,128) took before: -10.0, -9.0 and -10.3 % (the dQ blocks
-// fill the idle slots of the unequal sweeps the split evened out, without
-// its partials); on (4,4096,16,128) (eight rounds) the separate pre-pass
-// over O and dO costs more than the fusion saves (+1.8 %).
-bool fused128(const Shape &s, int causal, const DqSplit &qplan) {
-  if (!causal || s.D != 128 || qplan.split != 0) return false;
+// The fused backward launch (fa::fa_bwd_fused_kernel) runs the causal
+// backwards without the dQ split (whose halves the dK/dV kernel adds after
+// the dQ kernel), unsplit: every D = 32 / 64 one, and the D = 128 ones
+// whose eight-wave dK/dV grid is at most three rounds.  `qplan` is the dQ
+// split that will run (none without the workspace for it), so
+// fa_bwd_blocks, which never splits, takes the path fa_bwd takes with the
+// minimum workspace.  Measured (same-process A/B of the backward):
+//   against the dQ kernel (delta folded in) then the dK/dV kernel, D = 128:
+//   (1,2048,16,128) -18.6 %, (2,1100,32,128) -2.7 %, (1,4096,16,128)
+//   -1.6 %; on (4,4096,16,128) (eight rounds) the separate pre-pass over O
+//   and dO costs more than the fusion saves (+1.8 %);
+//   against the key-block split (inside the fused launch at D = 64, beside
+//   it at D = 128) on grids of one round: (1,2048,16,64) -13.2 %,
+//   (1,4096,8,64) -2.9 %, (1,4096,8,128) -9.9 %, (1,8192,4,128) -7.5 %,
+//   (2,4096,4,128) -9.7 % -- the dQ blocks fill the slots the unequal
+//   sweeps leave idle, as the split's second workgroups did, without its
+//   partials.
+bool bwd_fused(const Shape &s, int causal, const DqSplit &qplan) {
+  if (!causal || qplan.split != 0) return false;
+  if (s.D <= 64) return true;
   using T = fa::DkdvTile<128, 1>;
   const int64_t blocks = (s.Sk + T::BK - 1) / T::BK * ((int64_t)s.B * s.Hk);
   return blocks <= 3 * (int64_t)device_cus();
 }
 
 // Both backward splits for these sizes (what fa_bwd_gqa_workspace_bytes
-// makes room for): the dQ split, and the key-block split except where
-// the fused D = 128 launch runs, unsplit.
+// makes room for): the dQ split, and the key-block split beside it (the
+// fused launch runs unsplit).
 void bwd_plans(const Shape &s, int causal, DkdvSplit &plan, DqSplit &qplan) {
   qplan = dq_split_plan(s, causal);
-  plan = fused128(s, causal, qplan) ? DkdvSplit{} : dkdv_split_plan(s, causal);
+  plan = bwd_fused(s, causal, qplan) ? DkdvSplit{} : dkdv_split_plan(s, causal);
 }
 
 // two segments x BM rows x D fp32 per split query block
@@ -1147,16 +1156,6 @@ int check_bwd(const void *dout, const void *q, const void *k, const void *v, con
   if (!aligned16(lse)) return FA_ERR_ALIGNMENT;
   if (!isfinite(sm_scale)) return FA_ERR_SCALE;
   return FA_OK;
-}
-
-// The fused backward launch (fa::fa_bwd_fused_kernel) for causal
-// backwards without the dQ split (whose halves the dK/dV kernel adds after
-// the dQ kernel): every D = 32 / 64 one, and the D = 128 ones of
-// fused128.  `qplan` is the dQ split that will run (none without the
-// workspace for it), so fa_bwd_blocks, which never splits, takes the path
-// fa_bwd takes with the minimum workspace.
-bool bwd_fused(const Shape &s, int causal, const DqSplit &qplan) {
-  return causal && qplan.split == 0 && (s.D <= 64 || fused128(s, causal, qplan));
 }
 
 int run_bwd(const void *dout, const void *q, const void *k, const void *v, const void *o,

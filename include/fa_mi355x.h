@@ -205,14 +205,15 @@ size_t fa_bwd_workspace_bytes(int B, int S, int H, int D);
 /*
  * Bytes of device workspace with which fa_bwd / fa_bwd_gqa run their
  * fastest schedule for these sizes (0 on bad sizes): the
- * fa_bwd_workspace_bytes minimum plus, for causal D = 64 problems whose
- * key blocks fit one round of resident workgroups, room for the key-block
- * split (the longest causal key blocks swept by two workgroups each, fp32
- * partials added by whichever finishes second) and, when the dQ grid is
- * at most half a round (D = 64 / 128), for the query-block split of the
- * dQ kernel (its longest query blocks swept by two workgroups, fp32
- * halves added by the dK/dV kernel) -- at D = 128 with the key-block split
- * beside it: at most 80 MiB + 4 KiB more.
+ * fa_bwd_workspace_bytes minimum plus, for causal D = 64 / 128 problems
+ * whose dQ grid is at most half a round of resident workgroups, room for
+ * the query-block split of the dQ kernel (its longest query blocks swept
+ * by two workgroups, fp32 halves added by the dK/dV kernel) and, when the
+ * key blocks fit one round, for the key-block split beside it (the
+ * longest causal key blocks swept by two workgroups each, fp32 partials
+ * added by whichever finishes second): at most 80 MiB + 4 KiB more.
+ * (Without the dQ split the causal backward runs its fused launch,
+ * unsplit, which measured faster.)
  * Any workspace of at least the minimum is valid: with less than this
  * size the backward runs unsplit.  Split and unsplit results differ in
  * rounding only; each is bit-reproducible.
@@ -225,8 +226,9 @@ size_t fa_bwd_gqa_workspace_bytes(int B, int Sq, int Sk, int H, int Hk, int D, i
 /*
  * Backward attention: (dq, dk, dv) of L = <o, dout> with o = fa_fwd(q,k,v),
  * given the forward's `lse`. Two launches. Causal with D = 32 or 64, and
- * causal D = 128 without the dQ query-block split (below) on grids of at
- * most three workgroups of eight waves per compute unit (unsplit):
+ * causal D = 128 on grids of at most three workgroups of eight waves per
+ * compute unit, in both cases without the dQ query-block split (see
+ * fa_bwd_gqa_workspace_bytes) and unsplit:
  * fa_bwd_preprocess's kernel (delta = rowsum(o * dout) and the row-group
  * maxima into the workspace), then one launch running every dK/dV
  * workgroup (one per key block, or two for the longest blocks when the

@@ -274,15 +274,15 @@ def _bwd_capi(do, q, k, v, o, lse, causal, ws_bytes, fill):
 # workgroups: with the workspace fa_bwd_gqa_workspace_bytes sizes, the
 # longest key blocks are swept by two workgroups whose fp32 partials the
 # second to finish adds; likewise the dQ kernel's longest query blocks,
-# whose halves the dK/dV kernel adds (every D = 128 case splits dQ, which
-# is when the D = 128 key split runs -- without it the fused launch runs
-# unsplit; the fourth case splits keys only; the second, third and fifth
-# have a ragged last query block among their split ones).
+# whose halves the dK/dV kernel adds (every case splits dQ, which is when
+# the key split runs -- without it the fused launch runs unsplit; the
+# second, third and fifth have a ragged last query block among their split
+# ones).
 @pytest.mark.parametrize("B,Sq,Sk,H,Hk,D,dtype", [
     (1, 2048, 2048, 4, 4, 128, torch.float16),
     (1, 2100, 2400, 4, 2, 128, torch.float16),    # grouped heads, offset 300, ragged split block
     (1, 2100, 2100, 2, 2, 128, torch.bfloat16),   # ragged last key block (unsplit)
-    (1, 2048, 2048, 16, 16, 64, torch.float16),
+    (1, 2048, 2048, 8, 8, 64, torch.float16),
     (1, 1500, 2048, 16, 4, 64, torch.bfloat16),   # grouped heads, offset 548
     (2, 2048, 2048, 2, 2, 128, torch.float16),     # batch 2: slots and dQ rows per (b, h)
     (2, 2048, 2048, 4, 2, 64, torch.float16),      # batch 2, grouped heads

@@ -114,8 +114,8 @@ def test_split_workspace_bytes(lib):
     128 causal grids of at most one
     round of resident workgroups (one per CU at D = 128, three at D = 64;
     256 CUs here: without a GPU the count defaults to MI355X's) whose
-    longest sweep has at least 32 query tiles -- at D = 128 only beside the
-    dQ split (without it the fused launch runs, unsplit)."""
+    longest sweep has at least 32 query tiles -- the key-block split only
+    beside the dQ split (without it the fused launch runs, unsplit)."""
     mini = lib.fa_bwd_workspace_bytes(1, 4096, 8, 128)
     # (1,4096,8,128) causal: no dQ split (64 blocks x 8 heads is a full
     # round), so the fused D = 128 launch, unsplit: the minimum
@@ -135,11 +135,19 @@ def test_split_workspace_bytes(lib):
     assert lib.fa_bwd_gqa_workspace_bytes(1, 4096, 4096, 8, 8, 128, 0) == mini   # non-causal
     assert lib.fa_bwd_gqa_workspace_bytes(1, 4096, 4096, 16, 16, 64, 1) == \
         lib.fa_bwd_workspace_bytes(1, 4096, 16, 64)          # D = 64: 1024 blocks > 3 per CU
-    # (1,4096,8,64) causal: 64-key blocks x 8 heads = 512, one round at three
-    # per CU; blocks with more than 64 / 3 = 21 tiles (kt < 43) split
-    slots64 = 43 * 8
+    # (1,4096,8,64) causal: no dQ split (64 x 8 blocks are more than half a
+    # round), so the fused launch, unsplit: the minimum
     assert lib.fa_bwd_gqa_workspace_bytes(1, 4096, 4096, 8, 8, 64, 1) == \
-        lib.fa_bwd_workspace_bytes(1, 4096, 8, 64) + 1536 + slots64 * 2 * 2 * 64 * 64 * 4
+        lib.fa_bwd_workspace_bytes(1, 4096, 8, 64)
+    # (1,4096,4,64): the dQ split (64-row blocks x 4 heads, half a round at
+    # three per CU; the last 43 with more than 21 key tiles, 2 x 64 x 64
+    # fp32 each) and beside it the key-block split (64-key blocks x 4
+    # heads, those with more than 21 query tiles, kt < 43: 2 x 2 x 64 x 64
+    # fp32 each, 172 counters rounded up to 768 B)
+    slots64 = 43 * 4
+    assert lib.fa_bwd_gqa_workspace_bytes(1, 4096, 4096, 4, 4, 64, 1) == \
+        lib.fa_bwd_workspace_bytes(1, 4096, 4, 64) + 768 + slots64 * 2 * 2 * 64 * 64 * 4 + \
+        slots64 * 2 * 64 * 64 * 4
     assert lib.fa_bwd_gqa_workspace_bytes(1, 4096, 4096, 8, 8, 32, 1) == \
         lib.fa_bwd_workspace_bytes(1, 4096, 8, 32)                                 # D = 32
     assert lib.fa_bwd_gqa_workspace_bytes(1, 4096, 4096, 16, 16, 128, 1) == \
