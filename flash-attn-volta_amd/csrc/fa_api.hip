@@ -945,6 +945,7 @@ struct DqSplit {
   int nblocks = 0;     // query blocks per (b, h)
   int64_t slots = 0;   // split * B * H
   int d = 0;
+  int64_t sweep = 0;   // key tiles the last query block sweeps
 };
 
 DqSplit dq_split_plan(const Shape &s, int causal) {
@@ -978,6 +979,7 @@ DqSplit dq_split_plan(const Shape &s, int causal) {
   p.nblocks = (int)nq;
   p.slots = n * bh;
   p.d = s.D;
+  p.sweep = tmax;
   return p;
 }
 
@@ -1008,9 +1010,17 @@ bool bwd_fused(const Shape &s, int causal, const DqSplit &qplan) {
 
 // Both backward splits for these sizes (what fa_bwd_gqa_workspace_bytes
 // makes room for): the dQ split, and the key-block split beside it (the
-// fused launch runs unsplit).
+// fused launch runs unsplit).  Where the fused launch can run instead, the
+// dQ split runs only on sweeps of at least 64 key tiles; on shorter ones
+// the fused launch is faster (same-process A/B of the backward, fused
+// against the dQ split: (1,2048,8,64) -9.4 %, (2,2048,4,64) -9.0 %,
+// (1,2048,8,128) -5.4 %, (1,2048,4,64) -4.6 %, (1,2048,4,128) -1.6 %,
+// (2,2048,2,128) -1.5 %; at 64 tiles and more it is slower: (1,4096,4,64)
+// +4.1 %, (1,4096,2,64) +6.9 %, (1,4096,4,128) +6.3 %, (1,8192,2,128)
+// +14.9 %).
 void bwd_plans(const Shape &s, int causal, DkdvSplit &plan, DqSplit &qplan) {
   qplan = dq_split_plan(s, causal);
+  if (qplan.split != 0 && qplan.sweep < 64 && bwd_fused(s, causal, DqSplit{})) qplan = DqSplit{};
   plan = bwd_fused(s, causal, qplan) ? DkdvSplit{} : dkdv_split_plan(s, causal);
 }
 

@@ -275,17 +275,17 @@ def _bwd_capi(do, q, k, v, o, lse, causal, ws_bytes, fill):
 # longest key blocks are swept by two workgroups whose fp32 partials the
 # second to finish adds; likewise the dQ kernel's longest query blocks,
 # whose halves the dK/dV kernel adds (every case splits dQ, which is when
-# the key split runs -- without it the fused launch runs unsplit; the
-# second, third and fifth have a ragged last query block among their split
-# ones).
+# the key split runs -- without it the fused launch runs unsplit, as it
+# does on sweeps under 64 key tiles; the second, third and fifth have a
+# ragged last query block among their split ones).
 @pytest.mark.parametrize("B,Sq,Sk,H,Hk,D,dtype", [
-    (1, 2048, 2048, 4, 4, 128, torch.float16),
-    (1, 2100, 2400, 4, 2, 128, torch.float16),    # grouped heads, offset 300, ragged split block
-    (1, 2100, 2100, 2, 2, 128, torch.bfloat16),   # ragged last key block (unsplit)
-    (1, 2048, 2048, 8, 8, 64, torch.float16),
-    (1, 1500, 2048, 16, 4, 64, torch.bfloat16),   # grouped heads, offset 548
-    (2, 2048, 2048, 2, 2, 128, torch.float16),     # batch 2: slots and dQ rows per (b, h)
-    (2, 2048, 2048, 4, 2, 64, torch.float16),      # batch 2, grouped heads
+    (1, 4096, 4096, 4, 4, 128, torch.float16),
+    (1, 3000, 4200, 4, 2, 128, torch.float16),    # grouped heads, offset 1200, ragged split block
+    (1, 4100, 4100, 2, 2, 128, torch.bfloat16),   # ragged last key block (unsplit)
+    (1, 4096, 4096, 4, 4, 64, torch.float16),
+    (1, 3000, 4096, 8, 2, 64, torch.bfloat16),    # grouped heads, offset 1096
+    (2, 4096, 4096, 2, 2, 128, torch.float16),     # batch 2: slots and dQ rows per (b, h)
+    (2, 4096, 4096, 2, 1, 64, torch.float16),      # batch 2, grouped heads
 ])
 def test_backward_causal_key_block_split(B, Sq, Sk, H, Hk, D, dtype):
     from flash_attn_volta import _capi, flash_attn_forward_gqa
@@ -370,6 +370,7 @@ def _bwd_three_launches(do, q, k, v, o, lse, causal, sm_scale):
 @pytest.mark.parametrize("B,S,H,D,sm_scale,in_scale", [
     (1, 4096, 16, 64, None, 0.5),
     (4, 2048, 16, 64, None, 1.0),
+    (1, 2048, 8, 64, None, 1.0),       # half a round: fused in place of the dQ split
     (2, 1000, 8, 64, 1.0, 0.35),
     (4, 512, 4, 32, None, 1.0),
     (8, 1024, 32, 32, None, 1.0),
