@@ -986,14 +986,16 @@ DqSplit dq_split_plan(const Shape &s, int causal) {
 // The fused backward launch (fa::fa_bwd_fused_kernel) runs the causal
 // backwards without the dQ split (whose halves the dK/dV kernel adds after
 // the dQ kernel), unsplit: every D = 32 / 64 one, and the D = 128 ones
-// whose eight-wave dK/dV grid is at most three rounds.  `qplan` is the dQ
+// whose eight-wave dK/dV grid is at most four rounds.  `qplan` is the dQ
 // split that will run (none without the workspace for it), so
 // fa_bwd_blocks, which never splits, takes the path fa_bwd takes with the
 // minimum workspace.  Measured (same-process A/B of the backward):
 //   against the dQ kernel (delta folded in) then the dK/dV kernel, D = 128:
 //   (1,2048,16,128) -18.6 %, (2,1100,32,128) -2.7 %, (1,4096,16,128)
-//   -1.6 %; on (4,4096,16,128) (eight rounds) the separate pre-pass over O
-//   and dO costs more than the fusion saves (+1.8 %);
+//   -1.6 %, (2,4096,16,128) (four rounds) -1.0 %, (1,8192,16,128) -1.9 %;
+//   on six rounds and more the separate pre-pass over O and dO costs more
+//   than the fusion saves ((3,4096,16,128) +2.5 %, (6,1100,32,128)
+//   +5.5 %, (4,4096,16,128) +2.0 %);
 //   against the key-block split (inside the fused launch at D = 64, beside
 //   it at D = 128) on grids of one round: (1,2048,16,64) -13.2 %,
 //   (1,4096,8,64) -2.9 %, (1,4096,8,128) -9.9 %, (1,8192,4,128) -7.5 %,
@@ -1005,7 +1007,7 @@ bool bwd_fused(const Shape &s, int causal, const DqSplit &qplan) {
   if (s.D <= 64) return true;
   using T = fa::DkdvTile<128, 1>;
   const int64_t blocks = (s.Sk + T::BK - 1) / T::BK * ((int64_t)s.B * s.Hk);
-  return blocks <= 3 * (int64_t)device_cus();
+  return blocks <= 4 * (int64_t)device_cus();
 }
 
 // Both backward splits for these sizes (what fa_bwd_gqa_workspace_bytes

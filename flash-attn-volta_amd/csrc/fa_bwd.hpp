@@ -12,7 +12,7 @@
 //                            _fa_bwd_dkdv_kernel_*, :319-580)
 // and delta = rowsum(dO * O) in fp32 (the torch op at :650).  fa_bwd runs
 // them as
-//   causal, D <= 64, and causal D = 128 on grids of at most three rounds
+//   causal, D <= 64, and causal D = 128 on grids of at most four rounds
 //   without the dQ split:
 //                    fa_bwd_preprocess_kernel (delta), then ONE launch of
 //                    fa_bwd_fused_kernel, every dK/dV block and then every

@@ -227,7 +227,7 @@ size_t fa_bwd_gqa_workspace_bytes(int B, int Sq, int Sk, int H, int Hk, int D, i
 /*
  * Backward attention: (dq, dk, dv) of L = <o, dout> with o = fa_fwd(q,k,v),
  * given the forward's `lse`. Two launches. Causal with D = 32 or 64, and
- * causal D = 128 on grids of at most three workgroups of eight waves per
+ * causal D = 128 on grids of at most four workgroups of eight waves per
  * compute unit, in both cases without the dQ query-block split (see
  * fa_bwd_gqa_workspace_bytes) and unsplit:
  * fa_bwd_preprocess's kernel (delta = rowsum(o * dout) and the row-group

@@ -377,6 +377,7 @@ def _bwd_three_launches(do, q, k, v, o, lse, causal, sm_scale):
     (1, 4096, 16, 128, None, 0.5),
     (2, 1100, 32, 128, None, 1.0),
     (1, 2048, 16, 128, 1.0, 0.35),
+    (2, 2048, 32, 128, None, 1.0),     # four rounds of D = 128 dK/dV blocks, still fused
 ])
 def test_backward_fused_launch_matches_three_launches(B, S, H, D, sm_scale, in_scale):
     from flash_attn_volta import flash_attn_backward, flash_attn_forward
