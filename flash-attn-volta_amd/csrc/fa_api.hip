@@ -1013,16 +1013,19 @@ bool bwd_fused(const Shape &s, int causal, const DqSplit &qplan) {
 // Both backward splits for these sizes (what fa_bwd_gqa_workspace_bytes
 // makes room for): the dQ split, and the key-block split beside it (the
 // fused launch runs unsplit).  Where the fused launch can run instead, the
-// dQ split runs only on sweeps of at least 64 key tiles; on shorter ones
-// the fused launch is faster (same-process A/B of the backward, fused
-// against the dQ split: (1,2048,8,64) -9.4 %, (2,2048,4,64) -9.0 %,
-// (1,2048,8,128) -5.4 %, (1,2048,4,64) -4.6 %, (1,2048,4,128) -1.6 %,
-// (2,2048,2,128) -1.5 %; at 64 tiles and more it is slower: (1,4096,4,64)
-// +4.1 %, (1,4096,2,64) +6.9 %, (1,4096,4,128) +6.3 %, (1,8192,2,128)
-// +14.9 %).
+// dQ split runs only on sweeps of at least 64 key tiles (48 at D = 128);
+// on shorter ones the fused launch is faster (same-process A/B of the
+// backward, fused against the dQ split: (1,2048,8,64) -9.4 %,
+// (2,2048,4,64) -9.0 %, (1,3072,8,64) -6.9 %, (1,2048,4,64) -4.6 %,
+// (1,3072,4,64) -1.2 %, (1,2048,8,128) -5.4 %, (1,2048,4,128) -1.6 %,
+// (2,2048,2,128) -1.5 %); from there on it is slower ((1,3072,4,128)
+// +2.6 %, (1,3072,2,128) +7.7 %, (1,4096,4,64) +4.1 %, (1,4096,2,64)
+// +6.9 %, (1,4096,4,128) +6.3 %, (1,8192,2,128) +14.9 %).
 void bwd_plans(const Shape &s, int causal, DkdvSplit &plan, DqSplit &qplan) {
   qplan = dq_split_plan(s, causal);
-  if (qplan.split != 0 && qplan.sweep < 64 && bwd_fused(s, causal, DqSplit{})) qplan = DqSplit{};
+  const int64_t min_sweep = s.D >= 128 ? 48 : 64;
+  if (qplan.split != 0 && qplan.sweep < min_sweep && bwd_fused(s, causal, DqSplit{}))
+    qplan = DqSplit{};
   plan = bwd_fused(s, causal, qplan) ? DkdvSplit{} : dkdv_split_plan(s, causal);
 }
 

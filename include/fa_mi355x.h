@@ -207,7 +207,7 @@ size_t fa_bwd_workspace_bytes(int B, int S, int H, int D);
  * fastest schedule for these sizes (0 on bad sizes): the
  * fa_bwd_workspace_bytes minimum plus, for causal D = 64 / 128 problems
  * whose dQ grid is at most half a round of resident workgroups (and whose
- * last query block sweeps at least 64 key tiles where the fused launch
+ * last query block sweeps at least 64 key tiles, 48 at D = 128, where the fused launch
  * below could run instead), room for the query-block split of the dQ kernel (its longest query blocks swept
  * by two workgroups, fp32 halves added by the dK/dV kernel) and, when the
  * key blocks fit one round, for the key-block split beside it (the

@@ -114,8 +114,8 @@ def test_split_workspace_bytes(lib):
     128 causal grids of at most one
     round of resident workgroups (one per CU at D = 128, three at D = 64;
     256 CUs here: without a GPU the count defaults to MI355X's) whose
-    longest sweep has at least 32 query tiles (64 where the fused launch
-    could run instead) -- the key-block split only beside the dQ split
+    longest sweep has at least 32 query tiles (64, or 48 at D = 128, where
+    the fused launch could run instead) -- the key-block split only beside the dQ split
     (without it the fused launch runs, unsplit)."""
     mini = lib.fa_bwd_workspace_bytes(1, 4096, 8, 128)
     # (1,4096,8,128) causal: no dQ split (64 blocks x 8 heads is a full
@@ -162,10 +162,13 @@ def test_split_workspace_bytes(lib):
         lib.fa_bwd_workspace_bytes(1, 3000, 4, 128)
     # dQ grids of half a round whose last block sweeps under 64 key tiles:
     # the fused launch, unsplit, in place of the dQ split
-    for B, S, H, D in ((1, 2048, 8, 64), (2, 2048, 4, 64), (1, 2048, 8, 128),
-                       (1, 2048, 4, 128)):
+    # (under 48 at D = 128)
+    for B, S, H, D in ((1, 2048, 8, 64), (2, 2048, 4, 64), (1, 3072, 8, 64),
+                       (1, 2048, 8, 128), (1, 2048, 4, 128)):
         assert lib.fa_bwd_gqa_workspace_bytes(B, S, S, H, H, D, 1) == \
             lib.fa_bwd_workspace_bytes(B, S, H, D)
+    assert lib.fa_bwd_gqa_workspace_bytes(1, 3072, 3072, 4, 4, 128, 1) > \
+        lib.fa_bwd_workspace_bytes(1, 3072, 4, 128)                               # 48 tiles
     assert lib.fa_bwd_gqa_workspace_bytes(1, 2100, 2400, 4, 2, 128, 1) == \
         lib.fa_bwd_workspace_bytes(1, 2100, 4, 128)
     assert lib.fa_bwd_gqa_workspace_bytes(1, 700, 1000, 8, 2, 128, 1) == \
