@@ -152,7 +152,7 @@ size_t fa_fwd_splitkv_workspace_bytes(int B, int Sq, int Sk, int H, int Hk, int 
  * plus `workspace`, `workspace_bytes`.
  *   - Short query blocks against long keys: fa_fwd_splitkv's key split.
  *   - Causal, Sq == Sk, at least 64 query tiles of 64 rows per head and at
- *     most one tile per compute unit in the plain grid: query tiles paired
+ *     most 1.5 tiles per compute unit in the plain grid: query tiles paired
  *     light with heavy (tile p with tile nb - 1 - p), each pair cut in
  *     three work items of about a third of the pair each (the heavy tile's
  *     two key halves, the light tile); the heavy tile's halves go to the
