@@ -663,7 +663,7 @@ int run_fwd_splitkv(const void *q, const void *k, const void *v, void *o, float 
 // largest first, the split heavy tiles' halves merged by
 // fa_fwd_combine_kernel (pair mode).  For square causal grids (Sq == Sk)
 // with at least kBalMinTiles 64-row tiles per head whose plain grid is at
-// most one workgroup per CU, or 1.5 from 64 tiles per head.  There the plain schedule ends on single
+// most half a workgroup per CU, one from 48 tiles per head, 1.5 from 64.  There the plain schedule ends on single
 // workgroups sweeping every key tile alone (a lone workgroup's sweep runs
 // at about 90 % of a CU's two-workgroup throughput, so splitting it is what
 // shortens the kernel).  Measured on MI355X against the plain schedule
@@ -672,13 +672,15 @@ int run_fwd_splitkv(const void *q, const void *k, const void *v, void *o, float 
 // per CU (1, 4096, 5, 128) -16 %, (1, 4096, 6, 128) -11 %,
 // (1, 4096, 6, 64) -11 %, (1, 8192, 3, 128) -19 %; at 48 tiles per head
 // (1, 3072, 2, 128) -21 %, (1, 3072, 4, 128) -13 %, (1, 3072, 4, 64) -8 %,
-// but (1, 3072, 8, 64) (1.5 per CU) +4 %; with fewer tiles per head or two
-// workgroups per CU it loses (+3 to +50 %: every work item
+// but (1, 3072, 8, 64) (1.5 per CU) +4 %; at 32 tiles per head and half a
+// tile per CU (1, 2048, 2, 128) -12 %, (1, 2048, 4, 128) -9 %,
+// (2, 2048, 2, 128) -8 %, (1, 2048, 2, 64) -4 %; with fewer tiles per head
+// or more workgroups per CU it loses (+3 to +50 %: every work item
 // pays a workgroup's start-up of several microseconds, and the merge
 // launch costs about 4 us): (1, 2048, 8, 128) +3 %, (1, 4096, 8, 128)
 // +6 to +12 %, (1, 4096, 8, 64) +10 %, (4, 512, 4, 32) +50 %.
 
-constexpr int kBalMinTiles = 48;
+constexpr int kBalMinTiles = 32;
 
 struct BalPlan {
   int nb;   // 64-row query tiles per (b, h); 0: the balanced schedule does not apply
@@ -691,7 +693,7 @@ BalPlan bal_plan(const Shape &s, int causal) {
   const int64_t grid = (int64_t)nb * s.B * s.H;
   if (nb < kBalMinTiles) return BalPlan{0};
   const int64_t cus = device_cus();
-  if (nb >= 64 ? 2 * grid > 3 * cus : grid > cus) return BalPlan{0};
+  if (nb >= 64 ? 2 * grid > 3 * cus : nb >= 48 ? grid > cus : 2 * grid > cus) return BalPlan{0};
   return BalPlan{nb};
 }
 

@@ -151,9 +151,9 @@ size_t fa_fwd_splitkv_workspace_bytes(int B, int Sq, int Sk, int H, int Hk, int 
  * Same arguments and results as fa_fwd_gqa (to fp32 rounding of a merge),
  * plus `workspace`, `workspace_bytes`.
  *   - Short query blocks against long keys: fa_fwd_splitkv's key split.
- *   - Causal, Sq == Sk, at least 48 query tiles of 64 rows per head and at
- *     most one tile per compute unit in the plain grid (1.5 from 64 tiles
- *     per head): query tiles paired
+ *   - Causal, Sq == Sk, at least 32 query tiles of 64 rows per head and at
+ *     most half a tile per compute unit in the plain grid (one from 48
+ *     tiles per head, 1.5 from 64): query tiles paired
  *     light with heavy (tile p with tile nb - 1 - p), each pair cut in
  *     three work items of about a third of the pair each (the heavy tile's
  *     two key halves, the light tile); the heavy tile's halves go to the
