@@ -663,14 +663,15 @@ int run_fwd_splitkv(const void *q, const void *k, const void *v, void *o, float 
 // largest first, the split heavy tiles' halves merged by
 // fa_fwd_combine_kernel (pair mode).  For square causal grids (Sq == Sk)
 // with at least kBalMinTiles 64-row tiles per head whose plain grid is at
-// most half a workgroup per CU, one from 48 tiles per head, 1.5 from 64.  There the plain schedule ends on single
+// most half a workgroup per CU, one from 48 tiles per head, 1.75 from 64.  There the plain schedule ends on single
 // workgroups sweeping every key tile alone (a lone workgroup's sweep runs
 // at about 90 % of a CU's two-workgroup throughput, so splitting it is what
 // shortens the kernel).  Measured on MI355X against the plain schedule
 // (merge included): (1, 4096, 4, 128) -17 %, (1, 4096, 2, 128) -26 %,
 // (1, 8192, 2, 128) -30 %, (1, 4096, 4, 64) -15 %, and at 1.25 - 1.5 tiles
 // per CU (1, 4096, 5, 128) -16 %, (1, 4096, 6, 128) -11 %,
-// (1, 4096, 6, 64) -11 %, (1, 8192, 3, 128) -19 %; at 48 tiles per head
+// (1, 4096, 6, 64) -11 %, (1, 8192, 3, 128) -19 %, at 1.75
+// (1, 4096, 7, 64) -16 %, (1, 4096, 7, 128) -2.5 %; at 48 tiles per head
 // (1, 3072, 2, 128) -21 %, (1, 3072, 4, 128) -13 %, (1, 3072, 4, 64) -8 %,
 // but (1, 3072, 8, 64) (1.5 per CU) +4 %; at 32 tiles per head and half a
 // tile per CU (1, 2048, 2, 128) -12 %, (1, 2048, 4, 128) -9 %,
@@ -693,7 +694,7 @@ BalPlan bal_plan(const Shape &s, int causal) {
   const int64_t grid = (int64_t)nb * s.B * s.H;
   if (nb < kBalMinTiles) return BalPlan{0};
   const int64_t cus = device_cus();
-  if (nb >= 64 ? 2 * grid > 3 * cus : nb >= 48 ? grid > cus : 2 * grid > cus) return BalPlan{0};
+  if (nb >= 64 ? 4 * grid > 7 * cus : nb >= 48 ? grid > cus : 2 * grid > cus) return BalPlan{0};
   return BalPlan{nb};
 }
 

@@ -153,7 +153,7 @@ size_t fa_fwd_splitkv_workspace_bytes(int B, int Sq, int Sk, int H, int Hk, int 
  *   - Short query blocks against long keys: fa_fwd_splitkv's key split.
  *   - Causal, Sq == Sk, at least 32 query tiles of 64 rows per head and at
  *     most half a tile per compute unit in the plain grid (one from 48
- *     tiles per head, 1.5 from 64): query tiles paired
+ *     tiles per head, 1.75 from 64): query tiles paired
  *     light with heavy (tile p with tile nb - 1 - p), each pair cut in
  *     three work items of about a third of the pair each (the heavy tile's
  *     two key halves, the light tile); the heavy tile's halves go to the

@@ -313,7 +313,7 @@ def test_fwd_workspace_plan_and_validation(lib):
     """fa_fwd_ws: the workspace query (256 compute units assumed on the CPU)
     is the split-KV size for decode shapes, the balanced causal size for
     square causal grids of at least 32 tiles per head and at most half a
-    tile per CU (one from 48 tiles per head, 1.5 from 64),
+    tile per CU (one from 48 tiles per head, 1.75 from 64),
     0 otherwise; a call that would use a workspace rejects a misaligned one
     before any HIP call."""
     ws = lib.fa_fwd_workspace_bytes
@@ -326,7 +326,8 @@ def test_fwd_workspace_plan_and_validation(lib):
     assert ws(1, 4096, 4096, 4, 4, 128, 0) == 0  # not causal
     assert ws(1, 4096, 4096, 8, 8, 128, 1) == 0  # two tiles per CU (config C4b)
     assert ws(1, 4096, 4096, 6, 6, 128, 1) > n    # 1.5 tiles per CU
-    assert ws(1, 4096, 4096, 7, 7, 128, 1) == 0   # 1.75
+    assert ws(1, 4096, 4096, 7, 7, 128, 1) > n    # 1.75
+    assert ws(1, 8192, 8192, 4, 4, 128, 1) == 0   # 2
     assert ws(1, 2048, 2048, 4, 4, 128, 1) > 0   # 32 tiles, half a tile per CU
     assert ws(1, 2048, 2048, 8, 8, 128, 1) == 0  # 32 tiles, one per CU
     assert ws(1, 1984, 1984, 2, 2, 128, 1) == 0  # 31 tiles per head: too few

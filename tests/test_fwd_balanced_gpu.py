@@ -1,6 +1,6 @@
 """The balanced causal forward (fa_fwd_ws on square causal grids of at least 32
 query tiles per head and at most half a tile per compute unit, one from 48
-tiles per head, 1.5 from 64) against the float64 oracle and against the
+tiles per head, 1.75 from 64) against the float64 oracle and against the
 plain schedule.
 
 The schedule pairs light causal query tiles with heavy ones, cuts each
@@ -31,6 +31,7 @@ CASES = [
     # B, S, H, Hk, D, dtype, sm_scale
     (1, 4096, 4, 4, 128, torch.float16, None),     # 64 tiles x 4 heads: one per CU
     (1, 4096, 6, 3, 128, torch.float16, None),     # 1.5 tiles per CU, grouped heads
+    (1, 4096, 7, 7, 64, torch.bfloat16, None),     # 1.75 tiles per CU
     (1, 3100, 3, 3, 64, torch.float16, None),      # 49 tiles: odd, ragged, under 64
     (2, 2048, 2, 1, 128, torch.float16, None),     # 32 tiles, half a tile per CU, grouped
     (1, 4100, 2, 2, 64, torch.float16, None),      # 65 tiles: odd middle tile, ragged
